@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X selective-scan hot path.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]``
+
+One "step" is one forward selective scan over BASELINE config 2 (the headline: Mamba-2.8B layer
+shape, batch 4, d_inner 5120, L 4096, dstate 16, bf16 in / fp32 accumulate, z gate, delta_bias +
+softplus, last state returned), with all inputs resident in HBM before timing starts. ``value``
+is the algorithmic HBM throughput of that step (bytes of u, delta, z, B, C, A, D, delta_bias read
+and out_z, last_state written, each once) divided by the measured time per step, in GB/s.
+
+The JSON line also carries: ``roofline`` for the forward-scan kernel (HBM bound, 8 TB/s peak),
+``cpu_baseline`` (the CPU oracle timed on the host on a bounded sample of the same workload),
+per-config results for configs 1 and 3 and decode tokens/s for config 4 (unless --quick).
+Only one GPU is used; --gpus N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [REPO, os.path.join(REPO, "motif-mamba_amd")]
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "selective-scan fwd GB/s & % of binding roofline; decode tokens/s, 1 GPU"
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _time_loop(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step (events on the launch stream)
+
+
+def bench_scan(cfg_name, steps, warmup, torch, rotate=1):
+    from motif_mamba_amd import selective_scan_fn
+    from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_bytes, scan_inputs, scan_transcendentals
+    c = SCAN_CONFIGS[cfg_name]
+    sets = []
+    for r in range(rotate):
+        cc = c if r == 0 else type(c)(**{**c.__dict__, "seed": c.seed + 100 * r})
+        sets.append(scan_inputs(cc, device="cuda"))
+    in_bytes = 2 if c.dtype in ("bf16", "fp16") else 4
+
+    def step(i):
+        selective_scan_fn(**sets[i % rotate])
+
+    ms = _time_loop(step, steps, warmup, torch)
+    nbytes = scan_bytes(c.batch, c.dim, c.seqlen, c.dstate, c.n_groups, in_bytes)
+    trans = scan_transcendentals(c.batch, c.dim, c.seqlen, c.dstate)
+    elems = c.batch * c.dim * c.seqlen
+    del sets
+    torch.cuda.empty_cache()
+    return {
+        "shape": [c.batch, c.dim, c.seqlen, c.dstate], "n_groups": c.n_groups, "dtype": c.dtype,
+        "ms": ms, "GB_s": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
+        "elements_per_s": elems / (ms * 1e-3), "state_updates_per_s": elems * c.dstate / (ms * 1e-3),
+        "trans_per_s": trans / (ms * 1e-3), "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "input_rotation": rotate,
+    }
+
+
+def bench_decode(batch, steps, warmup, torch, sets_max=64):
+    from motif_mamba_amd import selective_state_update
+    from motif_mamba_amd.workloads import DECODE_CONFIGS, decode_bytes
+    c = DECODE_CONFIGS[f"cfg4_b{batch}"]
+    dt = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(c.seed)
+    S = min(steps, sets_max)
+    state = torch.randn(batch, c.dim, c.dstate, device="cuda", generator=g) * 0.1
+    x = torch.randn(S, batch, c.dim, device="cuda", generator=g).to(dt)
+    dts = torch.randn(S, batch, c.dim, device="cuda", generator=g).to(dt)
+    z = torch.randn(S, batch, c.dim, device="cuda", generator=g).to(dt)
+    B = torch.randn(S, batch, c.dstate, device="cuda", generator=g).to(dt)
+    C = torch.randn(S, batch, c.dstate, device="cuda", generator=g).to(dt)
+    A = -torch.arange(1, c.dstate + 1, dtype=torch.float32, device="cuda").repeat(c.dim, 1).contiguous()
+    D = torch.ones(c.dim, device="cuda")
+    bias = torch.empty(c.dim, device="cuda").uniform_(-6.907755, -2.302585, generator=g)
+
+    def step(i):
+        j = i % S
+        selective_state_update(state, x[j], dts[j], A, B[j], C[j], D, z[j], bias, True)
+
+    ms = _time_loop(step, steps, warmup, torch)
+    nbytes = decode_bytes(batch, c.dim, c.dstate)
+    return {"batch": batch, "dim": c.dim, "dstate": c.dstate, "steps": steps, "us_per_step": ms * 1e3,
+            "tokens_per_s": batch / (ms * 1e-3), "GB_s": nbytes / (ms * 1e-3) / 1e9,
+            "note": "state (batch*5120*16*4 B) fits the 256 MB Infinity Cache; GB/s may exceed HBM peak"}
+
+
+def cpu_baseline(torch, seconds_target=15.0):
+    """The CPU oracle (torch restatement of selective_scan_ref) on a bounded sample of config 2:
+    one batch row and a slice of channels at the full L = 4096, scaled to GB/s of the config's
+    algorithmic bytes per element."""
+    from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_bytes, scan_inputs
+    from oracle.ssm_ref import selective_scan_ref
+    c = SCAN_CONFIGS["cfg2"]
+    threads = torch.get_num_threads()
+    dims = 64
+    inputs = scan_inputs(c, batch=1, dim=dims)
+    inputs.pop("return_last_state")
+    t0 = time.time()
+    selective_scan_ref(**inputs, return_last_state=True)
+    t1 = time.time() - t0
+    reps = max(1, int(seconds_target / max(t1, 1e-3)))
+    t0 = time.time()
+    for _ in range(reps):
+        selective_scan_ref(**inputs, return_last_state=True)
+    per = (time.time() - t0) / reps
+    frac = (1 * dims) / (c.batch * c.dim)
+    nbytes = scan_bytes(c.batch, c.dim, c.seqlen, c.dstate, c.n_groups, 2) * frac
+    return {"value": nbytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 shape restricted to batch 1 x {dims} channels x L {c.seqlen} "
+                      f"(1/{int(1 / frac)} of the work), {reps} timed run(s) of {per:.3f}s; "
+                      f"oracle/ssm_ref.selective_scan_ref, torch {torch.__version__} on "
+                      f"{platform.processor() or platform.machine()} with {threads} threads"}
+
+
+def _traffic():
+    path = os.path.join(REPO, "profiles", "traffic_cfg2.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--quick", action="store_true", help="headline config only (no secondary configs)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from motif_mamba_amd import _native
+    _native.ext()  # the HIP library must be present: no fallback path exists
+    torch.cuda.init()
+    _log(f"device: {torch.cuda.get_device_name(0)}")
+
+    _log("config 2 (headline)")
+    head = bench_scan("cfg2", args.steps, args.warmup, torch)
+    extra = {}
+    if not args.quick:
+        _log("config 1 (rotating 2 input sets: 2 x 203 MB > Infinity Cache)")
+        extra["cfg1"] = bench_scan("cfg1", max(5, args.steps), 2, torch, rotate=2)
+        for name in ("cfg3_g1", "cfg3_g4"):
+            _log(f"config 3 ({name})")
+            extra[name] = bench_scan(name, max(3, args.steps // 4), 1, torch)
+        for b in (1, 64, 256):
+            _log(f"config 4 decode batch {b}")
+            extra[f"cfg4_b{b}"] = bench_decode(b, 1024, 16, torch)
+    cpu = None
+    if not args.no_cpu:
+        _log("CPU baseline (oracle on a bounded sample)")
+        cpu = cpu_baseline(torch)
+
+    value = head["GB_s"]
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(head["ms"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "cfg2: selective_scan_fn fwd, Mamba-2.8B layer (batch 4, d_inner 5120, "
+                               "L 4096, dstate 16, bf16, z gate, delta_bias+softplus, last_state)",
+                   "batch": 4, "dim": 5120, "seqlen": 4096, "dstate": 16, "n_groups": 1, "io_dtype": "bf16"},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": _traffic()},
+        "cpu_baseline": cpu,
+        "headline_detail": head,
+        "configs": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * mm_scan.h -- C ABI of the MI355X (gfx950) selective-scan library `libmm_scan.so`.
+ *
+ * Two entry points replace the two native calls on the Mamba selective-scan hot path:
+ *
+ *   mm_scan_fwd      replaces the pybind call `selective_scan_cuda.fwd(u, delta, A, B, C, D, z,
+ *                    delta_bias, P, Q, gamma, delta_softplus)` bound at
+ *                    csrc/selective_scan/selective_scan.cpp:620-627, i.e. selective_scan_fwd
+ *                    (selective_scan.cpp:270-413) -> selective_scan_fwd_cuda
+ *                    (selective_scan_fwd_kernel.cuh:593-623) for real A without P/Q/gamma.
+ *                    The parameter block mirrors SSMParamsBase (selective_scan.h:26-82) but with
+ *                    int64 element strides instead of uint32.
+ *
+ *   mm_state_update  replaces `selective_state_update(state, x, dt, A, B, C, D, z, dt_bias,
+ *                    dt_softplus)` as called at mamba_ssm/modules/mamba_simplemotif.py:397-399
+ *                    (upstream mamba_ssm.ops.triton.selective_state_update, not vendored in the
+ *                    reference; its in-tree math is mamba_simplemotif.py:369-376).
+ *
+ * Conventions
+ *   - All pointers are device pointers (HBM) except the parameter blocks themselves, which are
+ *     read on the host during the call and may be freed as soon as the call returns.
+ *   - Strides are in elements, not bytes. The innermost (sequence) dimension of u, delta, z,
+ *     out, out_z and of variable B/C must be contiguous (stride 1), as the reference requires
+ *     (selective_scan.cpp:304-305, 321, 326, 350).
+ *   - The library never allocates, frees or synchronises. Every call enqueues its kernels on
+ *     `stream` (a hipStream_t; NULL = the null stream of the current device) and returns.
+ *   - Return value: 0 on success. MM_ERR_INVALID_ARGUMENT (-1) when the parameter block fails
+ *     validation (nothing is launched), MM_ERR_UNSUPPORTED (-2) for a valid request this build
+ *     does not implement, otherwise the positive hipError_t of the failed launch.
+ *     mm_last_error() returns a message for the most recent failure on the calling thread.
+ */
+#ifndef MM_SCAN_H_
+#define MM_SCAN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MM_SCAN_ABI_VERSION 1
+
+#define MM_OK 0
+#define MM_ERR_INVALID_ARGUMENT (-1)
+#define MM_ERR_UNSUPPORTED (-2)
+
+/* Element types of the activations (u, delta, z, out, out_z, variable B/C). A, D, delta_bias,
+ * constant B/C, last_state and chunk_states are always float32, as in the reference
+ * (selective_scan.cpp:282-292, 332-346). */
+typedef enum mm_dtype {
+    MM_FLOAT32 = 0,
+    MM_FLOAT16 = 1,
+    MM_BFLOAT16 = 2
+} mm_dtype;
+
+/* Largest state dimension accepted by mm_scan_fwd (the reference limit, selective_scan.cpp:313). */
+#define MM_SCAN_MAX_DSTATE 256
+/* Sequence-chunk length of the chunk_states wire format (selective_scan.cpp:383). */
+#define MM_SCAN_CHUNK 2048
+
+/* Forward selective scan (real A only):
+ *   delta' = softplus(delta + delta_bias)            (softplus only when delta_softplus != 0)
+ *   h_t[n] = exp(delta'_t * A[d,n]) * h_{t-1}[n] + delta'_t * u_t * B[b, g(d), n, t],  h_{-1} = 0
+ *   y_t    = sum_n h_t[n] * C[b, g(d), n, t]
+ *   out_t  = y_t + D[d] * u_t ;  out_z_t = out_t * silu(z_t)
+ * with g(d) = d / (dim / n_groups). Constant B/C (is_variable_* == 0) are (dim, dstate) float32
+ * and use B[d, n] / C[d, n] instead. */
+typedef struct mm_scan_fwd_params {
+    int64_t batch, dim, seqlen, dstate, n_groups;
+    mm_dtype itype;          /* dtype of u, delta, z, out, out_z and variable B/C */
+    int32_t is_variable_B;   /* 1: B is (batch, n_groups, dstate, seqlen) of itype; 0: (dim, dstate) f32 */
+    int32_t is_variable_C;
+    int32_t delta_softplus;
+
+    const void *u;           /* (batch, dim, seqlen) */
+    const void *delta;       /* (batch, dim, seqlen) */
+    const float *A;          /* (dim, dstate) */
+    const void *B;
+    const void *C;
+    const float *D;          /* (dim,) or NULL */
+    const void *z;           /* (batch, dim, seqlen) or NULL */
+    const float *delta_bias; /* (dim,) or NULL */
+
+    void *out;               /* (batch, dim, seqlen) pre-gate output, or NULL (not written) */
+    void *out_z;             /* (batch, dim, seqlen) gated output; required iff z != NULL */
+    float *last_state;       /* (batch, dim, dstate) contiguous, or NULL */
+    float *chunk_states;     /* (batch, dim, ceil(seqlen/2048), 2*dstate) contiguous, or NULL:
+                                per chunk the running (prod a, h) pair of the reference's `x`
+                                (selective_scan_fwd_kernel.cuh:492-495) */
+
+    int64_t u_batch_stride, u_d_stride;
+    int64_t delta_batch_stride, delta_d_stride;
+    int64_t z_batch_stride, z_d_stride;
+    int64_t out_batch_stride, out_d_stride;
+    int64_t out_z_batch_stride, out_z_d_stride;
+    int64_t A_d_stride, A_dstate_stride;
+    int64_t B_batch_stride, B_group_stride, B_dstate_stride, B_d_stride;
+    int64_t C_batch_stride, C_group_stride, C_dstate_stride, C_d_stride;
+} mm_scan_fwd_params;
+
+/* Single-token decode update, in place on `state`:
+ *   dt' = softplus(dt + dt_bias) (softplus only when dt_softplus != 0)
+ *   state[b,d,n] = state[b,d,n] * exp(dt' * A[d,n]) + dt' * B[b,g(d),n] * x[b,d]
+ *   out[b,d] = (sum_n state[b,d,n] * C[b,g(d),n] + D[d] * x[b,d]) * silu(z[b,d])
+ * state is float32; x, dt, z, out, B, C are itype; A, D, dt_bias are float32. */
+typedef struct mm_state_update_params {
+    int64_t batch, dim, dstate, n_groups;
+    mm_dtype itype;
+    int32_t dt_softplus;
+
+    float *state;            /* (batch, dim, dstate), updated in place */
+    const void *x;           /* (batch, dim) */
+    const void *dt;          /* (batch, dim) */
+    const float *A;          /* (dim, dstate) */
+    const void *B;           /* (batch, n_groups, dstate) */
+    const void *C;           /* (batch, n_groups, dstate) */
+    const float *D;          /* (dim,) or NULL */
+    const void *z;           /* (batch, dim) or NULL */
+    const float *dt_bias;    /* (dim,) or NULL */
+    void *out;               /* (batch, dim) */
+
+    int64_t state_batch_stride, state_d_stride, state_dstate_stride;
+    int64_t x_batch_stride, x_d_stride;
+    int64_t dt_batch_stride, dt_d_stride;
+    int64_t z_batch_stride, z_d_stride;
+    int64_t out_batch_stride, out_d_stride;
+    int64_t A_d_stride, A_dstate_stride;
+    int64_t B_batch_stride, B_group_stride, B_dstate_stride;
+    int64_t C_batch_stride, C_group_stride, C_dstate_stride;
+} mm_state_update_params;
+
+/* Forward scan. Replaces selective_scan_cuda.fwd (selective_scan.cpp:270-413, pybind :620-627). */
+int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream);
+
+/* Decode step. Replaces selective_state_update (call site mamba_simplemotif.py:397-399). */
+int mm_state_update(const mm_state_update_params *params, void *stream);
+
+/* Message for the last non-zero return on this thread ("" if none). */
+const char *mm_last_error(void);
+
+/* MM_SCAN_ABI_VERSION of the loaded library; lets a binding refuse a stale build. */
+int mm_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MM_SCAN_H_ */

@@ -1,0 +1,109 @@
+// mm_common.h -- device helpers shared by the gfx950 selective-scan kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mm {
+
+// ---- element types -------------------------------------------------------------------------
+struct bf16_t { uint16_t bits; };
+struct f16_t { _Float16 v; };
+
+template <typename T> struct ElemSize { static constexpr int value = sizeof(T); };
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float(uint32_t(x.bits) << 16); }
+__device__ __forceinline__ float to_f32(f16_t x) { return float(x.v); }
+
+// float -> bf16 with round-to-nearest-even (NaN kept quiet), matching torch's .to(bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return uint16_t(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return bf16_t{f32_to_bf16_bits(x)}; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return f16_t{(_Float16)x}; }
+
+// ---- math ------------------------------------------------------------------------------------
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// softplus with torch's threshold: x > 20 ? x : log1p(exp(x)).
+__device__ __forceinline__ float softplus_f32(float x) {
+    return x > 20.f ? x : log1pf(expf(x));
+}
+
+// silu(z) = z / (1 + exp(-z)), in float32.
+__device__ __forceinline__ float silu_f32(float z) { return z / (1.f + expf(-z)); }
+
+// ---- vector I/O of 8 consecutive elements (16 B for 16-bit types, 32 B for float) -----------
+template <typename T> struct Vec8;
+template <> struct Vec8<float> { uint4 lo, hi; };
+template <> struct Vec8<bf16_t> { uint4 v; };
+template <> struct Vec8<f16_t> { uint4 v; };
+
+__device__ __forceinline__ void unpack8(const Vec8<float> &v, float *o) {
+    o[0] = __uint_as_float(v.lo.x); o[1] = __uint_as_float(v.lo.y);
+    o[2] = __uint_as_float(v.lo.z); o[3] = __uint_as_float(v.lo.w);
+    o[4] = __uint_as_float(v.hi.x); o[5] = __uint_as_float(v.hi.y);
+    o[6] = __uint_as_float(v.hi.z); o[7] = __uint_as_float(v.hi.w);
+}
+__device__ __forceinline__ void unpack_bf16x2(uint32_t w, float &a, float &b) {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+}
+__device__ __forceinline__ void unpack8(const Vec8<bf16_t> &v, float *o) {
+    unpack_bf16x2(v.v.x, o[0], o[1]); unpack_bf16x2(v.v.y, o[2], o[3]);
+    unpack_bf16x2(v.v.z, o[4], o[5]); unpack_bf16x2(v.v.w, o[6], o[7]);
+}
+__device__ __forceinline__ void unpack_f16x2(uint32_t w, float &a, float &b) {
+    union { uint32_t u; _Float16 h[2]; } c; c.u = w;
+    a = float(c.h[0]); b = float(c.h[1]);
+}
+__device__ __forceinline__ void unpack8(const Vec8<f16_t> &v, float *o) {
+    unpack_f16x2(v.v.x, o[0], o[1]); unpack_f16x2(v.v.y, o[2], o[3]);
+    unpack_f16x2(v.v.z, o[4], o[5]); unpack_f16x2(v.v.w, o[6], o[7]);
+}
+
+__device__ __forceinline__ Vec8<float> pack8_f32(const float *x) {
+    Vec8<float> v;
+    v.lo = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+    v.hi = make_uint4(__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7]));
+    return v;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return uint32_t(f32_to_bf16_bits(a)) | (uint32_t(f32_to_bf16_bits(b)) << 16);
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    union { uint32_t u; _Float16 h[2]; } c; c.h[0] = (_Float16)a; c.h[1] = (_Float16)b;
+    return c.u;
+}
+
+template <typename T> __device__ __forceinline__ Vec8<T> pack8(const float *x);
+template <> __device__ __forceinline__ Vec8<float> pack8<float>(const float *x) { return pack8_f32(x); }
+template <> __device__ __forceinline__ Vec8<bf16_t> pack8<bf16_t>(const float *x) {
+    Vec8<bf16_t> v;
+    v.v = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
+    return v;
+}
+template <> __device__ __forceinline__ Vec8<f16_t> pack8<f16_t>(const float *x) {
+    Vec8<f16_t> v;
+    v.v = make_uint4(pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]), pack_f16x2(x[4], x[5]), pack_f16x2(x[6], x[7]));
+    return v;
+}
+
+template <typename T> __device__ __forceinline__ void load8(const T *p, float *o) {
+    unpack8(*reinterpret_cast<const Vec8<T> *>(p), o);
+}
+template <typename T> __device__ __forceinline__ void store8(T *p, const float *x) {
+    *reinterpret_cast<Vec8<T> *>(p) = pack8<T>(x);
+}
+
+}  // namespace mm

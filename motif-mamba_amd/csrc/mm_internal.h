@@ -1,0 +1,21 @@
+// mm_internal.h -- declarations shared between the translation units of libmm_scan.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "mm_scan.h"
+
+namespace mm {
+
+// Records the launch status of the kernel just enqueued (hipGetLastError) and the error text.
+int launch_status(const char *what);
+// Records `msg` as the thread's last error and returns `code`.
+int set_error(int code, const char *msg);
+
+// Tiled forward kernel (mm_scan_tiled.hip). Returns MM_ERR_UNSUPPORTED, without launching,
+// when the request falls outside the shapes that kernel covers; the caller then uses the
+// lane-per-row kernel.
+template <typename T>
+int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream);
+
+}  // namespace mm

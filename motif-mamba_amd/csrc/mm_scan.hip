@@ -1,0 +1,395 @@
+// mm_scan.hip -- gfx950 (CDNA4) selective-scan kernels and the C ABI of libmm_scan.so.
+//
+// Entry points (declared in include/mm_scan.h):
+//   mm_scan_fwd      -- replaces selective_scan_cuda.fwd (reference csrc/selective_scan/
+//                       selective_scan.cpp:270-413) for real A without P/Q/gamma.
+//   mm_state_update  -- replaces the upstream selective_state_update called at
+//                       mamba_ssm/modules/mamba_simplemotif.py:397-399.
+//
+// Kernels in this file:
+//   scan_fwd_rowlane<T, NS, VEC>  one lane owns one (batch, channel) row and all of its NS states
+//                                 in registers and walks the sequence serially, 8 steps per
+//                                 iteration. Used for every shape the tiled kernel does not take.
+//   state_update<T, SPL>          one decode step; LPR lanes share a row, SPL states per lane.
+// The tiled forward kernel lives in mm_scan_tiled.hip.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "mm_common.h"
+#include "mm_internal.h"
+#include "mm_scan.h"
+
+namespace mm {
+
+// ================================================================================================
+// Forward scan, lane-per-row kernel.
+// ================================================================================================
+constexpr int kRowBlock = 64;
+
+template <typename T, int NS, bool VEC>
+__global__ void __launch_bounds__(kRowBlock)
+scan_fwd_rowlane(const mm_scan_fwd_params p, const int64_t ratio, const int32_t uniform_g) {
+    const int64_t d_raw = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t b = blockIdx.y;
+    const bool active = d_raw < p.dim;
+    const int64_t d = active ? d_raw : p.dim - 1;  // clamped for loads; stores are predicated
+    int64_t g = d / ratio;
+    if (uniform_g) g = __builtin_amdgcn_readfirstlane(int(g));
+    const int64_t L = p.seqlen;
+    const int N = int(p.dstate);
+
+    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
+    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
+    const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
+    T *op = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
+    T *ozp = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
+    const T *Bv = p.is_variable_B ? reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride : nullptr;
+    const T *Cv = p.is_variable_C ? reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride : nullptr;
+
+    float At[NS], h[NS], Bc[NS], Cc[NS];
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+        const bool on = n < N;
+        At[n] = on ? p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e : 0.f;
+        h[n] = 0.f;
+        Bc[n] = (on && !p.is_variable_B) ? reinterpret_cast<const float *>(p.B)[d * p.B_d_stride + n * p.B_dstate_stride] : 0.f;
+        Cc[n] = (on && !p.is_variable_C) ? reinterpret_cast<const float *>(p.C)[d * p.C_d_stride + n * p.C_dstate_stride] : 0.f;
+    }
+    const float Dv = p.D ? p.D[d] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+    float cum_dt = 0.f;  // running sum of delta' (chunk-state prod a = exp2(A log2e * cum_dt))
+
+    for (int64_t l0 = 0; l0 < L; l0 += 8) {
+        const int nt = int(L - l0 < 8 ? L - l0 : 8);
+        float uu[8], dd[8], zz[8];
+        if (VEC && nt == 8) {
+            load8(up + l0, uu);
+            load8(dp + l0, dd);
+            if (zp) load8(zp + l0, zz);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                uu[t] = t < nt ? to_f32(up[l0 + t]) : 0.f;
+                dd[t] = t < nt ? to_f32(dp[l0 + t]) : 0.f;
+                zz[t] = (zp && t < nt) ? to_f32(zp[l0 + t]) : 0.f;
+            }
+        }
+        float dtp[8], du[8], y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float x = dd[t] + bias;
+            dtp[t] = p.delta_softplus ? softplus_f32(x) : x;
+            du[t] = dtp[t] * uu[t];
+            y[t] = 0.f;
+            if (t < nt) cum_dt += dtp[t];
+        }
+#pragma unroll(NS <= 64 ? NS : 8)
+        for (int n = 0; n < NS; ++n) {
+            if (NS > 16 && n >= N) break;
+            float bb[8], cc[8];
+            if (Bv) {
+                if (VEC && nt == 8) {
+                    load8(Bv + n * p.B_dstate_stride + l0, bb);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) bb[t] = t < nt ? to_f32(Bv[n * p.B_dstate_stride + l0 + t]) : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) bb[t] = Bc[n];
+            }
+            if (Cv) {
+                if (VEC && nt == 8) {
+                    load8(Cv + n * p.C_dstate_stride + l0, cc);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = t < nt ? to_f32(Cv[n * p.C_dstate_stride + l0 + t]) : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) cc[t] = Cc[n];
+            }
+            float hn = h[n];
+            const float an = At[n];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                if (VEC || t < nt) {
+                    const float a = fast_exp2(dtp[t] * an);
+                    hn = __builtin_fmaf(a, hn, du[t] * bb[t]);
+                    y[t] = __builtin_fmaf(hn, cc[t], y[t]);
+                }
+            }
+            h[n] = hn;
+        }
+        float o[8], oz[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            o[t] = p.D ? __builtin_fmaf(Dv, uu[t], y[t]) : y[t];
+            oz[t] = zp ? o[t] * silu_f32(zz[t]) : o[t];
+        }
+        if (active) {
+            if (VEC && nt == 8) {
+                if (op) store8(op + l0, o);
+                if (ozp) store8(ozp + l0, oz);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    if (t < nt) {
+                        if (op) op[l0 + t] = from_f32<T>(o[t]);
+                        if (ozp) ozp[l0 + t] = from_f32<T>(oz[t]);
+                    }
+                }
+            }
+            const int64_t lend = l0 + nt;
+            if (p.chunk_states && (lend % MM_SCAN_CHUNK == 0 || lend == L)) {
+                const int64_t c = (lend - 1) / MM_SCAN_CHUNK;
+                float *cs = p.chunk_states + ((b * p.dim + d) * n_chunks + c) * 2 * N;
+#pragma unroll
+                for (int n = 0; n < NS; ++n) {
+                    if (n < N) {
+                        cs[2 * n] = fast_exp2(At[n] * cum_dt);
+                        cs[2 * n + 1] = h[n];
+                    }
+                }
+            }
+        }
+    }
+    if (active && p.last_state) {
+        float *ls = p.last_state + (b * p.dim + d) * N;
+#pragma unroll
+        for (int n = 0; n < NS; ++n)
+            if (n < N) ls[n] = h[n];
+    }
+}
+
+// ================================================================================================
+// Decode step: LPR lanes per (batch, channel) row, SPL states per lane.
+// ================================================================================================
+constexpr int kDecBlock = 256;
+
+template <typename T, int SPL, int LPR>
+__global__ void __launch_bounds__(kDecBlock)
+state_update_kernel(const mm_state_update_params p, const int64_t ratio) {
+    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t row = tid / LPR;
+    const int part = int(tid % LPR);
+    const int64_t nrows = p.batch * p.dim;
+    const bool active = row < nrows;
+    const int64_t rr = active ? row : nrows - 1;
+    const int64_t b = rr / p.dim;
+    const int64_t d = rr % p.dim;
+    const int64_t g = d / ratio;
+    const int N = int(p.dstate);
+
+    float dt = to_f32(reinterpret_cast<const T *>(p.dt)[b * p.dt_batch_stride + d * p.dt_d_stride]);
+    if (p.dt_bias) dt += p.dt_bias[d];
+    if (p.dt_softplus) dt = softplus_f32(dt);
+    const float x = to_f32(reinterpret_cast<const T *>(p.x)[b * p.x_batch_stride + d * p.x_d_stride]);
+    const float dtx = dt * x;
+    const T *Bp = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cp = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+    float *sp = p.state + b * p.state_batch_stride + d * p.state_d_stride;
+
+    float y = 0.f;
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+        const int n = part * SPL + k;
+        if (n < N) {
+            const float a = fast_exp2(dt * p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e);
+            float s = sp[n * p.state_dstate_stride];
+            s = __builtin_fmaf(s, a, dtx * to_f32(Bp[n * p.B_dstate_stride]));
+            if (active) sp[n * p.state_dstate_stride] = s;
+            y = __builtin_fmaf(s, to_f32(Cp[n * p.C_dstate_stride]), y);
+        }
+    }
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) y += __shfl_xor(y, off, LPR);
+    if (active && part == 0) {
+        if (p.D) y = __builtin_fmaf(p.D[d], x, y);
+        if (p.z) y *= silu_f32(to_f32(reinterpret_cast<const T *>(p.z)[b * p.z_batch_stride + d * p.z_d_stride]));
+        reinterpret_cast<T *>(p.out)[b * p.out_batch_stride + d * p.out_d_stride] = from_f32<T>(y);
+    }
+}
+
+}  // namespace mm
+
+// ================================================================================================
+// Host side: validation, dispatch, error reporting.
+// ================================================================================================
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int elem_bytes(mm_dtype t) { return t == MM_FLOAT32 ? 4 : 2; }
+
+bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+namespace mm {
+
+int launch_status(const char *what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(int(e), "%s: launch failed: %s", what, hipGetErrorString(e));
+    g_err[0] = '\0';
+    return MM_OK;
+}
+
+int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
+
+}  // namespace mm
+
+namespace {
+
+int validate_fwd(const mm_scan_fwd_params *p) {
+    if (!p) return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: params is NULL");
+    if (p->itype != MM_FLOAT32 && p->itype != MM_FLOAT16 && p->itype != MM_BFLOAT16)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: unknown itype %d", int(p->itype));
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: negative size");
+    if (p->dstate < 1 || p->dstate > MM_SCAN_MAX_DSTATE)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: selective_scan only supports state dimension <= %d (got %lld)",
+                    MM_SCAN_MAX_DSTATE, (long long)p->dstate);
+    if (p->n_groups < 1 || (p->dim > 0 && p->dim % p->n_groups != 0))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: dim (%lld) must be a multiple of n_groups (%lld)",
+                    (long long)p->dim, (long long)p->n_groups);
+    if (p->batch == 0 || p->dim == 0) return MM_OK;
+    if (!p->u || !p->delta || !p->A || !p->B || !p->C)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: u, delta, A, B and C are required");
+    if (p->z && !p->out_z)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: out_z is required when z is given");
+    if (!p->z && p->out_z)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: out_z given without z");
+    if (!p->out && !p->out_z && !p->last_state && !p->chunk_states)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: no output requested");
+    return MM_OK;
+}
+
+// 16-byte vector I/O is legal when every row start is 16-byte aligned and L is a multiple of 8.
+bool fwd_vector_ok(const mm_scan_fwd_params *p) {
+    const int64_t eb = elem_bytes(p->itype);
+    auto row_ok = [&](const void *base, int64_t s0, int64_t s1) {
+        return base == nullptr || (aligned16(base) && (s0 * eb) % 16 == 0 && (s1 * eb) % 16 == 0);
+    };
+    if (p->seqlen % 8 != 0) return false;
+    bool ok = row_ok(p->u, p->u_batch_stride, p->u_d_stride) && row_ok(p->delta, p->delta_batch_stride, p->delta_d_stride) &&
+              row_ok(p->z, p->z_batch_stride, p->z_d_stride) && row_ok(p->out, p->out_batch_stride, p->out_d_stride) &&
+              row_ok(p->out_z, p->out_z_batch_stride, p->out_z_d_stride);
+    if (p->is_variable_B)
+        ok = ok && aligned16(p->B) && (p->B_batch_stride * eb) % 16 == 0 && (p->B_group_stride * eb) % 16 == 0 &&
+             (p->B_dstate_stride * eb) % 16 == 0;
+    if (p->is_variable_C)
+        ok = ok && aligned16(p->C) && (p->C_batch_stride * eb) % 16 == 0 && (p->C_group_stride * eb) % 16 == 0 &&
+             (p->C_dstate_stride * eb) % 16 == 0;
+    return ok;
+}
+
+template <typename T, int NS>
+int launch_rowlane_ns(const mm_scan_fwd_params &p, hipStream_t s, bool vec) {
+    const int64_t ratio = p.dim / p.n_groups;
+    // The B/C row of a 64-lane block is uniform when no block straddles a group boundary.
+    const int32_t uniform_g = (p.n_groups == 1 || ratio % mm::kRowBlock == 0) ? 1 : 0;
+    dim3 grid(unsigned((p.dim + mm::kRowBlock - 1) / mm::kRowBlock), unsigned(p.batch));
+    if (vec)
+        hipLaunchKernelGGL((mm::scan_fwd_rowlane<T, NS, true>), grid, dim3(mm::kRowBlock), 0, s, p, ratio, uniform_g);
+    else
+        hipLaunchKernelGGL((mm::scan_fwd_rowlane<T, NS, false>), grid, dim3(mm::kRowBlock), 0, s, p, ratio, uniform_g);
+    return mm::launch_status("scan_fwd_rowlane");
+}
+
+template <typename T>
+int launch_rowlane(const mm_scan_fwd_params &p, hipStream_t s) {
+    const bool vec = fwd_vector_ok(&p);
+    if (p.dstate <= 16) return launch_rowlane_ns<T, 16>(p, s, vec);
+    if (p.dstate <= 32) return launch_rowlane_ns<T, 32>(p, s, vec);
+    if (p.dstate <= 64) return launch_rowlane_ns<T, 64>(p, s, vec);
+    return launch_rowlane_ns<T, MM_SCAN_MAX_DSTATE>(p, s, vec);
+}
+
+template <typename T>
+int dispatch_fwd(const mm_scan_fwd_params &p, hipStream_t s) {
+    int rc = mm::try_launch_tiled<T>(p, s);
+    if (rc != MM_ERR_UNSUPPORTED) return rc;
+    return launch_rowlane<T>(p, s);
+}
+
+// ------------------------------------------------------------------------------------------------
+int validate_su(const mm_state_update_params *p) {
+    if (!p) return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: params is NULL");
+    if (p->itype != MM_FLOAT32 && p->itype != MM_FLOAT16 && p->itype != MM_BFLOAT16)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: unknown itype %d", int(p->itype));
+    if (p->batch < 0 || p->dim < 0)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: negative size");
+    if (p->dstate < 1 || p->dstate > MM_SCAN_MAX_DSTATE)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: dstate must be in [1, %d]", MM_SCAN_MAX_DSTATE);
+    if (p->n_groups < 1 || (p->dim > 0 && p->dim % p->n_groups != 0))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: dim must be a multiple of n_groups");
+    if (p->batch == 0 || p->dim == 0) return MM_OK;
+    if (!p->state || !p->x || !p->dt || !p->A || !p->B || !p->C || !p->out)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: state, x, dt, A, B, C and out are required");
+    return MM_OK;
+}
+
+template <typename T, int SPL, int LPR>
+int launch_su(const mm_state_update_params &p, hipStream_t s) {
+    const int64_t threads = p.batch * p.dim * LPR;
+    dim3 grid(unsigned((threads + mm::kDecBlock - 1) / mm::kDecBlock));
+    hipLaunchKernelGGL((mm::state_update_kernel<T, SPL, LPR>), grid, dim3(mm::kDecBlock), 0, s, p, p.dim / p.n_groups);
+    return mm::launch_status("state_update");
+}
+
+template <typename T>
+int dispatch_su(const mm_state_update_params &p, hipStream_t s) {
+    if (p.dstate <= 16) return launch_su<T, 4, 4>(p, s);
+    if (p.dstate <= 64) return launch_su<T, 4, 16>(p, s);
+    return launch_su<T, 16, 16>(p, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream) {
+    int rc = validate_fwd(params);
+    if (rc != MM_OK) return rc;
+    const mm_scan_fwd_params &p = *params;
+    if (p.batch == 0 || p.dim == 0) return MM_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (p.itype) {
+        case MM_FLOAT32: return dispatch_fwd<float>(p, s);
+        case MM_FLOAT16: return dispatch_fwd<mm::f16_t>(p, s);
+        default: return dispatch_fwd<mm::bf16_t>(p, s);
+    }
+}
+
+int mm_state_update(const mm_state_update_params *params, void *stream) {
+    int rc = validate_su(params);
+    if (rc != MM_OK) return rc;
+    const mm_state_update_params &p = *params;
+    if (p.batch == 0 || p.dim == 0) return MM_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (p.itype) {
+        case MM_FLOAT32: return dispatch_su<float>(p, s);
+        case MM_FLOAT16: return dispatch_su<mm::f16_t>(p, s);
+        default: return dispatch_su<mm::bf16_t>(p, s);
+    }
+}
+
+const char *mm_last_error(void) { return g_err; }
+
+int mm_abi_version(void) { return MM_SCAN_ABI_VERSION; }
+
+}  // extern "C"

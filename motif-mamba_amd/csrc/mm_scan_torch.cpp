@@ -1,0 +1,346 @@
+// mm_scan_torch.cpp -- thin PyTorch-ROCm binding over the C ABI of libmm_scan.so.
+//
+// fwd(...)        mirrors selective_scan_cuda.fwd (reference csrc/selective_scan/selective_scan.cpp:
+//                 270-413, pybind :620-627): same argument names, checks and outputs
+//                 [out, x, out_z?], where x is the (batch, dim, ceil(L/2048), 2*dstate) float32
+//                 chunk-state tensor of interleaved (prod a, h) pairs.
+// fwd_infer(...)  the inference form used by SelectiveScanFn: writes only the returned output
+//                 (out_z when z is given, else out) and, on request, a contiguous last_state.
+// state_update(.) the decode step (replaces upstream selective_state_update, called at
+//                 mamba_ssm/modules/mamba_simplemotif.py:397-399).
+// Validation failures raise RuntimeError through TORCH_CHECK, like the reference binding.
+#include <torch/extension.h>
+
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <vector>
+
+#include "mm_scan.h"
+
+namespace {
+
+#define CHECK_SHAPE(x, ...) \
+    TORCH_CHECK(x.sizes() == torch::IntArrayRef({__VA_ARGS__}), #x " must have shape (" #__VA_ARGS__ ")")
+
+mm_dtype to_mm(at::ScalarType t) {
+    switch (t) {
+        case at::ScalarType::Float: return MM_FLOAT32;
+        case at::ScalarType::Half: return MM_FLOAT16;
+        case at::ScalarType::BFloat16: return MM_BFLOAT16;
+        default: AT_ERROR("selective_scan_fwd not implemented for input type '", c10::toString(t), "'");
+    }
+}
+
+void check_rc(int rc, const char *what) {
+    TORCH_CHECK(rc == MM_OK, what, " failed (code ", rc, "): ", mm_last_error());
+}
+
+struct FwdSetup {
+    mm_scan_fwd_params p;
+    int64_t n_chunks;
+};
+
+// Shared validation (selective_scan.cpp:280-381, without the P/Q/gamma and complex branches).
+FwdSetup setup_fwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A, const at::Tensor &B,
+                   const at::Tensor &C, const c10::optional<at::Tensor> &D_, const c10::optional<at::Tensor> &z_,
+                   const c10::optional<at::Tensor> &delta_bias_, bool delta_softplus) {
+    const auto input_type = u.scalar_type();
+    const auto weight_type = A.scalar_type();
+    TORCH_CHECK(input_type == at::ScalarType::Float || input_type == at::ScalarType::Half ||
+                input_type == at::ScalarType::BFloat16);
+    TORCH_CHECK(weight_type == at::ScalarType::Float || weight_type == at::ScalarType::ComplexFloat);
+    if (weight_type == at::ScalarType::ComplexFloat) {
+        throw c10::NotImplementedError({__func__, __FILE__, uint32_t(__LINE__)},
+                                       "complex A is not supported by the MI355X selective scan");
+    }
+    const bool is_variable_B = B.dim() >= 3;
+    const bool is_variable_C = C.dim() >= 3;
+    TORCH_CHECK(delta.scalar_type() == input_type);
+    TORCH_CHECK(B.scalar_type() == (!is_variable_B ? weight_type : input_type));
+    TORCH_CHECK(C.scalar_type() == (!is_variable_C ? weight_type : input_type));
+    TORCH_CHECK(u.is_cuda());
+    TORCH_CHECK(delta.is_cuda());
+    TORCH_CHECK(A.is_cuda());
+    TORCH_CHECK(B.is_cuda());
+    TORCH_CHECK(C.is_cuda());
+    TORCH_CHECK(u.stride(-1) == 1 || u.size(-1) == 1);
+    TORCH_CHECK(delta.stride(-1) == 1 || delta.size(-1) == 1);
+
+    TORCH_CHECK(u.dim() == 3, "u must have shape (batch, dim, seqlen)");
+    const int64_t batch_size = u.size(0), dim = u.size(1), seqlen = u.size(2);
+    TORCH_CHECK(A.dim() == 2, "A must have shape (dim, dstate)");
+    const int64_t dstate = A.size(1);
+    TORCH_CHECK(!is_variable_B || B.dim() == 4, "variable B must be 4-D (batch, n_groups, dstate, seqlen)");
+    const int64_t n_groups = is_variable_B ? B.size(1) : 1;
+    TORCH_CHECK(dstate <= MM_SCAN_MAX_DSTATE, "selective_scan only supports state dimension <= 256");
+
+    CHECK_SHAPE(u, batch_size, dim, seqlen);
+    CHECK_SHAPE(delta, batch_size, dim, seqlen);
+    CHECK_SHAPE(A, dim, dstate);
+    if (!is_variable_B) {
+        CHECK_SHAPE(B, dim, dstate);
+    } else {
+        CHECK_SHAPE(B, batch_size, n_groups, dstate, seqlen);
+        TORCH_CHECK(B.stride(-1) == 1 || B.size(-1) == 1);
+    }
+    if (!is_variable_C) {
+        CHECK_SHAPE(C, dim, dstate);
+    } else {
+        TORCH_CHECK(C.dim() == 4, "variable C must be 4-D (batch, n_groups, dstate, seqlen)");
+        CHECK_SHAPE(C, batch_size, n_groups, dstate, seqlen);
+        TORCH_CHECK(C.stride(-1) == 1 || C.size(-1) == 1);
+    }
+    TORCH_CHECK(n_groups >= 1 && dim % n_groups == 0, "dim must be a multiple of n_groups");
+    if (D_.has_value()) {
+        const auto &D = D_.value();
+        TORCH_CHECK(D.scalar_type() == at::ScalarType::Float);
+        TORCH_CHECK(D.is_cuda());
+        TORCH_CHECK(D.stride(-1) == 1 || D.size(-1) == 1);
+        CHECK_SHAPE(D, dim);
+    }
+    if (delta_bias_.has_value()) {
+        const auto &db = delta_bias_.value();
+        TORCH_CHECK(db.scalar_type() == at::ScalarType::Float);
+        TORCH_CHECK(db.is_cuda());
+        TORCH_CHECK(db.stride(-1) == 1 || db.size(-1) == 1);
+        CHECK_SHAPE(db, dim);
+    }
+    if (z_.has_value()) {
+        const auto &z = z_.value();
+        TORCH_CHECK(z.scalar_type() == input_type);
+        TORCH_CHECK(z.is_cuda());
+        TORCH_CHECK(z.stride(-1) == 1 || z.size(-1) == 1);
+        CHECK_SHAPE(z, batch_size, dim, seqlen);
+    }
+
+    FwdSetup s;
+    std::memset(&s.p, 0, sizeof(s.p));
+    mm_scan_fwd_params &p = s.p;
+    p.batch = batch_size;
+    p.dim = dim;
+    p.seqlen = seqlen;
+    p.dstate = dstate;
+    p.n_groups = n_groups;
+    p.itype = to_mm(input_type);
+    p.is_variable_B = is_variable_B;
+    p.is_variable_C = is_variable_C;
+    p.delta_softplus = delta_softplus;
+    p.u = u.data_ptr();
+    p.delta = delta.data_ptr();
+    p.A = A.data_ptr<float>();
+    p.B = B.data_ptr();
+    p.C = C.data_ptr();
+    p.D = D_.has_value() ? D_.value().data_ptr<float>() : nullptr;
+    p.z = z_.has_value() ? z_.value().data_ptr() : nullptr;
+    p.delta_bias = delta_bias_.has_value() ? delta_bias_.value().data_ptr<float>() : nullptr;
+    p.u_batch_stride = u.stride(0);
+    p.u_d_stride = u.stride(1);
+    p.delta_batch_stride = delta.stride(0);
+    p.delta_d_stride = delta.stride(1);
+    if (z_.has_value()) {
+        p.z_batch_stride = z_.value().stride(0);
+        p.z_d_stride = z_.value().stride(1);
+    }
+    p.A_d_stride = A.stride(0);
+    p.A_dstate_stride = A.stride(1);
+    if (is_variable_B) {
+        p.B_batch_stride = B.stride(0);
+        p.B_group_stride = B.stride(1);
+        p.B_dstate_stride = B.stride(2);
+    } else {
+        p.B_d_stride = B.stride(0);
+        p.B_dstate_stride = B.stride(1);
+    }
+    if (is_variable_C) {
+        p.C_batch_stride = C.stride(0);
+        p.C_group_stride = C.stride(1);
+        p.C_dstate_stride = C.stride(2);
+    } else {
+        p.C_d_stride = C.stride(0);
+        p.C_dstate_stride = C.stride(1);
+    }
+    s.n_chunks = (seqlen + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+    return s;
+}
+
+void set_out(mm_scan_fwd_params &p, const at::Tensor &out) {
+    p.out = out.data_ptr();
+    p.out_batch_stride = out.stride(0);
+    p.out_d_stride = out.stride(1);
+}
+
+void set_out_z(mm_scan_fwd_params &p, const at::Tensor &out_z) {
+    p.out_z = out_z.data_ptr();
+    p.out_z_batch_stride = out_z.stride(0);
+    p.out_z_d_stride = out_z.stride(1);
+}
+
+std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A,
+                            const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
+                            const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &delta_bias_,
+                            const c10::optional<at::Tensor> &P_, const c10::optional<at::Tensor> &Q_,
+                            const c10::optional<at::Tensor> &gamma_, bool delta_softplus) {
+    if (P_.has_value() || Q_.has_value() || gamma_.has_value()) {
+        throw c10::NotImplementedError({__func__, __FILE__, uint32_t(__LINE__)},
+                                       "P/Q/gamma (MotifMamba low-rank coupling) are not part of the MI355X scan");
+    }
+    FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
+    mm_scan_fwd_params &p = s.p;
+    // Output layouts follow the reference: out like delta, out_z like z, x contiguous.
+    at::Tensor out = torch::empty_like(delta);
+    at::Tensor x = torch::empty({p.batch, p.dim, s.n_chunks, p.dstate * 2}, u.options().dtype(A.scalar_type()));
+    at::Tensor out_z;
+    set_out(p, out);
+    if (z_.has_value()) {
+        out_z = torch::empty_like(z_.value());
+        set_out_z(p, out_z);
+    }
+    p.chunk_states = x.data_ptr<float>();
+    c10::hip::HIPGuard device_guard{u.device()};
+    check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
+    std::vector<at::Tensor> result = {out, x};
+    if (z_.has_value()) result.push_back(out_z);
+    return result;
+}
+
+std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A,
+                                  const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
+                                  const c10::optional<at::Tensor> &z_,
+                                  const c10::optional<at::Tensor> &delta_bias_, bool delta_softplus,
+                                  bool return_last_state) {
+    FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
+    mm_scan_fwd_params &p = s.p;
+    at::Tensor main;
+    if (z_.has_value()) {
+        main = torch::empty_like(z_.value());
+        set_out_z(p, main);
+    } else {
+        main = torch::empty_like(delta);
+        set_out(p, main);
+    }
+    at::Tensor last_state;
+    if (return_last_state) {
+        last_state = torch::empty({p.batch, p.dim, p.dstate}, u.options().dtype(at::ScalarType::Float));
+        p.last_state = last_state.data_ptr<float>();
+    }
+    c10::hip::HIPGuard device_guard{u.device()};
+    check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
+    if (return_last_state) return {main, last_state};
+    return {main};
+}
+
+at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::Tensor &dt, const at::Tensor &A,
+                        const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
+                        const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &dt_bias_,
+                        bool dt_softplus) {
+    TORCH_CHECK(state.dim() == 3, "state must have shape (batch, dim, dstate)");
+    TORCH_CHECK(state.scalar_type() == at::ScalarType::Float, "state must be float32");
+    const int64_t batch = state.size(0), dim = state.size(1), dstate = state.size(2);
+    const auto itype = x.scalar_type();
+    TORCH_CHECK(state.is_cuda() && x.is_cuda() && dt.is_cuda() && A.is_cuda() && B.is_cuda() && C.is_cuda());
+    CHECK_SHAPE(x, batch, dim);
+    CHECK_SHAPE(dt, batch, dim);
+    CHECK_SHAPE(A, dim, dstate);
+    TORCH_CHECK(dt.scalar_type() == itype, "dt must have the dtype of x");
+    TORCH_CHECK(A.scalar_type() == at::ScalarType::Float, "A must be float32");
+    TORCH_CHECK(B.dim() == 2 || B.dim() == 3, "B must be (batch, dstate) or (batch, n_groups, dstate)");
+    TORCH_CHECK(C.dim() == B.dim(), "B and C must have the same rank");
+    const int64_t n_groups = B.dim() == 3 ? B.size(1) : 1;
+    if (B.dim() == 2) {
+        CHECK_SHAPE(B, batch, dstate);
+        CHECK_SHAPE(C, batch, dstate);
+    } else {
+        CHECK_SHAPE(B, batch, n_groups, dstate);
+        CHECK_SHAPE(C, batch, n_groups, dstate);
+    }
+    TORCH_CHECK(B.scalar_type() == itype && C.scalar_type() == itype, "B and C must have the dtype of x");
+    TORCH_CHECK(n_groups >= 1 && dim % n_groups == 0, "dim must be a multiple of n_groups");
+    if (D_.has_value()) {
+        CHECK_SHAPE(D_.value(), dim);
+        TORCH_CHECK(D_.value().scalar_type() == at::ScalarType::Float && D_.value().is_cuda(), "D must be float32 on the GPU");
+    }
+    if (dt_bias_.has_value()) {
+        CHECK_SHAPE(dt_bias_.value(), dim);
+        TORCH_CHECK(dt_bias_.value().scalar_type() == at::ScalarType::Float && dt_bias_.value().is_cuda(),
+                    "dt_bias must be float32 on the GPU");
+    }
+    if (z_.has_value()) {
+        CHECK_SHAPE(z_.value(), batch, dim);
+        TORCH_CHECK(z_.value().scalar_type() == itype && z_.value().is_cuda(), "z must have the dtype of x");
+    }
+    at::Tensor out = torch::empty({batch, dim}, x.options());
+    at::Tensor Dc = D_.has_value() ? D_.value().contiguous() : at::Tensor();
+    at::Tensor bc = dt_bias_.has_value() ? dt_bias_.value().contiguous() : at::Tensor();
+
+    mm_state_update_params p;
+    std::memset(&p, 0, sizeof(p));
+    p.batch = batch;
+    p.dim = dim;
+    p.dstate = dstate;
+    p.n_groups = n_groups;
+    p.itype = to_mm(itype);
+    p.dt_softplus = dt_softplus;
+    p.state = state.data_ptr<float>();
+    p.x = x.data_ptr();
+    p.dt = dt.data_ptr();
+    p.A = A.data_ptr<float>();
+    p.B = B.data_ptr();
+    p.C = C.data_ptr();
+    p.D = Dc.defined() ? Dc.data_ptr<float>() : nullptr;
+    p.z = z_.has_value() ? z_.value().data_ptr() : nullptr;
+    p.dt_bias = bc.defined() ? bc.data_ptr<float>() : nullptr;
+    p.out = out.data_ptr();
+    p.state_batch_stride = state.stride(0);
+    p.state_d_stride = state.stride(1);
+    p.state_dstate_stride = state.stride(2);
+    p.x_batch_stride = x.stride(0);
+    p.x_d_stride = x.stride(1);
+    p.dt_batch_stride = dt.stride(0);
+    p.dt_d_stride = dt.stride(1);
+    if (z_.has_value()) {
+        p.z_batch_stride = z_.value().stride(0);
+        p.z_d_stride = z_.value().stride(1);
+    }
+    p.out_batch_stride = out.stride(0);
+    p.out_d_stride = out.stride(1);
+    p.A_d_stride = A.stride(0);
+    p.A_dstate_stride = A.stride(1);
+    if (B.dim() == 3) {
+        p.B_batch_stride = B.stride(0);
+        p.B_group_stride = B.stride(1);
+        p.B_dstate_stride = B.stride(2);
+        p.C_batch_stride = C.stride(0);
+        p.C_group_stride = C.stride(1);
+        p.C_dstate_stride = C.stride(2);
+    } else {
+        p.B_batch_stride = B.stride(0);
+        p.B_dstate_stride = B.stride(1);
+        p.C_batch_stride = C.stride(0);
+        p.C_dstate_stride = C.stride(1);
+    }
+    c10::hip::HIPGuard device_guard{state.device()};
+    check_rc(mm_state_update(&p, c10::hip::getCurrentHIPStream().stream()), "mm_state_update");
+    return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+    m.def("fwd", &fwd, "Selective scan forward (reference-compatible outputs [out, x, out_z?])",
+          pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
+          pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
+          pybind11::arg("delta_bias") = pybind11::none(), pybind11::arg("P") = pybind11::none(),
+          pybind11::arg("Q") = pybind11::none(), pybind11::arg("gamma") = pybind11::none(),
+          pybind11::arg("delta_softplus") = false);
+    m.def("fwd_infer", &fwd_infer, "Selective scan forward, inference outputs [out_z|out, last_state?]",
+          pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
+          pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
+          pybind11::arg("delta_bias") = pybind11::none(), pybind11::arg("delta_softplus") = false,
+          pybind11::arg("return_last_state") = false);
+    m.def("state_update", &state_update, "Single-token selective state update (in place on state)",
+          pybind11::arg("state"), pybind11::arg("x"), pybind11::arg("dt"), pybind11::arg("A"), pybind11::arg("B"),
+          pybind11::arg("C"), pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
+          pybind11::arg("dt_bias") = pybind11::none(), pybind11::arg("dt_softplus") = false);
+    m.def("abi_version", []() { return mm_abi_version(); });
+}

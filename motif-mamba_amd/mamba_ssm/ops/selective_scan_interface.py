@@ -1,0 +1,5 @@
+"""``mamba_ssm.ops.selective_scan_interface`` hot-path names, served by the gfx950 kernels
+(reference mamba_ssm/ops/selective_scan_interface.py:24-61, 237-259)."""
+from motif_mamba_amd.selective_scan import SelectiveScanFn, selective_scan_fn
+
+__all__ = ["SelectiveScanFn", "selective_scan_fn"]

@@ -1,0 +1,114 @@
+"""ctypes wrapper of scan_f64.c -- TEST INFRASTRUCTURE ONLY.
+
+``build()`` compiles ``scan_f64.c`` with gcc (OpenMP) into ``oracle/_build/libscan_f64.so``;
+``scan_rows`` evaluates selected (batch, dim) rows of a selective scan in float64 on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SRC = os.path.join(_HERE, "scan_f64.c")
+_LIB = os.path.join(_HERE, "_build", "libscan_f64.so")
+_lib = None
+
+
+def build(force: bool = True) -> str:
+    """Compile the float64 oracle (gcc -O2 -fopenmp). Returns the library path."""
+    os.makedirs(os.path.dirname(_LIB), exist_ok=True)
+    if force or not os.path.exists(_LIB):
+        tmp = _LIB + ".tmp"
+        subprocess.check_call(["gcc", "-O2", "-fopenmp", "-fPIC", "-shared", "-std=c11",
+                               _SRC, "-o", tmp, "-lm"])
+        os.replace(tmp, _LIB)
+    return _LIB
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB):
+            build(force=False)
+        lib = ctypes.CDLL(_LIB)
+        f = lib.mm_oracle_scan_rows_f64
+        i64, dp = ctypes.c_int64, ctypes.c_void_p
+        f.argtypes = [i64, i64, i64, dp, dp, dp, dp,
+                      dp, i64, i64, i64, dp, i64, i64, i64,
+                      dp, dp, ctypes.c_int, dp, dp, dp, i64, dp]
+        f.restype = None
+        _lib = lib
+    return _lib
+
+
+def torch_index(i):
+    import torch
+    return torch.from_numpy(i)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def scan_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+              rows=None, chunk=0):
+    """Float64 scan of the rows ``rows`` (list of (b, d) pairs; all rows if None).
+
+    Tensors are torch CPU tensors or numpy arrays in the reference layouts (u/delta/z
+    (batch, dim, L); A (dim, N); B/C (dim, N), (batch, N, L) or (batch, G, N, L)).
+    Returns dict with 'out' (R, L), 'out_z' (R, L) or None, 'last_state' (R, N) and, when
+    ``chunk`` > 0, 'h_chunks' (R, n_chunks, N) -- all float64 numpy arrays.
+    """
+    def npf(x):
+        if x is None:
+            return None
+        if hasattr(x, "detach"):
+            x = x.detach().cpu().float().numpy()
+        return np.asarray(x, dtype=np.float64)
+
+    batch, dim, L = u.shape
+    N = A.shape[1]
+    if rows is None:
+        rows = [(b, d) for b in range(batch) for d in range(dim)]
+    bi = np.array([r[0] for r in rows], dtype=np.int64)
+    di = np.array([r[1] for r in rows], dtype=np.int64)
+    R = len(rows)
+
+    def take(x, idx):  # gather rows before converting, so full-size tensors are never copied
+        if x is None:
+            return None
+        if hasattr(x, "detach"):
+            return npf(x[tuple(torch_index(i) for i in idx)])
+        return npf(np.asarray(x)[idx])
+
+    def gather_bc(X):
+        nd = X.dim() if hasattr(X, "dim") else np.ndim(X)
+        if nd == 2:  # constant (dim, N): broadcast over l with l_stride 0
+            return np.ascontiguousarray(take(X, (di,))), N, 1, 0
+        if nd == 3:  # (batch, N, L): one group
+            rowsX = take(X, (bi,))
+        else:        # (batch, G, N, L): channel d reads group d // (dim / G)
+            rowsX = take(X, (bi, di // (dim // X.shape[1])))
+        return np.ascontiguousarray(rowsX), N * L, L, 1
+
+    ur = np.ascontiguousarray(take(u, (bi, di)))
+    dr = np.ascontiguousarray(take(delta, (bi, di)))
+    zr = np.ascontiguousarray(take(z, (bi, di))) if z is not None else None
+    Ar = np.ascontiguousarray(take(A, (di,)))
+    Dr = np.ascontiguousarray(take(D, (di,))) if D is not None else None
+    br = np.ascontiguousarray(take(delta_bias, (di,))) if delta_bias is not None else None
+    Bs, bR, bN, bL = gather_bc(B)
+    Cs, cR, cN, cL = gather_bc(C)
+    out = np.zeros((R, L))
+    outz = np.zeros((R, L)) if zr is not None else None
+    last = np.zeros((R, N))
+    n_chunks = (L + chunk - 1) // chunk if chunk > 0 else 0
+    hch = np.zeros((R, n_chunks, N)) if chunk > 0 else None
+    _load().mm_oracle_scan_rows_f64(R, L, N, _p(ur), _p(dr), _p(zr), _p(Ar),
+                                    _p(Bs), bR, bN, bL, _p(Cs), cR, cN, cL,
+                                    _p(Dr), _p(br), int(bool(delta_softplus)),
+                                    _p(out), _p(outz), _p(last), int(chunk), _p(hch))
+    return {"out": out, "out_z": outz, "last_state": last, "h_chunks": hch}

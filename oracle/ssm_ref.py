@@ -1,0 +1,207 @@
+"""Torch (CPU) restatement of the reference selective-scan algorithms -- TEST INFRASTRUCTURE ONLY.
+
+``selective_scan_ref`` follows ``selective_scan_ref`` of the reference,
+``mamba_ssm/ops/selective_scan_interface.py:353-451``, for real A without P/Q/gamma, keeping its
+op sequence so that the rounding behaviour is that of the reference on the same torch build:
+
+* u and delta upcast to float32, ``delta += delta_bias[..., None]``, ``F.softplus`` (threshold 20)
+  (ssi.py:367-374);
+* ``deltaA = exp(einsum('bdl,dn->bdln'))`` and the three-operand ``deltaB_u`` einsum; 4-D B/C
+  are repeated ``B G N L -> B (G H) N L`` so channel d reads group ``d // (D/G)``
+  (ssi.py:388-400);
+* a per-timestep loop ``x = deltaA[..., t] * x + deltaB_u[..., t]`` and ``y = einsum(x, C_t)``
+  (ssi.py:422-445);
+* ``out = y + u * D``; ``out *= F.silu(z)`` with z in its *original* dtype; cast to the input
+  dtype; ``last_state`` is the float32 state after the last step (ssi.py:441-451).
+
+``selective_state_update_ref`` restates the single-token decode update. The reference calls the
+un-vendored upstream ``selective_state_update`` (mamba_simplemotif.py:397-399) whose in-tree
+restatement is the torch fallback ``mamba_simplemotif.py:369-376``. The fallback runs the
+discretisation in the activation dtype; the upstream kernel and this restatement run it in
+float32 (dt + dt_bias promotes to float32), which is the behaviour the kernel must match.
+``mamba_step_fallback_ref`` keeps the fallback's literal dtype behaviour for comparison.
+
+Pins (see tests/test_oracle.py): float64 brute-force sum on tiny shapes, a hand-worked
+known-answer case, closed forms (L=1, delta=0, memoryless decay, N=1 geometric filter against
+numpy.convolve, z-gate composition), invariants (linearity in u, group split, decode/scan
+consistency) and the C float64 restatement ``scan_f64.c``.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from einops import rearrange, repeat
+
+
+def _softplus_f32(x: torch.Tensor) -> torch.Tensor:
+    return F.softplus(x)
+
+
+def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                       return_last_state=False):
+    """CPU restatement of ssi.py:353-451 (real A, no P/Q). Shapes as in the reference:
+    u, delta, z: (batch, dim, L); A: (dim, N); B, C: (dim, N) | (batch, N, L) | (batch, G, N, L).
+    """
+    if A.is_complex():
+        raise NotImplementedError("complex A is out of scope")
+    in_dtype = u.dtype
+    u32 = u.float()
+    dt = delta.float()
+    if delta_bias is not None:
+        dt = dt + delta_bias[..., None].float()
+    if delta_softplus:
+        dt = _softplus_f32(dt)
+    nbatch, ndim, nstate = u.shape[0], A.shape[0], A.shape[1]
+    var_B = B.dim() >= 3
+    var_C = C.dim() >= 3
+    Bf = B.float()
+    Cf = C.float()
+    decay = torch.exp(torch.einsum("bdl,dn->bdln", dt, A))
+    if not var_B:
+        drive = torch.einsum("bdl,dn,bdl->bdln", dt, Bf, u32)
+    elif Bf.dim() == 3:
+        drive = torch.einsum("bdl,bnl,bdl->bdln", dt, Bf, u32)
+    else:
+        Bf = repeat(Bf, "B G N L -> B (G H) N L", H=ndim // Bf.shape[1])
+        drive = torch.einsum("bdl,bdnl,bdl->bdln", dt, Bf, u32)
+    if var_C and Cf.dim() == 4:
+        Cf = repeat(Cf, "B G N L -> B (G H) N L", H=ndim // Cf.shape[1])
+    state = A.new_zeros((nbatch, ndim, nstate))
+    ys = []
+    for t in range(u.shape[2]):
+        state = decay[:, :, t] * state + drive[:, :, t]
+        if not var_C:
+            ys.append(torch.einsum("bdn,dn->bd", state, Cf))
+        elif Cf.dim() == 3:
+            ys.append(torch.einsum("bdn,bn->bd", state, Cf[:, :, t]))
+        else:
+            ys.append(torch.einsum("bdn,bdn->bd", state, Cf[:, :, :, t]))
+    y = torch.stack(ys, dim=2)
+    out = y if D is None else y + u32 * rearrange(D, "d -> d 1")
+    if z is not None:
+        out = out * F.silu(z)
+    out = out.to(dtype=in_dtype)
+    return out if not return_last_state else (out, state)
+
+
+def selective_scan_ref_chunked(u, delta, A, B, C, D=None, z=None, delta_bias=None,
+                               delta_softplus=False, return_last_state=False, chunk=512):
+    """Same arithmetic as ``selective_scan_ref`` but materialising the (B, D, chunk, N)
+    intermediates one sequence chunk at a time, carrying the state between chunks. Used only
+    as the CPU baseline when the full (B, D, L, N) intermediates do not fit the host's RAM;
+    every per-element operation and its order are those of ``selective_scan_ref``."""
+    in_dtype = u.dtype
+    L = u.shape[2]
+    nbatch, ndim, nstate = u.shape[0], A.shape[0], A.shape[1]
+    state = A.new_zeros((nbatch, ndim, nstate))
+    outs = []
+    for s in range(0, L, chunk):
+        e = min(L, s + chunk)
+        sl = slice(s, e)
+        u32 = u[:, :, sl].float()
+        dt = delta[:, :, sl].float()
+        if delta_bias is not None:
+            dt = dt + delta_bias[..., None].float()
+        if delta_softplus:
+            dt = _softplus_f32(dt)
+        Bs = B[..., sl].float() if B.dim() >= 3 else B.float()
+        Cs = C[..., sl].float() if C.dim() >= 3 else C.float()
+        decay = torch.exp(torch.einsum("bdl,dn->bdln", dt, A))
+        if B.dim() < 3:
+            drive = torch.einsum("bdl,dn,bdl->bdln", dt, Bs, u32)
+        elif B.dim() == 3:
+            drive = torch.einsum("bdl,bnl,bdl->bdln", dt, Bs, u32)
+        else:
+            Bs = repeat(Bs, "B G N L -> B (G H) N L", H=ndim // Bs.shape[1])
+            drive = torch.einsum("bdl,bdnl,bdl->bdln", dt, Bs, u32)
+        if C.dim() == 4:
+            Cs = repeat(Cs, "B G N L -> B (G H) N L", H=ndim // Cs.shape[1])
+        ys = []
+        for t in range(e - s):
+            state = decay[:, :, t] * state + drive[:, :, t]
+            if C.dim() < 3:
+                ys.append(torch.einsum("bdn,dn->bd", state, Cs))
+            elif C.dim() == 3:
+                ys.append(torch.einsum("bdn,bn->bd", state, Cs[:, :, t]))
+            else:
+                ys.append(torch.einsum("bdn,bdn->bd", state, Cs[:, :, :, t]))
+        y = torch.stack(ys, dim=2)
+        out = y if D is None else y + u32 * rearrange(D, "d -> d 1")
+        if z is not None:
+            out = out * F.silu(z[:, :, sl])
+        outs.append(out.to(dtype=in_dtype))
+    out = torch.cat(outs, dim=2)
+    return out if not return_last_state else (out, state)
+
+
+def chunk_states_ref(delta, A, delta_bias=None, delta_softplus=False, last_states=None,
+                     chunk=2048):
+    """Expected prod-a component of the reference's chunk-state tensor ``x``
+    (selective_scan_fwd_kernel.cuh:476-495): for chunk c, prod over t < min(L, 2048(c+1)) of
+    exp(delta'_t A[d, n]) = exp(A[d, n] * sum_t delta'_t). Returned as (B, D, n_chunks, N)
+    float64 (the h component is the state at the chunk end, checked separately)."""
+    dt = delta.double()
+    if delta_bias is not None:
+        dt = dt + delta_bias[..., None].double()
+    if delta_softplus:
+        dt = F.softplus(dt)
+    L = dt.shape[-1]
+    n_chunks = (L + chunk - 1) // chunk
+    ends = [min(L, chunk * (c + 1)) for c in range(n_chunks)]
+    cums = torch.stack([dt[:, :, :e].sum(-1) for e in ends], dim=2)  # (B, D, n_chunks)
+    return torch.exp(cums[..., None] * A.double()[None, :, None, :])
+
+
+def selective_state_update_ref(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
+                               dt_softplus=False):
+    """One decode step, in place on ``state`` (float32, (batch, dim, dstate)).
+
+    x, dt, z: (batch, dim); A: (dim, dstate); B, C: (batch, dstate) or (batch, G, dstate);
+    D, dt_bias: (dim,). Discretisation and readout in float32 (dt + dt_bias promotes to
+    float32 as in the upstream kernel); output cast to x.dtype.
+    """
+    batch, dim, nstate = state.shape
+    dtf = dt.float()
+    if dt_bias is not None:
+        dtf = dtf + dt_bias.float()
+    if dt_softplus:
+        dtf = F.softplus(dtf)
+    Bf = B.float()
+    Cf = C.float()
+    if Bf.dim() == 2:
+        Bf = Bf[:, None, :]
+    if Cf.dim() == 2:
+        Cf = Cf[:, None, :]
+    Bf = repeat(Bf, "b g n -> b (g h) n", h=dim // Bf.shape[1])
+    Cf = repeat(Cf, "b g n -> b (g h) n", h=dim // Cf.shape[1])
+    dA = torch.exp(dtf[:, :, None] * A.float()[None])
+    dB = dtf[:, :, None] * Bf
+    new_state = state.float() * dA + dB * x.float()[:, :, None]
+    state.copy_(new_state.to(state.dtype))
+    out = torch.einsum("bdn,bdn->bd", new_state, Cf)
+    if D is not None:
+        out = out + x.float() * D.float()
+    if z is not None:
+        out = out * F.silu(z.float())
+    return out.to(x.dtype)
+
+
+def mamba_step_fallback_ref(state, x, dt, A, B, C, D, z, dt_bias):
+    """Literal dtype behaviour of the reference's torch fallback
+    (mamba_simplemotif.py:369-376): discretisation in dt's dtype, readout of
+    ``state.to(x.dtype)``. Updates ``state`` in place and returns y (x.dtype)."""
+    dtype = x.dtype
+    dtl = F.softplus(dt + dt_bias.to(dtype=dt.dtype))
+    dA = torch.exp(torch.einsum("bd,dn->bdn", dtl, A))
+    dB = torch.einsum("bd,bn->bdn", dtl, B)
+    state.copy_(state * dA + rearrange(x, "b d -> b d 1") * dB)
+    y = torch.einsum("bdn,bn->bd", state.to(dtype), C)
+    y = y + D.to(dtype) * x
+    return y * F.silu(z)
+
+
+def softplus_f64(x: float) -> float:
+    """float64 softplus with torch's threshold of 20 (used by the brute-force restatement)."""
+    return x if x > 20.0 else math.log1p(math.exp(x))

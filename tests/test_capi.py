@@ -1,0 +1,123 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads, exports every function the header
+declares, its parameter structs have the layout of include/mm_scan.h, and invalid requests are
+rejected before anything is launched. No GPU needed (no call here reaches a kernel launch)."""
+import ctypes
+import os
+import subprocess
+
+import pytest
+import torch
+
+from tests import capi
+
+
+def test_library_exports_every_header_function():
+    lib = capi.load()
+    names = capi.header_functions()
+    assert set(names) == {"mm_scan_fwd", "mm_state_update", "mm_last_error", "mm_abi_version"}
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.mm_abi_version() == 1
+
+
+def _c_layout(struct, fields, tmp_path):
+    src = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mm_scan.h"', 'int main(void) {',
+             f'  printf("%zu\\n", sizeof({struct}));']
+    lines += [f'  printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
+    lines += ['  return 0;', '}']
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.check_call(["gcc", "-std=c11", f"-I{os.path.join(capi.REPO, 'include')}", str(src), "-o", str(exe)])
+    return [int(x) for x in subprocess.check_output([str(exe)]).split()]
+
+
+@pytest.mark.parametrize("cname,pystruct", [("mm_scan_fwd_params", capi.ScanFwdParams),
+                                            ("mm_state_update_params", capi.StateUpdateParams)])
+def test_struct_layout_matches_header(tmp_path, cname, pystruct):
+    fields = [f for f, _ in pystruct._fields_]
+    got = _c_layout(cname, fields, tmp_path)
+    assert got[0] == ctypes.sizeof(pystruct)
+    assert got[1:] == [getattr(pystruct, f).offset for f in fields]
+
+
+def _valid_looking_params():
+    p = capi.ScanFwdParams()
+    p.batch, p.dim, p.seqlen, p.dstate, p.n_groups = 2, 8, 16, 16, 1
+    p.itype = 2
+    p.is_variable_B = p.is_variable_C = 1
+    fake = 0x1000
+    p.u = p.delta = p.A = p.B = p.C = p.out = fake
+    return p
+
+
+@pytest.mark.parametrize("mutate,needle", [
+    (lambda p: setattr(p, "dstate", 257), "state dimension"),
+    (lambda p: setattr(p, "dstate", 0), "state dimension"),
+    (lambda p: setattr(p, "n_groups", 3), "multiple of n_groups"),
+    (lambda p: setattr(p, "itype", 7), "itype"),
+    (lambda p: setattr(p, "seqlen", -1), "negative"),
+    (lambda p: setattr(p, "u", None), "required"),
+    (lambda p: setattr(p, "z", 0x2000), "out_z is required"),
+    (lambda p: (setattr(p, "out", None)), "no output"),
+])
+def test_scan_fwd_rejects_invalid_params(mutate, needle):
+    lib = capi.load()
+    p = _valid_looking_params()
+    mutate(p)
+    rc = lib.mm_scan_fwd(ctypes.byref(p), None)
+    assert rc == capi.MM_ERR_INVALID_ARGUMENT
+    assert needle in lib.mm_last_error().decode()
+
+
+def test_scan_fwd_null_params_and_empty_batch():
+    lib = capi.load()
+    assert lib.mm_scan_fwd(None, None) == capi.MM_ERR_INVALID_ARGUMENT
+    p = _valid_looking_params()
+    p.batch = 0          # nothing to do: returns before touching any pointer or the GPU
+    assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_OK
+
+
+def test_state_update_rejects_invalid_params():
+    lib = capi.load()
+    assert lib.mm_state_update(None, None) == capi.MM_ERR_INVALID_ARGUMENT
+    p = capi.StateUpdateParams()
+    p.batch, p.dim, p.dstate, p.n_groups, p.itype = 1, 4, 16, 1, 2
+    assert lib.mm_state_update(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "required" in lib.mm_last_error().decode()
+    p.dstate = 300
+    assert lib.mm_state_update(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+
+
+def test_binding_checks_mirror_reference():
+    """TORCH_CHECK failures raise RuntimeError like selective_scan.cpp:280-381 (CPU tensors fail
+    the is_cuda check before anything is launched)."""
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    u = torch.zeros(1, 4, 8)
+    A = -torch.ones(4, 16)
+    B = torch.zeros(1, 1, 16, 8)
+    with pytest.raises(RuntimeError):
+        ext.fwd(u, u, A, B, B)
+    with pytest.raises(RuntimeError):
+        ext.fwd(u.to(torch.int32), u, A, B, B)
+    with pytest.raises(NotImplementedError):
+        ext.fwd(u, u, A, B, B, P=A)
+    with pytest.raises(RuntimeError):
+        ext.state_update(torch.zeros(1, 4, 16), u[:, :, 0], u[:, :, 0], A, B[:, 0, :, 0], B[:, 0, :, 0])
+
+
+def test_python_api_refuses_out_of_scope_paths():
+    from motif_mamba_amd import selective_scan_fn
+    u = torch.zeros(1, 4, 8)
+    with pytest.raises(NotImplementedError):
+        selective_scan_fn(u, u, -torch.ones(4, 16), torch.zeros(1, 16, 8), torch.zeros(1, 16, 8), P=torch.zeros(16, 2))
+
+
+def test_mamba_ssm_import_paths_resolve_to_hip_kernels():
+    import mamba_ssm.ops.selective_scan_interface as ssi
+    import mamba_ssm.ops.triton.selective_state_update as ssu
+    import motif_mamba_amd
+    assert ssi.selective_scan_fn is motif_mamba_amd.selective_scan_fn
+    assert ssi.SelectiveScanFn is motif_mamba_amd.SelectiveScanFn
+    assert ssu.selective_state_update is motif_mamba_amd.selective_state_update

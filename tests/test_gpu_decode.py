@@ -1,0 +1,183 @@
+"""GPU parity of the single-token decode update (``selective_state_update``) against the CPU
+oracle ``oracle.ssm_ref.selective_state_update_ref`` (decode math of mamba_simplemotif.py:369-376,
+discretisation in float32 as in the upstream kernel). Calls go through the C ABI (binding or
+ctypes). Tolerances: fp32 rtol 1e-4 / atol 1e-5; bf16/fp16 rtol 3e-2 / atol 5e-2 on the output;
+the float32 state is held to rtol 1e-4 / atol 1e-5 after one step (bf16 inputs are exact in fp32).
+"""
+import ctypes
+import math
+import sys
+
+import pytest
+import torch
+
+from oracle.ssm_ref import selective_scan_ref, selective_state_update_ref
+from tests import capi, fixtures
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg):
+    print(f"\n[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _inputs(seed, batch, dim, N, dtype, G=0, with_D=True, with_z=True, with_bias=True):
+    g = torch.Generator().manual_seed(seed)
+    state = torch.randn(batch, dim, N, generator=g) * 0.1
+    x = torch.randn(batch, dim, generator=g).to(dtype)
+    dt = torch.randn(batch, dim, generator=g).to(dtype)
+    z = torch.randn(batch, dim, generator=g).to(dtype) if with_z else None
+    A = -(torch.rand(dim, N, generator=g) * 8 + 0.05)
+    shp = (batch, G, N) if G else (batch, N)
+    B = torch.randn(*shp, generator=g).to(dtype)
+    C = torch.randn(*shp, generator=g).to(dtype)
+    D = torch.randn(dim, generator=g) if with_D else None
+    lo, hi = math.log(1e-3), math.log(1e-1)
+    bias = (torch.rand(dim, generator=g) * (hi - lo) + lo).float() if with_bias else None
+    return dict(state=state, x=x, dt=dt, A=A, B=B, C=C, D=D, z=z, dt_bias=bias)
+
+
+def _gpu(d):
+    return {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in d.items()}
+
+
+CASES = [(1, 64, 16, 0), (3, 100, 16, 0), (64, 128, 16, 0), (2, 64, 8, 0), (2, 64, 32, 0),
+         (2, 64, 64, 2), (2, 32, 100, 0), (4, 128, 16, 4), (2, 64, 1, 0)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}d{c[1]}N{c[2]}G{c[3]}" for c in CASES])
+def test_state_update_vs_oracle(case, dtype):
+    batch, dim, N, G = case
+    _say(f"decode {case} {dtype}")
+    inp = _inputs(5, batch, dim, N, dtype, G)
+    ref_state = inp["state"].clone()
+    exp = selective_state_update_ref(ref_state, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                     inp["z"], inp["dt_bias"], dt_softplus=True)
+    from motif_mamba_amd import selective_state_update
+    g = _gpu(inp)
+    out = selective_state_update(g["state"], g["x"], g["dt"], g["A"], g["B"], g["C"], g["D"], g["z"],
+                                 g["dt_bias"], dt_softplus=True)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == (batch, dim)
+    rtol, atol = fixtures.tolerances(dtype)
+    torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=rtol, atol=atol)
+    torch.testing.assert_close(g["state"].cpu(), ref_state, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("flags", [dict(with_D=False), dict(with_z=False), dict(with_bias=False)],
+                         ids=["noD", "noz", "nobias"])
+def test_state_update_optional_inputs(flags):
+    _say(f"decode optional {flags}")
+    inp = _inputs(6, 4, 64, 16, torch.bfloat16, **flags)
+    for softplus in (True, False):
+        ref_state = inp["state"].clone()
+        exp = selective_state_update_ref(ref_state, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                         inp["z"], inp["dt_bias"], dt_softplus=softplus)
+        from motif_mamba_amd import selective_state_update
+        g = _gpu(inp)
+        out = selective_state_update(g["state"], g["x"], g["dt"], g["A"], g["B"], g["C"], g["D"], g["z"],
+                                     g["dt_bias"], dt_softplus=softplus)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+        torch.testing.assert_close(g["state"].cpu(), ref_state, rtol=1e-4, atol=1e-5)
+
+
+def test_state_update_strided_state_and_multihead():
+    """state as a non-contiguous slice of a larger cache, and the (batch, nheads, headdim, dstate)
+    form flattened to dim = nheads * headdim."""
+    _say("decode strided + multihead")
+    from motif_mamba_amd import selective_state_update
+    inp = _inputs(7, 3, 64, 16, torch.bfloat16)
+    cache = torch.zeros(3, 64, 32, device=DEV)
+    cache[:, :, 8:24] = inp["state"].to(DEV)
+    view = cache[:, :, 8:24]
+    assert not view.is_contiguous()
+    ref_state = inp["state"].clone()
+    exp = selective_state_update_ref(ref_state, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                     inp["z"], inp["dt_bias"], dt_softplus=True)
+    g = _gpu(inp)
+    out = selective_state_update(view, g["x"], g["dt"], g["A"], g["B"], g["C"], g["D"], g["z"], g["dt_bias"], True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+    torch.testing.assert_close(view.cpu(), ref_state, rtol=1e-4, atol=1e-5)
+    assert torch.count_nonzero(cache[:, :, :8]) == 0 and torch.count_nonzero(cache[:, :, 24:]) == 0
+    # multi-head: 4 heads x 16 headdim
+    st4 = inp["state"].view(3, 4, 16, 16).clone().to(DEV)
+    out4 = selective_state_update(st4, g["x"].view(3, 4, 16), g["dt"].view(3, 4, 16), g["A"].view(4, 16, 16),
+                                  g["B"].view(3, 1, 16), g["C"].view(3, 1, 16), g["D"].view(4, 16),
+                                  g["z"].view(3, 4, 16), g["dt_bias"].view(4, 16), True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out4.cpu().reshape(3, 64).float(), exp.float(), rtol=3e-2, atol=5e-2)
+    torch.testing.assert_close(st4.cpu().reshape(3, 64, 16), ref_state, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_decode_steps_match_gpu_scan(dtype):
+    """L decode steps from a zero state reproduce the GPU scan over the same L tokens (outputs and
+    final state), and both match the oracle scan."""
+    _say(f"decode-vs-scan {dtype}")
+    from motif_mamba_amd import selective_scan_fn, selective_state_update
+    batch, dim, L, N = 2, 64, 40, 16
+    g = torch.Generator().manual_seed(8)
+    u = torch.randn(batch, dim, L, generator=g).to(dtype)
+    delta = torch.randn(batch, dim, L, generator=g).to(dtype)
+    z = torch.randn(batch, dim, L, generator=g).to(dtype)
+    B = torch.randn(batch, N, L, generator=g).to(dtype)
+    C = torch.randn(batch, N, L, generator=g).to(dtype)
+    A = -(torch.rand(dim, N, generator=g) * 4 + 0.1)
+    D = torch.randn(dim, generator=g)
+    bias = torch.rand(dim, generator=g) - 3
+    exp, exp_last = selective_scan_ref(u, delta, A, B, C, D, z, bias, True, return_last_state=True)
+    gu, gd, gz, gB, gC, gA, gD, gb = (t.to(DEV) for t in (u, delta, z, B, C, A, D, bias))
+    scan_out, scan_last = selective_scan_fn(gu, gd, gA, gB, gC, gD, gz, gb, True, return_last_state=True)
+    state = torch.zeros(batch, dim, N, device=DEV)
+    outs = []
+    for t in range(L):
+        outs.append(selective_state_update(state, gu[:, :, t], gd[:, :, t], gA, gB[:, :, t].contiguous(),
+                                           gC[:, :, t].contiguous(), gD, gz[:, :, t], gb, True))
+    dec = torch.stack(outs, dim=2)
+    torch.cuda.synchronize()
+    rtol, atol = fixtures.tolerances(dtype)
+    torch.testing.assert_close(dec.cpu().float(), scan_out.cpu().float(), rtol=rtol, atol=atol)
+    torch.testing.assert_close(state.cpu(), scan_last.cpu(), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(dec.cpu().float(), exp.float(), rtol=rtol, atol=atol)
+
+
+@pytest.mark.parametrize("batch", [1, 64, 256])
+def test_config4_shapes_steps(batch):
+    """BASELINE config 4 (d_inner 5120, bf16, fp32 state): 8 consecutive steps vs the oracle."""
+    from motif_mamba_amd import selective_state_update
+    from motif_mamba_amd.workloads import DECODE_CONFIGS, decode_inputs
+    cfg = DECODE_CONFIGS[f"cfg4_b{batch}"]
+    _say(f"config-4 decode batch {batch}")
+    t = decode_inputs(cfg, steps=8)
+    ref_state = t["state"].clone()
+    g = _gpu(t)
+    for s in range(8):
+        exp = selective_state_update_ref(ref_state, t["x"][s], t["dt"][s], t["A"], t["B"][s], t["C"][s], t["D"],
+                                         t["z"][s], t["dt_bias"], dt_softplus=True)
+        out = selective_state_update(g["state"], g["x"][s], g["dt"][s], g["A"], g["B"][s], g["C"][s], g["D"],
+                                     g["z"][s], g["dt_bias"], dt_softplus=True)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+    torch.testing.assert_close(g["state"].cpu(), ref_state, rtol=1e-4, atol=1e-5)
+
+
+def test_state_update_c_abi_direct():
+    _say("decode C ABI via ctypes")
+    lib = capi.load()
+    inp = _inputs(9, 4, 128, 16, torch.bfloat16)
+    ref_state = inp["state"].clone()
+    exp = selective_state_update_ref(ref_state, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                     inp["z"], inp["dt_bias"], dt_softplus=True)
+    g = _gpu(inp)
+    out = torch.empty(4, 128, dtype=torch.bfloat16, device=DEV)
+    p = capi.state_update_params(g["state"], g["x"], g["dt"], g["A"], g["B"], g["C"], out, g["D"], g["z"],
+                                 g["dt_bias"], True)
+    assert lib.mm_state_update(ctypes.byref(p), capi.stream_handle()) == 0, lib.mm_last_error()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+    torch.testing.assert_close(g["state"].cpu(), ref_state, rtol=1e-4, atol=1e-5)

@@ -1,0 +1,233 @@
+"""GPU parity of the forward selective scan against the CPU oracle (MI355X only).
+
+Every call goes through the C ABI of libmm_scan.so -- via the PyTorch-ROCm binding behind
+``selective_scan_fn`` or directly through ctypes -- and is compared with
+``oracle.ssm_ref.selective_scan_ref`` (restating ssi.py:353-451) on the same seeded inputs, or,
+at the full benchmark shapes, with the float64 C restatement on sampled rows.
+Tolerances (north_star): fp32 rtol 1e-4 / atol 1e-5; bf16/fp16 inputs rtol 3e-2 / atol 5e-2.
+"""
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+from einops import rearrange
+
+from oracle import cscan
+from oracle.ssm_ref import chunk_states_ref, selective_scan_ref
+from tests import capi, fixtures
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg):
+    print(f"\n[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _to(d, dev):
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in d.items()}
+
+
+def _run(inputs, **kw):
+    from motif_mamba_amd import selective_scan_fn
+    g = _to(inputs, DEV)
+    out, last = selective_scan_fn(**g, return_last_state=True, **kw)
+    torch.cuda.synchronize()
+    return out.cpu(), last.cpu()
+
+
+def _close(a, b, dtype, what):
+    rtol, atol = fixtures.tolerances(dtype)
+    torch.testing.assert_close(a.float(), b.float(), rtol=rtol, atol=atol, msg=lambda m: f"{what}: {m}")
+
+
+def _case(seed, batch, dim, L, N, dtype, bkind="3d", G=1, with_D=True, with_z=True, with_bias=True,
+          softplus=True):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(batch, dim, L, generator=g).to(dtype)
+    delta = torch.randn(batch, dim, L, generator=g).to(dtype)
+    z = torch.randn(batch, dim, L, generator=g).to(dtype) if with_z else None
+    lo, hi = math.log(1e-3), math.log(1e-1)
+    bias = (torch.rand(dim, generator=g) * (hi - lo) + lo).float() if with_bias else None
+    if bkind == "4d":
+        B = torch.randn(batch, G, N, L, generator=g).to(dtype)
+        C = torch.randn(batch, G, N, L, generator=g).to(dtype)
+    elif bkind == "3d":
+        B = torch.randn(batch, N, L, generator=g).to(dtype)
+        C = torch.randn(batch, N, L, generator=g).to(dtype)
+    else:
+        B = torch.randn(dim, N, generator=g)
+        C = torch.randn(dim, N, generator=g)
+    A = -(torch.rand(dim, N, generator=g) * 8 + 0.05)
+    D = torch.randn(dim, generator=g) if with_D else None
+    return dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, delta_bias=bias, delta_softplus=softplus)
+
+
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name", fixtures.names())
+def test_golden_fixture(name):
+    _say(f"golden fixture {name}")
+    inputs, exp = fixtures.load(name)
+    out, last = _run(inputs)
+    assert out.dtype == exp["out"].dtype
+    _close(out, exp["out"], inputs["u"].dtype, f"{name} out")
+    _close(last, exp["last_state"], inputs["u"].dtype, f"{name} last_state")
+
+
+SHAPES = [
+    # (batch, dim, L, N, bkind, G)
+    (2, 64, 1, 16, "3d", 1),
+    (2, 64, 5, 16, "3d", 1),
+    (2, 64, 64, 16, "3d", 1),
+    (3, 96, 130, 16, "4d", 2),
+    (1, 128, 257, 16, "4d", 4),
+    (2, 40, 33, 16, "3d", 1),        # dim not a multiple of 64
+    (2, 64, 96, 8, "3d", 1),         # N < 16
+    (1, 64, 48, 1, "3d", 1),
+    (2, 64, 72, 32, "4d", 2),
+    (1, 64, 40, 64, "3d", 1),
+    (1, 8, 24, 100, "3d", 1),        # N > 64 (generic path)
+    (2, 64, 50, 16, "const", 1),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"b{s[0]}d{s[1]}L{s[2]}N{s[3]}{s[4]}G{s[5]}" for s in SHAPES])
+def test_random_shapes(shape, dtype):
+    batch, dim, L, N, bkind, G = shape
+    _say(f"random shape {shape} {dtype}")
+    case = _case(7, batch, dim, L, N, dtype, bkind, G)
+    exp, exp_last = selective_scan_ref(**case, return_last_state=True)
+    out, last = _run(case)
+    _close(out, exp, dtype, "out_z")
+    _close(last, exp_last, dtype, "last_state")
+
+
+@pytest.mark.parametrize("flags", [dict(with_D=False), dict(with_z=False), dict(with_bias=False),
+                                   dict(softplus=False), dict(with_D=False, with_z=False, with_bias=False,
+                                                              softplus=False)],
+                         ids=["noD", "noz", "nobias", "nosoftplus", "bare"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_optional_inputs(flags, dtype):
+    _say(f"optional inputs {flags} {dtype}")
+    case = _case(8, 2, 64, 80, 16, dtype, **flags)
+    exp, exp_last = selective_scan_ref(**case, return_last_state=True)
+    out, last = _run(case)
+    _close(out, exp, dtype, "out")
+    _close(last, exp_last, dtype, "last_state")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_strided_inputs_like_mamba_block(dtype):
+    """x, z = xz.chunk(2, dim=1) and delta with strides (L, B*L, 1), as Mambamotif passes them
+    (mamba_simplemotif.py:288, 308-313)."""
+    _say(f"strided inputs {dtype}")
+    batch, dim, L, N = 2, 64, 96, 16
+    g = torch.Generator().manual_seed(9)
+    xz = torch.randn(batch, 2 * dim, L, generator=g).to(dtype)
+    dt_base = torch.randn(dim, batch * L, generator=g).to(dtype)
+    B = torch.randn(batch, N, L, generator=g).to(dtype)
+    C = torch.randn(batch, N, L, generator=g).to(dtype)
+    A = -torch.rand(dim, N, generator=g) * 4
+    D = torch.randn(dim, generator=g)
+    bias = torch.rand(dim, generator=g) - 4
+
+    def views(xz_, dt_base_):
+        x, z = xz_.chunk(2, dim=1)
+        return x, z, rearrange(dt_base_, "d (b l) -> b d l", l=L)
+
+    x, z, dt = views(xz, dt_base)
+    exp, exp_last = selective_scan_ref(x, dt, A, B, C, D, z, bias, True, return_last_state=True)
+    gx, gz, gdt = views(xz.to(DEV), dt_base.to(DEV))
+    assert not gx.is_contiguous() and gdt.stride() == (L, batch * L, 1)
+    from motif_mamba_amd import selective_scan_fn
+    out, last = selective_scan_fn(gx, gdt, A.to(DEV), B.to(DEV), C.to(DEV), D.to(DEV), gz, bias.to(DEV),
+                                  True, return_last_state=True)
+    torch.cuda.synchronize()
+    _close(out.cpu(), exp, dtype, "out_z")
+    _close(last.cpu(), exp_last, dtype, "last_state")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_reference_fwd_outputs(dtype):
+    """ext.fwd returns [out, x, out_z] in the layout of selective_scan_cuda.fwd
+    (selective_scan.cpp:383-412): out pre-gate, x = (B, D, ceil(L/2048), 2N) (prod a, h) pairs."""
+    _say(f"reference-format fwd {dtype}")
+    from motif_mamba_amd import _native
+    L = 4100
+    case = _case(10, 1, 64, L, 16, dtype, bkind="4d", G=1)
+    exp_z, exp_last = selective_scan_ref(**case, return_last_state=True)
+    exp_out = selective_scan_ref(**{**case, "z": None})
+    g = _to(case, DEV)
+    out, x, out_z = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], D=g["D"], z=g["z"],
+                                      delta_bias=g["delta_bias"], delta_softplus=True)
+    torch.cuda.synchronize()
+    assert x.shape == (1, 64, 3, 32) and x.dtype == torch.float32
+    _close(out.cpu(), exp_out, dtype, "out")
+    _close(out_z.cpu(), exp_z, dtype, "out_z")
+    _close(x[:, :, -1, 1::2].cpu(), exp_last, dtype, "x[..., -1, 1::2]")
+    rows = [(0, d) for d in range(0, 64, 9)]
+    r = cscan.scan_rows(**case, rows=rows, chunk=2048)
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(x[b, d, :, 1::2].cpu().double().numpy(), r["h_chunks"][i], rtol=1e-3, atol=1e-3)
+    pa = chunk_states_ref(case["delta"], case["A"], case["delta_bias"], True)
+    np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
+
+
+def test_c_abi_direct_call():
+    """libmm_scan.so called through ctypes (no torch binding) on the config-0 fixture."""
+    _say("C ABI via ctypes, cfg0")
+    lib = capi.load()
+    inputs, exp = fixtures.load("cfg0")
+    g = _to(inputs, DEV)
+    Bv = g["B"].unsqueeze(1)
+    Cv = g["C"].unsqueeze(1)
+    out_z = torch.empty_like(g["z"])
+    last = torch.empty(g["u"].shape[0], g["u"].shape[1], g["A"].shape[1], device=DEV)
+    p = capi.scan_fwd_params(g["u"], g["delta"], g["A"], Bv, Cv, g["D"], g["z"], g["delta_bias"], True,
+                             out_z=out_z, last_state=last)
+    rc = lib.mm_scan_fwd(ctypes.byref(p), capi.stream_handle())
+    assert rc == 0, lib.mm_last_error()
+    torch.cuda.synchronize()
+    _close(out_z.cpu(), exp["out"], torch.float32, "out_z")
+    _close(last.cpu(), exp["last_state"], torch.float32, "last_state")
+
+
+def test_deterministic():
+    _say("determinism cfg-like bf16")
+    case = _to(_case(11, 2, 128, 600, 16, torch.bfloat16), DEV)
+    from motif_mamba_amd import selective_scan_fn
+    a, la = selective_scan_fn(**case, return_last_state=True)
+    b, lb = selective_scan_fn(**case, return_last_state=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+# ---------------------------------------------------------------------------------------------
+# Full benchmark shapes: sampled rows against the float64 C restatement, plus global properties.
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3_g1", "cfg3_g4"])
+def test_full_size_config(cfg):
+    from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_inputs
+    c = SCAN_CONFIGS[cfg]
+    _say(f"full-size {cfg}: {c}")
+    inputs = scan_inputs(c)
+    inputs.pop("return_last_state")
+    dtype = inputs["u"].dtype
+    out, last = _run(inputs)
+    assert out.shape == inputs["u"].shape and out.dtype == dtype
+    assert torch.isfinite(out.float()).all() and torch.isfinite(last).all()
+    gsz = c.dim // c.n_groups
+    ds = sorted({0, 1, 63, 64, gsz - 1, gsz, c.dim - 1, c.dim // 2 + 5, 777 % c.dim, 1234 % c.dim})
+    rows = [(b, d) for b in sorted({0, c.batch - 1}) for d in ds if d < c.dim]
+    r = cscan.scan_rows(**inputs, rows=rows)
+    rtol, atol = fixtures.tolerances(dtype)
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(out[b, d].double().numpy(), r["out_z"][i], rtol=rtol, atol=atol,
+                                   err_msg=f"{cfg} row {(b, d)} out_z")
+        np.testing.assert_allclose(last[b, d].double().numpy(), r["last_state"][i], rtol=rtol, atol=atol,
+                                   err_msg=f"{cfg} row {(b, d)} last_state")
