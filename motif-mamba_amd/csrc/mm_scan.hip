@@ -89,7 +89,7 @@ scan_fwd_rowlane(const mm_scan_fwd_params p, const int64_t ratio, const int32_t 
         }
 #pragma unroll(NS <= 64 ? NS : 8)
         for (int n = 0; n < NS; ++n) {
-            if (NS > 16 && n >= N) break;
+            if (n >= N) break;  // states past dstate: no B/C rows exist there
             float bb[8], cc[8];
             if (Bv) {
                 if (VEC && nt == 8) {

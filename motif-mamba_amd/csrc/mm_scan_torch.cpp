@@ -9,9 +9,11 @@
 // state_update(.) the decode step (replaces upstream selective_state_update, called at
 //                 mamba_ssm/modules/mamba_simplemotif.py:397-399).
 // Validation failures raise RuntimeError through TORCH_CHECK, like the reference binding.
+// ROCm torch reports GPU tensors with device type "cuda"; the generic c10::DeviceGuard accepts it,
+// and c10::hip::getCurrentHIPStream() is the stream torch launches its own HIP work on.
 #include <torch/extension.h>
 
-#include <c10/hip/HIPGuard.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
 #include <vector>
@@ -197,7 +199,7 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
         set_out_z(p, out_z);
     }
     p.chunk_states = x.data_ptr<float>();
-    c10::hip::HIPGuard device_guard{u.device()};
+    const c10::DeviceGuard device_guard{u.device()};
     check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
     std::vector<at::Tensor> result = {out, x};
     if (z_.has_value()) result.push_back(out_z);
@@ -224,7 +226,7 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
         last_state = torch::empty({p.batch, p.dim, p.dstate}, u.options().dtype(at::ScalarType::Float));
         p.last_state = last_state.data_ptr<float>();
     }
-    c10::hip::HIPGuard device_guard{u.device()};
+    const c10::DeviceGuard device_guard{u.device()};
     check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
     if (return_last_state) return {main, last_state};
     return {main};
@@ -319,7 +321,7 @@ at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::
         p.C_batch_stride = C.stride(0);
         p.C_dstate_stride = C.stride(1);
     }
-    c10::hip::HIPGuard device_guard{state.device()};
+    const c10::DeviceGuard device_guard{state.device()};
     check_rc(mm_state_update(&p, c10::hip::getCurrentHIPStream().stream()), "mm_state_update");
     return out;
 }

@@ -31,10 +31,16 @@ def _edge_case(seed, batch, dim, L, N, G, dtype, bkind, with_D=True, with_z=True
                softplus=True):
     g = torch.Generator().manual_seed(seed)
     u = torch.randn(batch, dim, L, generator=g).to(dtype)
-    delta = torch.randn(batch, dim, L, generator=g).to(dtype)
+    delta = torch.randn(batch, dim, L, generator=g)
     z = torch.randn(batch, dim, L, generator=g).to(dtype) if with_z else None
     lo, hi = np.log(1e-3), np.log(1e-1)
     bias = (torch.rand(dim, generator=g) * (hi - lo) + lo).float() if with_bias else None
+    if not softplus:
+        # the raw step size is used: keep it non-negative, as callers without softplus do
+        delta = delta.abs() * 0.1
+        if bias is not None:
+            bias = bias.exp()
+    delta = delta.to(dtype)
     if bkind == "4d":
         B = torch.randn(batch, G, N, L, generator=g).to(dtype)
         C = torch.randn(batch, G, N, L, generator=g).to(dtype)

@@ -49,10 +49,16 @@ def _case(seed, batch, dim, L, N, dtype, bkind="3d", G=1, with_D=True, with_z=Tr
           softplus=True):
     g = torch.Generator().manual_seed(seed)
     u = torch.randn(batch, dim, L, generator=g).to(dtype)
-    delta = torch.randn(batch, dim, L, generator=g).to(dtype)
+    delta = torch.randn(batch, dim, L, generator=g)
     z = torch.randn(batch, dim, L, generator=g).to(dtype) if with_z else None
     lo, hi = math.log(1e-3), math.log(1e-1)
     bias = (torch.rand(dim, generator=g) * (hi - lo) + lo).float() if with_bias else None
+    if not softplus:
+        # without softplus the step size is used raw: keep delta + bias >= 0 as real callers do
+        delta = delta.abs() * 0.1
+        if bias is not None:
+            bias = bias.exp()
+    delta = delta.to(dtype)
     if bkind == "4d":
         B = torch.randn(batch, G, N, L, generator=g).to(dtype)
         C = torch.randn(batch, G, N, L, generator=g).to(dtype)
