@@ -43,6 +43,25 @@ __device__ __forceinline__ float softplus_f32(float x) {
 // silu(z) = z / (1 + exp(-z)), in float32.
 __device__ __forceinline__ float silu_f32(float z) { return z / (1.f + expf(-z)); }
 
+// softplus with torch's threshold (x > 20 ? x : log1p(exp(x))) built on v_exp_f32 / v_log_f32.
+// log1p(e) = log(u) + (e - (u - 1)) / u with u = fl(1 + e): the second term restores the part of e
+// lost when rounding 1 + e (exact for e <= 1 by Fast2Sum). 1/u is replaced by max(2 - u, 0): exact
+// at u = 1, and for u >= 2 the term is below 2^-24 relative to log(u) >= 0.69, so dropping it costs
+// under an ulp. Relative error stays at a few ulp for every x, including x << 0 where log1p(e) ~ e.
+__device__ __forceinline__ float softplus_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * kLog2e);
+    const float u = 1.f + e;
+    const float lost = e - (u - 1.f);
+    const float corr = lost * __builtin_fmaxf(2.f - u, 0.f);
+    const float r = __builtin_fmaf(__builtin_amdgcn_logf(u), kLn2, corr);
+    return x > 20.f ? x : r;
+}
+
+// silu(z) = z * 1 / (1 + 2^(-z log2 e)) with v_exp_f32 and v_rcp_f32 (both ~1 ulp).
+__device__ __forceinline__ float silu_fast(float z) {
+    return z * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
+}
+
 // ---- vector I/O of 8 consecutive elements (16 B for 16-bit types, 32 B for float) -----------
 template <typename T> struct Vec8;
 template <> struct Vec8<float> { uint4 lo, hi; };
@@ -78,8 +97,12 @@ __device__ __forceinline__ Vec8<float> pack8_f32(const float *x) {
     v.hi = make_uint4(__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7]));
     return v;
 }
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// Two floats -> packed bf16 pair, round-to-nearest-even (one v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return uint32_t(f32_to_bf16_bits(a)) | (uint32_t(f32_to_bf16_bits(b)) << 16);
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     union { uint32_t u; _Float16 h[2]; } c; c.h[0] = (_Float16)a; c.h[1] = (_Float16)b;

@@ -12,6 +12,10 @@ int launch_status(const char *what);
 // Records `msg` as the thread's last error and returns `code`.
 int set_error(int code, const char *msg);
 
+// True when every activation row start (u, delta, z, out, out_z, variable B/C) is 16-byte aligned
+// and seqlen is a multiple of 8, so rows can be moved in 16-byte vectors.
+bool fwd_vector_ok(const mm_scan_fwd_params *p);
+
 // Tiled forward kernel (mm_scan_tiled.hip). Returns MM_ERR_UNSUPPORTED, without launching,
 // when the request falls outside the shapes that kernel covers; the caller then uses the
 // lane-per-row kernel.

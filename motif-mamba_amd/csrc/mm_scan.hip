@@ -250,6 +250,26 @@ int launch_status(const char *what) {
 
 int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
 
+// 16-byte vector I/O is legal when every row start is 16-byte aligned and L is a multiple of 8.
+bool fwd_vector_ok(const mm_scan_fwd_params *p) {
+    const int64_t eb = elem_bytes(p->itype);
+    auto row_ok = [&](const void *base, int64_t s0, int64_t s1) {
+        return base == nullptr || (aligned16(base) && (s0 * eb) % 16 == 0 && (s1 * eb) % 16 == 0);
+    };
+    if (p->seqlen % 8 != 0) return false;
+    bool ok = row_ok(p->u, p->u_batch_stride, p->u_d_stride) && row_ok(p->delta, p->delta_batch_stride, p->delta_d_stride) &&
+              row_ok(p->z, p->z_batch_stride, p->z_d_stride) && row_ok(p->out, p->out_batch_stride, p->out_d_stride) &&
+              row_ok(p->out_z, p->out_z_batch_stride, p->out_z_d_stride);
+    if (p->is_variable_B)
+        ok = ok && aligned16(p->B) && (p->B_batch_stride * eb) % 16 == 0 && (p->B_group_stride * eb) % 16 == 0 &&
+             (p->B_dstate_stride * eb) % 16 == 0;
+    if (p->is_variable_C)
+        ok = ok && aligned16(p->C) && (p->C_batch_stride * eb) % 16 == 0 && (p->C_group_stride * eb) % 16 == 0 &&
+             (p->C_dstate_stride * eb) % 16 == 0;
+    return ok;
+}
+
+
 }  // namespace mm
 
 namespace {
@@ -278,25 +298,6 @@ int validate_fwd(const mm_scan_fwd_params *p) {
     return MM_OK;
 }
 
-// 16-byte vector I/O is legal when every row start is 16-byte aligned and L is a multiple of 8.
-bool fwd_vector_ok(const mm_scan_fwd_params *p) {
-    const int64_t eb = elem_bytes(p->itype);
-    auto row_ok = [&](const void *base, int64_t s0, int64_t s1) {
-        return base == nullptr || (aligned16(base) && (s0 * eb) % 16 == 0 && (s1 * eb) % 16 == 0);
-    };
-    if (p->seqlen % 8 != 0) return false;
-    bool ok = row_ok(p->u, p->u_batch_stride, p->u_d_stride) && row_ok(p->delta, p->delta_batch_stride, p->delta_d_stride) &&
-              row_ok(p->z, p->z_batch_stride, p->z_d_stride) && row_ok(p->out, p->out_batch_stride, p->out_d_stride) &&
-              row_ok(p->out_z, p->out_z_batch_stride, p->out_z_d_stride);
-    if (p->is_variable_B)
-        ok = ok && aligned16(p->B) && (p->B_batch_stride * eb) % 16 == 0 && (p->B_group_stride * eb) % 16 == 0 &&
-             (p->B_dstate_stride * eb) % 16 == 0;
-    if (p->is_variable_C)
-        ok = ok && aligned16(p->C) && (p->C_batch_stride * eb) % 16 == 0 && (p->C_group_stride * eb) % 16 == 0 &&
-             (p->C_dstate_stride * eb) % 16 == 0;
-    return ok;
-}
-
 template <typename T, int NS>
 int launch_rowlane_ns(const mm_scan_fwd_params &p, hipStream_t s, bool vec) {
     const int64_t ratio = p.dim / p.n_groups;
@@ -312,7 +313,7 @@ int launch_rowlane_ns(const mm_scan_fwd_params &p, hipStream_t s, bool vec) {
 
 template <typename T>
 int launch_rowlane(const mm_scan_fwd_params &p, hipStream_t s) {
-    const bool vec = fwd_vector_ok(&p);
+    const bool vec = mm::fwd_vector_ok(&p);
     if (p.dstate <= 16) return launch_rowlane_ns<T, 16>(p, s, vec);
     if (p.dstate <= 32) return launch_rowlane_ns<T, 32>(p, s, vec);
     if (p.dstate <= 64) return launch_rowlane_ns<T, 64>(p, s, vec);
