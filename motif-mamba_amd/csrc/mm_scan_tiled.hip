@@ -2,24 +2,26 @@
 //
 // Reference behaviour: selective_scan_fwd_kernel (csrc/selective_scan/selective_scan_fwd_kernel.cuh:
 // 301-544) / selective_scan_ref (mamba_ssm/ops/selective_scan_interface.py:353-451). The design is
-// this file's own: instead of one 128-thread block per (batch, channel) row with a block-wide scan
-// per state, one wave64 owns 16 channels x 16 states and walks the sequence serially:
+// this file's own. Instead of one thread block per (batch, channel) row running a block-wide scan
+// per state, a workgroup of NW wave64s owns 16 channels x 16 states of one batch row and walks the
+// sequence serially, every state update being one dependent FMA in a lane's registers:
 //
-//   lane = 16 * q + c      q = state group (states 4q .. 4q+3, held in registers), c = channel
+//   wave w, lane = 16 q + c:  channel c of the group, states (4 w + q) K .. +K-1,  K = 4 / NW
 //
-// so every state update is a dependent FMA in one lane's registers (no scan operator, no partial
-// products). The operands each row of 16 lanes shares -- B[n, t] and C[n, t] of its four states --
-// are loaded once per 32-step tile, one 8-step vector per lane, and broadcast to the row with
-// DPP row_newbcast fused into the instruction that consumes them. The per-element terms shared by
-// the four rows -- delta' = softplus(delta + bias) and delta' * u -- are computed once per element
-// (each lane owns 8 consecutive steps of one channel per tile) and exchanged through LDS; the four
-// per-row partial sums of y = sum_n h_n C_n go back through LDS and are added by the lane that owns
-// the element, which also applies D * u, the silu(z) gate and the output conversion. Global loads
-// for tile i+1 are issued before the scan of tile i.
-//
-// Per state update the VALU executes: delta' * A (v_mul), exp2 (v_exp_f32), B * delta'u (v_mul with
-// DPP), h = a h + b (v_fma), y += C h (v_fmac with DPP).
+// so each row of 16 lanes shares its K states, and each column shares a channel.
+//  * B[n, t] and C[n, t] of the row's K states are loaded once per 32-step tile, one small vector
+//    per lane, and broadcast along the row by DPP row_newbcast fused into the instruction that
+//    consumes them (v_mul_f32_dpp for B * delta'u, v_fmac_f32_dpp for y += C h).
+//  * delta' = softplus(delta + bias) and delta' u are computed once per (channel, step) -- each lane
+//    owns 8/NW consecutive steps of one channel per tile -- and exchanged through LDS.
+//  * The 4 NW per-row partial sums of y = sum_n C_n h_n go back through LDS; the lane that owns the
+//    element adds them in a fixed order, applies D u and the silu(z) gate and stores the output.
+//  * Global loads for tile i+1 are issued before the scan of tile i.
+// NW trades per-update overhead (smaller K shares the per-step work among fewer updates) for more
+// concurrent waves per SIMD, which gfx950 needs to reach its VALU/transcendental issue rate.
 #include <hip/hip_runtime.h>
+
+#include <stdlib.h>
 
 #include <type_traits>
 
@@ -30,7 +32,7 @@ namespace mm {
 namespace tiled {
 
 constexpr int kTile = 32;   // sequence steps per tile
-constexpr int kCh = 16;     // channels per wave
+constexpr int kCh = 16;     // channels per workgroup
 constexpr int kPad = 36;    // LDS row stride (floats) of the [channel][step] tiles: 16-B aligned, spreads banks
 
 template <int LANE>
@@ -38,9 +40,9 @@ __device__ __forceinline__ float row_bcast(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + LANE, 0xf, 0xf, false));
 }
 
-// acc += bcast_row(src, LANE) * x  as a single v_fmac_f32_dpp (the compiler does not fuse DPP into
-// the tied-operand v_fmac). The DPP source register must not be written by a VALU instruction in
-// the two preceding wait states; see the s_nop guard where the sources are produced.
+// acc += bcast_row(src, LANE) * x as one v_fmac_f32_dpp (the compiler does not fuse DPP into the
+// tied-operand v_fmac). The DPP source register must not be written by a VALU instruction in the
+// two preceding wait states; the s_nop guard where the sources are produced provides that.
 template <int LANE>
 __device__ __forceinline__ void fmac_row_bcast(float &acc, float src, float x) {
     asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(src), "v"(x), "i"(LANE));
@@ -55,30 +57,87 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-template <typename T>
-__device__ __forceinline__ Vec8<T> load_vec(const T *p) { return *reinterpret_cast<const Vec8<T> *>(p); }
+// N consecutive elements moved as one vector (N * sizeof(T) bytes: 4, 8, 16 or 32).
+template <typename T, int N> struct RawVec { uint32_t w[(N * sizeof(T) + 3) / 4]; };
 
-template <typename T>
-__device__ __forceinline__ Vec8<T> zero_vec() {
-    Vec8<T> v;
-    __builtin_memset(&v, 0, sizeof(v));
-    return v;
+template <typename T, int N>
+__device__ __forceinline__ RawVec<T, N> load_raw(const T *p) {
+    RawVec<T, N> r;
+    constexpr int W = sizeof(r.w) / 4;
+    if constexpr (W == 8) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(p);
+        const uint4 a = q[0], b = q[1];
+        r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w; r.w[4] = b.x; r.w[5] = b.y; r.w[6] = b.z; r.w[7] = b.w;
+    } else if constexpr (W == 4) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(p);
+        r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+    } else if constexpr (W == 2) {
+        const uint2 a = *reinterpret_cast<const uint2 *>(p);
+        r.w[0] = a.x; r.w[1] = a.y;
+    } else {
+        r.w[0] = *reinterpret_cast<const uint32_t *>(p);
+    }
+    return r;
 }
 
-template <typename T, bool SOFTPLUS, bool CHUNKS>
-__global__ void __launch_bounds__(64)
+template <typename T, int N>
+__device__ __forceinline__ void unpack_raw(const RawVec<T, N> &r, float *o) {
+    if constexpr (std::is_same_v<T, float>) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) o[i] = __uint_as_float(r.w[i]);
+    } else if constexpr (std::is_same_v<T, bf16_t>) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) unpack_bf16x2(r.w[i], o[2 * i], o[2 * i + 1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) unpack_f16x2(r.w[i], o[2 * i], o[2 * i + 1]);
+    }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T *p, const float *x) {
+    if constexpr (std::is_same_v<T, float>) {
+        if constexpr (N == 8) {
+            uint4 *q = reinterpret_cast<uint4 *>(p);
+            q[0] = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+            q[1] = make_uint4(__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7]));
+        } else if constexpr (N == 4) {
+            *reinterpret_cast<uint4 *>(p) = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+        } else {
+            *reinterpret_cast<uint2 *>(p) = make_uint2(__float_as_uint(x[0]), __float_as_uint(x[1]));
+        }
+    } else {
+        uint32_t w[N / 2];
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i)
+            w[i] = std::is_same_v<T, bf16_t> ? pack_bf16x2(x[2 * i], x[2 * i + 1]) : pack_f16x2(x[2 * i], x[2 * i + 1]);
+        if constexpr (N == 8) *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+        else if constexpr (N == 4) *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+        else *reinterpret_cast<uint32_t *>(p) = w[0];
+    }
+}
+
+template <typename T, int NW, bool SOFTPLUS, bool CHUNKS>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 4)))
 scan_fwd_tiled16(const mm_scan_fwd_params p, const int64_t ratio) {
+    constexpr int K = 4 / NW;            // states per lane
+    constexpr int E = 8 / NW;            // prologue/epilogue steps per lane per tile
+    constexpr int LPS = 16 / K;          // lanes of a row holding one state's B/C
+    constexpr int SPL = kTile / LPS;     // B/C steps per lane per tile (= 2K)
+    constexpr int NR = 4 * NW;           // rows (state groups) in the workgroup
     __shared__ __align__(16) float sDt[kCh * kPad];
     __shared__ __align__(16) float sDu[kCh * kPad];
-    __shared__ __align__(16) float sY[4 * kCh * kPad];
+    __shared__ __align__(16) float sY[NR * kCh * kPad];
 
-    const int lane = threadIdx.x;
-    const int q = lane >> 4;   // state group of the scan; 8-step slot of the prologue/epilogue
-    const int c = lane & 15;   // channel within the wave
+    const int w = threadIdx.x >> 6;        // wave
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 4;               // row within the wave
+    const int r = 4 * w + q;               // row within the workgroup: state group, and prologue slot
+    const int c = lane & 15;               // channel within the group
     const int64_t b = blockIdx.y;
     const int64_t d0 = int64_t(blockIdx.x) * kCh;
     const int64_t d = d0 + c;
-    const int64_t g = d0 / ratio;  // all 16 channels share one group (checked on the host)
+    const int64_t g = d0 / ratio;          // all 16 channels share one group (checked on the host)
     const int64_t L = p.seqlen;
 
     const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
@@ -86,162 +145,198 @@ scan_fwd_tiled16(const mm_scan_fwd_params p, const int64_t ratio) {
     const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
     T *op = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
     T *ozp = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
-    // The B/C slice this lane loads for its row: state 4q + c/4, steps 8 (c % 4) .. +7 of each tile.
-    const int sb = 8 * (c & 3);
-    const int64_t nrow = 4 * q + (c >> 2);
-    const T *Bp = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + nrow * p.B_dstate_stride + sb;
-    const T *Cp = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + nrow * p.C_dstate_stride + sb;
+    // The B/C slice this lane loads for its row: state r K + c / LPS, steps SPL (c % LPS) .. +SPL-1.
+    const int sb = SPL * (c % LPS);
+    const int64_t nrow = int64_t(r) * K + c / LPS;
+    const T *Bp = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + nrow * p.B_dstate_stride;
+    const T *Cp = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + nrow * p.C_dstate_stride;
 
-    float At[4], h[4];
+    float At[K], h[K];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        At[k] = p.A[d * p.A_d_stride + (4 * q + k) * p.A_dstate_stride] * kLog2e;
+    for (int k = 0; k < K; ++k) {
+        At[k] = p.A[d * p.A_d_stride + (r * K + k) * p.A_dstate_stride] * kLog2e;
         h[k] = 0.f;
     }
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
-    const int es = 8 * q;  // first step (within a tile) of this lane's 8 prologue/epilogue elements
+    const int es = E * r;                  // first step (within a tile) of this lane's elements
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
     float cum_dt = 0.f;
 
-    // Loads past the end of a row are redirected to the row's last 8 elements (always in bounds,
-    // L >= 8 and L % 8 == 0); the prologue zeroes delta' and delta' u of those steps, so they leave
-    // the state unchanged and their outputs are not stored.
-    const int64_t last8 = L - 8;
-    auto clampi = [&](int64_t i) { return i < last8 ? i : last8; };
-    Vec8<T> ru = load_vec(up + clampi(es));
-    Vec8<T> rd = load_vec(dp + clampi(es));
-    Vec8<T> rz = zp ? load_vec(zp + clampi(es)) : zero_vec<T>();
-    Vec8<T> rb = load_vec(Bp - sb + clampi(sb));
-    Vec8<T> rc = load_vec(Cp - sb + clampi(sb));
+    // Loads at or past the end of a row are redirected into the row's last elements (always in
+    // bounds: L >= 8, L % 8 == 0). The prologue zeroes delta' and delta' u of padded steps, so
+    // they leave the state unchanged; their outputs are not stored.
+    const int64_t lastE = L - E, lastS = L - SPL;
+    auto ce = [&](int64_t i) { return i < lastE ? i : lastE; };
+    auto cs = [&](int64_t i) { return i < lastS ? i : lastS; };
+    RawVec<T, E> ru = load_raw<T, E>(up + ce(es));
+    RawVec<T, E> rd = load_raw<T, E>(dp + ce(es));
+    RawVec<T, E> rz = {};
+    if (zp) rz = load_raw<T, E>(zp + ce(es));
+    RawVec<T, SPL> rb = load_raw<T, SPL>(Bp + cs(sb));
+    RawVec<T, SPL> rc = load_raw<T, SPL>(Cp + cs(sb));
 
     for (int64_t t0 = 0; t0 < L; t0 += kTile) {
-        const bool ev = t0 + es < L;  // this lane's 8 elements exist (L is a multiple of 8)
-        float uu[8], dd[8], zz[8], bv[8], cv[8];
-        unpack8(ru, uu);
-        unpack8(rd, dd);
-        unpack8(rz, zz);
-        unpack8(rb, bv);
-        unpack8(rc, cv);
-        // Prefetch the next tile while this one is processed.
+        const bool ev = t0 + es < L;  // this lane's E elements exist (L is a multiple of 8)
+        float uu[E], dd[E], zz[E], bv[SPL], cv[SPL];
+        unpack_raw<T, E>(ru, uu);
+        unpack_raw<T, E>(rd, dd);
+        unpack_raw<T, E>(rz, zz);
+        unpack_raw<T, SPL>(rb, bv);
+        unpack_raw<T, SPL>(rc, cv);
+        // Prefetch the next tile (clamped addresses: always issued, never out of bounds).
         const int64_t t1 = t0 + kTile;
-        if (t1 < L) {
-            ru = load_vec(up + clampi(t1 + es));
-            rd = load_vec(dp + clampi(t1 + es));
-            if (zp) rz = load_vec(zp + clampi(t1 + es));
-            rb = load_vec(Bp - sb + clampi(t1 + sb));
-            rc = load_vec(Cp - sb + clampi(t1 + sb));
-        }
-        // Prologue: delta' and delta' u for (channel c, steps es .. es+7); zero past the end so the
-        // padded steps leave the state unchanged (a = 1, b = 0).
-        float dtp[8], dup[8];
+        ru = load_raw<T, E>(up + ce(t1 + es));
+        rd = load_raw<T, E>(dp + ce(t1 + es));
+        if (zp) rz = load_raw<T, E>(zp + ce(t1 + es));
+        rb = load_raw<T, SPL>(Bp + cs(t1 + sb));
+        rc = load_raw<T, SPL>(Cp + cs(t1 + sb));
+
+        // Prologue: delta' and delta' u for (channel c, steps es .. es+E-1).
+        float dtp[E], dup[E];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < E; ++i) {
             const float x = dd[i] + bias;
             dtp[i] = SOFTPLUS ? softplus_fast(x) : x;
         }
-        if (t1 > L && !ev) {  // padded steps of the last, partial tile
+        if (t1 > L && !ev) {  // padded steps of a last, partial tile
 #pragma unroll
-            for (int i = 0; i < 8; ++i) dtp[i] = 0.f;
+            for (int i = 0; i < E; ++i) dtp[i] = 0.f;
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dup[i] = dtp[i] * uu[i];
-        *reinterpret_cast<float4 *>(&sDt[c * kPad + es]) = make_float4(dtp[0], dtp[1], dtp[2], dtp[3]);
-        *reinterpret_cast<float4 *>(&sDt[c * kPad + es + 4]) = make_float4(dtp[4], dtp[5], dtp[6], dtp[7]);
-        *reinterpret_cast<float4 *>(&sDu[c * kPad + es]) = make_float4(dup[0], dup[1], dup[2], dup[3]);
-        *reinterpret_cast<float4 *>(&sDu[c * kPad + es + 4]) = make_float4(dup[4], dup[5], dup[6], dup[7]);
+        for (int i = 0; i < E; ++i) dup[i] = dtp[i] * uu[i];
+#pragma unroll
+        for (int i = 0; i < E; i += 2) {
+            *reinterpret_cast<float2 *>(&sDt[c * kPad + es + i]) = make_float2(dtp[i], dtp[i + 1]);
+            *reinterpret_cast<float2 *>(&sDu[c * kPad + es + i]) = make_float2(dup[i], dup[i + 1]);
+        }
         // Two wait states between the VALU writes of the DPP sources and their first DPP read.
-        asm volatile("s_nop 1"
-                     : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(bv[4]), "+v"(bv[5]), "+v"(bv[6]), "+v"(bv[7]),
-                       "+v"(cv[0]), "+v"(cv[1]), "+v"(cv[2]), "+v"(cv[3]), "+v"(cv[4]), "+v"(cv[5]), "+v"(cv[6]), "+v"(cv[7]));
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) asm volatile("s_nop 1" : "+v"(bv[i]), "+v"(cv[i]));
         __syncthreads();
 
-        // Scan: 32 steps, 4 per LDS read.
+        // Scan: 32 steps, 4 per LDS read; y partial (sum over this lane's K states) per step.
         static_for<0, kTile / 4>([&](auto S4) {
             constexpr int s4 = decltype(S4)::value;
             const float4 dtq = *reinterpret_cast<const float4 *>(&sDt[c * kPad + 4 * s4]);
             const float4 duq = *reinterpret_cast<const float4 *>(&sDu[c * kPad + 4 * s4]);
             const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
             const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
-            float pv[4];
+            // The decay factors and input terms of the 4 steps do not depend on the state: compute
+            // them all first (16 independent exp2 per lane for K = 4), then run the recurrences.
+            // B and C of state r K + k at step t sit in lane k LPS + t / SPL of this row, register
+            // t % SPL.
+            float av[4][K], bbv[4][K];
             static_for<0, 4>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 constexpr int t = 4 * s4 + j;
                 if (CHUNKS) cum_dt += dts[j];
+                static_for<0, K>([&](auto KK) {
+                    constexpr int k = decltype(KK)::value;
+                    constexpr int src = k * LPS + t / SPL;
+                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    bbv[j][k] = row_bcast<src>(bv[t % SPL]) * dus[j];
+                });
+            });
+            float pv[4];
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int t = 4 * s4 + j;
                 float acc;
-                static_for<0, 4>([&](auto K) {
-                    constexpr int k = decltype(K)::value;
-                    // B and C of state 4q + k at step t sit in lane 4k + t/8 of this row, register t % 8.
-                    constexpr int src = 4 * k + t / 8;
-                    const float a = __builtin_amdgcn_exp2f(dts[j] * At[k]);
-                    const float bb = row_bcast<src>(bv[t % 8]) * dus[j];
-                    h[k] = __builtin_fmaf(a, h[k], bb);
+                static_for<0, K>([&](auto KK) {
+                    constexpr int k = decltype(KK)::value;
+                    constexpr int src = k * LPS + t / SPL;
+                    h[k] = __builtin_fmaf(av[j][k], h[k], bbv[j][k]);
                     if constexpr (k == 0)
-                        acc = row_bcast<src>(cv[t % 8]) * h[k];
+                        acc = row_bcast<src>(cv[t % SPL]) * h[k];
                     else
-                        fmac_row_bcast<src>(acc, cv[t % 8], h[k]);
+                        fmac_row_bcast<src>(acc, cv[t % SPL], h[k]);
                 });
                 pv[j] = acc;
             });
-            *reinterpret_cast<float4 *>(&sY[(q * kCh + c) * kPad + 4 * s4]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kPad + 4 * s4]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
         });
         __syncthreads();
 
-        // Epilogue: y for (channel c, steps es .. es+7) = sum of the four row partials.
-        float y[8];
+        // Epilogue: y for (channel c, steps es .. es+E-1) = the NR row partials, added in row order.
+        float y[E];
 #pragma unroll
-        for (int i = 0; i < 8; i += 4) {
-            float4 acc = *reinterpret_cast<const float4 *>(&sY[(0 * kCh + c) * kPad + es + i]);
+        for (int i = 0; i < E; i += 2) {
+            float2 acc = *reinterpret_cast<const float2 *>(&sY[(0 * kCh + c) * kPad + es + i]);
 #pragma unroll
-            for (int r = 1; r < 4; ++r) {
-                const float4 v = *reinterpret_cast<const float4 *>(&sY[(r * kCh + c) * kPad + es + i]);
-                acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+            for (int rr = 1; rr < NR; ++rr) {
+                const float2 v = *reinterpret_cast<const float2 *>(&sY[(rr * kCh + c) * kPad + es + i]);
+                acc.x += v.x;
+                acc.y += v.y;
             }
-            y[i] = acc.x; y[i + 1] = acc.y; y[i + 2] = acc.z; y[i + 3] = acc.w;
+            y[i] = acc.x;
+            y[i + 1] = acc.y;
         }
         if (ev) {
-            float o[8], oz[8];
+            float o[E];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                o[i] = p.D ? __builtin_fmaf(Dv, uu[i], y[i]) : y[i];
-                oz[i] = zp ? o[i] * silu_fast(zz[i]) : o[i];
+            for (int i = 0; i < E; ++i) o[i] = __builtin_fmaf(Dv, uu[i], y[i]);
+            if (op) store_vec<T, E>(op + t0 + es, o);
+            if (zp) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) o[i] *= silu_fast(zz[i]);
+                store_vec<T, E>(ozp + t0 + es, o);
             }
-            if (op) store8(op + t0 + es, o);
-            if (ozp) store8(ozp + t0 + es, oz);
         }
         if (CHUNKS && p.chunk_states) {
             const int64_t tend = t1 < L ? t1 : L;
             if (tend % MM_SCAN_CHUNK == 0 || tend == L) {
                 const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
-                float *cs = p.chunk_states + ((b * p.dim + d) * n_chunks + ci) * 32 + 8 * q;
+                float *csp = p.chunk_states + ((b * p.dim + d) * n_chunks + ci) * 32 + 2 * K * r;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    cs[2 * k] = __builtin_amdgcn_exp2f(At[k] * cum_dt);
-                    cs[2 * k + 1] = h[k];
+                for (int k = 0; k < K; ++k) {
+                    csp[2 * k] = __builtin_amdgcn_exp2f(At[k] * cum_dt);
+                    csp[2 * k + 1] = h[k];
                 }
             }
         }
     }
     if (p.last_state) {
-        *reinterpret_cast<float4 *>(p.last_state + (b * p.dim + d) * 16 + 4 * q) = make_float4(h[0], h[1], h[2], h[3]);
+        float *ls = p.last_state + (b * p.dim + d) * 16 + K * r;
+#pragma unroll
+        for (int k = 0; k < K; ++k) ls[k] = h[k];
     }
 }
 
+template <typename T, int NW>
+int launch_nw(const mm_scan_fwd_params &p, hipStream_t stream) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
+    auto *kern = p.delta_softplus
+                     ? (p.chunk_states ? scan_fwd_tiled16<T, NW, true, true> : scan_fwd_tiled16<T, NW, true, false>)
+                     : (p.chunk_states ? scan_fwd_tiled16<T, NW, false, true> : scan_fwd_tiled16<T, NW, false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * NW), 0, stream, p, ratio);
+    return launch_status("scan_fwd_tiled16");
+}
+
 }  // namespace tiled
+
+// Waves per 16-channel workgroup; MM_SCAN_NW in the environment overrides the default (1, 2, 4).
+static int tiled_waves() {
+    static int nw = [] {
+        const char *e = getenv("MM_SCAN_NW");
+        const int v = e ? atoi(e) : 2;
+        return (v == 1 || v == 2 || v == 4) ? v : 2;
+    }();
+    return nw;
+}
 
 template <typename T>
 int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return MM_ERR_UNSUPPORTED;
     if (p.dim % tiled::kCh != 0 || (p.dim / p.n_groups) % tiled::kCh != 0) return MM_ERR_UNSUPPORTED;
-    if (p.seqlen < 1 || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
+    if (p.seqlen < 8 || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
     if (p.batch > 65535) return MM_ERR_UNSUPPORTED;
-    if (p.last_state && (reinterpret_cast<uintptr_t>(p.last_state) & 15u)) return MM_ERR_UNSUPPORTED;
-    const int64_t ratio = p.dim / p.n_groups;
-    dim3 grid(unsigned(p.dim / tiled::kCh), unsigned(p.batch));
-    auto *kern = p.delta_softplus ? (p.chunk_states ? tiled::scan_fwd_tiled16<T, true, true> : tiled::scan_fwd_tiled16<T, true, false>)
-                                  : (p.chunk_states ? tiled::scan_fwd_tiled16<T, false, true> : tiled::scan_fwd_tiled16<T, false, false>);
-    hipLaunchKernelGGL(kern, grid, dim3(64), 0, stream, p, ratio);
-    return launch_status("scan_fwd_tiled16");
+    switch (tiled_waves()) {
+        case 1: return tiled::launch_nw<T, 1>(p, stream);
+        case 4: return tiled::launch_nw<T, 4>(p, stream);
+        default: return tiled::launch_nw<T, 2>(p, stream);
+    }
 }
 
 template int try_launch_tiled<float>(const mm_scan_fwd_params &, hipStream_t);
