@@ -147,6 +147,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="headline config only (no secondary configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-ref", action="store_true",
+                    help="also run three 1 GiB device-to-device copies: the reference that scales the "
+                         "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -161,6 +164,14 @@ def main():
 
     _log("config 2 (headline)")
     head = bench_scan("cfg2", args.steps, args.warmup, torch)
+    if args.copy_ref:
+        src = torch.ones(256 * 1024 * 1024, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
     extra = {}
     if not args.quick:
         _log("config 1 (rotating 2 input sets: 2 x 203 MB > Infinity Cache)")

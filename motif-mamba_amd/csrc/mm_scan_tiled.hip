@@ -22,7 +22,9 @@
 #include <hip/hip_runtime.h>
 
 #include <stdlib.h>
+#include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "mm_common.h"
@@ -303,6 +305,545 @@ scan_fwd_tiled16(const mm_scan_fwd_params p, const int64_t ratio) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// scan_fwd_pipe<K>: K states per lane, NW = 4 / K waves = 16 channels x 16 states per workgroup.
+//
+//   lane l of wave w:  row r = 4 w + l / 16 holding states r K .. r K + K-1,  channel c = l % 16
+//
+// The sequence is walked in 16-step tiles with two barriers per tile:
+//
+//   [A]  scan tile j: h_k = exp2(dt' A_k) h_k + B_k dt'u;  sum_k C_k h_k -> sY[r][c][t]
+//   [B]  role group j % 2 (waves [g NW/2, (g+1) NW/2)) finishes tile j: y = sum of the 16/K row
+//        partials, D u, silu(z) gate, store; the other group prepares tile j+1:
+//        dt' = softplus(dt + bias), dt' u -> sDt/sDu[(j+1) % 2]
+//
+// so the per-element work of one tile overlaps the scan bookkeeping of the next and no wave idles
+// between the barriers. Each group owns the elements of every other tile: its 32 NW lanes x E = 2K
+// consecutive steps x 16 channels. B and C of a row's K states are held E steps per lane (LPS lanes
+// per state) and broadcast along the row with DPP. Global loads (B/C for 32 steps, each lane's
+// u/delta/z slice) run PF tile pairs ahead of use.
+//
+// K = 1 gives 5 waves on every SIMD for config 2 (1280 workgroups of 256 threads: 5 per CU), but
+// 2 LDS floats read and 1 written per state update; K = 2 halves that traffic, which on gfx950 (LDS
+// writes ~74 B/clk/CU) decides the rate, at the price of 2-3 waves per SIMD.
+// ---------------------------------------------------------------------------------------------
+constexpr int kT1 = 16;   // steps per tile
+constexpr int kP1 = 20;   // LDS row stride (floats) of sDt/sDu: 16 steps + 4, float4 rows stay 16-B aligned
+
+template <typename T, int K>
+struct PairData {                  // one lane's global data for one 32-step tile pair
+    RawVec<T, 2 * K> b, c;         // B, C of one of the row's states, 2K steps
+    RawVec<T, 2 * K> u, dl, z;     // u, delta, z of the lane's element slice in its group's tile
+};
+
+template <typename T, int K, int PF, bool SOFTPLUS, bool CHUNKS>
+__global__ void __launch_bounds__(256 / K) __attribute__((amdgpu_waves_per_eu(5 - 2 * (K - 1), 8)))
+scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
+    constexpr int NW = 4 / K;              // waves per workgroup
+    constexpr int NR = 16 / K;             // rows per workgroup
+    constexpr int E = 2 * K;               // element steps per lane per tile (and B/C steps per lane per pair)
+    constexpr int LPS = 16 / K;            // lanes of a row holding one state's B/C
+    constexpr int GL = 32 * NW;            // lanes per role group
+    __shared__ __align__(16) float sDt[2][kCh * kP1];
+    __shared__ __align__(16) float sDu[2][kCh * kP1];
+    // Row partials of y [row][channel][16 steps]; the 4-float blocks of each 16-float row are
+    // XOR-swizzled by channel / 4, so the scan's float4 writes and the epilogue's reads are
+    // free of bank conflicts.
+    __shared__ __align__(16) float sY[NR * kCh * kT1];
+
+    const int lane = threadIdx.x & 63;
+    const int r = threadIdx.x >> 4;        // row of this lane in the scan
+    const int c = lane & 15;               // channel of this lane in the scan
+    const int grp = int(threadIdx.x) / GL; // role group (wave-uniform)
+    const int gl = int(threadIdx.x) % GL;
+    const int ce = gl / (16 / E);          // channel of this lane's element slice
+    const int es = E * (gl % (16 / E));    // first step (within a tile) of the slice
+    const int64_t b = blockIdx.y;
+    const int64_t d0 = int64_t(blockIdx.x) * kCh;
+    const int64_t g = d0 / ratio;
+    const int64_t L = p.seqlen;
+    const int64_t n_pairs = (L + 2 * kT1 - 1) / (2 * kT1);
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+
+    const int64_t de = d0 + ce;
+    // Uniform row-group bases (scalar registers) plus 32-bit per-lane element offsets; the host
+    // checks that every offset of the group fits in 31 bits.
+    const T *ub = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d0 * p.u_d_stride;
+    const T *db = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d0 * p.delta_d_stride;
+    const T *zb = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d0 * p.z_d_stride : nullptr;
+    T *ob = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d0 * p.out_d_stride : nullptr;
+    T *ozb = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d0 * p.out_z_d_stride : nullptr;
+    const T *Bb = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cb = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+    const uint32_t u_row = uint32_t(ce * p.u_d_stride), d_row = uint32_t(ce * p.delta_d_stride);
+    const uint32_t z_row = uint32_t(ce * p.z_d_stride), o_row = uint32_t(ce * p.out_d_stride);
+    const uint32_t oz_row = uint32_t(ce * p.out_z_d_stride);
+    const int nl = r * K + c / LPS;        // the state whose B/C this lane loads
+    const uint32_t B_row = uint32_t(nl * p.B_dstate_stride), C_row = uint32_t(nl * p.C_dstate_stride);
+    const int sb = E * (c % LPS);          // first step (within a pair) of this lane's B/C slice
+
+    float At[K], h[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        At[k] = p.A[(d0 + c) * p.A_d_stride + int64_t(r * K + k) * p.A_dstate_stride] * kLog2e;
+        h[k] = 0.f;
+    }
+    const float Dv = p.D ? p.D[de] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
+    float cum_dt = 0.f;
+
+    // Global loads of tile pair i; positions at or past the end of a row are clamped into the
+    // row's last E elements (L >= 8, L % 8 == 0), the prologue zeroes delta' of such steps.
+    const uint32_t lastE = uint32_t(L - E);
+    auto clampE = [&](int64_t t) { return t < int64_t(lastE) ? uint32_t(t) : lastE; };
+    auto load_pair = [&](int64_t i, PairData<T, K> &dst) {
+        const int64_t t0 = i * (2 * kT1);
+        const uint32_t tb = clampE(t0 + sb);
+        dst.b = load_raw<T, E>(Bb + (B_row + tb));
+        dst.c = load_raw<T, E>(Cb + (C_row + tb));
+        const uint32_t te = clampE(t0 + kT1 * grp + es);
+        dst.u = load_raw<T, E>(ub + (u_row + te));
+        dst.dl = load_raw<T, E>(db + (d_row + te));
+        if (zb) dst.z = load_raw<T, E>(zb + (z_row + te));
+        else dst.z = {};
+    };
+
+    // Prologue of the tile starting at t0 (this lane's slice): delta', delta' u -> LDS buffer buf.
+    float uu[E], zz[E];
+    auto prologue = [&](const PairData<T, K> &src, int64_t t0, int buf) {
+        float dd[E], dtp[E], dup[E];
+        unpack_raw<T, E>(src.u, uu);
+        unpack_raw<T, E>(src.dl, dd);
+        unpack_raw<T, E>(src.z, zz);
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float x = dd[k] + bias;
+            dtp[k] = SOFTPLUS ? softplus_fast(x) : x;
+        }
+        if (t0 + es >= L) {  // padded steps of a last, partial tile (L % 8 == 0: all E or none)
+#pragma unroll
+            for (int k = 0; k < E; ++k) dtp[k] = 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < E; ++k) dup[k] = dtp[k] * uu[k];
+#pragma unroll
+        for (int k = 0; k < E; k += 2) {
+            *reinterpret_cast<float2 *>(&sDt[buf][ce * kP1 + es + k]) = make_float2(dtp[k], dtp[k + 1]);
+            *reinterpret_cast<float2 *>(&sDu[buf][ce * kP1 + es + k]) = make_float2(dup[k], dup[k + 1]);
+        }
+    };
+
+    // Epilogue of the tile starting at t0 (this lane's slice): rows added in a fixed order.
+    auto epilogue = [&](int64_t t0) {
+        const int ecol = (((es >> 2) ^ (ce >> 2)) << 2) + (es & 3);
+        float y[E];
+        if constexpr (E == 4) {
+            float4 a = *reinterpret_cast<const float4 *>(&sY[ce * kT1 + ecol]);
+#pragma unroll
+            for (int rr = 1; rr < NR; ++rr) {
+                const float4 v = *reinterpret_cast<const float4 *>(&sY[(rr * kCh + ce) * kT1 + ecol]);
+                a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+            }
+            y[0] = a.x; y[1] = a.y; y[2] = a.z; y[3] = a.w;
+        } else {
+            float2 a = *reinterpret_cast<const float2 *>(&sY[ce * kT1 + ecol]);
+#pragma unroll
+            for (int rr = 1; rr < NR; ++rr) {
+                const float2 v = *reinterpret_cast<const float2 *>(&sY[(rr * kCh + ce) * kT1 + ecol]);
+                a.x += v.x; a.y += v.y;
+            }
+            y[0] = a.x; y[1] = a.y;
+        }
+        if (t0 + es < L) {
+            float o[E];
+#pragma unroll
+            for (int k = 0; k < E; ++k) o[k] = __builtin_fmaf(Dv, uu[k], y[k]);
+            const uint32_t t = uint32_t(t0 + es);
+            if (ob) store_vec<T, E>(ob + (o_row + t), o);
+            if (zb) {
+#pragma unroll
+                for (int k = 0; k < E; ++k) o[k] *= silu_fast(zz[k]);
+                store_vec<T, E>(ozb + (oz_row + t), o);
+            }
+        }
+    };
+
+    // Scan of one 16-step tile from LDS buffer buf. B/C of state r K + k at step t of the pair
+    // half H sit in lane k LPS + (16 H + t) / E of this row, register (16 H + t) % E.
+    float bv[E], cv[E];
+    auto scan_tile = [&](auto Hc, int64_t t0, int buf) {
+        constexpr int H = decltype(Hc)::value;
+        static_for<0, kT1 / 4>([&](auto S4) {
+            constexpr int s4 = decltype(S4)::value;
+            const float4 dtq = *reinterpret_cast<const float4 *>(&sDt[buf][c * kP1 + 4 * s4]);
+            const float4 duq = *reinterpret_cast<const float4 *>(&sDu[buf][c * kP1 + 4 * s4]);
+            const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
+            const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
+            float av[4][K], bbv[4][K], pv[4];
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                if (CHUNKS) cum_dt += dts[j];
+                static_for<0, K>([&](auto KK) {
+                    constexpr int k = decltype(KK)::value;
+                    constexpr int src = k * LPS + s / E;
+                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    bbv[j][k] = row_bcast<src>(bv[s % E]) * dus[j];
+                });
+            });
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                float acc;
+                static_for<0, K>([&](auto KK) {
+                    constexpr int k = decltype(KK)::value;
+                    constexpr int src = k * LPS + s / E;
+                    h[k] = __builtin_fmaf(av[j][k], h[k], bbv[j][k]);
+                    if constexpr (k == 0)
+                        acc = row_bcast<src>(cv[s % E]) * h[k];
+                    else
+                        fmac_row_bcast<src>(acc, cv[s % E], h[k]);
+                });
+                pv[j] = acc;
+            });
+            *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        });
+        if (CHUNKS && p.chunk_states) {
+            const int64_t tend = t0 + kT1 < L ? t0 + kT1 : L;
+            if (t0 < L && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
+                const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
+                float *csp = p.chunk_states + ((b * p.dim + d0 + c) * n_chunks + ci) * 32 + 2 * K * r;
+#pragma unroll
+                for (int k = 0; k < K; ++k) {
+                    csp[2 * k] = __builtin_amdgcn_exp2f(At[k] * cum_dt);
+                    csp[2 * k + 1] = h[k];
+                }
+            }
+        }
+    };
+
+    PairData<T, K> ring[PF];
+#pragma unroll
+    for (int s = 0; s < PF; ++s) load_pair(s, ring[s]);
+    if (grp == 0) prologue(ring[0], 0, 0);
+
+    for (int64_t i0 = 0; i0 < n_pairs; i0 += PF) {
+        static_for<0, PF>([&](auto Sc) {
+            constexpr int S = decltype(Sc)::value;
+            const int64_t i = i0 + S;
+            if (i < n_pairs) {
+                const int64_t t0 = i * (2 * kT1);
+                unpack_raw<T, E>(ring[S].b, bv);
+                unpack_raw<T, E>(ring[S].c, cv);
+                // Two wait states between the VALU writes of the DPP sources and their first DPP
+                // read by the fmac inline asm (the compiler covers its own DPP instructions).
+#pragma unroll
+                for (int k = 0; k < E; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                PairData<T, K> mine = ring[S];  // group 1's slice of this pair (used below)
+                load_pair(i + PF, ring[S]);
+                // Tile 2i: group 0 finishes it, group 1 prepares tile 2i+1.
+                __syncthreads();
+                scan_tile(std::integral_constant<int, 0>{}, t0, 0);
+                __syncthreads();
+                if (grp == 0) epilogue(t0);
+                else prologue(mine, t0 + kT1, 1);
+                // Tile 2i+1: group 1 finishes it, group 0 prepares tile 2i+2.
+                __syncthreads();
+                scan_tile(std::integral_constant<int, 1>{}, t0 + kT1, 1);
+                __syncthreads();
+                if (grp == 1) epilogue(t0 + kT1);
+                else prologue(ring[(S + 1) % PF], t0 + 2 * kT1, 0);
+            }
+        });
+    }
+    if (p.last_state) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) p.last_state[(b * p.dim + d0 + c) * 16 + r * K + k] = h[k];
+    }
+}
+
+template <typename T, int K, int PF>
+int launch_pipe(const mm_scan_fwd_params &p, hipStream_t stream) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
+    auto *kern = p.delta_softplus
+                     ? (p.chunk_states ? scan_fwd_pipe<T, K, PF, true, true> : scan_fwd_pipe<T, K, PF, true, false>)
+                     : (p.chunk_states ? scan_fwd_pipe<T, K, PF, false, true> : scan_fwd_pipe<T, K, PF, false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(256 / K), 0, stream, p, ratio);
+    return launch_status("scan_fwd_pipe");
+}
+
+// ---------------------------------------------------------------------------------------------
+// scan_fwd_k2i: two states per lane, two waves = 16 channels x 16 states per workgroup, and one
+// barrier per 16-step tile, the per-element work interleaved with the scan:
+//
+//   interval j:  both waves scan tile j           (dt', dt'u from sDt/sDu[j % 4] -> row partials sY[j % 2])
+//                wave j % 2 prepares tile j + 2   (softplus(dt + bias), dt' u -> sDt/sDu[(j + 2) % 4])
+//                wave (j+1) % 2 finishes tile j-1 (sum of the 8 row partials in sY[(j - 1) % 2], D u,
+//                                                  silu(z) gate, store)
+//                barrier
+//
+// Tile t belongs to wave t % 2: each of its 64 lanes owns 4 consecutive steps of one channel, loads
+// them, prepares them two intervals before the scan and finishes them one interval after it, keeping
+// u and z in registers in between. Both waves do the same work in every interval, and the
+// prologue/epilogue instructions sit in the same basic block as the scan, so they fill its latency
+// gaps instead of forming a latency-bound phase of their own.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+struct K2Data {                 // one lane's global data for pair iteration i
+    RawVec<T, 4> b, c;          // B, C of one of the lane's row states: 4 steps of tile pair i
+    RawVec<T, 4> u, dl, z;      // u, delta, z: 4 steps of this wave's tile of pair i + 1
+};
+
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
+scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
+    static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
+    constexpr int E = 4, LPS = 8, NR = 8;
+    __shared__ __align__(16) float sDt0[kCh * kP1], sDt1[kCh * kP1], sDt2[kCh * kP1], sDt3[kCh * kP1];
+    __shared__ __align__(16) float sDu0[kCh * kP1], sDu1[kCh * kP1], sDu2[kCh * kP1], sDu3[kCh * kP1];
+    // Row partials of y [row][channel][16 steps], 4-float blocks XOR-swizzled by channel / 4.
+    __shared__ __align__(16) float sY0[NR * kCh * kT1], sY1[NR * kCh * kT1];
+    auto DT = [&](auto I) -> float * {
+        constexpr int i = decltype(I)::value & 3;
+        if constexpr (i == 0) return sDt0; else if constexpr (i == 1) return sDt1;
+        else if constexpr (i == 2) return sDt2; else return sDt3;
+    };
+    auto DU = [&](auto I) -> float * {
+        constexpr int i = decltype(I)::value & 3;
+        if constexpr (i == 0) return sDu0; else if constexpr (i == 1) return sDu1;
+        else if constexpr (i == 2) return sDu2; else return sDu3;
+    };
+    auto YB = [&](auto I) -> float * {
+        if constexpr ((decltype(I)::value & 1) == 0) return sY0; else return sY1;
+    };
+
+    const int w = threadIdx.x >> 6;        // wave: owns tiles t with t % 2 == w
+    const int lane = threadIdx.x & 63;
+    const int r = threadIdx.x >> 4;        // row (states 2r, 2r+1) of this lane in the scan
+    const int c = lane & 15;               // channel of this lane in the scan
+    const int ce = lane >> 2;              // channel of this lane's element slice
+    const int es = E * (lane & 3);         // first step (within a tile) of the slice
+    const int64_t b = blockIdx.y;
+    const int64_t d0 = int64_t(blockIdx.x) * kCh;
+    const int64_t g = d0 / ratio;
+    const int64_t L = p.seqlen;
+    const int64_t n_pairs = (L + 2 * kT1 - 1) / (2 * kT1);
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+
+    const int64_t de = d0 + ce;
+    // Uniform row-group bases (scalar registers) plus 32-bit per-lane element offsets; the host
+    // checks that every offset of the group fits in 31 bits.
+    const T *ub = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d0 * p.u_d_stride;
+    const T *db = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d0 * p.delta_d_stride;
+    const T *zb = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d0 * p.z_d_stride : nullptr;
+    T *ob = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d0 * p.out_d_stride : nullptr;
+    T *ozb = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d0 * p.out_z_d_stride : nullptr;
+    const T *Bb = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cb = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+    const uint32_t u_row = uint32_t(ce * p.u_d_stride), d_row = uint32_t(ce * p.delta_d_stride);
+    const uint32_t z_row = uint32_t(ce * p.z_d_stride), o_row = uint32_t(ce * p.out_d_stride);
+    const uint32_t oz_row = uint32_t(ce * p.out_z_d_stride);
+    const int nl = 2 * r + c / LPS;        // the state whose B/C this lane loads
+    const uint32_t B_row = uint32_t(nl * p.B_dstate_stride), C_row = uint32_t(nl * p.C_dstate_stride);
+    const int sb = E * (c % LPS);          // first step (within a pair) of this lane's B/C slice
+
+    float At[2], h[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        At[k] = p.A[(d0 + c) * p.A_d_stride + int64_t(2 * r + k) * p.A_dstate_stride] * kLog2e;
+        h[k] = 0.f;
+    }
+    const float Dv = p.D ? p.D[de] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
+    float cum_dt = 0.f;
+
+    // Positions at or past the end of a row are clamped into the row's last 4 elements (L >= 8,
+    // L % 8 == 0); the prologue zeroes delta' of such steps, so they leave the state unchanged.
+    const uint32_t last4 = uint32_t(L - E);
+    auto clamp4 = [&](int64_t t) { return t < int64_t(last4) ? uint32_t(t) : last4; };
+    auto load_elems = [&](int64_t pair_i, RawVec<T, E> &u, RawVec<T, E> &dl, RawVec<T, E> &z) {
+        const uint32_t te = clamp4(pair_i * (2 * kT1) + kT1 * w + es);
+        u = load_raw<T, E>(ub + (u_row + te));
+        dl = load_raw<T, E>(db + (d_row + te));
+        if (zb) z = load_raw<T, E>(zb + (z_row + te));
+        else z = {};
+    };
+    auto load_data = [&](int64_t i, K2Data<T> &dst) {
+        const uint32_t tb = clamp4(i * (2 * kT1) + sb);
+        dst.b = load_raw<T, E>(Bb + (B_row + tb));
+        dst.c = load_raw<T, E>(Cb + (C_row + tb));
+        load_elems(i + 1, dst.u, dst.dl, dst.z);
+    };
+
+    // This lane's u and z of the two tiles it owns that are in flight: tile t uses slot (t / 2) % 2
+    // (wave 0: tile 2i+2 is prepared into slot 1-P while tile 2i, slot P, waits for its epilogue;
+    // wave 1: tile 2i-1 is finished from slot 1-P, then tile 2i+3 is prepared into it).
+    float uu[2][E], zz[2][E];
+
+    // Prologue of tile t0 / 16 (this lane's slice): delta', delta' u -> dt/du, u and z -> slot.
+    auto prologue = [&](const RawVec<T, E> &ru, const RawVec<T, E> &rd, const RawVec<T, E> &rz, int64_t t0,
+                        float *dt, float *du, auto Slot) {
+        constexpr int sl = decltype(Slot)::value;
+        float dd[E], dtp[E];
+        unpack_raw<T, E>(ru, uu[sl]);
+        unpack_raw<T, E>(rd, dd);
+        unpack_raw<T, E>(rz, zz[sl]);
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float x = dd[k] + bias;
+            dtp[k] = SOFTPLUS ? softplus_fast(x) : x;
+        }
+        if (t0 + es >= L) {  // padded steps (L % 8 == 0: all four or none)
+#pragma unroll
+            for (int k = 0; k < E; ++k) dtp[k] = 0.f;
+        }
+        *reinterpret_cast<float4 *>(&dt[ce * kP1 + es]) = make_float4(dtp[0], dtp[1], dtp[2], dtp[3]);
+        *reinterpret_cast<float4 *>(&du[ce * kP1 + es]) =
+            make_float4(dtp[0] * uu[sl][0], dtp[1] * uu[sl][1], dtp[2] * uu[sl][2], dtp[3] * uu[sl][3]);
+    };
+
+    // Epilogue of tile t0 / 16 (this lane's slice): the 8 row partials added in row order.
+    auto epilogue = [&](int64_t t0, const float *yb, auto Slot) {
+        constexpr int sl = decltype(Slot)::value;
+        const int ecol = ((es >> 2) ^ (ce >> 2)) << 2;
+        float4 a = *reinterpret_cast<const float4 *>(&yb[ce * kT1 + ecol]);
+#pragma unroll
+        for (int rr = 1; rr < NR; ++rr) {
+            const float4 v = *reinterpret_cast<const float4 *>(&yb[(rr * kCh + ce) * kT1 + ecol]);
+            a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+        }
+        if (t0 + es < L) {
+            float o[E] = {__builtin_fmaf(Dv, uu[sl][0], a.x), __builtin_fmaf(Dv, uu[sl][1], a.y),
+                          __builtin_fmaf(Dv, uu[sl][2], a.z), __builtin_fmaf(Dv, uu[sl][3], a.w)};
+            const uint32_t t = uint32_t(t0 + es);
+            if (ob) store_vec<T, E>(ob + (o_row + t), o);
+            if (zb) {
+#pragma unroll
+                for (int k = 0; k < E; ++k) o[k] *= silu_fast(zz[sl][k]);
+                store_vec<T, E>(ozb + (oz_row + t), o);
+            }
+        }
+    };
+
+    // Scan of one tile (pair half H) from dt/du into the row partials yb. B/C of state 2r + k at
+    // step s of the pair sit in lane 8k + s / 4 of this row, register s % 4.
+    float bv[E], cv[E];
+    auto scan_tile = [&](auto Hc, int64_t t0, const float *dt, const float *du, float *yb) {
+        constexpr int H = decltype(Hc)::value;
+        static_for<0, kT1 / 4>([&](auto S4) {
+            constexpr int s4 = decltype(S4)::value;
+            const float4 dtq = *reinterpret_cast<const float4 *>(&dt[c * kP1 + 4 * s4]);
+            const float4 duq = *reinterpret_cast<const float4 *>(&du[c * kP1 + 4 * s4]);
+            const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
+            const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
+            float av[4][2], bbv[4][2], pv[4];
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                if (CHUNKS) cum_dt += dts[j];
+                static_for<0, 2>([&](auto KK) {
+                    constexpr int k = decltype(KK)::value;
+                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    bbv[j][k] = row_bcast<k * LPS + s / E>(bv[s % E]) * dus[j];
+                });
+            });
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                h[0] = __builtin_fmaf(av[j][0], h[0], bbv[j][0]);
+                h[1] = __builtin_fmaf(av[j][1], h[1], bbv[j][1]);
+                float acc = row_bcast<s / E>(cv[s % E]) * h[0];
+                fmac_row_bcast<LPS + s / E>(acc, cv[s % E], h[1]);
+                pv[j] = acc;
+            });
+            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) =
+                make_float4(pv[0], pv[1], pv[2], pv[3]);
+        });
+        if (CHUNKS && p.chunk_states) {
+            const int64_t tend = t0 + kT1 < L ? t0 + kT1 : L;
+            if (t0 < L && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
+                const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
+                float *csp = p.chunk_states + ((b * p.dim + d0 + c) * n_chunks + ci) * 32 + 4 * r;
+                csp[0] = __builtin_amdgcn_exp2f(At[0] * cum_dt);
+                csp[1] = h[0];
+                csp[2] = __builtin_amdgcn_exp2f(At[1] * cum_dt);
+                csp[3] = h[1];
+            }
+        }
+    };
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    K2Data<T> ring[PF];
+    {
+        RawVec<T, E> u0, d0v, z0;
+        load_elems(0, u0, d0v, z0);
+#pragma unroll
+        for (int s = 0; s < PF; ++s) load_data(s, ring[s]);
+        // Tiles 0 and 1 are prepared before the first interval (slot 0 for both waves).
+        if (w == 0) prologue(u0, d0v, z0, 0, DT(I0{}), DU(I0{}), I0{});
+        else prologue(u0, d0v, z0, kT1, DT(I1{}), DU(I1{}), I0{});
+    }
+    __syncthreads();
+
+    for (int64_t i0 = 0; i0 < n_pairs; i0 += PF) {
+        static_for<0, PF>([&](auto Sc) {
+            constexpr int S = decltype(Sc)::value;
+            constexpr int P = S & 1;       // parity of the pair index (PF is even)
+            using IP = std::integral_constant<int, P>;
+            using I1P = std::integral_constant<int, 1 - P>;
+            const int64_t i = i0 + S;
+            if (i < n_pairs) {
+                const int64_t t0 = i * (2 * kT1);
+                unpack_raw<T, E>(ring[S].b, bv);
+                unpack_raw<T, E>(ring[S].c, cv);
+                // Two wait states between the VALU writes of the DPP sources and their first DPP
+                // read by the fmac inline asm (the compiler covers its own DPP instructions).
+#pragma unroll
+                for (int k = 0; k < E; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                const RawVec<T, E> nu = ring[S].u, nd = ring[S].dl, nz = ring[S].z;  // pair i + 1
+                load_data(i + PF, ring[S]);
+                // Interval 2i: wave 0 prepares tile 2i+2, wave 1 finishes tile 2i-1.
+                scan_tile(I0{}, t0, DT(std::integral_constant<int, 2 * P>{}), DU(std::integral_constant<int, 2 * P>{}),
+                          YB(I0{}));
+                if (w == 0) prologue(nu, nd, nz, t0 + 2 * kT1, DT(std::integral_constant<int, 2 * P + 2>{}),
+                                     DU(std::integral_constant<int, 2 * P + 2>{}), I1P{});
+                else if (i > 0) epilogue(t0 - kT1, YB(I1{}), I1P{});
+                __syncthreads();
+                // Interval 2i+1: wave 1 prepares tile 2i+3, wave 0 finishes tile 2i.
+                scan_tile(I1{}, t0 + kT1, DT(std::integral_constant<int, 2 * P + 1>{}),
+                          DU(std::integral_constant<int, 2 * P + 1>{}), YB(I1{}));
+                if (w == 1) prologue(nu, nd, nz, t0 + 3 * kT1, DT(std::integral_constant<int, 2 * P + 3>{}),
+                                     DU(std::integral_constant<int, 2 * P + 3>{}), I1P{});
+                else epilogue(t0, YB(I0{}), IP{});
+                __syncthreads();
+            }
+        });
+    }
+    // The last tile, 2 n_pairs - 1, belongs to wave 1.
+    if (w == 1) {
+        const int64_t tl = (2 * n_pairs - 1) * kT1;
+        if (((n_pairs - 1) & 1) == 0) epilogue(tl, YB(I1{}), I0{});
+        else epilogue(tl, YB(I1{}), I1{});
+    }
+    if (p.last_state) {
+        p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r] = h[0];
+        p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r + 1] = h[1];
+    }
+}
+
+template <typename T, int PF>
+int launch_k2i(const mm_scan_fwd_params &p, hipStream_t stream) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
+    auto *kern = p.delta_softplus
+                     ? (p.chunk_states ? scan_fwd_k2i<T, PF, true, true> : scan_fwd_k2i<T, PF, true, false>)
+                     : (p.chunk_states ? scan_fwd_k2i<T, PF, false, true> : scan_fwd_k2i<T, PF, false, false>);
+    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
+    return launch_status("scan_fwd_k2i");
+}
+
 template <typename T, int NW>
 int launch_nw(const mm_scan_fwd_params &p, hipStream_t stream) {
     const int64_t ratio = p.dim / p.n_groups;
@@ -316,14 +857,41 @@ int launch_nw(const mm_scan_fwd_params &p, hipStream_t stream) {
 
 }  // namespace tiled
 
-// Waves per 16-channel workgroup; MM_SCAN_NW in the environment overrides the default (1, 2, 4).
-static int tiled_waves() {
-    static int nw = [] {
-        const char *e = getenv("MM_SCAN_NW");
-        const int v = e ? atoi(e) : 2;
-        return (v == 1 || v == 2 || v == 4) ? v : 2;
+// Kernel choice for dstate 16: MM_SCAN_KERNEL in the environment selects "k2i" (default: two states
+// per lane, per-element work interleaved with the scan), "k2" / "k1" (two / one state per lane,
+// alternating prologue/epilogue phases), or "nw1" / "nw2" / "nw4" (multi-state-per-lane kernel
+// without pipelining, 1, 2 or 4 waves per group). MM_SCAN_PF (1, 2, 3; default 2) sets the load
+// distance in 32-step tile pairs of k2 / k1 (k2i loads 2 pairs ahead). fp32 inputs use k2 by default.
+static int tiled_variant() {
+    static int v = [] {
+        const char *e = getenv("MM_SCAN_KERNEL");
+        if (!e) return 0;
+        if (!strcmp(e, "k1")) return 10;
+        if (!strcmp(e, "k2")) return 20;
+        if (!strcmp(e, "nw1")) return 1;
+        if (!strcmp(e, "nw2")) return 2;
+        if (!strcmp(e, "nw4")) return 4;
+        return 0;
     }();
-    return nw;
+    return v;
+}
+
+static int pipe_prefetch() {
+    static int pf = [] {
+        const char *e = getenv("MM_SCAN_PF");
+        const int v = e ? atoi(e) : 2;
+        return (v >= 1 && v <= 3) ? v : 2;
+    }();
+    return pf;
+}
+
+template <typename T, int K>
+static int launch_pipe_pf(const mm_scan_fwd_params &p, hipStream_t stream) {
+    switch (pipe_prefetch()) {
+        case 1: return tiled::launch_pipe<T, K, 1>(p, stream);
+        case 3: return tiled::launch_pipe<T, K, 3>(p, stream);
+        default: return tiled::launch_pipe<T, K, 2>(p, stream);
+    }
 }
 
 template <typename T>
@@ -332,10 +900,21 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (p.dim % tiled::kCh != 0 || (p.dim / p.n_groups) % tiled::kCh != 0) return MM_ERR_UNSUPPORTED;
     if (p.seqlen < 8 || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
     if (p.batch > 65535) return MM_ERR_UNSUPPORTED;
-    switch (tiled_waves()) {
+    // The pipelined kernels address a 16-channel group with 32-bit element offsets from a per-group base.
+    const int64_t lim = int64_t(1) << 31;
+    const int64_t span = p.seqlen + 15 * std::max({p.u_d_stride, p.delta_d_stride, p.z_d_stride, p.out_d_stride,
+                                                   p.out_z_d_stride, p.B_dstate_stride, p.C_dstate_stride});
+    const bool pipe_ok = span < lim;
+    switch (pipe_ok ? tiled_variant() : 2) {
         case 1: return tiled::launch_nw<T, 1>(p, stream);
+        case 2: return tiled::launch_nw<T, 2>(p, stream);
         case 4: return tiled::launch_nw<T, 4>(p, stream);
-        default: return tiled::launch_nw<T, 2>(p, stream);
+        case 10: return launch_pipe_pf<T, 1>(p, stream);
+        case 20: return launch_pipe_pf<T, 2>(p, stream);
+        default:
+            // fp32 rows double the in-flight registers of the interleaved kernel (it would spill).
+            if constexpr (std::is_same_v<T, float>) return launch_pipe_pf<T, 2>(p, stream);
+            else return tiled::launch_k2i<T, 2>(p, stream);
     }
 }
 
