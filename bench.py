@@ -27,6 +27,9 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [REPO, os.path.join(REPO, "motif-mamba_amd")]
 
 HBM_PEAK_GBS = 8000.0
+# v_exp_f32 throughput of the whole MI355X, measured with a kernel-time microbenchmark (8 waves per
+# SIMD, independent chains): the transcendental issue roofline of the scan.
+TRANS_PEAK_PER_S = 16.14e12
 METRIC = "selective-scan fwd GB/s & % of binding roofline; decode tokens/s, 1 GPU"
 
 
@@ -72,6 +75,8 @@ def bench_scan(cfg_name, steps, warmup, torch, rotate=1):
         "ms": ms, "GB_s": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
         "elements_per_s": elems / (ms * 1e-3), "state_updates_per_s": elems * c.dstate / (ms * 1e-3),
         "trans_per_s": trans / (ms * 1e-3), "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "t_floor_us": max(nbytes / (HBM_PEAK_GBS * 1e9), trans / TRANS_PEAK_PER_S) * 1e6,
+        "floor_frac": max(nbytes / (HBM_PEAK_GBS * 1e9), trans / TRANS_PEAK_PER_S) / (ms * 1e-3),
         "input_rotation": rotate,
     }
 
@@ -197,6 +202,10 @@ def main():
                    "batch": 4, "dim": 5120, "seqlen": 4096, "dstate": 16, "n_groups": 1, "io_dtype": "bf16"},
         "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": _traffic()},
+        "roofline_trans": {"bound": "v_exp_f32 issue", "achieved": round(head["trans_per_s"] / 1e12, 3),
+                           "peak": TRANS_PEAK_PER_S / 1e12, "unit": "T/s",
+                           "frac": round(head["trans_per_s"] / TRANS_PEAK_PER_S, 4),
+                           "t_floor_us": round(head["t_floor_us"], 2), "floor_frac": round(head["floor_frac"], 4)},
         "cpu_baseline": cpu,
         "headline_detail": head,
         "configs": extra,

@@ -215,6 +215,65 @@ state_update_kernel(const mm_state_update_params p, const int64_t ratio) {
     }
 }
 
+// Four consecutive elements of T as fp32 (8-byte load for 16-bit types, 16-byte for fp32).
+template <typename T>
+__device__ __forceinline__ float4 load4(const T *p) {
+    if constexpr (std::is_same_v<T, float>) {
+        return *reinterpret_cast<const float4 *>(p);
+    } else {
+        const uint2 w = *reinterpret_cast<const uint2 *>(p);
+        float4 r;
+        if constexpr (std::is_same_v<T, bf16_t>) {
+            unpack_bf16x2(w.x, r.x, r.y);
+            unpack_bf16x2(w.y, r.z, r.w);
+        } else {
+            unpack_f16x2(w.x, r.x, r.y);
+            unpack_f16x2(w.y, r.z, r.w);
+        }
+        return r;
+    }
+}
+
+// dstate 16 with every row of state, A, B and C contiguous and 4-element aligned (checked on the
+// host): four lanes per (batch, channel) row, each moving four consecutive states as one 16-byte
+// vector, so a wave reads and writes 16 whole state rows (1 KB) per instruction.
+template <typename T>
+__global__ void __launch_bounds__(kDecBlock)
+state_update_vec16(const mm_state_update_params p, const int64_t ratio) {
+    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t row = tid >> 2;
+    const int part = int(tid & 3);
+    if (row >= p.batch * p.dim) return;  // all four lanes of a row leave together
+    const int64_t b = row / p.dim;
+    const int64_t d = row - b * p.dim;
+    const int64_t g = d / ratio;
+
+    float dt = to_f32(reinterpret_cast<const T *>(p.dt)[b * p.dt_batch_stride + d * p.dt_d_stride]);
+    if (p.dt_bias) dt += p.dt_bias[d];
+    if (p.dt_softplus) dt = softplus_f32(dt);
+    const float x = to_f32(reinterpret_cast<const T *>(p.x)[b * p.x_batch_stride + d * p.x_d_stride]);
+    const float dtx = dt * x;
+    float4 *sp = reinterpret_cast<float4 *>(p.state + b * p.state_batch_stride + d * p.state_d_stride) + part;
+    const float4 a4 = *reinterpret_cast<const float4 *>(p.A + d * p.A_d_stride + 4 * part);
+    const float4 b4 = load4(reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + 4 * part);
+    const float4 c4 = load4(reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + 4 * part);
+    float4 s = *sp;
+    const float dl = dt * kLog2e;
+    s.x = __builtin_fmaf(s.x, fast_exp2(dl * a4.x), dtx * b4.x);
+    s.y = __builtin_fmaf(s.y, fast_exp2(dl * a4.y), dtx * b4.y);
+    s.z = __builtin_fmaf(s.z, fast_exp2(dl * a4.z), dtx * b4.z);
+    s.w = __builtin_fmaf(s.w, fast_exp2(dl * a4.w), dtx * b4.w);
+    *sp = s;
+    float y = __builtin_fmaf(s.x, c4.x, __builtin_fmaf(s.y, c4.y, __builtin_fmaf(s.z, c4.z, s.w * c4.w)));
+    y += __shfl_xor(y, 1, 4);
+    y += __shfl_xor(y, 2, 4);
+    if (part == 0) {
+        if (p.D) y = __builtin_fmaf(p.D[d], x, y);
+        if (p.z) y *= silu_f32(to_f32(reinterpret_cast<const T *>(p.z)[b * p.z_batch_stride + d * p.z_d_stride]));
+        reinterpret_cast<T *>(p.out)[b * p.out_batch_stride + d * p.out_d_stride] = from_f32<T>(y);
+    }
+}
+
 }  // namespace mm
 
 // ================================================================================================
@@ -352,8 +411,25 @@ int launch_su(const mm_state_update_params &p, hipStream_t s) {
     return mm::launch_status("state_update");
 }
 
+// The vectorised dstate-16 kernel's layout requirements: unit state strides and 4-element aligned
+// rows of state, A, B and C.
+bool su_vec16_ok(const mm_state_update_params &p) {
+    const int64_t eb = elem_bytes(p.itype);
+    auto al = [](const void *ptr, int64_t bytes) { return (reinterpret_cast<uintptr_t>(ptr) % uintptr_t(bytes)) == 0; };
+    return p.dstate == 16 && p.state_dstate_stride == 1 && p.A_dstate_stride == 1 && p.B_dstate_stride == 1 &&
+           p.C_dstate_stride == 1 && al(p.state, 16) && p.state_batch_stride % 4 == 0 && p.state_d_stride % 4 == 0 &&
+           al(p.A, 16) && p.A_d_stride % 4 == 0 && al(p.B, 4 * eb) && al(p.C, 4 * eb) && p.B_batch_stride % 4 == 0 &&
+           p.B_group_stride % 4 == 0 && p.C_batch_stride % 4 == 0 && p.C_group_stride % 4 == 0;
+}
+
 template <typename T>
 int dispatch_su(const mm_state_update_params &p, hipStream_t s) {
+    if (su_vec16_ok(p)) {
+        const int64_t threads = p.batch * p.dim * 4;
+        dim3 grid(unsigned((threads + mm::kDecBlock - 1) / mm::kDecBlock));
+        hipLaunchKernelGGL((mm::state_update_vec16<T>), grid, dim3(mm::kDecBlock), 0, s, p, p.dim / p.n_groups);
+        return mm::launch_status("state_update");
+    }
     if (p.dstate <= 16) return launch_su<T, 4, 4>(p, s);
     if (p.dstate <= 64) return launch_su<T, 4, 16>(p, s);
     return launch_su<T, 16, 16>(p, s);
