@@ -24,6 +24,7 @@
  *     (selective_scan.cpp:304-305, 321, 326, 350).
  *   - The library never allocates, frees or synchronises. Every call enqueues its kernels on
  *     `stream` (a hipStream_t; NULL = the null stream of the current device) and returns.
+ *     Scratch memory, where a shape benefits from it, is provided by the caller (`workspace`).
  *   - Return value: 0 on success. MM_ERR_INVALID_ARGUMENT (-1) when the parameter block fails
  *     validation (nothing is launched), MM_ERR_UNSUPPORTED (-2) for a valid request this build
  *     does not implement, otherwise the positive hipError_t of the failed launch.
@@ -38,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 1
+#define MM_SCAN_ABI_VERSION 2
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -96,6 +97,14 @@ typedef struct mm_scan_fwd_params {
     int64_t A_d_stride, A_dstate_stride;
     int64_t B_batch_stride, B_group_stride, B_dstate_stride, B_d_stride;
     int64_t C_batch_stride, C_group_stride, C_dstate_stride, C_d_stride;
+
+    /* Optional device scratch of `workspace_bytes` bytes (16-byte aligned), owned by the caller.
+     * Shapes with few (batch, channel) rows and long sequences scan the sequence in parallel
+     * segments and need mm_scan_fwd_workspace_size() bytes for the segment carries; with a NULL or
+     * smaller workspace the same results come from the single-pass kernels. No counterpart in
+     * SSMParamsBase: the reference scans each row with one thread block. */
+    void *workspace;
+    int64_t workspace_bytes;
 } mm_scan_fwd_params;
 
 /* Single-token decode update, in place on `state`:
@@ -131,6 +140,12 @@ typedef struct mm_state_update_params {
 
 /* Forward scan. Replaces selective_scan_cuda.fwd (selective_scan.cpp:270-413, pybind :620-627). */
 int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream);
+
+/* Bytes of `workspace` that let mm_scan_fwd use sequence-parallel segments for this request
+ * (0: the single-pass kernels are used anyway). Reads only sizes, flags and strides of `params`;
+ * returns 0 for a request mm_scan_fwd would reject. No counterpart in the reference (its forward
+ * allocates nothing beyond the outputs, selective_scan.cpp:383-389). */
+int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params);
 
 /* Decode step. Replaces selective_state_update (call site mamba_simplemotif.py:397-399). */
 int mm_state_update(const mm_state_update_params *params, void *stream);

@@ -465,6 +465,12 @@ int mm_state_update(const mm_state_update_params *params, void *stream) {
     }
 }
 
+int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params) {
+    if (validate_fwd(params) != MM_OK) return 0;
+    if (params->batch == 0 || params->dim == 0) return 0;
+    return mm::segment_workspace_bytes(*params, mm::segment_count(*params));
+}
+
 const char *mm_last_error(void) { return g_err; }
 
 int mm_abi_version(void) { return MM_SCAN_ABI_VERSION; }

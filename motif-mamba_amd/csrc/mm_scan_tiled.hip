@@ -50,6 +50,16 @@ __device__ __forceinline__ void fmac_row_bcast(float &acc, float src, float x) {
     asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(src), "v"(x), "i"(LANE));
 }
 
+// bcast_row(src, LANE) * x as one v_mul_f32_dpp, fixed in the instruction stream (the compiler may
+// otherwise split the broadcast into a v_mov_b32_dpp and fold the product elsewhere). Same source
+// hazard rule as fmac_row_bcast.
+template <int LANE>
+__device__ __forceinline__ float mul_row_bcast(float src, float x) {
+    float r;
+    asm("v_mul_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(src), "v"(x), "i"(LANE));
+    return r;
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -336,9 +346,21 @@ struct PairData {                  // one lane's global data for one 32-step til
     RawVec<T, 2 * K> u, dl, z;     // u, delta, z of the lane's element slice in its group's tile
 };
 
-template <typename T, int K, int PF, bool SOFTPLUS, bool CHUNKS>
+// Sequence segments of one launch (blockIdx.z = segment): MODE 0 scans whole rows; MODE 1 scans
+// segments 0 .. n_seg-2 from a zero state and writes only their end state (h) and the sum of
+// delta' (sumdt); MODE 2 scans every segment from the carried state h[segment] with the delta'
+// prefix cum[segment] and writes all outputs (last_state from the last segment).
+struct SegArgs {
+    int64_t pairs;   // 32-step tile pairs per segment
+    int32_t n_seg;
+    float *h;        // (batch * dim, n_seg, 16)
+    float *sumdt;    // (batch * dim, n_seg)
+    float *cum;      // (batch * dim, n_seg)
+};
+
+template <typename T, int K, int PF, bool SOFTPLUS, bool CHUNKS, int MODE>
 __global__ void __launch_bounds__(256 / K) __attribute__((amdgpu_waves_per_eu(5 - 2 * (K - 1), 8)))
-scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
+scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) {
     constexpr int NW = 4 / K;              // waves per workgroup
     constexpr int NR = 16 / K;             // rows per workgroup
     constexpr int E = 2 * K;               // element steps per lane per tile (and B/C steps per lane per pair)
@@ -364,6 +386,10 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
     const int64_t L = p.seqlen;
     const int64_t n_pairs = (L + 2 * kT1 - 1) / (2 * kT1);
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+    const int seg = MODE == 0 ? 0 : int(blockIdx.z);
+    const int64_t pb = MODE == 0 ? 0 : seg * sg.pairs;                                      // first pair
+    const int64_t pe = MODE == 0 ? n_pairs : (pb + sg.pairs < n_pairs ? pb + sg.pairs : n_pairs);  // end
+    const int64_t srow = (b * p.dim + d0 + c) * int64_t(sg.n_seg) + seg;                   // segment slot
 
     const int64_t de = d0 + ce;
     // Uniform row-group bases (scalar registers) plus 32-bit per-lane element offsets; the host
@@ -386,11 +412,11 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
         At[k] = p.A[(d0 + c) * p.A_d_stride + int64_t(r * K + k) * p.A_dstate_stride] * kLog2e;
-        h[k] = 0.f;
+        h[k] = MODE == 2 ? sg.h[srow * 16 + r * K + k] : 0.f;
     }
     const float Dv = p.D ? p.D[de] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
-    float cum_dt = 0.f;
+    float cum_dt = (MODE == 2 && CHUNKS) ? sg.cum[srow] : 0.f;
 
     // Global loads of tile pair i; positions at or past the end of a row are clamped into the
     // row's last E elements (L >= 8, L % 8 == 0), the prologue zeroes delta' of such steps.
@@ -435,6 +461,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
 
     // Epilogue of the tile starting at t0 (this lane's slice): rows added in a fixed order.
     auto epilogue = [&](int64_t t0) {
+        if constexpr (MODE == 1) return;  // state-only segments produce no outputs
         const int ecol = (((es >> 2) ^ (ce >> 2)) << 2) + (es & 3);
         float y[E];
         if constexpr (E == 4) {
@@ -483,12 +510,12 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
             static_for<0, 4>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 constexpr int s = kT1 * H + 4 * s4 + j;
-                if (CHUNKS) cum_dt += dts[j];
+                if (CHUNKS || MODE == 1) cum_dt += dts[j];
                 static_for<0, K>([&](auto KK) {
                     constexpr int k = decltype(KK)::value;
                     constexpr int src = k * LPS + s / E;
                     av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
-                    bbv[j][k] = row_bcast<src>(bv[s % E]) * dus[j];
+                    bbv[j][k] = mul_row_bcast<src>(bv[s % E], dus[j]);
                 });
             });
             static_for<0, 4>([&](auto J) {
@@ -499,16 +526,22 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
                     constexpr int k = decltype(KK)::value;
                     constexpr int src = k * LPS + s / E;
                     h[k] = __builtin_fmaf(av[j][k], h[k], bbv[j][k]);
-                    if constexpr (k == 0)
-                        acc = row_bcast<src>(cv[s % E]) * h[k];
-                    else
-                        fmac_row_bcast<src>(acc, cv[s % E], h[k]);
+                    if constexpr (MODE != 1) {
+                        if constexpr (k == 0)
+                            acc = row_bcast<src>(cv[s % E]) * h[k];
+                        else
+                            fmac_row_bcast<src>(acc, cv[s % E], h[k]);
+                    }
                 });
-                pv[j] = acc;
+                if constexpr (MODE != 1) pv[j] = acc;
             });
-            *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            if constexpr (MODE != 1)
+                *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+            // Without the y-partial chain the scheduler would hoist the exponentials of a whole tile
+            // and run out of registers: keep the state-only scan in 4-step groups.
+            if constexpr (MODE == 1) __builtin_amdgcn_sched_barrier(0);
         });
-        if (CHUNKS && p.chunk_states) {
+        if (MODE != 1 && CHUNKS && p.chunk_states) {
             const int64_t tend = t0 + kT1 < L ? t0 + kT1 : L;
             if (t0 < L && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
                 const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
@@ -524,14 +557,14 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
 
     PairData<T, K> ring[PF];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) load_pair(s, ring[s]);
-    if (grp == 0) prologue(ring[0], 0, 0);
+    for (int s = 0; s < PF; ++s) load_pair(pb + s, ring[s]);
+    if (grp == 0) prologue(ring[0], pb * (2 * kT1), 0);
 
-    for (int64_t i0 = 0; i0 < n_pairs; i0 += PF) {
+    for (int64_t i0 = pb; i0 < pe; i0 += PF) {
         static_for<0, PF>([&](auto Sc) {
             constexpr int S = decltype(Sc)::value;
             const int64_t i = i0 + S;
-            if (i < n_pairs) {
+            if (i < pe) {
                 const int64_t t0 = i * (2 * kT1);
                 unpack_raw<T, E>(ring[S].b, bv);
                 unpack_raw<T, E>(ring[S].c, cv);
@@ -556,21 +589,70 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio) {
             }
         });
     }
-    if (p.last_state) {
+    if constexpr (MODE == 1) {
 #pragma unroll
-        for (int k = 0; k < K; ++k) p.last_state[(b * p.dim + d0 + c) * 16 + r * K + k] = h[k];
+        for (int k = 0; k < K; ++k) sg.h[srow * 16 + r * K + k] = h[k];
+        if (r == 0) sg.sumdt[srow] = cum_dt;
+    } else {
+        if (p.last_state && (MODE == 0 || seg == sg.n_seg - 1)) {
+#pragma unroll
+            for (int k = 0; k < K; ++k) p.last_state[(b * p.dim + d0 + c) * 16 + r * K + k] = h[k];
+        }
     }
+}
+
+// Carries between segments, one thread per (batch, channel, state): the start state of segment s+1
+// is exp2(A log2e sum(delta' of s)) * start(s) + end_from_zero(s); written in place over h, with
+// the delta' prefix of every segment in cum.
+__global__ void __launch_bounds__(256)
+seg_carry_kernel(const float *A, int64_t A_d_stride, int64_t A_dstate_stride, int64_t rows, int64_t dim,
+                 const SegArgs sg) {
+    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (tid >= rows * 16) return;
+    const int64_t row = tid >> 4;
+    const int n = int(tid & 15);
+    const int64_t d = row % dim;
+    const float A2 = A[d * A_d_stride + n * A_dstate_stride] * kLog2e;
+    float H = 0.f, cd = 0.f;
+    for (int s = 0; s < sg.n_seg; ++s) {
+        float *hp = sg.h + (row * sg.n_seg + s) * 16 + n;
+        const bool last = s == sg.n_seg - 1;
+        const float he = last ? 0.f : *hp;
+        const float sd = last ? 0.f : sg.sumdt[row * sg.n_seg + s];
+        *hp = H;
+        if (n == 0) sg.cum[row * sg.n_seg + s] = cd;
+        H = __builtin_fmaf(__builtin_amdgcn_exp2f(A2 * sd), H, he);
+        cd += sd;
+    }
+}
+
+template <typename T, int K, int PF, int MODE>
+int launch_pipe_mode(const mm_scan_fwd_params &p, hipStream_t stream, const SegArgs &sg, unsigned nz) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch), nz);
+    auto *kern = p.delta_softplus
+                     ? (p.chunk_states ? scan_fwd_pipe<T, K, PF, true, true, MODE> : scan_fwd_pipe<T, K, PF, true, false, MODE>)
+                     : (p.chunk_states ? scan_fwd_pipe<T, K, PF, false, true, MODE> : scan_fwd_pipe<T, K, PF, false, false, MODE>);
+    hipLaunchKernelGGL(kern, grid, dim3(256 / K), 0, stream, p, ratio, sg);
+    return launch_status("scan_fwd_pipe");
 }
 
 template <typename T, int K, int PF>
 int launch_pipe(const mm_scan_fwd_params &p, hipStream_t stream) {
-    const int64_t ratio = p.dim / p.n_groups;
-    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
-    auto *kern = p.delta_softplus
-                     ? (p.chunk_states ? scan_fwd_pipe<T, K, PF, true, true> : scan_fwd_pipe<T, K, PF, true, false>)
-                     : (p.chunk_states ? scan_fwd_pipe<T, K, PF, false, true> : scan_fwd_pipe<T, K, PF, false, false>);
-    hipLaunchKernelGGL(kern, grid, dim3(256 / K), 0, stream, p, ratio);
-    return launch_status("scan_fwd_pipe");
+    return launch_pipe_mode<T, K, PF, 0>(p, stream, SegArgs{0, 1, nullptr, nullptr, nullptr}, 1);
+}
+
+// Segmented scan: state-only pass over segments 0 .. n_seg-2, carry chain, full pass.
+template <typename T>
+int launch_pipe_segmented(const mm_scan_fwd_params &p, hipStream_t stream, const SegArgs &sg) {
+    int rc = launch_pipe_mode<T, 2, 2, 1>(p, stream, sg, unsigned(sg.n_seg - 1));
+    if (rc != MM_OK) return rc;
+    const int64_t rows = p.batch * p.dim;
+    hipLaunchKernelGGL(seg_carry_kernel, dim3(unsigned((rows * 16 + 255) / 256)), dim3(256), 0, stream, p.A,
+                       p.A_d_stride, p.A_dstate_stride, rows, p.dim, sg);
+    rc = launch_status("seg_carry");
+    if (rc != MM_OK) return rc;
+    return launch_pipe_mode<T, 2, 2, 2>(p, stream, sg, unsigned(sg.n_seg));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -894,17 +976,53 @@ static int launch_pipe_pf(const mm_scan_fwd_params &p, hipStream_t stream) {
     }
 }
 
-template <typename T>
-int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
-    if (p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return MM_ERR_UNSUPPORTED;
-    if (p.dim % tiled::kCh != 0 || (p.dim / p.n_groups) % tiled::kCh != 0) return MM_ERR_UNSUPPORTED;
-    if (p.seqlen < 8 || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
-    if (p.batch > 65535) return MM_ERR_UNSUPPORTED;
-    // The pipelined kernels address a 16-channel group with 32-bit element offsets from a per-group base.
-    const int64_t lim = int64_t(1) << 31;
+// Shape conditions of the dstate-16 kernels that do not depend on pointer alignment.
+static bool tiled_shape_ok(const mm_scan_fwd_params &p) {
+    if (p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
+    if (p.dim % tiled::kCh != 0 || (p.dim / p.n_groups) % tiled::kCh != 0) return false;
+    return p.seqlen >= 8 && p.seqlen % 8 == 0 && p.batch <= 65535;
+}
+
+// The pipelined kernels address a 16-channel group with 32-bit element offsets from a per-group base.
+static bool pipe_offsets_ok(const mm_scan_fwd_params &p) {
     const int64_t span = p.seqlen + 15 * std::max({p.u_d_stride, p.delta_d_stride, p.z_d_stride, p.out_d_stride,
                                                    p.out_z_d_stride, p.B_dstate_stride, p.C_dstate_stride});
-    const bool pipe_ok = span < lim;
+    return span < (int64_t(1) << 31);
+}
+
+// Sequence segments for shapes whose (batch, 16-channel) groups give fewer than one wave per SIMD
+// (two waves per group): enough segments for ~3 waves per SIMD, each at least 512 steps. The
+// segmented scan does ~1.75x the work of one pass, which pays only at such low occupancy.
+int64_t segment_count(const mm_scan_fwd_params &p) {
+    if (!tiled_shape_ok(p) || !pipe_offsets_ok(p)) return 1;
+    const int64_t waves = 2 * p.batch * (p.dim / tiled::kCh);
+    if (waves >= 1024) return 1;
+    const int64_t n_pairs = (p.seqlen + 2 * tiled::kT1 - 1) / (2 * tiled::kT1);
+    int64_t n_seg = (3072 + waves - 1) / waves;
+    n_seg = std::min(n_seg, n_pairs / 16);
+    if (n_seg < 2) return 1;
+    const int64_t pairs = (n_pairs + n_seg - 1) / n_seg;
+    return (n_pairs + pairs - 1) / pairs;
+}
+
+int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg) {
+    return n_seg > 1 ? p.batch * p.dim * n_seg * (16 + 2) * int64_t(sizeof(float)) : 0;
+}
+
+template <typename T>
+int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
+    if (!tiled_shape_ok(p) || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
+    const bool pipe_ok = pipe_offsets_ok(p);
+    const int64_t n_seg = pipe_ok ? segment_count(p) : 1;
+    if (n_seg > 1 && p.workspace && p.workspace_bytes >= segment_workspace_bytes(p, n_seg) &&
+        (reinterpret_cast<uintptr_t>(p.workspace) & 15u) == 0) {
+        const int64_t n_pairs = (p.seqlen + 2 * tiled::kT1 - 1) / (2 * tiled::kT1);
+        const int64_t rows = p.batch * p.dim;
+        float *ws = static_cast<float *>(p.workspace);
+        const tiled::SegArgs sg{(n_pairs + n_seg - 1) / n_seg, int32_t(n_seg), ws, ws + rows * n_seg * 16,
+                                ws + rows * n_seg * 17};
+        return tiled::launch_pipe_segmented<T>(p, stream, sg);
+    }
     switch (pipe_ok ? tiled_variant() : 2) {
         case 1: return tiled::launch_nw<T, 1>(p, stream);
         case 2: return tiled::launch_nw<T, 2>(p, stream);

@@ -178,6 +178,17 @@ void set_out_z(mm_scan_fwd_params &p, const at::Tensor &out_z) {
     p.out_z_d_stride = out_z.stride(1);
 }
 
+// Scratch for the sequence-parallel segments (only for shapes that use them), from the caching
+// allocator on the launch stream: released when the caller's reference drops, stream-ordered.
+at::Tensor attach_workspace(mm_scan_fwd_params &p, const at::Tensor &like) {
+    const int64_t bytes = mm_scan_fwd_workspace_size(&p);
+    if (bytes <= 0) return at::Tensor();
+    at::Tensor ws = torch::empty({bytes}, like.options().dtype(at::ScalarType::Byte));
+    p.workspace = ws.data_ptr();
+    p.workspace_bytes = bytes;
+    return ws;
+}
+
 std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A,
                             const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                             const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &delta_bias_,
@@ -200,6 +211,7 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
     }
     p.chunk_states = x.data_ptr<float>();
     const c10::DeviceGuard device_guard{u.device()};
+    const at::Tensor ws = attach_workspace(p, u);
     check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
     std::vector<at::Tensor> result = {out, x};
     if (z_.has_value()) result.push_back(out_z);
@@ -227,6 +239,7 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
         p.last_state = last_state.data_ptr<float>();
     }
     const c10::DeviceGuard device_guard{u.device()};
+    const at::Tensor ws = attach_workspace(p, u);
     check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
     if (return_last_state) return {main, last_state};
     return {main};

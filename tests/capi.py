@@ -29,7 +29,8 @@ class ScanFwdParams(ctypes.Structure):
                 ("out_z_batch_stride", i64), ("out_z_d_stride", i64),
                 ("A_d_stride", i64), ("A_dstate_stride", i64),
                 ("B_batch_stride", i64), ("B_group_stride", i64), ("B_dstate_stride", i64), ("B_d_stride", i64),
-                ("C_batch_stride", i64), ("C_group_stride", i64), ("C_dstate_stride", i64), ("C_d_stride", i64)]
+                ("C_batch_stride", i64), ("C_group_stride", i64), ("C_dstate_stride", i64), ("C_d_stride", i64),
+                ("workspace", vp), ("workspace_bytes", i64)]
 
 
 class StateUpdateParams(ctypes.Structure):
@@ -61,6 +62,8 @@ def load():
     lib.mm_scan_fwd.restype = ctypes.c_int
     lib.mm_state_update.argtypes = [ctypes.POINTER(StateUpdateParams), vp]
     lib.mm_state_update.restype = ctypes.c_int
+    lib.mm_scan_fwd_workspace_size.argtypes = [ctypes.POINTER(ScanFwdParams)]
+    lib.mm_scan_fwd_workspace_size.restype = ctypes.c_int64
     return lib
 
 
@@ -69,7 +72,7 @@ def _ptr(t):
 
 
 def scan_fwd_params(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                    out=None, out_z=None, last_state=None, chunk_states=None):
+                    out=None, out_z=None, last_state=None, chunk_states=None, workspace=None):
     """Fill ScanFwdParams from torch tensors in the reference layouts (B/C 4-D or 2-D)."""
     p = ScanFwdParams()
     p.batch, p.dim, p.seqlen = u.shape
@@ -99,6 +102,8 @@ def scan_fwd_params(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_so
         p.C_batch_stride, p.C_group_stride, p.C_dstate_stride = C.stride(0), C.stride(1), C.stride(2)
     else:
         p.C_d_stride, p.C_dstate_stride = C.stride(0), C.stride(1)
+    if workspace is not None:
+        p.workspace, p.workspace_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
     return p
 
 

@@ -14,10 +14,11 @@ from tests import capi
 def test_library_exports_every_header_function():
     lib = capi.load()
     names = capi.header_functions()
-    assert set(names) == {"mm_scan_fwd", "mm_state_update", "mm_last_error", "mm_abi_version"}
+    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_state_update", "mm_last_error",
+                          "mm_abi_version"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 1
+    assert lib.mm_abi_version() == 2
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -121,3 +122,31 @@ def test_mamba_ssm_import_paths_resolve_to_hip_kernels():
     assert ssi.selective_scan_fn is motif_mamba_amd.selective_scan_fn
     assert ssi.SelectiveScanFn is motif_mamba_amd.SelectiveScanFn
     assert ssu.selective_state_update is motif_mamba_amd.selective_state_update
+
+
+def test_workspace_size_query():
+    """mm_scan_fwd_workspace_size reads sizes, flags and strides only (fake pointers are never
+    dereferenced): segments for few channel groups and long sequences, none otherwise."""
+    lib = capi.load()
+
+    def params(batch, dim, L, N=16, itype=2):
+        p = capi.ScanFwdParams()
+        p.batch, p.dim, p.seqlen, p.dstate, p.n_groups = batch, dim, L, N, 1
+        p.itype, p.is_variable_B, p.is_variable_C, p.delta_softplus = itype, 1, 1, 1
+        p.u = p.delta = p.A = p.B = p.C = p.z = p.out_z = 4096
+        p.u_batch_stride = p.delta_batch_stride = p.z_batch_stride = p.out_z_batch_stride = dim * L
+        p.u_d_stride = p.delta_d_stride = p.z_d_stride = p.out_z_d_stride = L
+        p.A_d_stride, p.A_dstate_stride = N, 1
+        p.B_batch_stride = p.C_batch_stride = p.B_group_stride = p.C_group_stride = N * L
+        p.B_dstate_stride = p.C_dstate_stride = L
+        return p
+
+    seg = lib.mm_scan_fwd_workspace_size(ctypes.byref(params(1, 2560, 65536, itype=0)))
+    assert seg > 0 and seg % (1 * 2560 * 18 * 4) == 0           # config 3: segmented
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(params(4, 5120, 4096))) == 0   # config 2: one pass
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(params(1, 64, 256))) == 0      # too short to split
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(params(1, 64, 8192, N=32))) == 0  # not dstate 16
+    bad = params(1, 64, 8192)
+    bad.dstate = 0
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(bad)) == 0                      # invalid request
+    assert lib.mm_scan_fwd_workspace_size(None) == 0

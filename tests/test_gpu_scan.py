@@ -237,3 +237,77 @@ def test_full_size_config(cfg):
                                    err_msg=f"{cfg} row {(b, d)} out_z")
         np.testing.assert_allclose(last[b, d].double().numpy(), r["last_state"][i], rtol=rtol, atol=atol,
                                    err_msg=f"{cfg} row {(b, d)} last_state")
+
+
+# ---------------------------------------------------------------------------------------------
+# Sequence-parallel segments: few (batch, 16-channel) groups and a long sequence.
+# ---------------------------------------------------------------------------------------------
+
+def _seg_rows(out, last, case, what):
+    rows = [(0, d) for d in range(case["u"].shape[1])]
+    r = cscan.scan_rows(**case, rows=rows)
+    rtol, atol = fixtures.tolerances(case["u"].dtype)
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(out[b, d].double().numpy(), r["out_z"][i], rtol=rtol, atol=atol,
+                                   err_msg=f"{what} row {(b, d)} out_z")
+        np.testing.assert_allclose(last[b, d].double().numpy(), r["last_state"][i], rtol=rtol, atol=atol,
+                                   err_msg=f"{what} row {(b, d)} last_state")
+
+
+@pytest.mark.parametrize("G", [1, 2])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_segmented_scan(dtype, G):
+    """batch 1 x 64 channels x L 8192 is 4 channel groups, so the scan runs in 16 sequence
+    segments (state-only pass, carry chain, full pass); every row against the float64 restatement."""
+    _say(f"segmented scan {dtype} G={G}")
+    case = _case(20 + G, 1, 64, 8192, 16, dtype, bkind="4d", G=G)
+    out, last = _run(case)
+    _seg_rows(out, last, case, f"segmented G={G}")
+
+
+def test_segmented_reference_fwd_chunk_states():
+    """The reference-format fwd on a segmented shape: x's (prod a, h) per 2048-step chunk carry
+    the delta' prefix and the state across segment boundaries."""
+    _say("segmented reference-format fwd")
+    from motif_mamba_amd import _native
+    case = _case(30, 1, 64, 8192 + 96, 16, torch.float32, bkind="4d", G=1)
+    g = _to(case, DEV)
+    out, x, out_z = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], D=g["D"], z=g["z"],
+                                      delta_bias=g["delta_bias"], delta_softplus=True)
+    torch.cuda.synchronize()
+    assert x.shape == (1, 64, 5, 32)
+    rows = [(0, d) for d in range(64)]
+    r = cscan.scan_rows(**case, rows=rows, chunk=2048)
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(x[b, d, :, 1::2].cpu().double().numpy(), r["h_chunks"][i], rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(out_z[b, d].cpu().double().numpy(), r["out_z"][i], rtol=1e-4, atol=1e-5)
+    pa = chunk_states_ref(case["delta"], case["A"], case["delta_bias"], True)
+    np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
+    exp_out = selective_scan_ref(**{**case, "z": None})
+    _close(out.cpu(), exp_out, torch.float32, "out (pre-gate)")
+
+
+def test_segmented_c_abi_with_and_without_workspace():
+    """Through ctypes: with the queried workspace the segmented kernels run, without it the single
+    pass; both match the float64 restatement."""
+    _say("segmented C ABI, workspace / none")
+    lib = capi.load()
+    case = _case(31, 1, 32, 4096, 16, torch.bfloat16, bkind="4d", G=1)
+    g = _to(case, DEV)
+    res = []
+    for use_ws in (True, False):
+        out_z = torch.empty_like(g["z"])
+        last = torch.empty(1, 32, 16, device=DEV)
+        p = capi.scan_fwd_params(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], True,
+                                 out_z=out_z, last_state=last)
+        need = lib.mm_scan_fwd_workspace_size(ctypes.byref(p))
+        assert need > 0
+        ws = torch.empty(need, dtype=torch.uint8, device=DEV) if use_ws else None
+        if ws is not None:
+            p.workspace, p.workspace_bytes = ws.data_ptr(), need
+        rc = lib.mm_scan_fwd(ctypes.byref(p), capi.stream_handle())
+        assert rc == 0, lib.mm_last_error()
+        torch.cuda.synchronize()
+        res.append((out_z.cpu(), last.cpu()))
+    for (o, l), what in zip(res, ("with workspace", "without workspace")):
+        _seg_rows(o, l, case, what)
