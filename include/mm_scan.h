@@ -7,9 +7,11 @@
  *                    delta_bias, P, Q, gamma, delta_softplus)` bound at
  *                    csrc/selective_scan/selective_scan.cpp:620-627, i.e. selective_scan_fwd
  *                    (selective_scan.cpp:270-413) -> selective_scan_fwd_cuda
- *                    (selective_scan_fwd_kernel.cuh:593-623) for real A without P/Q/gamma.
- *                    The parameter block mirrors SSMParamsBase (selective_scan.h:26-82) but with
- *                    int64 element strides instead of uint32.
+ *                    (selective_scan_fwd_kernel.cuh:593-623) for real A, including the
+ *                    MotifMamba low-rank P/Q coupling (selective_scan.cpp:342-369,
+ *                    selective_scan_interface.py:237-350). The parameter block mirrors
+ *                    SSMParamsBase (selective_scan.h:26-82) but with int64 element strides
+ *                    instead of uint32.
  *
  *   mm_state_update  replaces `selective_state_update(state, x, dt, A, B, C, D, z, dt_bias,
  *                    dt_softplus)` as called at mamba_ssm/modules/mamba_simplemotif.py:397-399
@@ -39,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 2
+#define MM_SCAN_ABI_VERSION 3
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -105,6 +107,24 @@ typedef struct mm_scan_fwd_params {
      * SSMParamsBase: the reference scans each row with one thread block. */
     void *workspace;
     int64_t workspace_bytes;
+
+    /* MotifMamba low-rank coupling (SSMParamsBase::has_pq / pq_rank / P_* / Q_* / gamma_*,
+     * selective_scan.h:36-37, 58-65, 80-82; checks of selective_scan.cpp:342-369). With P and Q
+     * set, the recurrence becomes
+     *   h_t = exp(delta'_t A[d,:]) * h_{t-1} + delta'_t P_d (Q_d h_{t-1}) + delta'_t u_t B_t
+     * (selective_scan_interface.py:320-337), P_d = P[d] (dstate, pq_rank) and Q_d = Q[d]
+     * (pq_rank, dstate), float32; a pair shared by every channel has P_d_stride = Q_d_stride = 0.
+     * pq_rank is 0..8 (0: no coupling). chunk_states then holds (1, h) per chunk, as the
+     * reference's dense forward writes it (selective_scan_fwd_kernel.cuh:244-249). gamma
+     * ((dstate,) or (dim, dstate)) is carried for interface parity and, as in both reference
+     * forward paths, not read. NULL P and Q: the diagonal scan above. */
+    const float *P;
+    const float *Q;
+    const float *gamma;
+    int64_t pq_rank;
+    int64_t P_d_stride, P_dstate_stride, P_r_stride;
+    int64_t Q_d_stride, Q_r_stride, Q_dstate_stride;
+    int64_t gamma_d_stride, gamma_dstate_stride;
 } mm_scan_fwd_params;
 
 /* Single-token decode update, in place on `state`:
@@ -138,7 +158,8 @@ typedef struct mm_state_update_params {
     int64_t C_batch_stride, C_group_stride, C_dstate_stride;
 } mm_state_update_params;
 
-/* Forward scan. Replaces selective_scan_cuda.fwd (selective_scan.cpp:270-413, pybind :620-627). */
+/* Forward scan. Replaces selective_scan_cuda.fwd (selective_scan.cpp:270-413, pybind :620-627),
+ * the diagonal kernels and the dense P/Q kernel (selective_scan_fwd_kernel.cuh:159-251, 587-598). */
 int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream);
 
 /* Bytes of `workspace` that let mm_scan_fwd use sequence-parallel segments for this request

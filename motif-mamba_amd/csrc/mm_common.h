@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace mm {
 
 // ---- element types -------------------------------------------------------------------------
@@ -127,6 +129,76 @@ template <typename T> __device__ __forceinline__ void load8(const T *p, float *o
 }
 template <typename T> __device__ __forceinline__ void store8(T *p, const float *x) {
     *reinterpret_cast<Vec8<T> *>(p) = pack8<T>(x);
+}
+
+// ---- vectors of N consecutive elements of T, as raw words --------------------------------
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// N consecutive elements moved as one vector (N * sizeof(T) bytes: 4, 8, 16 or 32).
+template <typename T, int N> struct RawVec { uint32_t w[(N * sizeof(T) + 3) / 4]; };
+
+template <typename T, int N>
+__device__ __forceinline__ RawVec<T, N> load_raw(const T *p) {
+    RawVec<T, N> r;
+    constexpr int W = sizeof(r.w) / 4;
+    if constexpr (W == 8) {
+        const uint4 *q = reinterpret_cast<const uint4 *>(p);
+        const uint4 a = q[0], b = q[1];
+        r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w; r.w[4] = b.x; r.w[5] = b.y; r.w[6] = b.z; r.w[7] = b.w;
+    } else if constexpr (W == 4) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(p);
+        r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+    } else if constexpr (W == 2) {
+        const uint2 a = *reinterpret_cast<const uint2 *>(p);
+        r.w[0] = a.x; r.w[1] = a.y;
+    } else {
+        r.w[0] = *reinterpret_cast<const uint32_t *>(p);
+    }
+    return r;
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void unpack_raw(const RawVec<T, N> &r, float *o) {
+    if constexpr (std::is_same_v<T, float>) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) o[i] = __uint_as_float(r.w[i]);
+    } else if constexpr (std::is_same_v<T, bf16_t>) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) unpack_bf16x2(r.w[i], o[2 * i], o[2 * i + 1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) unpack_f16x2(r.w[i], o[2 * i], o[2 * i + 1]);
+    }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_vec(T *p, const float *x) {
+    if constexpr (std::is_same_v<T, float>) {
+        if constexpr (N == 8) {
+            uint4 *q = reinterpret_cast<uint4 *>(p);
+            q[0] = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+            q[1] = make_uint4(__float_as_uint(x[4]), __float_as_uint(x[5]), __float_as_uint(x[6]), __float_as_uint(x[7]));
+        } else if constexpr (N == 4) {
+            *reinterpret_cast<uint4 *>(p) = make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+        } else {
+            *reinterpret_cast<uint2 *>(p) = make_uint2(__float_as_uint(x[0]), __float_as_uint(x[1]));
+        }
+    } else {
+        uint32_t w[N / 2];
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i)
+            w[i] = std::is_same_v<T, bf16_t> ? pack_bf16x2(x[2 * i], x[2 * i + 1]) : pack_f16x2(x[2 * i], x[2 * i + 1]);
+        if constexpr (N == 8) *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+        else if constexpr (N == 4) *reinterpret_cast<uint2 *>(p) = make_uint2(w[0], w[1]);
+        else *reinterpret_cast<uint32_t *>(p) = w[0];
+    }
 }
 
 }  // namespace mm

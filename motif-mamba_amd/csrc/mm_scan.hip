@@ -2,7 +2,8 @@
 //
 // Entry points (declared in include/mm_scan.h):
 //   mm_scan_fwd      -- replaces selective_scan_cuda.fwd (reference csrc/selective_scan/
-//                       selective_scan.cpp:270-413) for real A without P/Q/gamma.
+//                       selective_scan.cpp:270-413) for real A; requests with P/Q go to
+//                       mm_scan_pq.hip.
 //   mm_state_update  -- replaces the upstream selective_state_update called at
 //                       mamba_ssm/modules/mamba_simplemotif.py:397-399.
 //
@@ -11,6 +12,8 @@
 //                                 in registers and walks the sequence serially, 8 steps per
 //                                 iteration. Used for every shape the tiled kernel does not take.
 //   state_update<T, SPL>          one decode step; LPR lanes share a row, SPL states per lane.
+//   state_update_vec16<T>         one decode step for dstate 16 with aligned unit-stride rows: four
+//                                 lanes per row, four states each as one 16-byte vector.
 // The tiled forward kernel lives in mm_scan_tiled.hip.
 #include <hip/hip_runtime.h>
 
@@ -354,6 +357,12 @@ int validate_fwd(const mm_scan_fwd_params *p) {
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: out_z given without z");
     if (!p->out && !p->out_z && !p->last_state && !p->chunk_states)
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: no output requested");
+    // Low-rank coupling (selective_scan.cpp:342-359): P and Q together, rank <= 8.
+    if ((p->P == nullptr) != (p->Q == nullptr))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: P and Q must be given together");
+    if (p->P && (p->pq_rank < 0 || p->pq_rank > 8))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: pq_rank must be in [0, 8] (got %lld)",
+                    (long long)p->pq_rank);
     return MM_OK;
 }
 
@@ -381,6 +390,7 @@ int launch_rowlane(const mm_scan_fwd_params &p, hipStream_t s) {
 
 template <typename T>
 int dispatch_fwd(const mm_scan_fwd_params &p, hipStream_t s) {
+    if (p.P) return mm::launch_pq<T>(p, s);
     int rc = mm::try_launch_tiled<T>(p, s);
     if (rc != MM_ERR_UNSUPPORTED) return rc;
     return launch_rowlane<T>(p, s);
@@ -467,7 +477,7 @@ int mm_state_update(const mm_state_update_params *params, void *stream) {
 
 int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params) {
     if (validate_fwd(params) != MM_OK) return 0;
-    if (params->batch == 0 || params->dim == 0) return 0;
+    if (params->batch == 0 || params->dim == 0 || params->P) return 0;
     return mm::segment_workspace_bytes(*params, mm::segment_count(*params));
 }
 

@@ -1,0 +1,489 @@
+// mm_scan_pq.hip -- gfx950 forward selective scan with the MotifMamba low-rank P/Q coupling.
+//
+// Reference behaviour: selective_scan_full_matrix_cuda (mamba_ssm/ops/selective_scan_interface.py:
+// 262-350), the path selective_scan_fn takes for P/Q (selective_scan_interface.py:237-259), and the
+// dense CUDA forward selective_scan_fwd_dense_pq_kernel (csrc/selective_scan/
+// selective_scan_fwd_kernel.cuh:159-251, one thread per (batch, channel) row). The recurrence
+//
+//     h_t = exp(dt'_t A[d,:]) * h_{t-1} + dt'_t P_d (Q_d h_{t-1}) + dt'_t u_t B_t
+//
+// couples every state of a row to every other one through the rank-R product, so a row is not a
+// set of independent per-state scans: each state needs Q h_{t-1} before it can take step t. The
+// design of this file is its own:
+//
+//   scan_fwd_pq_tiled<T, S, LPR, R>   a wave64 owns 64/LPR channels of one (batch, group); the LPR
+//       consecutive lanes of a channel hold S states each (S * LPR >= dstate, padded with states
+//       whose A, P, Q, B and C are zero, which stay zero). Per step each lane forms its partial
+//       Q h over its S states, a DPP butterfly inside the LPR lanes sums the partials (every lane
+//       ends with the same bits), and the lane updates its S states with P (dt' q) + dt' u B.
+//       The lane's rows of P and Q live in registers for the whole sequence.
+//       * B and C of the (batch, group) are staged per 32-step tile in LDS as float32, [step][state],
+//         and each step reads the lane's S states as one vector.
+//       * dt' = softplus(delta + bias) and dt' u are computed once per (channel, step): each lane
+//         owns 32/LPR consecutive steps of its channel per tile and shares them through LDS.
+//       * Per-lane partial sums of y = sum_n C_n h_n go back through LDS; the owner of the step adds
+//         the LPR partials in lane order, applies D u and the silu(z) gate and stores.
+//       * Global loads for tile i+1 are issued before the scan of tile i.
+//   scan_fwd_pq_rowlane<T>   one lane per row, the row's states in LDS, P/Q read through the cache
+//       every step: any dstate <= 256, constant B/C, any strides and lengths.
+#include <hip/hip_runtime.h>
+
+#include <stdlib.h>
+
+#include <type_traits>
+
+#include "mm_common.h"
+#include "mm_internal.h"
+
+namespace mm {
+namespace pq {
+
+constexpr int kT = 32;      // sequence steps per tile
+constexpr int kPad = 36;    // LDS row stride (floats) of per-channel step rows: 16-B aligned, spreads banks
+constexpr int kMaxRank = 8; // selective_scan.cpp:359
+
+// x + x[lane permuted by CTRL] as one v_add_f32 with a DPP operand (the compiler inserts the DPP
+// read hazard wait states itself for the builtin).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false);
+    return x + __builtin_bit_cast(float, o);
+}
+
+// Sum over the LPR consecutive lanes of a channel. Every step pairs two partial sums and adds them
+// in both lanes (a + b == b + a exactly), so all LPR lanes hold bit-identical totals.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(LPR == 4 || LPR == 8 || LPR == 16, "LPR");
+    x = dpp_add<0xB1>(x);                         // quad_perm [1,0,3,2]
+    x = dpp_add<0x4E>(x);                         // quad_perm [2,3,0,1]
+    if constexpr (LPR >= 8) x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of 8 lanes
+    if constexpr (LPR >= 16) x = dpp_add<0x140>(x); // row_mirror: the other half of the 16-lane row
+    return x;
+}
+
+// S consecutive floats of LDS (16-B, 8-B or 4-B aligned by construction).
+template <int S>
+__device__ __forceinline__ void lds_read_vec(const float *src, float *o) {
+    if constexpr (S == 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(src);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    } else if constexpr (S == 2) {
+        const float2 v = *reinterpret_cast<const float2 *>(src);
+        o[0] = v.x; o[1] = v.y;
+    } else {
+        o[0] = *src;
+    }
+}
+
+template <typename T, int S, int LPR, int R>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
+scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t blocks_per_group) {
+    constexpr int NP = S * LPR;            // padded states per channel
+    constexpr int CPW = 64 / LPR;          // channels per wave
+    constexpr int E = kT / LPR;            // prologue / epilogue steps per lane per tile
+    constexpr int BCS = 2 * NP + 4;        // sBC row stride (floats): NP B values, then NP C values
+    constexpr int HR = NP / 16;            // B/C half-rows (16 steps of one state) staged per lane
+    static_assert(HR >= 1 && E >= 2 && E % 2 == 0 && 2 * CPW <= 64, "tile shape");
+    __shared__ __align__(16) float sBC[kT * BCS];
+    // During the scan: dt' rows then dt'u rows of the wave's channels; after it: the y partials.
+    __shared__ __align__(16) float sX[64 * kPad];
+    float *sDt = sX;
+    float *sDu = sX + CPW * kPad;
+    float *sY = sX;
+
+    const int lane = threadIdx.x;
+    const int cw = lane / LPR;             // channel slot in the wave
+    const int k = lane % LPR;              // state slice: states k S .. k S + S - 1
+    const int64_t b = blockIdx.y;
+    const int64_t g = blockIdx.x / blocks_per_group;
+    const int64_t cl = int64_t(blockIdx.x % blocks_per_group) * CPW + cw;  // channel within the group
+    const bool active = cl < ratio;
+    const int64_t d = g * ratio + (active ? cl : ratio - 1);  // inactive slots mirror a real channel
+    const int64_t L = p.seqlen;
+    const int N = int(p.dstate);
+    const int rank = int(p.pq_rank);
+
+    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
+    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
+    const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
+    T *op = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
+    T *ozp = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
+    const T *Bg = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cg = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+
+    float A2[S], h[S], Pr[S][R], Qr[R][S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int n = k * S + s;
+        const bool on = n < N;
+        A2[s] = on ? p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e : 0.f;
+        h[s] = 0.f;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const bool use = on && j < rank;
+            Pr[s][j] = use ? p.P[d * p.P_d_stride + n * p.P_dstate_stride + j * p.P_r_stride] : 0.f;
+            Qr[j][s] = use ? p.Q[d * p.Q_d_stride + j * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
+        }
+    }
+    const float Dv = p.D ? p.D[d] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+    const bool softplus = p.delta_softplus != 0;
+    const int es = E * k;                  // first step (within a tile) of this lane's elements
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+
+    // The B/C half-rows this lane stages: index hr = lane HR + i -> tensor hr / (2 NP) (0: B, 1: C),
+    // state (hr % 2NP) / 2, steps 16 (hr % 2) .. +15 of the tile.
+    const T *bcp[HR];
+    int bc_lds[HR], bc_half[HR];
+    bool bc_on[HR];
+#pragma unroll
+    for (int i = 0; i < HR; ++i) {
+        const int hr = lane * HR + i;
+        const int tensor = hr / (2 * NP);
+        const int n = (hr % (2 * NP)) / 2;
+        bc_half[i] = hr % 2;
+        bc_on[i] = n < N;
+        const int64_t nn = n < N ? n : 0;
+        bcp[i] = tensor == 0 ? Bg + nn * p.B_dstate_stride : Cg + nn * p.C_dstate_stride;
+        bc_lds[i] = 16 * bc_half[i] * BCS + tensor * NP + n;
+    }
+
+    // Loads at or past the end of a row are redirected into the row's last elements (always in
+    // bounds: L is a multiple of 8); the steps they feed are padding with dt' = 0 and B = C = 0.
+    const int64_t lastE = L - E, last8 = L - 8;
+    auto ce = [&](int64_t i) { return i < lastE ? i : lastE; };
+    auto c8 = [&](int64_t i) { return i < last8 ? i : last8; };
+    RawVec<T, E> ru = load_raw<T, E>(up + ce(es));
+    RawVec<T, E> rd = load_raw<T, E>(dp + ce(es));
+    RawVec<T, E> rz = {};
+    if (zp) rz = load_raw<T, E>(zp + ce(es));
+    RawVec<T, 8> rbc[HR][2];
+    auto load_bc = [&](int64_t t0) {
+#pragma unroll
+        for (int i = 0; i < HR; ++i) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                rbc[i][h2] = {};
+                if (bc_on[i]) rbc[i][h2] = load_raw<T, 8>(bcp[i] + c8(t0 + 16 * bc_half[i] + 8 * h2));
+            }
+        }
+    };
+    // Tile rows [step][B states | C states] as float32; states past dstate and steps past L are 0.
+    auto stage_bc = [&](int64_t t0) {
+#pragma unroll
+        for (int i = 0; i < HR; ++i) {
+            const int64_t first = t0 + 16 * bc_half[i];
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                float v[8];
+                unpack_raw<T, 8>(rbc[i][h2], v);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int64_t t = first + 8 * h2 + e;
+                    sBC[bc_lds[i] + (8 * h2 + e) * BCS] = (bc_on[i] && t < L) ? v[e] : 0.f;
+                }
+            }
+        }
+    };
+    load_bc(0);
+    stage_bc(0);
+
+    for (int64_t t0 = 0; t0 < L; t0 += kT) {
+        const int64_t t1 = t0 + kT;
+        const bool ev = t0 + es < L;       // this lane's E elements exist (L is a multiple of E)
+        float uu[E], dd[E], zz[E];
+        unpack_raw<T, E>(ru, uu);
+        unpack_raw<T, E>(rd, dd);
+        unpack_raw<T, E>(rz, zz);
+        // Prefetch the next tile (clamped addresses: always in bounds).
+        ru = load_raw<T, E>(up + ce(t1 + es));
+        rd = load_raw<T, E>(dp + ce(t1 + es));
+        if (zp) rz = load_raw<T, E>(zp + ce(t1 + es));
+        load_bc(t1);
+
+        // Prologue: dt' and dt' u of (channel, steps es .. es + E - 1).
+        float dtp[E], dup[E];
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const float x = dd[i] + bias;
+            dtp[i] = softplus ? softplus_fast(x) : x;
+            if (!ev) dtp[i] = 0.f;         // padded steps of a last, partial tile
+            dup[i] = dtp[i] * uu[i];
+        }
+#pragma unroll
+        for (int i = 0; i < E; i += 2) {
+            *reinterpret_cast<float2 *>(&sDt[cw * kPad + es + i]) = make_float2(dtp[i], dtp[i + 1]);
+            *reinterpret_cast<float2 *>(&sDu[cw * kPad + es + i]) = make_float2(dup[i], dup[i + 1]);
+        }
+        __syncthreads();
+
+        // Scan: 32 steps in groups of 4. The decay factors and the input terms of a group do not
+        // depend on the state and are formed first; then the coupled updates run in order.
+        float yp[kT];
+        static_for<0, kT / 4>([&](auto G4) {
+            constexpr int s4 = decltype(G4)::value;
+            const float4 dt4 = *reinterpret_cast<const float4 *>(&sDt[cw * kPad + 4 * s4]);
+            const float4 du4 = *reinterpret_cast<const float4 *>(&sDu[cw * kPad + 4 * s4]);
+            const float dts[4] = {dt4.x, dt4.y, dt4.z, dt4.w};
+            const float dus[4] = {du4.x, du4.y, du4.z, du4.w};
+            float av[4][S], bu[4][S], cv[4][S];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int t = 4 * s4 + j;
+                float bv[S];
+                lds_read_vec<S>(&sBC[t * BCS + k * S], bv);
+                lds_read_vec<S>(&sBC[t * BCS + NP + k * S], cv[j]);
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    av[j][s] = __builtin_amdgcn_exp2f(dts[j] * A2[s]);
+                    bu[j][s] = dus[j] * bv[s];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float q[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float acc = Qr[r][0] * h[0];
+#pragma unroll
+                    for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
+                    q[r] = group_sum<LPR>(acc) * dts[j];
+                }
+                float y = 0.f;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    float w = bu[j][s];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                    h[s] = __builtin_fmaf(av[j][s], h[s], w);
+                    y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
+                }
+                yp[4 * s4 + j] = y;
+            }
+        });
+        __syncthreads();                   // sDt / sDu / sBC reads done: sY and sBC are rewritten
+
+#pragma unroll
+        for (int t = 0; t < kT; t += 4)
+            *reinterpret_cast<float4 *>(&sY[(cw * LPR + k) * kPad + t]) = make_float4(yp[t], yp[t + 1], yp[t + 2], yp[t + 3]);
+        if (t1 < L) stage_bc(t1);
+        __syncthreads();
+
+        // Epilogue: y of (channel, steps es .. es + E - 1) = the LPR partials, added in lane order.
+        float y[E];
+#pragma unroll
+        for (int i = 0; i < E; i += 2) {
+            float2 acc = *reinterpret_cast<const float2 *>(&sY[(cw * LPR) * kPad + es + i]);
+#pragma unroll
+            for (int kk = 1; kk < LPR; ++kk) {
+                const float2 v = *reinterpret_cast<const float2 *>(&sY[(cw * LPR + kk) * kPad + es + i]);
+                acc.x += v.x;
+                acc.y += v.y;
+            }
+            y[i] = acc.x;
+            y[i + 1] = acc.y;
+        }
+        if (active && ev) {
+            float o[E];
+#pragma unroll
+            for (int i = 0; i < E; ++i) o[i] = p.D ? __builtin_fmaf(Dv, uu[i], y[i]) : y[i];
+            if (op) store_vec<T, E>(op + t0 + es, o);
+            if (zp) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) o[i] *= silu_fast(zz[i]);
+                store_vec<T, E>(ozp + t0 + es, o);
+            }
+        }
+        if (active && p.chunk_states) {
+            const int64_t tend = t1 < L ? t1 : L;
+            if (tend % MM_SCAN_CHUNK == 0 || tend == L) {
+                const int64_t c = (tend - 1) / MM_SCAN_CHUNK;
+                float *cs = p.chunk_states + ((b * p.dim + d) * n_chunks + c) * 2 * N;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    const int n = k * S + s;
+                    if (n < N) {
+                        cs[2 * n] = 1.f;
+                        cs[2 * n + 1] = h[s];
+                    }
+                }
+            }
+        }
+        __syncthreads();                   // sY reads done before the next prologue overwrites sX
+    }
+    if (active && p.last_state) {
+        float *ls = p.last_state + (b * p.dim + d) * N;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int n = k * S + s;
+            if (n < N) ls[n] = h[s];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// General kernel: one lane per (batch, channel) row; the row's states in LDS (dstate x 64 floats per
+// block, lane-minor so every access is conflict-free), P and Q read through the cache.
+// ------------------------------------------------------------------------------------------------
+constexpr int kRowBlock = 64;
+
+template <typename T>
+__global__ void __launch_bounds__(kRowBlock)
+scan_fwd_pq_rowlane(const mm_scan_fwd_params p, const int64_t ratio) {
+    extern __shared__ float sH[];          // [dstate][64]
+    const int lane = threadIdx.x;
+    const int64_t d_raw = int64_t(blockIdx.x) * blockDim.x + lane;
+    const int64_t b = blockIdx.y;
+    const bool active = d_raw < p.dim;
+    const int64_t d = active ? d_raw : p.dim - 1;  // clamped for loads; stores are predicated
+    const int64_t g = d / ratio;
+    const int64_t L = p.seqlen;
+    const int N = int(p.dstate);
+    const int rank = int(p.pq_rank);
+
+    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
+    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
+    const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
+    T *op = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
+    T *ozp = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
+    const T *Bv = p.is_variable_B ? reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride : nullptr;
+    const T *Cv = p.is_variable_C ? reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride : nullptr;
+    const float *Bc = reinterpret_cast<const float *>(p.B) + d * p.B_d_stride;
+    const float *Cc = reinterpret_cast<const float *>(p.C) + d * p.C_d_stride;
+    const float *Ad = p.A + d * p.A_d_stride;
+    const float *Pd = p.P + d * p.P_d_stride;
+    const float *Qd = p.Q + d * p.Q_d_stride;
+
+    for (int n = 0; n < N; ++n) sH[n * kRowBlock + lane] = 0.f;
+    const float Dv = p.D ? p.D[d] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+
+    for (int64_t t = 0; t < L; ++t) {
+        float dt = to_f32(dp[t]) + bias;
+        if (p.delta_softplus) dt = softplus_fast(dt);
+        const float uu = to_f32(up[t]);
+        const float du = dt * uu;
+        // q = dt' (Q h_{t-1}), from the state before this step.
+        float q[kMaxRank];
+#pragma unroll
+        for (int j = 0; j < kMaxRank; ++j) q[j] = 0.f;
+        for (int n = 0; n < N; ++n) {
+            const float hn = sH[n * kRowBlock + lane];
+#pragma unroll
+            for (int j = 0; j < kMaxRank; ++j)
+                if (j < rank) q[j] = __builtin_fmaf(Qd[j * p.Q_r_stride + n * p.Q_dstate_stride], hn, q[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxRank; ++j) q[j] *= dt;
+        float y = 0.f;
+        for (int n = 0; n < N; ++n) {
+            const float bn = Bv ? to_f32(Bv[n * p.B_dstate_stride + t]) : Bc[n * p.B_dstate_stride];
+            const float cn = Cv ? to_f32(Cv[n * p.C_dstate_stride + t]) : Cc[n * p.C_dstate_stride];
+            float w = du * bn;
+#pragma unroll
+            for (int j = 0; j < kMaxRank; ++j)
+                if (j < rank) w = __builtin_fmaf(Pd[n * p.P_dstate_stride + j * p.P_r_stride], q[j], w);
+            const float a = __builtin_amdgcn_exp2f(dt * (Ad[n * p.A_dstate_stride] * kLog2e));
+            const float hn = __builtin_fmaf(a, sH[n * kRowBlock + lane], w);
+            sH[n * kRowBlock + lane] = hn;
+            y = __builtin_fmaf(hn, cn, y);
+        }
+        if (active) {
+            const float o = p.D ? __builtin_fmaf(Dv, uu, y) : y;
+            if (op) op[t] = from_f32<T>(o);
+            if (ozp) ozp[t] = from_f32<T>(o * silu_fast(to_f32(zp[t])));
+            if (p.chunk_states && ((t + 1) % MM_SCAN_CHUNK == 0 || t == L - 1)) {
+                float *cs = p.chunk_states + ((b * p.dim + d) * n_chunks + t / MM_SCAN_CHUNK) * 2 * N;
+                for (int n = 0; n < N; ++n) {
+                    cs[2 * n] = 1.f;
+                    cs[2 * n + 1] = sH[n * kRowBlock + lane];
+                }
+            }
+        }
+    }
+    if (active && p.last_state) {
+        float *ls = p.last_state + (b * p.dim + d) * N;
+        for (int n = 0; n < N; ++n) ls[n] = sH[n * kRowBlock + lane];
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Host side.
+// ------------------------------------------------------------------------------------------------
+struct TiledShape { int S, LPR; };
+
+// Waves wanted before fewer states per lane (more lanes per channel) are preferred: two per SIMD.
+int64_t min_waves() {
+    const char *e = getenv("MM_PQ_MIN_WAVES");
+    return e ? atoll(e) : 2048;
+}
+
+// The (S, LPR) of the tiled kernel for this request, or {0, 0} when the request needs the general
+// kernel: variable B and C, dstate <= 64, seqlen >= 8, rows movable as 16-byte vectors.
+TiledShape tiled_shape(const mm_scan_fwd_params &p) {
+    if (!p.is_variable_B || !p.is_variable_C || p.dstate > 64 || p.seqlen < 8 || !fwd_vector_ok(&p)) return {0, 0};
+    const int64_t ratio = p.dim / p.n_groups;
+    auto waves = [&](int lpr) { return p.batch * p.n_groups * ((ratio + 64 / lpr - 1) / (64 / lpr)); };
+    const char *forced = getenv("MM_PQ_LPR");
+    const int want = forced ? atoi(forced) : 0;
+    TiledShape cands[3];
+    int nc = 0;
+    if (p.dstate <= 16) { cands[nc++] = {4, 4}; cands[nc++] = {2, 8}; cands[nc++] = {1, 16}; }
+    else if (p.dstate <= 32) { cands[nc++] = {4, 8}; cands[nc++] = {2, 16}; }
+    else { cands[nc++] = {4, 16}; }
+    for (int i = 0; i < nc; ++i)
+        if (cands[i].LPR == want) return cands[i];
+    for (int i = 0; i < nc; ++i)
+        if (waves(cands[i].LPR) >= min_waves()) return cands[i];
+    return cands[nc - 1];
+}
+
+template <typename T, int S, int LPR, int R>
+int launch_tiled_sr(const mm_scan_fwd_params &p, hipStream_t s) {
+    constexpr int CPW = 64 / LPR;
+    const int64_t ratio = p.dim / p.n_groups;
+    const int64_t bpg = (ratio + CPW - 1) / CPW;
+    dim3 grid(unsigned(bpg * p.n_groups), unsigned(p.batch));
+    hipLaunchKernelGGL((scan_fwd_pq_tiled<T, S, LPR, R>), grid, dim3(64), 0, s, p, ratio, int32_t(bpg));
+    return launch_status("scan_fwd_pq_tiled");
+}
+
+template <typename T, int S, int LPR>
+int launch_tiled_s(const mm_scan_fwd_params &p, hipStream_t s) {
+    if (p.pq_rank <= 2) return launch_tiled_sr<T, S, LPR, 2>(p, s);
+    if (p.pq_rank <= 4) return launch_tiled_sr<T, S, LPR, 4>(p, s);
+    return launch_tiled_sr<T, S, LPR, 8>(p, s);
+}
+
+template <typename T>
+int launch_rowlane(const mm_scan_fwd_params &p, hipStream_t s) {
+    dim3 grid(unsigned((p.dim + kRowBlock - 1) / kRowBlock), unsigned(p.batch));
+    const size_t lds = size_t(p.dstate) * kRowBlock * sizeof(float);  // <= 64 KB at dstate 256
+    hipLaunchKernelGGL((scan_fwd_pq_rowlane<T>), grid, dim3(kRowBlock), lds, s, p, p.dim / p.n_groups);
+    return launch_status("scan_fwd_pq_rowlane");
+}
+
+}  // namespace pq
+
+int64_t pq_tiled_lanes_per_row(const mm_scan_fwd_params &p) { return pq::tiled_shape(p).LPR; }
+
+template <typename T>
+int launch_pq(const mm_scan_fwd_params &p, hipStream_t s) {
+    const pq::TiledShape sh = pq::tiled_shape(p);
+    if (sh.LPR == 4) return pq::launch_tiled_s<T, 4, 4>(p, s);
+    if (sh.LPR == 8) return sh.S == 4 ? pq::launch_tiled_s<T, 4, 8>(p, s) : pq::launch_tiled_s<T, 2, 8>(p, s);
+    if (sh.LPR == 16) {
+        if (sh.S == 4) return pq::launch_tiled_s<T, 4, 16>(p, s);
+        if (sh.S == 2) return pq::launch_tiled_s<T, 2, 16>(p, s);
+        return pq::launch_tiled_s<T, 1, 16>(p, s);
+    }
+    return pq::launch_rowlane<T>(p, s);
+}
+
+template int launch_pq<float>(const mm_scan_fwd_params &, hipStream_t);
+template int launch_pq<f16_t>(const mm_scan_fwd_params &, hipStream_t);
+template int launch_pq<bf16_t>(const mm_scan_fwd_params &, hipStream_t);
+
+}  // namespace mm

@@ -43,7 +43,8 @@ struct FwdSetup {
     int64_t n_chunks;
 };
 
-// Shared validation (selective_scan.cpp:280-381, without the P/Q/gamma and complex branches).
+// Shared validation (selective_scan.cpp:280-381, without the P/Q/gamma and complex branches,
+// which attach_pq and the complex-A refusal below cover).
 FwdSetup setup_fwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A, const at::Tensor &B,
                    const at::Tensor &C, const c10::optional<at::Tensor> &D_, const c10::optional<at::Tensor> &z_,
                    const c10::optional<at::Tensor> &delta_bias_, bool delta_softplus) {
@@ -178,6 +179,58 @@ void set_out_z(mm_scan_fwd_params &p, const at::Tensor &out_z) {
     p.out_z_d_stride = out_z.stride(1);
 }
 
+// Low-rank coupling P/Q and gamma (checks of selective_scan.cpp:342-369, strides as
+// set_ssm_params_fwd, selective_scan.cpp:149-164). P and Q are read as float32: the reference's
+// dense kernel reinterprets them as float and its full-matrix path upcasts them with .float().
+// gamma is validated and carried, not read (neither reference forward reads it). Returns the
+// float32 P/Q the parameter block points at; the caller keeps them alive until the launch.
+std::vector<at::Tensor> attach_pq(mm_scan_fwd_params &p, const at::Tensor &u, const c10::optional<at::Tensor> &P_,
+                                  const c10::optional<at::Tensor> &Q_, const c10::optional<at::Tensor> &gamma_) {
+    TORCH_CHECK(!P_.has_value() || Q_.has_value(), "Q must be provided when P is provided");
+    TORCH_CHECK(!Q_.has_value() || P_.has_value(), "P must be provided when Q is provided");
+    std::vector<at::Tensor> keep;
+    if (P_.has_value()) {
+        const at::Tensor &P = P_.value(), &Q = Q_.value();
+        TORCH_CHECK(P.is_cuda() && Q.is_cuda(), "P and Q must be CUDA tensors");
+        TORCH_CHECK(P.device() == u.device() && Q.device() == u.device(), "P and Q must be on the device of u");
+        TORCH_CHECK(P.dim() == Q.dim() && (P.dim() == 2 || P.dim() == 3), "P/Q must be 2D or 3D with same rank");
+        if (P.dim() == 2) {
+            TORCH_CHECK(P.size(0) == p.dstate && Q.size(1) == p.dstate && P.size(1) == Q.size(0),
+                        "Expect P(dstate, r), Q(r, dstate)");
+        } else {
+            TORCH_CHECK(P.size(0) == p.dim && Q.size(0) == p.dim, "P/Q dim mismatch");
+            TORCH_CHECK(P.size(1) == p.dstate && Q.size(2) == p.dstate && P.size(2) == Q.size(1),
+                        "Expect P(dim, dstate, r), Q(dim, r, dstate)");
+        }
+        TORCH_CHECK(P.size(-1) <= 8, "Current dense CUDA forward supports pq_rank <= 8");
+        const at::Tensor Pf = P.to(at::ScalarType::Float), Qf = Q.to(at::ScalarType::Float);
+        keep = {Pf, Qf};
+        p.P = Pf.data_ptr<float>();
+        p.Q = Qf.data_ptr<float>();
+        p.pq_rank = P.size(-1);
+        p.P_d_stride = P.dim() == 3 ? Pf.stride(0) : 0;
+        p.P_dstate_stride = Pf.stride(P.dim() - 2);
+        p.P_r_stride = Pf.stride(P.dim() - 1);
+        p.Q_d_stride = Q.dim() == 3 ? Qf.stride(0) : 0;
+        p.Q_r_stride = Qf.stride(Q.dim() - 2);
+        p.Q_dstate_stride = Qf.stride(Q.dim() - 1);
+    }
+    if (gamma_.has_value()) {
+        const at::Tensor &gamma = gamma_.value();
+        TORCH_CHECK(gamma.is_cuda(), "gamma must be CUDA tensor");
+        TORCH_CHECK(gamma.dim() == 1 || gamma.dim() == 2, "gamma must be 1D or 2D");
+        if (gamma.dim() == 1) {
+            TORCH_CHECK(gamma.size(0) == p.dstate, "gamma(1D) shape must be (dstate,)");
+        } else {
+            TORCH_CHECK(gamma.size(0) == p.dim && gamma.size(1) == p.dstate, "gamma(2D) shape must be (dim, dstate)");
+        }
+        p.gamma = static_cast<const float *>(gamma.data_ptr());
+        p.gamma_d_stride = gamma.dim() == 2 ? gamma.stride(0) : 0;
+        p.gamma_dstate_stride = gamma.stride(-1);
+    }
+    return keep;
+}
+
 // Scratch for the sequence-parallel segments (only for shapes that use them), from the caching
 // allocator on the launch stream: released when the caller's reference drops, stream-ordered.
 at::Tensor attach_workspace(mm_scan_fwd_params &p, const at::Tensor &like) {
@@ -194,12 +247,9 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
                             const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &delta_bias_,
                             const c10::optional<at::Tensor> &P_, const c10::optional<at::Tensor> &Q_,
                             const c10::optional<at::Tensor> &gamma_, bool delta_softplus) {
-    if (P_.has_value() || Q_.has_value() || gamma_.has_value()) {
-        throw c10::NotImplementedError({__func__, __FILE__, uint32_t(__LINE__)},
-                                       "P/Q/gamma (MotifMamba low-rank coupling) are not part of the MI355X scan");
-    }
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     mm_scan_fwd_params &p = s.p;
+    const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
     // Output layouts follow the reference: out like delta, out_z like z, x contiguous.
     at::Tensor out = torch::empty_like(delta);
     at::Tensor x = torch::empty({p.batch, p.dim, s.n_chunks, p.dstate * 2}, u.options().dtype(A.scalar_type()));
@@ -222,9 +272,11 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
                                   const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                                   const c10::optional<at::Tensor> &z_,
                                   const c10::optional<at::Tensor> &delta_bias_, bool delta_softplus,
-                                  bool return_last_state) {
+                                  bool return_last_state, const c10::optional<at::Tensor> &P_,
+                                  const c10::optional<at::Tensor> &Q_, const c10::optional<at::Tensor> &gamma_) {
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     mm_scan_fwd_params &p = s.p;
+    const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
     at::Tensor main;
     if (z_.has_value()) {
         main = torch::empty_like(z_.value());
@@ -352,7 +404,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
           pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
           pybind11::arg("delta_bias") = pybind11::none(), pybind11::arg("delta_softplus") = false,
-          pybind11::arg("return_last_state") = false);
+          pybind11::arg("return_last_state") = false, pybind11::arg("P") = pybind11::none(),
+          pybind11::arg("Q") = pybind11::none(), pybind11::arg("gamma") = pybind11::none());
     m.def("state_update", &state_update, "Single-token selective state update (in place on state)",
           pybind11::arg("state"), pybind11::arg("x"), pybind11::arg("dt"), pybind11::arg("A"), pybind11::arg("B"),
           pybind11::arg("C"), pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),

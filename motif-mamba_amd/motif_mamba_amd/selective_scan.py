@@ -9,8 +9,16 @@ same argument names, defaults, input normalisation and return values:
 * returns ``out_z`` when z is given, else ``out``; with ``return_last_state`` also the float32
   ``(batch, dim, dstate)`` state after the last step (ssi.py:54-61).
 
-Differences (all raise instead of computing something else): the backward pass, the MotifMamba
-P/Q/gamma paths (ssi.py:243-258) and complex A are not part of this build.
+With P/Q (the MotifMamba low-rank coupling, ssi.py:243-258) ``selective_scan_fn`` computes
+``h_t = exp(dt A) h_{t-1} + dt P (Q h_{t-1}) + dt u B_t`` on the GPU whether or not z is given: the
+reference sends z-less calls to its dense CUDA kernel (``SelectiveScanPQFn``, ssi.py:93-150) and
+calls with z to a torch loop (``selective_scan_full_matrix_cuda``, ssi.py:262-350); both compute
+the same function, and so does this build's single kernel. Argument errors are the reference's
+(ValueError for P without Q, mismatched P/Q shapes or non-CUDA tensors). gamma is validated
+and, as in both reference paths, not used.
+
+Differences (all raise instead of computing something else): the backward pass and complex A are
+not part of this build.
 """
 from __future__ import annotations
 
@@ -53,6 +61,66 @@ class SelectiveScanFn(torch.autograd.Function):
             "selective_scan backward is not implemented by the MI355X build (forward and decode only)")
 
 
+class SelectiveScanPQFn(torch.autograd.Function):
+    """Forward of the low-rank coupled scan (ssi.py:93-150 and ssi.py:262-350), z optional."""
+
+    @staticmethod
+    def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                return_last_state=False, P=None, Q=None, gamma=None):
+        if u.stride(-1) != 1:
+            u = u.contiguous()
+        if delta.stride(-1) != 1:
+            delta = delta.contiguous()
+        if D is not None:
+            D = D.contiguous()
+        if B.stride(-1) != 1:
+            B = B.contiguous()
+        if C.stride(-1) != 1:
+            C = C.contiguous()
+        if z is not None and z.stride(-1) != 1:
+            z = z.contiguous()
+        if delta_bias is not None and delta_bias.stride(-1) != 1:
+            delta_bias = delta_bias.contiguous()
+        if B.dim() == 3:
+            B = rearrange(B, "b dstate l -> b 1 dstate l")
+        if C.dim() == 3:
+            C = rearrange(C, "b dstate l -> b 1 dstate l")
+        res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
+                              delta_softplus=delta_softplus, return_last_state=return_last_state,
+                              P=P, Q=Q, gamma=gamma)
+        if return_last_state:
+            return res[0], res[1]
+        return res[0]
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(
+            "selective_scan P/Q backward is not implemented by the MI355X build (forward only)")
+
+
+def _check_pq(u, delta, A, B, C, P, Q):
+    """The argument errors of selective_scan_full_matrix_cuda (ssi.py:266-271, 303-318)."""
+    if P is None or Q is None:
+        raise ValueError("P and Q must both be provided for full-matrix path")
+    if A.is_complex():
+        raise NotImplementedError("Full-matrix P/Q path currently supports real A only")
+    if not (u.is_cuda and delta.is_cuda and A.is_cuda and B.is_cuda and C.is_cuda and P.is_cuda and Q.is_cuda):
+        raise ValueError("Full-matrix path requires CUDA tensors")
+    dim, dstate = u.shape[1], A.shape[1]
+    if P.dim() == 2 and Q.dim() == 2:
+        if P.shape[0] != dstate or Q.shape[1] != dstate or P.shape[1] != Q.shape[0]:
+            raise ValueError("Expected P(n, r), Q(r, n) with n=dstate")
+    elif P.dim() == 3 and Q.dim() == 3:
+        if P.shape[0] != dim or Q.shape[0] != dim:
+            raise ValueError("Expected P(dim, n, r), Q(dim, r, n)")
+        if P.shape[1] != dstate or Q.shape[2] != dstate or P.shape[2] != Q.shape[1]:
+            raise ValueError("Expected P(dim, n, r), Q(dim, r, n)")
+    else:
+        raise ValueError("P and Q must both be 2D or both be 3D")
+    if P.shape[-1] > 8:
+        raise NotImplementedError("pq_rank > 8 is not supported (the reference's dense forward limit)")
+
+
 def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
                       return_last_state=False, P=None, Q=None, gamma=None):
     """if return_last_state is True, returns (out, last_state)
@@ -60,6 +128,7 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
     not considered in the backward pass.
     """
     if P is not None or Q is not None or gamma is not None:
-        raise NotImplementedError(
-            "the MotifMamba P/Q/gamma low-rank coupling path is not part of the MI355X selective scan")
+        _check_pq(u, delta, A, B, C, P, Q)
+        return SelectiveScanPQFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
+                                       return_last_state, P, Q, gamma)
     return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state)

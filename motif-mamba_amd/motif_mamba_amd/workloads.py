@@ -141,3 +141,57 @@ def decode_bytes(batch, dim, dstate, n_groups=1, in_bytes=2):
     written, B and C read, A, D, dt_bias read."""
     return (batch * (2 * dim * dstate * 4 + 4 * dim * in_bytes + 2 * n_groups * dstate * in_bytes)
             + dim * dstate * 4 + 2 * dim * 4)
+
+
+@dataclass(frozen=True)
+class PQConfig:
+    """A MotifMamba layer with the low-rank P/Q coupling (mamba_simplemotif.py:139-151, 314-332)."""
+    name: str
+    batch: int
+    dim: int
+    seqlen: int
+    dstate: int = 16
+    rank: int = 2
+    per_dim: bool = True
+    dtype: str = "fp16"
+    pq_std: float = 0.1
+    seed: int = 5
+
+
+# Mamba-1.4B (d_model 2048, d_inner 4096, d_state 16), the model train_kpq_motif_pile_lm.py adapts,
+# with its defaults: pq_rank 2, per-channel P/Q, float16 activations.
+PQ_CONFIGS = {
+    "pq_1p4b": PQConfig("pq_1p4b", 4, 4096, 2048),
+}
+
+
+def pq_inputs(cfg: PQConfig, device="cpu"):
+    """Inputs of one selective_scan_fn(..., P=P, Q=Q) call as the Motif module makes it (z gate,
+    delta_bias + softplus, last state). Draw order: u, delta, z, delta_bias, B, C, P, Q.
+    P, Q ~ N(0, pq_std) (the module draws N(0, 1e-2) and scales P by pq_k; a larger spread keeps
+    the coupling visible in parity checks and does not change the work)."""
+    N, L, R = cfg.dstate, cfg.seqlen, cfg.rank
+    dt = _DT[cfg.dtype]
+    g = torch.Generator().manual_seed(cfg.seed)
+    u = torch.randn(cfg.batch, cfg.dim, L, generator=g).to(dt)
+    delta = torch.randn(cfg.batch, cfg.dim, L, generator=g).to(dt)
+    z = torch.randn(cfg.batch, cfg.dim, L, generator=g).to(dt)
+    lo, hi = math.log(1e-3), math.log(1e-1)
+    delta_bias = (torch.rand(cfg.dim, generator=g) * (hi - lo) + lo).float()
+    B = torch.randn(cfg.batch, N, L, generator=g).to(dt)
+    C = torch.randn(cfg.batch, N, L, generator=g).to(dt)
+    shp_p, shp_q = ((cfg.dim, N, R), (cfg.dim, R, N)) if cfg.per_dim else ((N, R), (R, N))
+    P = (torch.randn(*shp_p, generator=g) * cfg.pq_std).float()
+    Q = (torch.randn(*shp_q, generator=g) * cfg.pq_std).float()
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(cfg.dim, 1).contiguous()
+    D = torch.ones(cfg.dim, dtype=torch.float32)
+    t = dict(u=u, delta=delta, A=A, B=B, C=C, D=D, z=z, delta_bias=delta_bias, P=P, Q=Q)
+    if device != "cpu":
+        t = {k: v.to(device) for k, v in t.items()}
+    t.update(delta_softplus=True, return_last_state=True)
+    return t
+
+
+def pq_flops(batch, dim, seqlen, dstate, rank):
+    """Multiply-adds of the coupling per step (Q h then P q: 2 N R) as flops, per call."""
+    return batch * dim * seqlen * 4 * dstate * rank

@@ -40,6 +40,12 @@ def _load():
                       dp, i64, i64, i64, dp, i64, i64, i64,
                       dp, dp, ctypes.c_int, dp, dp, dp, i64, dp]
         f.restype = None
+        g = lib.mm_oracle_scan_pq_rows_f64
+        g.argtypes = [i64, i64, i64, i64, dp, dp, dp, dp,
+                      dp, i64, i64, i64, dp, i64, i64, i64,
+                      dp, i64, dp, i64,
+                      dp, dp, ctypes.c_int, dp, dp, dp, i64, dp]
+        g.restype = None
         _lib = lib
     return _lib
 
@@ -54,8 +60,11 @@ def _p(a):
 
 
 def scan_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-              rows=None, chunk=0):
+              rows=None, chunk=0, P=None, Q=None):
     """Float64 scan of the rows ``rows`` (list of (b, d) pairs; all rows if None).
+
+    With P and Q (2-D (N, R) / (R, N) shared, or 3-D (dim, N, R) / (dim, R, N) per channel) the
+    low-rank coupled scan ``mm_oracle_scan_pq_rows_f64`` is evaluated instead.
 
     Tensors are torch CPU tensors or numpy arrays in the reference layouts (u/delta/z
     (batch, dim, L); A (dim, N); B/C (dim, N), (batch, N, L) or (batch, G, N, L)).
@@ -107,6 +116,20 @@ def scan_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus
     last = np.zeros((R, N))
     n_chunks = (L + chunk - 1) // chunk if chunk > 0 else 0
     hch = np.zeros((R, n_chunks, N)) if chunk > 0 else None
+    if P is not None:
+        K = P.shape[-1]
+        if P.dim() == 2:
+            Ps, pR = np.ascontiguousarray(npf(P)), 0
+            Qs, qR = np.ascontiguousarray(npf(Q)), 0
+        else:
+            Ps, pR = np.ascontiguousarray(take(P, (di,))), N * K
+            Qs, qR = np.ascontiguousarray(take(Q, (di,))), K * N
+        _load().mm_oracle_scan_pq_rows_f64(R, L, N, K, _p(ur), _p(dr), _p(zr), _p(Ar),
+                                           _p(Bs), bR, bN, bL, _p(Cs), cR, cN, cL,
+                                           _p(Ps), pR, _p(Qs), qR,
+                                           _p(Dr), _p(br), int(bool(delta_softplus)),
+                                           _p(out), _p(outz), _p(last), int(chunk), _p(hch))
+        return {"out": out, "out_z": outz, "last_state": last, "h_chunks": hch}
     _load().mm_oracle_scan_rows_f64(R, L, N, _p(ur), _p(dr), _p(zr), _p(Ar),
                                     _p(Bs), bR, bN, bL, _p(Cs), cR, cN, cL,
                                     _p(Dr), _p(br), int(bool(delta_softplus)),

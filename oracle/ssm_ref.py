@@ -21,6 +21,13 @@ discretisation in the activation dtype; the upstream kernel and this restatement
 float32 (dt + dt_bias promotes to float32), which is the behaviour the kernel must match.
 ``mamba_step_fallback_ref`` keeps the fallback's literal dtype behaviour for comparison.
 
+``selective_scan_pq_ref`` restates the MotifMamba low-rank coupled scan
+``selective_scan_full_matrix_cuda`` (ssi.py:262-350): h_t = exp(delta' A) h_{t-1} + delta' P (Q h_{t-1})
++ delta' u B_t, the path ``selective_scan_fn`` takes for P/Q (ssi.py:243-258). Pinned against the
+transition-matrix brute force of ``brute.scan_pq_brute``, the C float64 restatement
+``mm_oracle_scan_pq_rows_f64``, its P = 0 reduction to ``selective_scan_ref``, a scalar closed form
+and the P -> P M, Q -> M^-1 Q invariance (tests/test_oracle_pq.py).
+
 Pins (see tests/test_oracle.py): float64 brute-force sum on tiny shapes, a hand-worked
 known-answer case, closed forms (L=1, delta=0, memoryless decay, N=1 geometric filter against
 numpy.convolve, z-gate composition), invariants (linearity in u, group split, decode/scan
@@ -205,3 +212,83 @@ def mamba_step_fallback_ref(state, x, dt, A, B, C, D, z, dt_bias):
 def softplus_f64(x: float) -> float:
     """float64 softplus with torch's threshold of 20 (used by the brute-force restatement)."""
     return x if x > 20.0 else math.log1p(math.exp(x))
+
+
+def selective_scan_pq_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
+                          return_last_state=False, P=None, Q=None, gamma=None):
+    """CPU restatement of the MotifMamba low-rank coupled scan ``selective_scan_full_matrix_cuda``
+    (reference ``mamba_ssm/ops/selective_scan_interface.py:262-350``), op for op:
+
+    * argument checks and their ValueError / NotImplementedError (ssi.py:266-271, 306-318);
+    * float32 upcasts, ``delta += delta_bias``, ``F.softplus`` (ssi.py:273-280);
+    * 3-D B/C broadcast over channels, 4-D B/C repeated ``B G N L -> B (G H) N L``, 2-D B/C constant
+      (ssi.py:287-301); 2-D P (N, R) / Q (R, N) expanded to every channel, 3-D used per channel
+      (ssi.py:303-316);
+    * per step: ``A_diag = exp(dt * A)``, ``input_term = (dt * u) * B_t``, ``q = einsum('drn,bdn->bdr')``,
+      ``pq = einsum('dnr,bdr->bdn')``, ``x = A_diag * x + dt * pq + input_term``, ``y_t = sum(x * C_t)``
+      (ssi.py:320-341);
+    * ``out = y + u * D``, ``out *= silu(z.float())``, cast to the input dtype; returns ``(out, x)``
+      with x the float32 state after the last step (ssi.py:343-350).
+
+    gamma is accepted and ignored, as in the reference (neither forward path reads it).
+    The reference requires CUDA tensors (ssi.py:270-271); this restatement runs on CPU tensors.
+    """
+    if P is None or Q is None:
+        raise ValueError("P and Q must both be provided for full-matrix path")
+    if A.is_complex():
+        raise NotImplementedError("Full-matrix P/Q path currently supports real A only")
+    dtype_in = u.dtype
+    u_f = u.float()
+    delta_f = delta.float()
+    A_f = A.float()
+    if delta_bias is not None:
+        delta_f = delta_f + delta_bias[..., None].float()
+    if delta_softplus:
+        delta_f = F.softplus(delta_f)
+    batch, dim, seqlen = u.shape
+    dstate = A.shape[1]
+    var_B = B.dim() >= 3
+    var_C = C.dim() >= 3
+    B_f = B.float()
+    C_f = C.float()
+    if var_B:
+        B_full = (B_f.unsqueeze(1).expand(-1, dim, -1, -1) if B_f.dim() == 3
+                  else repeat(B_f, "B G N L -> B (G H) N L", H=dim // B_f.shape[1]))
+    if var_C:
+        C_full = (C_f.unsqueeze(1).expand(-1, dim, -1, -1) if C_f.dim() == 3
+                  else repeat(C_f, "B G N L -> B (G H) N L", H=dim // C_f.shape[1]))
+    if P.dim() == 2 and Q.dim() == 2:
+        if P.shape[0] != dstate or Q.shape[1] != dstate or P.shape[1] != Q.shape[0]:
+            raise ValueError("Expected P(n, r), Q(r, n) with n=dstate")
+        P_d = P.float().unsqueeze(0).expand(dim, -1, -1)
+        Q_d = Q.float().unsqueeze(0).expand(dim, -1, -1)
+    elif P.dim() == 3 and Q.dim() == 3:
+        if P.shape[0] != dim or Q.shape[0] != dim:
+            raise ValueError("Expected P(dim, n, r), Q(dim, r, n)")
+        if P.shape[1] != dstate or Q.shape[2] != dstate or P.shape[2] != Q.shape[1]:
+            raise ValueError("Expected P(dim, n, r), Q(dim, r, n)")
+        P_d = P.float()
+        Q_d = Q.float()
+    else:
+        raise ValueError("P and Q must both be 2D or both be 3D")
+    x = A_f.new_zeros((batch, dim, dstate))
+    ys = []
+    A_expand = A_f.unsqueeze(0)
+    for t in range(seqlen):
+        dt = delta_f[:, :, t]
+        A_diag = torch.exp(dt.unsqueeze(-1) * A_expand)
+        B_t = B_full[:, :, :, t] if var_B else B_f.unsqueeze(0).expand(batch, -1, -1)
+        input_term = (dt * u_f[:, :, t]).unsqueeze(-1) * B_t
+        q = torch.einsum("drn,bdn->bdr", Q_d, x)
+        pq_term = torch.einsum("dnr,bdr->bdn", P_d, q)
+        x = A_diag * x + dt.unsqueeze(-1) * pq_term + input_term
+        if var_C:
+            ys.append((x * C_full[:, :, :, t]).sum(dim=-1))
+        else:
+            ys.append((x * C_f.unsqueeze(0)).sum(dim=-1))
+    y = torch.stack(ys, dim=2)
+    out = y if D is None else y + u_f * D.float().view(1, -1, 1)
+    if z is not None:
+        out = out * F.silu(z.float())
+    out = out.to(dtype=dtype_in)
+    return out if not return_last_state else (out, x)

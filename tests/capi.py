@@ -30,7 +30,11 @@ class ScanFwdParams(ctypes.Structure):
                 ("A_d_stride", i64), ("A_dstate_stride", i64),
                 ("B_batch_stride", i64), ("B_group_stride", i64), ("B_dstate_stride", i64), ("B_d_stride", i64),
                 ("C_batch_stride", i64), ("C_group_stride", i64), ("C_dstate_stride", i64), ("C_d_stride", i64),
-                ("workspace", vp), ("workspace_bytes", i64)]
+                ("workspace", vp), ("workspace_bytes", i64),
+                ("P", vp), ("Q", vp), ("gamma", vp), ("pq_rank", i64),
+                ("P_d_stride", i64), ("P_dstate_stride", i64), ("P_r_stride", i64),
+                ("Q_d_stride", i64), ("Q_r_stride", i64), ("Q_dstate_stride", i64),
+                ("gamma_d_stride", i64), ("gamma_dstate_stride", i64)]
 
 
 class StateUpdateParams(ctypes.Structure):
@@ -72,8 +76,10 @@ def _ptr(t):
 
 
 def scan_fwd_params(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                    out=None, out_z=None, last_state=None, chunk_states=None, workspace=None):
-    """Fill ScanFwdParams from torch tensors in the reference layouts (B/C 4-D or 2-D)."""
+                    out=None, out_z=None, last_state=None, chunk_states=None, workspace=None,
+                    P=None, Q=None, gamma=None):
+    """Fill ScanFwdParams from torch tensors in the reference layouts (B/C 4-D or 2-D; P/Q 2-D
+    shared or 3-D per channel, float32)."""
     p = ScanFwdParams()
     p.batch, p.dim, p.seqlen = u.shape
     p.dstate = A.shape[1]
@@ -104,6 +110,20 @@ def scan_fwd_params(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_so
         p.C_d_stride, p.C_dstate_stride = C.stride(0), C.stride(1)
     if workspace is not None:
         p.workspace, p.workspace_bytes = _ptr(workspace), workspace.numel() * workspace.element_size()
+    if P is not None:
+        p.P, p.Q, p.pq_rank = _ptr(P), _ptr(Q), P.shape[-1]
+        if P.dim() == 3:
+            p.P_d_stride, p.P_dstate_stride, p.P_r_stride = P.stride()
+            p.Q_d_stride, p.Q_r_stride, p.Q_dstate_stride = Q.stride()
+        else:
+            p.P_dstate_stride, p.P_r_stride = P.stride()
+            p.Q_r_stride, p.Q_dstate_stride = Q.stride()
+    if gamma is not None:
+        p.gamma = _ptr(gamma)
+        if gamma.dim() == 2:
+            p.gamma_d_stride, p.gamma_dstate_stride = gamma.stride()
+        else:
+            p.gamma_dstate_stride = gamma.stride(0)
     return p
 
 

@@ -18,7 +18,7 @@ def test_library_exports_every_header_function():
                           "mm_abi_version"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 2
+    assert lib.mm_abi_version() == 3
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -102,17 +102,40 @@ def test_binding_checks_mirror_reference():
         ext.fwd(u, u, A, B, B)
     with pytest.raises(RuntimeError):
         ext.fwd(u.to(torch.int32), u, A, B, B)
-    with pytest.raises(NotImplementedError):
-        ext.fwd(u, u, A, B, B, P=A)
+    with pytest.raises(RuntimeError):
+        ext.fwd(u, u, A, B, B, P=torch.zeros(16, 2), Q=torch.zeros(2, 16))
     with pytest.raises(RuntimeError):
         ext.state_update(torch.zeros(1, 4, 16), u[:, :, 0], u[:, :, 0], A, B[:, 0, :, 0], B[:, 0, :, 0])
 
 
-def test_python_api_refuses_out_of_scope_paths():
+def test_python_api_pq_argument_errors():
+    """The argument errors of selective_scan_full_matrix_cuda (ssi.py:266-271, 303-318), raised
+    before anything reaches the GPU."""
     from motif_mamba_amd import selective_scan_fn
     u = torch.zeros(1, 4, 8)
+    A = -torch.ones(4, 16)
+    B = torch.zeros(1, 16, 8)
+    with pytest.raises(ValueError, match="both be provided"):
+        selective_scan_fn(u, u, A, B, B, P=torch.zeros(16, 2))
+    with pytest.raises(ValueError, match="both be provided"):
+        selective_scan_fn(u, u, A, B, B, gamma=torch.zeros(16))
     with pytest.raises(NotImplementedError):
-        selective_scan_fn(u, u, -torch.ones(4, 16), torch.zeros(1, 16, 8), torch.zeros(1, 16, 8), P=torch.zeros(16, 2))
+        selective_scan_fn(u, u, A.to(torch.complex64), B, B, P=torch.zeros(16, 2), Q=torch.zeros(2, 16))
+    with pytest.raises(ValueError, match="CUDA"):
+        selective_scan_fn(u, u, A, B, B, P=torch.zeros(16, 2), Q=torch.zeros(2, 16))
+
+
+def test_scan_fwd_rejects_invalid_pq_params():
+    lib = capi.load()
+    p = _valid_looking_params()
+    p.P = 0x3000
+    assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "P and Q" in lib.mm_last_error().decode()
+    p.Q, p.pq_rank = 0x4000, 9
+    assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "pq_rank" in lib.mm_last_error().decode()
+    p.pq_rank = 2
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(p)) == 0   # the P/Q kernels use no scratch
 
 
 def test_mamba_ssm_import_paths_resolve_to_hip_kernels():
