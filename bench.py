@@ -10,8 +10,10 @@ is the algorithmic HBM throughput of that step (bytes of u, delta, z, B, C, A, D
 and out_z, last_state written, each once) divided by the measured time per step, in GB/s.
 
 The JSON line also carries: ``roofline`` for the forward-scan kernel (HBM bound, 8 TB/s peak),
-``cpu_baseline`` (the CPU oracle timed on the host on a bounded sample of the same workload),
-per-config results for configs 1 and 3 and decode tokens/s for config 4 (unless --quick).
+``roofline_trans`` (the same kernel against the v_exp_f32 issue rate, which binds it), ``cpu_baseline``
+(the CPU oracle timed on the host on a bounded sample of the same workload), per-config results for
+configs 1 and 3, decode tokens/s for config 4 and the MotifMamba P/Q forward on a Mamba-1.4B layer
+(unless --quick).
 Only one GPU is used; --gpus N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -109,6 +111,31 @@ def bench_decode(batch, steps, warmup, torch, sets_max=64):
             "note": "state (batch*5120*16*4 B) fits the 256 MB Infinity Cache; GB/s may exceed HBM peak"}
 
 
+def bench_pq(name, steps, warmup, torch):
+    """Forward of the low-rank coupled scan (selective_scan_fn with P/Q) on a MotifMamba layer."""
+    from motif_mamba_amd import selective_scan_fn
+    from motif_mamba_amd.workloads import PQ_CONFIGS, pq_flops, pq_inputs, scan_bytes, scan_transcendentals
+    c = PQ_CONFIGS[name]
+    inputs = pq_inputs(c, device="cuda")
+
+    def step(i):
+        selective_scan_fn(**inputs)
+
+    ms = _time_loop(step, steps, warmup, torch)
+    in_bytes = 2 if c.dtype in ("bf16", "fp16") else 4
+    nbytes = scan_bytes(c.batch, c.dim, c.seqlen, c.dstate, 1, in_bytes) + 2 * c.dim * c.dstate * c.rank * 4
+    trans = scan_transcendentals(c.batch, c.dim, c.seqlen, c.dstate)
+    flops = pq_flops(c.batch, c.dim, c.seqlen, c.dstate, c.rank)
+    elems = c.batch * c.dim * c.seqlen
+    floor = max(nbytes / (HBM_PEAK_GBS * 1e9), trans / TRANS_PEAK_PER_S)
+    del inputs
+    torch.cuda.empty_cache()
+    return {"shape": [c.batch, c.dim, c.seqlen, c.dstate], "rank": c.rank, "per_dim": c.per_dim, "dtype": c.dtype,
+            "ms": ms, "GB_s": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes, "elements_per_s": elems / (ms * 1e-3),
+            "trans_per_s": trans / (ms * 1e-3), "coupling_TFLOP_s": flops / (ms * 1e-3) / 1e12,
+            "t_floor_us": floor * 1e6, "floor_frac": floor / (ms * 1e-3)}
+
+
 def cpu_baseline(torch, seconds_target=15.0):
     """The CPU oracle (torch restatement of selective_scan_ref) on a bounded sample of config 2:
     one batch row and a slice of channels at the full L = 4096, scaled to GB/s of the config's
@@ -155,6 +182,9 @@ def main():
     ap.add_argument("--copy-ref", action="store_true",
                     help="also run three 1 GiB device-to-device copies: the reference that scales the "
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
+    ap.add_argument("--only", default=None,
+                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b) "
+                         "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -166,6 +196,17 @@ def main():
     _native.ext()  # the HIP library must be present: no fallback path exists
     torch.cuda.init()
     _log(f"device: {torch.cuda.get_device_name(0)}")
+
+    if args.only:
+        name = args.only
+        if name.startswith("cfg4_b"):
+            res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
+        elif name.startswith("pq_"):
+            res = bench_pq(name, args.steps, args.warmup, torch)
+        else:
+            res = bench_scan(name, args.steps, args.warmup, torch, rotate=2 if name == "cfg1" else 1)
+        print(json.dumps({"config": name, **res}), flush=True)
+        return
 
     _log("config 2 (headline)")
     head = bench_scan("cfg2", args.steps, args.warmup, torch)
@@ -187,6 +228,8 @@ def main():
         for b in (1, 64, 256):
             _log(f"config 4 decode batch {b}")
             extra[f"cfg4_b{b}"] = bench_decode(b, 1024, 16, torch)
+        _log("MotifMamba P/Q forward (Mamba-1.4B layer, rank 2, per-channel P/Q)")
+        extra["pq_1p4b"] = bench_pq("pq_1p4b", max(5, args.steps), 2, torch)
     cpu = None
     if not args.no_cpu:
         _log("CPU baseline (oracle on a bounded sample)")
