@@ -1,7 +1,7 @@
 /*
  * mm_scan.h -- C ABI of the MI355X (gfx950) selective-scan library `libmm_scan.so`.
  *
- * Two entry points replace the two native calls on the Mamba selective-scan hot path:
+ * Three entry points replace the native calls on the Mamba selective-scan hot path:
  *
  *   mm_scan_fwd      replaces the pybind call `selective_scan_cuda.fwd(u, delta, A, B, C, D, z,
  *                    delta_bias, P, Q, gamma, delta_softplus)` bound at
@@ -12,6 +12,10 @@
  *                    selective_scan_interface.py:237-350). The parameter block mirrors
  *                    SSMParamsBase (selective_scan.h:26-82) but with int64 element strides
  *                    instead of uint32.
+ *
+ *   mm_scan_bwd      replaces `selective_scan_cuda.bwd(u, delta, A, B, C, D, z, delta_bias, P, Q,
+ *                    gamma, dout, x, out, dz, dP_out, dQ_out, delta_softplus, recompute_out_z)`
+ *                    (selective_scan.cpp:415-612, pybind :628-637) for real A without P/Q.
  *
  *   mm_state_update  replaces `selective_state_update(state, x, dt, A, B, C, D, z, dt_bias,
  *                    dt_softplus)` as called at mamba_ssm/modules/mamba_simplemotif.py:397-399
@@ -41,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 3
+#define MM_SCAN_ABI_VERSION 4
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -127,6 +131,69 @@ typedef struct mm_scan_fwd_params {
     int64_t gamma_d_stride, gamma_dstate_stride;
 } mm_scan_fwd_params;
 
+/* Backward of the diagonal forward scan: the gradients of every input for a given gradient `dout`
+ * of the returned output (out_z when z is given, else out), as selective_scan_cuda.bwd computes them
+ * (selective_scan.cpp:415-612, selective_scan_bwd_kernel.cuh:405-880), for real A without P/Q:
+ *   g_t   = dout_t * silu(z_t)                      dz_t = dout_t * out_t * silu'(z_t)
+ *   gh_t  = C_t g_t + exp(delta'_{t+1} A) gh_{t+1}  (reverse scan per state, gh after L = 0)
+ *   du_t  = D g_t + delta'_t sum_n gh_t B_t          ddelta'_t = sum_n gh_t (u_t B_t + A (h_t - delta'_t u_t B_t))
+ *   dB_t += gh_t delta'_t u_t ;  dC_t += g_t h_t ;   dA += gh_t delta'_t (h_t - delta'_t u_t B_t)
+ *   ddelta_t = ddelta'_t * sigmoid(delta_t + bias) with softplus (1 past the threshold 20)
+ *   dD += g_t u_t ;  ddelta_bias += ddelta_t
+ * The forward states are recomputed from h_{-1} = 0 (the chunk states of the forward are not
+ * needed). dA, dB, dC, dD and ddelta_bias are sums over rows and steps: the call overwrites them
+ * (it clears them on `stream` first) and accumulates in float32 with device atomics, so their
+ * low-order bits depend on the order in which workgroups finish, as in the reference. */
+typedef struct mm_scan_bwd_params {
+    int64_t batch, dim, seqlen, dstate, n_groups;
+    mm_dtype itype;          /* dtype of u, delta, z, out, dout, du, ddelta, dz and variable B/C */
+    int32_t is_variable_B;
+    int32_t is_variable_C;
+    int32_t delta_softplus;
+
+    const void *u;           /* (batch, dim, seqlen) */
+    const void *delta;       /* (batch, dim, seqlen) */
+    const float *A;          /* (dim, dstate) */
+    const void *B;           /* as in mm_scan_fwd_params */
+    const void *C;
+    const float *D;          /* (dim,) or NULL */
+    const void *z;           /* (batch, dim, seqlen) or NULL */
+    const float *delta_bias; /* (dim,) or NULL */
+    const void *dout;        /* (batch, dim, seqlen) */
+    const void *out;         /* (batch, dim, seqlen) pre-gate forward output; required iff z != NULL */
+
+    void *du;                /* (batch, dim, seqlen) */
+    void *ddelta;            /* (batch, dim, seqlen) */
+    void *dz;                /* (batch, dim, seqlen); required iff z != NULL */
+    void *out_z;             /* (batch, dim, seqlen) out * silu(z) recomputed, or NULL */
+    float *dA;               /* (dim, dstate) */
+    float *dB;               /* float32, the shape of B: (batch, n_groups, dstate, seqlen) or (dim, dstate) */
+    float *dC;               /* float32, the shape of C */
+    float *dD;               /* (dim,); required iff D != NULL */
+    float *ddelta_bias;      /* (dim,); required iff delta_bias != NULL */
+
+    int64_t u_batch_stride, u_d_stride;
+    int64_t delta_batch_stride, delta_d_stride;
+    int64_t z_batch_stride, z_d_stride;
+    int64_t out_batch_stride, out_d_stride;
+    int64_t dout_batch_stride, dout_d_stride;
+    int64_t du_batch_stride, du_d_stride;
+    int64_t ddelta_batch_stride, ddelta_d_stride;
+    int64_t dz_batch_stride, dz_d_stride;
+    int64_t out_z_batch_stride, out_z_d_stride;
+    int64_t A_d_stride, A_dstate_stride;
+    int64_t B_batch_stride, B_group_stride, B_dstate_stride, B_d_stride;
+    int64_t C_batch_stride, C_group_stride, C_dstate_stride, C_d_stride;
+    int64_t dA_d_stride, dA_dstate_stride;
+    int64_t dB_batch_stride, dB_group_stride, dB_dstate_stride, dB_d_stride;
+    int64_t dC_batch_stride, dC_group_stride, dC_dstate_stride, dC_d_stride;
+
+    /* Device scratch of mm_scan_bwd_workspace_size() bytes (16-byte aligned), owned by the caller:
+     * the recomputed forward states at every 32-step tile start. Required. */
+    void *workspace;
+    int64_t workspace_bytes;
+} mm_scan_bwd_params;
+
 /* Single-token decode update, in place on `state`:
  *   dt' = softplus(dt + dt_bias) (softplus only when dt_softplus != 0)
  *   state[b,d,n] = state[b,d,n] * exp(dt' * A[d,n]) + dt' * B[b,g(d),n] * x[b,d]
@@ -167,6 +234,14 @@ int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream);
  * returns 0 for a request mm_scan_fwd would reject. No counterpart in the reference (its forward
  * allocates nothing beyond the outputs, selective_scan.cpp:383-389). */
 int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params);
+
+/* Backward scan. Replaces selective_scan_cuda.bwd (selective_scan.cpp:415-612, pybind :628-637). */
+int mm_scan_bwd(const mm_scan_bwd_params *params, void *stream);
+
+/* Bytes of `workspace` mm_scan_bwd needs for `params` (0 for a request it would reject or that has
+ * nothing to do). Reads only sizes. No counterpart in the reference (its backward recomputes each
+ * 2048-step chunk inside one thread block). */
+int64_t mm_scan_bwd_workspace_size(const mm_scan_bwd_params *params);
 
 /* Decode step. Replaces selective_state_update (call site mamba_simplemotif.py:397-399). */
 int mm_state_update(const mm_state_update_params *params, void *stream);

@@ -34,4 +34,10 @@ template <typename T>
 int launch_pq(const mm_scan_fwd_params &p, hipStream_t stream);
 int64_t pq_tiled_lanes_per_row(const mm_scan_fwd_params &p);
 
+// Backward (mm_scan_bwd.hip): clears the accumulated gradients and launches the backward kernels
+// on `stream`; bwd_workspace_bytes() is the checkpoint scratch it needs.
+template <typename T>
+int launch_bwd(const mm_scan_bwd_params &p, hipStream_t stream);
+int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p);
+
 }  // namespace mm

@@ -4,6 +4,8 @@
 //   mm_scan_fwd      -- replaces selective_scan_cuda.fwd (reference csrc/selective_scan/
 //                       selective_scan.cpp:270-413) for real A; requests with P/Q go to
 //                       mm_scan_pq.hip.
+//   mm_scan_bwd      -- replaces selective_scan_cuda.bwd (selective_scan.cpp:415-612); kernels in
+//                       mm_scan_bwd.hip.
 //   mm_state_update  -- replaces the upstream selective_state_update called at
 //                       mamba_ssm/modules/mamba_simplemotif.py:397-399.
 //
@@ -397,6 +399,37 @@ int dispatch_fwd(const mm_scan_fwd_params &p, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------------------------------------
+int validate_bwd(const mm_scan_bwd_params *p) {
+    if (!p) return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: params is NULL");
+    if (p->itype != MM_FLOAT32 && p->itype != MM_FLOAT16 && p->itype != MM_BFLOAT16)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: unknown itype %d", int(p->itype));
+    if (p->batch < 0 || p->dim < 0 || p->seqlen < 0)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: negative size");
+    if (p->dstate < 1 || p->dstate > MM_SCAN_MAX_DSTATE)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: selective_scan only supports state dimension <= %d (got %lld)",
+                    MM_SCAN_MAX_DSTATE, (long long)p->dstate);
+    if (p->n_groups < 1 || (p->dim > 0 && p->dim % p->n_groups != 0))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: dim (%lld) must be a multiple of n_groups (%lld)",
+                    (long long)p->dim, (long long)p->n_groups);
+    if (p->batch == 0 || p->dim == 0) return MM_OK;
+    if (!p->u || !p->delta || !p->A || !p->B || !p->C || !p->dout)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: u, delta, A, B, C and dout are required");
+    if (!p->du || !p->ddelta || !p->dA || !p->dB || !p->dC)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: du, ddelta, dA, dB and dC are required");
+    if (p->z && (!p->out || !p->dz))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: out and dz are required when z is given");
+    if ((p->D == nullptr) != (p->dD == nullptr))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: dD is required exactly when D is given");
+    if ((p->delta_bias == nullptr) != (p->ddelta_bias == nullptr))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: ddelta_bias is required exactly when delta_bias is given");
+    const int64_t need = mm::bwd_workspace_bytes(*p);
+    if (p->seqlen > 0 && (!p->workspace || p->workspace_bytes < need || reinterpret_cast<uintptr_t>(p->workspace) % 16))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: needs a 16-byte aligned workspace of %lld bytes (got %lld)",
+                    (long long)need, (long long)p->workspace_bytes);
+    return MM_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
 int validate_su(const mm_state_update_params *p) {
     if (!p) return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: params is NULL");
     if (p->itype != MM_FLOAT32 && p->itype != MM_FLOAT16 && p->itype != MM_BFLOAT16)
@@ -473,6 +506,26 @@ int mm_state_update(const mm_state_update_params *params, void *stream) {
         case MM_FLOAT16: return dispatch_su<mm::f16_t>(p, s);
         default: return dispatch_su<mm::bf16_t>(p, s);
     }
+}
+
+int mm_scan_bwd(const mm_scan_bwd_params *params, void *stream) {
+    int rc = validate_bwd(params);
+    if (rc != MM_OK) return rc;
+    const mm_scan_bwd_params &p = *params;
+    if (p.batch == 0 || p.dim == 0) return MM_OK;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (p.itype) {
+        case MM_FLOAT32: return mm::launch_bwd<float>(p, s);
+        case MM_FLOAT16: return mm::launch_bwd<mm::f16_t>(p, s);
+        default: return mm::launch_bwd<mm::bf16_t>(p, s);
+    }
+}
+
+int64_t mm_scan_bwd_workspace_size(const mm_scan_bwd_params *params) {
+    if (!params || params->batch < 0 || params->dim < 0 || params->seqlen < 0 || params->dstate < 1 ||
+        params->dstate > MM_SCAN_MAX_DSTATE)
+        return 0;
+    return mm::bwd_workspace_bytes(*params);
 }
 
 int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params) {

@@ -297,6 +297,120 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
     return {main};
 }
 
+
+// selective_scan_cuda.bwd (selective_scan.cpp:415-612): [du, ddelta, dA, dB, dC, dD, ddelta_bias,
+// dz?, out_z?]. x (the forward's chunk states) is checked like the reference but not read: the
+// backward recomputes the forward states itself. P/Q are not part of this backward.
+std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A, const at::Tensor &B,
+                            const at::Tensor &C, const c10::optional<at::Tensor> &D_,
+                            const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &delta_bias_,
+                            const c10::optional<at::Tensor> &P_, const c10::optional<at::Tensor> &Q_,
+                            const c10::optional<at::Tensor> &gamma_, const at::Tensor &dout,
+                            const c10::optional<at::Tensor> &x_, const c10::optional<at::Tensor> &out_,
+                            c10::optional<at::Tensor> dz_, const c10::optional<at::Tensor> &dP_out_,
+                            const c10::optional<at::Tensor> &dQ_out_, bool delta_softplus, bool recompute_out_z) {
+    if (P_.has_value() || Q_.has_value() || gamma_.has_value() || dP_out_.has_value() || dQ_out_.has_value()) {
+        throw c10::NotImplementedError({__func__, __FILE__, uint32_t(__LINE__)},
+                                       "the P/Q backward is not part of the MI355X selective scan");
+    }
+    FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
+    const mm_scan_fwd_params &f = s.p;
+    TORCH_CHECK(dout.scalar_type() == u.scalar_type());
+    TORCH_CHECK(dout.is_cuda());
+    TORCH_CHECK(dout.stride(-1) == 1 || dout.size(-1) == 1);
+    CHECK_SHAPE(dout, f.batch, f.dim, f.seqlen);
+    at::Tensor out, dz, out_z;
+    const bool has_z = z_.has_value();
+    if (has_z) {
+        TORCH_CHECK(out_.has_value());
+        out = out_.value();
+        TORCH_CHECK(out.scalar_type() == u.scalar_type());
+        TORCH_CHECK(out.is_cuda());
+        TORCH_CHECK(out.stride(-1) == 1 || out.size(-1) == 1);
+        CHECK_SHAPE(out, f.batch, f.dim, f.seqlen);
+        if (dz_.has_value()) {
+            dz = dz_.value();
+            TORCH_CHECK(dz.scalar_type() == u.scalar_type());
+            TORCH_CHECK(dz.is_cuda());
+            TORCH_CHECK(dz.stride(-1) == 1 || dz.size(-1) == 1);
+            CHECK_SHAPE(dz, f.batch, f.dim, f.seqlen);
+        } else {
+            dz = torch::empty_like(z_.value());
+        }
+        if (recompute_out_z) out_z = torch::empty_like(out);
+    }
+    if (s.n_chunks > 1) TORCH_CHECK(x_.has_value());
+    if (x_.has_value()) {
+        const at::Tensor &x = x_.value();
+        TORCH_CHECK(x.scalar_type() == A.scalar_type());
+        TORCH_CHECK(x.is_cuda());
+        TORCH_CHECK(x.is_contiguous());
+        CHECK_SHAPE(x, f.batch, f.dim, s.n_chunks, 2 * f.dstate);
+    }
+    at::Tensor du = torch::empty_like(u);
+    at::Tensor ddelta = torch::empty_like(delta);
+    at::Tensor dA = torch::empty_like(A);
+    at::Tensor dB = torch::empty(B.sizes(), B.options().dtype(at::ScalarType::Float));
+    at::Tensor dC = torch::empty(C.sizes(), C.options().dtype(at::ScalarType::Float));
+    at::Tensor dD, ddelta_bias;
+    if (D_.has_value()) dD = torch::empty_like(D_.value());
+    if (delta_bias_.has_value()) ddelta_bias = torch::empty_like(delta_bias_.value());
+
+    mm_scan_bwd_params p;
+    std::memset(&p, 0, sizeof(p));
+    p.batch = f.batch; p.dim = f.dim; p.seqlen = f.seqlen; p.dstate = f.dstate; p.n_groups = f.n_groups;
+    p.itype = f.itype; p.is_variable_B = f.is_variable_B; p.is_variable_C = f.is_variable_C;
+    p.delta_softplus = f.delta_softplus;
+    p.u = f.u; p.delta = f.delta; p.A = f.A; p.B = f.B; p.C = f.C; p.D = f.D; p.z = f.z; p.delta_bias = f.delta_bias;
+    p.u_batch_stride = f.u_batch_stride; p.u_d_stride = f.u_d_stride;
+    p.delta_batch_stride = f.delta_batch_stride; p.delta_d_stride = f.delta_d_stride;
+    p.z_batch_stride = f.z_batch_stride; p.z_d_stride = f.z_d_stride;
+    p.A_d_stride = f.A_d_stride; p.A_dstate_stride = f.A_dstate_stride;
+    p.B_batch_stride = f.B_batch_stride; p.B_group_stride = f.B_group_stride;
+    p.B_dstate_stride = f.B_dstate_stride; p.B_d_stride = f.B_d_stride;
+    p.C_batch_stride = f.C_batch_stride; p.C_group_stride = f.C_group_stride;
+    p.C_dstate_stride = f.C_dstate_stride; p.C_d_stride = f.C_d_stride;
+    p.dout = dout.data_ptr();
+    p.dout_batch_stride = dout.stride(0); p.dout_d_stride = dout.stride(1);
+    if (has_z) {
+        p.out = out.data_ptr(); p.out_batch_stride = out.stride(0); p.out_d_stride = out.stride(1);
+        p.dz = dz.data_ptr(); p.dz_batch_stride = dz.stride(0); p.dz_d_stride = dz.stride(1);
+        if (recompute_out_z) {
+            p.out_z = out_z.data_ptr(); p.out_z_batch_stride = out_z.stride(0); p.out_z_d_stride = out_z.stride(1);
+        }
+    }
+    p.du = du.data_ptr(); p.du_batch_stride = du.stride(0); p.du_d_stride = du.stride(1);
+    p.ddelta = ddelta.data_ptr(); p.ddelta_batch_stride = ddelta.stride(0); p.ddelta_d_stride = ddelta.stride(1);
+    p.dA = dA.data_ptr<float>(); p.dA_d_stride = dA.stride(0); p.dA_dstate_stride = dA.stride(1);
+    p.dB = dB.data_ptr<float>();
+    p.dC = dC.data_ptr<float>();
+    if (f.is_variable_B) {
+        p.dB_batch_stride = dB.stride(0); p.dB_group_stride = dB.stride(1); p.dB_dstate_stride = dB.stride(2);
+    } else {
+        p.dB_d_stride = dB.stride(0); p.dB_dstate_stride = dB.stride(1);
+    }
+    if (f.is_variable_C) {
+        p.dC_batch_stride = dC.stride(0); p.dC_group_stride = dC.stride(1); p.dC_dstate_stride = dC.stride(2);
+    } else {
+        p.dC_d_stride = dC.stride(0); p.dC_dstate_stride = dC.stride(1);
+    }
+    if (D_.has_value()) p.dD = dD.data_ptr<float>();
+    if (delta_bias_.has_value()) p.ddelta_bias = ddelta_bias.data_ptr<float>();
+    const c10::DeviceGuard device_guard{u.device()};
+    at::Tensor ws;
+    const int64_t ws_bytes = mm_scan_bwd_workspace_size(&p);
+    if (ws_bytes > 0) {
+        ws = torch::empty({ws_bytes}, u.options().dtype(at::ScalarType::Byte));
+        p.workspace = ws.data_ptr();
+        p.workspace_bytes = ws_bytes;
+    }
+    check_rc(mm_scan_bwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_bwd");
+    std::vector<at::Tensor> result = {du, ddelta, dA, dB.to(B.scalar_type()), dC.to(C.scalar_type()), dD, ddelta_bias};
+    if (has_z) result.push_back(dz);
+    if (recompute_out_z) result.push_back(out_z);
+    return result;
+}
+
 at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::Tensor &dt, const at::Tensor &A,
                         const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                         const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &dt_bias_,
@@ -400,6 +514,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           pybind11::arg("delta_bias") = pybind11::none(), pybind11::arg("P") = pybind11::none(),
           pybind11::arg("Q") = pybind11::none(), pybind11::arg("gamma") = pybind11::none(),
           pybind11::arg("delta_softplus") = false);
+    m.def("bwd", &bwd, "Selective scan backward (reference-compatible outputs)",
+          pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
+          pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
+          pybind11::arg("delta_bias") = pybind11::none(), pybind11::arg("P") = pybind11::none(),
+          pybind11::arg("Q") = pybind11::none(), pybind11::arg("gamma") = pybind11::none(), pybind11::arg("dout"),
+          pybind11::arg("x"), pybind11::arg("out"), pybind11::arg("dz"), pybind11::arg("dP_out") = pybind11::none(),
+          pybind11::arg("dQ_out") = pybind11::none(), pybind11::arg("delta_softplus"),
+          pybind11::arg("recompute_out_z"));
     m.def("fwd_infer", &fwd_infer, "Selective scan forward, inference outputs [out_z|out, last_state?]",
           pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
           pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),

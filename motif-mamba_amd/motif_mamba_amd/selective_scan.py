@@ -17,7 +17,11 @@ the same function, and so does this build's single kernel. Argument errors are t
 (ValueError for P without Q, mismatched P/Q shapes or non-CUDA tensors). gamma is validated
 and, as in both reference paths, not used.
 
-Differences (all raise instead of computing something else): the backward pass and complex A are
+``SelectiveScanFn.backward`` (ssi.py:63-91) runs the gfx950 backward (``selective_scan_cuda.bwd``
+equivalent); with gradients required, the forward saves the reference's tensors (u, delta, A, B,
+C, D, [z], delta_bias, x, [out]); without, it writes only what it returns.
+
+Differences (all raise instead of computing something else): the P/Q backward and complex A are
 not part of this build.
 """
 from __future__ import annotations
@@ -47,18 +51,52 @@ class SelectiveScanFn(torch.autograd.Function):
             z = z.contiguous()
         if B.dim() == 3:
             B = rearrange(B, "b dstate l -> b 1 dstate l")
+            ctx.squeeze_B = True
         if C.dim() == 3:
             C = rearrange(C, "b dstate l -> b 1 dstate l")
-        res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
-                              delta_softplus=delta_softplus, return_last_state=return_last_state)
-        if return_last_state:
-            return res[0], res[1]
-        return res[0]
+            ctx.squeeze_C = True
+        if not any(ctx.needs_input_grad[:8]):
+            # Inference: only what is returned is written (no pre-gate out, no chunk states).
+            res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
+                                  delta_softplus=delta_softplus, return_last_state=return_last_state)
+            if return_last_state:
+                return res[0], res[1]
+            return res[0]
+        # Training: the reference's outputs and saved tensors (ssi.py:47-61).
+        out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, None, None, None, delta_softplus)
+        ctx.delta_softplus = delta_softplus
+        ctx.has_z = z is not None
+        last_state = x[:, :, -1, 1::2]
+        if not ctx.has_z:
+            ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, x)
+            return out if not return_last_state else (out, last_state)
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, x, out)
+        out_z = rest[0]
+        return out_z if not return_last_state else (out_z, last_state)
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(
-            "selective_scan backward is not implemented by the MI355X build (forward and decode only)")
+    def backward(ctx, dout, *args):
+        """ssi.py:63-91: the gradient of last_state is not propagated, as in the reference."""
+        if not ctx.has_z:
+            u, delta, A, B, C, D, delta_bias, x = ctx.saved_tensors
+            z = None
+            out = None
+        else:
+            u, delta, A, B, C, D, z, delta_bias, x, out = ctx.saved_tensors
+        if dout.stride(-1) != 1:
+            dout = dout.contiguous()
+        du, ddelta, dA, dB, dC, dD, ddelta_bias, *rest = ext().bwd(
+            u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, dout=dout, x=x, out=out, dz=None,
+            delta_softplus=ctx.delta_softplus, recompute_out_z=False)
+        dz = rest[0] if ctx.has_z else None
+        dB = dB.squeeze(1) if getattr(ctx, "squeeze_B", False) else dB
+        dC = dC.squeeze(1) if getattr(ctx, "squeeze_C", False) else dC
+        return (du, ddelta, dA, dB, dC,
+                dD if D is not None else None,
+                dz,
+                ddelta_bias if delta_bias is not None else None,
+                None,
+                None)
 
 
 class SelectiveScanPQFn(torch.autograd.Function):

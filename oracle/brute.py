@@ -113,3 +113,92 @@ def scan_pq_brute(u, delta, A, B, C, P, Q, D=None, z=None, delta_bias=None, delt
                 if t == L - 1:
                     last[b][d] = h
     return out, outz, last
+
+
+def scan_bwd_brute(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_softplus=False,
+                   b_kind="3d", c_kind="3d"):
+    """Float64 reverse-mode adjoint of the selective scan written out as recurrences (the
+    computation of selective_scan_bwd_kernel.cuh:405-880), independent of autograd:
+
+      g_t  = dout_t * silu(z_t)                (z given; dz_t = dout_t * out_t * silu'(z_t))
+      gh_t = C_t g_t + a_{t+1} gh_{t+1},  gh_L = 0              (reverse scan, per state)
+      dC_t += g_t h_t ; dB_t += gh_t dt_t u_t ; du_t = D g_t + dt_t sum_n gh_t B_t
+      ddt_t = sum_n gh_t (u_t B_t + A (a_t h_{t-1})) ; dA += gh_t dt_t a_t h_{t-1}
+      ddelta_t = ddt_t * sigmoid(delta_t + bias) (softplus; 1 past the threshold 20)
+      dD += g_t u_t ; ddelta_bias += ddelta_t
+
+    Returns a dict of nested lists (du, ddelta, dA, dB, dC, dD, ddelta_bias, dz)."""
+    batch, dim, L, N = len(u), len(u[0]), len(u[0][0]), len(A[0])
+
+    def zeros_like_bc(X, kind):
+        if kind == "const":
+            return [[0.0] * N for _ in range(dim)]
+        if kind == "3d":
+            return [[[0.0] * L for _ in range(N)] for _ in range(batch)]
+        G = len(X[0])
+        return [[[[0.0] * L for _ in range(N)] for _ in range(G)] for _ in range(batch)]
+
+    def add_bc(acc, kind, b, d, n, t, v):
+        if kind == "const":
+            acc[d][n] += v
+        elif kind == "3d":
+            acc[b][n][t] += v
+        else:
+            G = len(acc[b])
+            acc[b][d // (dim // G)][n][t] += v
+
+    du = [[[0.0] * L for _ in range(dim)] for _ in range(batch)]
+    ddelta = [[[0.0] * L for _ in range(dim)] for _ in range(batch)]
+    dz = [[[0.0] * L for _ in range(dim)] for _ in range(batch)] if z is not None else None
+    dA = [[0.0] * N for _ in range(dim)]
+    dB = zeros_like_bc(B, b_kind)
+    dC = zeros_like_bc(C, c_kind)
+    dD = [0.0] * dim if D is not None else None
+    dbias = [0.0] * dim if delta_bias is not None else None
+    for b in range(batch):
+        for d in range(dim):
+            raw = [float(delta[b][d][t]) + (float(delta_bias[d]) if delta_bias is not None else 0.0) for t in range(L)]
+            dts = [softplus_f64(x) if delta_softplus else x for x in raw]
+            uu = [float(u[b][d][t]) for t in range(L)]
+            a = [[math.exp(dts[t] * float(A[d][n])) for n in range(N)] for t in range(L)]
+            Bv = [[float(_b_at(B, b, d, n, t, dim, b_kind)) for n in range(N)] for t in range(L)]
+            Cv = [[float(_b_at(C, b, d, n, t, dim, c_kind)) for n in range(N)] for t in range(L)]
+            h = [[0.0] * N for _ in range(L)]
+            prev = [0.0] * N
+            for t in range(L):
+                for n in range(N):
+                    h[t][n] = a[t][n] * prev[n] + dts[t] * uu[t] * Bv[t][n]
+                prev = h[t]
+            g = []
+            for t in range(L):
+                go = float(dout[b][d][t])
+                if z is not None:
+                    zz = float(z[b][d][t])
+                    sg = 1.0 / (1.0 + math.exp(-zz))
+                    y = sum(h[t][n] * Cv[t][n] for n in range(N)) + (float(D[d]) * uu[t] if D is not None else 0.0)
+                    dz[b][d][t] = go * y * sg * (1.0 + zz * (1.0 - sg))
+                    go = go * zz * sg
+                g.append(go)
+            gh = [0.0] * N
+            for t in range(L - 1, -1, -1):
+                for n in range(N):
+                    gh[n] = Cv[t][n] * g[t] + (a[t + 1][n] * gh[n] if t + 1 < L else 0.0)
+                hprev = h[t - 1] if t > 0 else [0.0] * N
+                ddt = 0.0
+                s_du = 0.0
+                for n in range(N):
+                    ah = a[t][n] * hprev[n]
+                    add_bc(dC, c_kind, b, d, n, t, g[t] * h[t][n])
+                    add_bc(dB, b_kind, b, d, n, t, gh[n] * dts[t] * uu[t])
+                    s_du += gh[n] * Bv[t][n]
+                    ddt += gh[n] * (uu[t] * Bv[t][n] + float(A[d][n]) * ah)
+                    dA[d][n] += gh[n] * dts[t] * ah
+                du[b][d][t] = dts[t] * s_du + (float(D[d]) * g[t] if D is not None else 0.0)
+                if delta_softplus and raw[t] <= 20.0:
+                    ddt *= 1.0 / (1.0 + math.exp(-raw[t]))
+                ddelta[b][d][t] = ddt
+                if D is not None:
+                    dD[d] += g[t] * uu[t]
+                if dbias is not None:
+                    dbias[d] += ddt
+    return {"du": du, "ddelta": ddelta, "dA": dA, "dB": dB, "dC": dC, "dD": dD, "ddelta_bias": dbias, "dz": dz}

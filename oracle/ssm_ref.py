@@ -47,24 +47,27 @@ def _softplus_f32(x: torch.Tensor) -> torch.Tensor:
 
 
 def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                       return_last_state=False):
+                       return_last_state=False, compute_dtype=torch.float32):
     """CPU restatement of ssi.py:353-451 (real A, no P/Q). Shapes as in the reference:
     u, delta, z: (batch, dim, L); A: (dim, N); B, C: (dim, N) | (batch, N, L) | (batch, G, N, L).
+    The reference upcasts to float32 (``.float()``); ``compute_dtype=torch.float64`` evaluates the
+    same op sequence in float64 (used for exact gradients in precision checks).
     """
     if A.is_complex():
         raise NotImplementedError("complex A is out of scope")
     in_dtype = u.dtype
-    u32 = u.float()
-    dt = delta.float()
+    u32 = u.to(compute_dtype)
+    dt = delta.to(compute_dtype)
     if delta_bias is not None:
-        dt = dt + delta_bias[..., None].float()
+        dt = dt + delta_bias[..., None].to(compute_dtype)
     if delta_softplus:
         dt = _softplus_f32(dt)
+    A = A.to(compute_dtype)
     nbatch, ndim, nstate = u.shape[0], A.shape[0], A.shape[1]
     var_B = B.dim() >= 3
     var_C = C.dim() >= 3
-    Bf = B.float()
-    Cf = C.float()
+    Bf = B.to(compute_dtype)
+    Cf = C.to(compute_dtype)
     decay = torch.exp(torch.einsum("bdl,dn->bdln", dt, A))
     if not var_B:
         drive = torch.einsum("bdl,dn,bdl->bdln", dt, Bf, u32)
@@ -86,7 +89,7 @@ def selective_scan_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta
         else:
             ys.append(torch.einsum("bdn,bdn->bd", state, Cf[:, :, :, t]))
     y = torch.stack(ys, dim=2)
-    out = y if D is None else y + u32 * rearrange(D, "d -> d 1")
+    out = y if D is None else y + u32 * rearrange(D.to(compute_dtype), "d -> d 1")
     if z is not None:
         out = out * F.silu(z)
     out = out.to(dtype=in_dtype)
@@ -292,3 +295,53 @@ def selective_scan_pq_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, de
         out = out * F.silu(z.float())
     out = out.to(dtype=dtype_in)
     return out if not return_last_state else (out, x)
+
+
+def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_softplus=False,
+                           dtype=None):
+    """Gradients of ``selective_scan_ref`` (the restatement of ssi.py:353-451) with respect to every
+    input, by torch autograd -- the function the reference's ``selective_scan_cuda.bwd``
+    (csrc/selective_scan/selective_scan.cpp:415-612, kernel selective_scan_bwd_kernel.cuh:405-880)
+    computes, returned in its output order and shapes: du, ddelta (input dtype), dA, dB, dC
+    (float32, cast to B's / C's dtype as selective_scan.cpp:609 does), dD, ddelta_bias (float32 or
+    None) and dz (input dtype or None). ``dout`` is the gradient of the returned output (out_z when
+    z is given, else out).
+
+    ``dtype`` (default: float32) is the precision of the differentiated computation; float64
+    gives the exact gradient of the same function for precision checks."""
+    wt = torch.float32 if dtype is None else dtype
+    leaves = {}
+
+    def leaf(name, t, cast=True):
+        if t is None:
+            return None
+        v = t.detach().to(wt) if cast else t.detach().clone()
+        v.requires_grad_(True)
+        leaves[name] = v
+        return v
+
+    # float32: the leaves keep the caller's dtypes (the forward upcasts as the reference does);
+    # float64: every leaf is float64 and so is the computation.
+    cast = dtype is not None
+    uu = leaf("u", u, cast)
+    dd = leaf("delta", delta, cast)
+    AA = leaf("A", A, cast)
+    BB = leaf("B", B, cast)
+    CC = leaf("C", C, cast)
+    DD = leaf("D", D, cast)
+    zz = leaf("z", z, cast)
+    bb = leaf("delta_bias", delta_bias, cast)
+    out = selective_scan_ref(uu, dd, AA, BB, CC, DD, zz, bb, delta_softplus, compute_dtype=wt)
+    out.backward(dout.to(out.dtype))
+    g = {k: v.grad for k, v in leaves.items()}
+    res = {
+        "du": g["u"].to(u.dtype) if dtype is None else g["u"],
+        "ddelta": g["delta"].to(delta.dtype) if dtype is None else g["delta"],
+        "dA": g["A"],
+        "dB": g["B"].to(B.dtype) if dtype is None else g["B"],
+        "dC": g["C"].to(C.dtype) if dtype is None else g["C"],
+        "dD": g.get("D"),
+        "ddelta_bias": g.get("delta_bias"),
+        "dz": (g["z"].to(z.dtype) if dtype is None else g["z"]) if z is not None else None,
+    }
+    return res

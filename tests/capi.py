@@ -37,6 +37,31 @@ class ScanFwdParams(ctypes.Structure):
                 ("gamma_d_stride", i64), ("gamma_dstate_stride", i64)]
 
 
+class ScanBwdParams(ctypes.Structure):
+    _fields_ = [("batch", i64), ("dim", i64), ("seqlen", i64), ("dstate", i64), ("n_groups", i64),
+                ("itype", i32), ("is_variable_B", i32), ("is_variable_C", i32), ("delta_softplus", i32),
+                ("u", vp), ("delta", vp), ("A", vp), ("B", vp), ("C", vp), ("D", vp), ("z", vp),
+                ("delta_bias", vp), ("dout", vp), ("out", vp),
+                ("du", vp), ("ddelta", vp), ("dz", vp), ("out_z", vp), ("dA", vp), ("dB", vp), ("dC", vp),
+                ("dD", vp), ("ddelta_bias", vp),
+                ("u_batch_stride", i64), ("u_d_stride", i64),
+                ("delta_batch_stride", i64), ("delta_d_stride", i64),
+                ("z_batch_stride", i64), ("z_d_stride", i64),
+                ("out_batch_stride", i64), ("out_d_stride", i64),
+                ("dout_batch_stride", i64), ("dout_d_stride", i64),
+                ("du_batch_stride", i64), ("du_d_stride", i64),
+                ("ddelta_batch_stride", i64), ("ddelta_d_stride", i64),
+                ("dz_batch_stride", i64), ("dz_d_stride", i64),
+                ("out_z_batch_stride", i64), ("out_z_d_stride", i64),
+                ("A_d_stride", i64), ("A_dstate_stride", i64),
+                ("B_batch_stride", i64), ("B_group_stride", i64), ("B_dstate_stride", i64), ("B_d_stride", i64),
+                ("C_batch_stride", i64), ("C_group_stride", i64), ("C_dstate_stride", i64), ("C_d_stride", i64),
+                ("dA_d_stride", i64), ("dA_dstate_stride", i64),
+                ("dB_batch_stride", i64), ("dB_group_stride", i64), ("dB_dstate_stride", i64), ("dB_d_stride", i64),
+                ("dC_batch_stride", i64), ("dC_group_stride", i64), ("dC_dstate_stride", i64), ("dC_d_stride", i64),
+                ("workspace", vp), ("workspace_bytes", i64)]
+
+
 class StateUpdateParams(ctypes.Structure):
     _fields_ = [("batch", i64), ("dim", i64), ("dstate", i64), ("n_groups", i64),
                 ("itype", i32), ("dt_softplus", i32),
@@ -68,6 +93,10 @@ def load():
     lib.mm_state_update.restype = ctypes.c_int
     lib.mm_scan_fwd_workspace_size.argtypes = [ctypes.POINTER(ScanFwdParams)]
     lib.mm_scan_fwd_workspace_size.restype = ctypes.c_int64
+    lib.mm_scan_bwd.argtypes = [ctypes.POINTER(ScanBwdParams), vp]
+    lib.mm_scan_bwd.restype = ctypes.c_int
+    lib.mm_scan_bwd_workspace_size.argtypes = [ctypes.POINTER(ScanBwdParams)]
+    lib.mm_scan_bwd_workspace_size.restype = ctypes.c_int64
     return lib
 
 

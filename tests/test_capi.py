@@ -14,11 +14,11 @@ from tests import capi
 def test_library_exports_every_header_function():
     lib = capi.load()
     names = capi.header_functions()
-    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_state_update", "mm_last_error",
-                          "mm_abi_version"}
+    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_scan_bwd", "mm_scan_bwd_workspace_size",
+                          "mm_state_update", "mm_last_error", "mm_abi_version"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 3
+    assert lib.mm_abi_version() == 4
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -34,6 +34,7 @@ def _c_layout(struct, fields, tmp_path):
 
 
 @pytest.mark.parametrize("cname,pystruct", [("mm_scan_fwd_params", capi.ScanFwdParams),
+                                            ("mm_scan_bwd_params", capi.ScanBwdParams),
                                             ("mm_state_update_params", capi.StateUpdateParams)])
 def test_struct_layout_matches_header(tmp_path, cname, pystruct):
     fields = [f for f, _ in pystruct._fields_]
@@ -173,3 +174,34 @@ def test_workspace_size_query():
     bad.dstate = 0
     assert lib.mm_scan_fwd_workspace_size(ctypes.byref(bad)) == 0                      # invalid request
     assert lib.mm_scan_fwd_workspace_size(None) == 0
+
+
+def test_scan_bwd_rejects_invalid_params():
+    """Validation of mm_scan_bwd happens before anything is launched (fake pointers)."""
+    lib = capi.load()
+    assert lib.mm_scan_bwd(None, None) == capi.MM_ERR_INVALID_ARGUMENT
+    p = capi.ScanBwdParams()
+    p.batch, p.dim, p.seqlen, p.dstate, p.n_groups, p.itype = 2, 8, 64, 16, 1, 2
+    p.is_variable_B = p.is_variable_C = 1
+    fake = 0x1000
+    p.u = p.delta = p.A = p.B = p.C = p.dout = fake
+    assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "du, ddelta" in lib.mm_last_error().decode()
+    p.du = p.ddelta = p.dA = p.dB = p.dC = fake
+    p.z = fake
+    assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "out and dz" in lib.mm_last_error().decode()
+    p.z = None
+    p.D = fake
+    assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "dD" in lib.mm_last_error().decode()
+    p.D = None
+    need = lib.mm_scan_bwd_workspace_size(ctypes.byref(p))
+    assert need == 2 * 8 * (64 // 16) * 16 * 4                     # one float per state per 16-step tile
+    assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "workspace" in lib.mm_last_error().decode()
+    p.dstate = 300
+    assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert lib.mm_scan_bwd_workspace_size(ctypes.byref(p)) == 0
+    p.dstate, p.batch = 16, 0   # nothing to do: returns before touching any pointer or the GPU
+    assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_OK

@@ -1,0 +1,201 @@
+"""GPU parity of the selective-scan backward (MI355X only).
+
+``SelectiveScanFn.backward`` / the binding's ``bwd`` (selective_scan_cuda.bwd equivalent,
+selective_scan.cpp:415-612) run the kernels of mm_scan_bwd.hip through the C ABI; the gradients
+are compared with the exact (float64) gradients of the oracle ``selective_scan_ref`` on the same
+inputs (``oracle.ssm_ref.selective_scan_bwd_ref``, pinned in tests/test_oracle_bwd.py).
+
+Tolerances: the forward's (north_star) pair (rtol, atol) = (1e-4, 1e-5) for fp32 and (3e-2, 5e-2)
+for 16-bit inputs, element-wise as |err| <= rtol |exact| + atol max(1, max |exact|): the gradients
+of A, B, C, D and delta_bias are sums over rows and steps, whose rounding grows with the tensor's
+scale, so the absolute part is taken relative to it.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from oracle.ssm_ref import selective_scan_bwd_ref, selective_scan_ref
+from tests import capi
+from tests.test_gpu_scan import _case
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias"]
+GRAD = {"u": "du", "delta": "ddelta", "A": "dA", "B": "dB", "C": "dC", "D": "dD", "z": "dz", "delta_bias": "ddelta_bias"}
+
+
+def _say(msg):
+    print(f"\n[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _tol(dtype):
+    return (1e-4, 1e-5) if dtype == torch.float32 else (3e-2, 5e-2)
+
+
+def _check(got, exact, dtype, what):
+    rtol, atol = _tol(dtype)
+    got = got.double().cpu()
+    scale = max(1.0, exact.abs().max().item()) if exact.numel() else 1.0
+    err = (got - exact).abs()
+    bound = rtol * exact.abs() + atol * scale
+    bad = err > bound
+    assert not bool(bad.any()), (f"{what}: {int(bad.sum())}/{err.numel()} beyond tolerance; max err "
+                                 f"{err.max().item():.3g} (scale {scale:.3g})")
+
+
+def _dout(seed, shape, dtype):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)).to(dtype)
+
+
+def _autograd(case, dout, return_last_state=False):
+    from motif_mamba_amd import selective_scan_fn
+    g = {k: (v.to(DEV).requires_grad_(True) if torch.is_tensor(v) else v) for k, v in case.items()}
+    res = selective_scan_fn(**g, return_last_state=return_last_state)
+    out = res[0] if return_last_state else res
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    return out.detach().cpu(), {n: g[n].grad for n in NAMES if torch.is_tensor(g[n])}
+
+
+def _vs_exact(case, dout, dtype, what):
+    _, grads = _autograd(case, dout)
+    exact = selective_scan_bwd_ref(**case, dout=dout, dtype=torch.float64)
+    for n, gr in grads.items():
+        assert gr.dtype == case[n].dtype, (n, gr.dtype)
+        assert gr.shape == case[n].shape, (n, gr.shape)
+        _check(gr, exact[GRAD[n]], dtype, f"{what} {GRAD[n]}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N", [16, 4, 64])
+def test_bwd_shapes(dtype, N):
+    _say(f"bwd N={N} {dtype}")
+    case = _case(600 + N, 2, 32, 136, N, dtype)
+    _vs_exact(case, _dout(601, (2, 32, 136), dtype), dtype, f"N{N}")
+
+
+@pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False), dict(with_bias=False),
+                                   dict(softplus=False), dict(bkind="4d", G=2), dict(bkind="4d", G=4),
+                                   dict(bkind="const")])
+def test_bwd_options(flags):
+    _say(f"bwd options {flags}")
+    case = _case(610 + len(str(flags)), 2, 32, 100, 16, torch.float32, **flags)
+    _vs_exact(case, _dout(611, (2, 32, 100), torch.float32), torch.float32, str(flags))
+
+
+@pytest.mark.parametrize("L", [1, 7, 2049, 4100])
+def test_bwd_lengths(L):
+    _say(f"bwd L={L}")
+    case = _case(620 + L, 1, 16, L, 16, torch.float32)
+    _vs_exact(case, _dout(621, (1, 16, L), torch.float32), torch.float32, f"L{L}")
+
+
+def test_bwd_large_dstate_mixed_bc():
+    _say("bwd dstate 130, constant B, variable C")
+    case = _case(630, 2, 8, 64, 130, torch.float32)
+    case["B"] = torch.randn(8, 130, generator=torch.Generator().manual_seed(631))
+    _vs_exact(case, _dout(632, (2, 8, 64), torch.float32), torch.float32, "N130")
+
+
+def test_bwd_partial_grads_and_three_dim_bc():
+    """Only some inputs require grad; 3-D B/C come back with their own shape (ssi.py:84-85)."""
+    _say("bwd partial requires_grad")
+    from motif_mamba_amd import selective_scan_fn
+    case = _case(640, 2, 16, 64, 16, torch.float32)
+    dout = _dout(641, (2, 16, 64), torch.float32)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    g["u"].requires_grad_(True)
+    g["B"].requires_grad_(True)
+    out = selective_scan_fn(**g)
+    out.backward(dout.to(DEV))
+    exact = selective_scan_bwd_ref(**case, dout=dout, dtype=torch.float64)
+    assert g["B"].grad.shape == case["B"].shape == (2, 16, 64)
+    _check(g["u"].grad, exact["du"], torch.float32, "du")
+    _check(g["B"].grad, exact["dB"], torch.float32, "dB")
+    assert g["delta"].grad is None and g["A"].grad is None
+
+
+def test_bwd_training_forward_matches_inference_forward():
+    _say("bwd training forward = inference forward")
+    from motif_mamba_amd import selective_scan_fn
+    case = _case(650, 2, 32, 256, 16, torch.bfloat16)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    inf, inf_last = selective_scan_fn(**g, return_last_state=True)
+    g["u"] = g["u"].clone().requires_grad_(True)
+    tr, tr_last = selective_scan_fn(**g, return_last_state=True)
+    torch.testing.assert_close(tr.detach(), inf, rtol=0, atol=0)
+    torch.testing.assert_close(tr_last, inf_last, rtol=1e-6, atol=1e-6)
+
+
+def test_bwd_native_api_outputs():
+    """selective_scan_cuda.bwd's output list, with recompute_out_z (selective_scan.cpp:609-611)."""
+    _say("bwd native API")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(660, 2, 16, 2100, 16, torch.bfloat16, bkind="4d", G=2)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    out, x, out_z = ext.fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"],
+                            None, None, None, True)
+    dout = _dout(661, (2, 16, 2100), torch.bfloat16).to(DEV)
+    res = ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None,
+                  dout, x, out, None, None, None, True, True)
+    assert len(res) == 9
+    du, ddelta, dA, dB, dC, dD, dbias, dz, out_z2 = res
+    assert dB.dtype == dC.dtype == torch.bfloat16 and dA.dtype == torch.float32
+    torch.testing.assert_close(out_z2, out_z, rtol=1e-2, atol=1e-2)
+    exact = selective_scan_bwd_ref(**case, dout=dout.cpu(), dtype=torch.float64)
+    for name, t in (("du", du), ("ddelta", ddelta), ("dA", dA), ("dB", dB), ("dC", dC), ("dD", dD),
+                    ("ddelta_bias", dbias), ("dz", dz)):
+        _check(t, exact[name], torch.bfloat16, f"native {name}")
+    with pytest.raises(RuntimeError):   # x is required past one chunk, as in the reference
+        ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None,
+                dout, None, out, None, None, None, True, False)
+    with pytest.raises(NotImplementedError):
+        ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"],
+                torch.zeros(16, 2, device=DEV), torch.zeros(2, 16, device=DEV), None,
+                dout, x, out, None, None, None, True, False)
+
+
+def test_bwd_c_abi_direct():
+    _say("bwd C ABI direct")
+    lib = capi.load()
+    case = _case(670, 2, 32, 96, 16, torch.float32, bkind="4d", G=1)
+    dout = _dout(671, (2, 32, 96), torch.float32)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    pre = selective_scan_ref(**{**case, "z": None}).to(DEV)   # the forward's pre-gate output
+    do = dout.to(DEV)
+    du, ddelta, dz = torch.empty_like(g["u"]), torch.empty_like(g["delta"]), torch.empty_like(g["z"])
+    dA = torch.full_like(g["A"], 7.0)            # overwritten, not accumulated into
+    dB, dC = torch.full_like(g["B"], 7.0), torch.full_like(g["C"], 7.0)
+    dD, dbias = torch.full_like(g["D"], 7.0), torch.full_like(g["delta_bias"], 7.0)
+    p = capi.ScanBwdParams()
+    p.batch, p.dim, p.seqlen, p.dstate, p.n_groups = 2, 32, 96, 16, 1
+    p.itype, p.is_variable_B, p.is_variable_C, p.delta_softplus = 0, 1, 1, 1
+    ptr = lambda t: t.data_ptr()
+    p.u, p.delta, p.A, p.B, p.C, p.D, p.z, p.delta_bias = map(ptr, (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"],
+                                                                  g["z"], g["delta_bias"]))
+    p.dout, p.out = ptr(do), ptr(pre)
+    p.du, p.ddelta, p.dz, p.dA, p.dB, p.dC, p.dD, p.ddelta_bias = map(ptr, (du, ddelta, dz, dA, dB, dC, dD, dbias))
+    for nm, t in (("u", g["u"]), ("delta", g["delta"]), ("z", g["z"]), ("out", pre), ("dout", do), ("du", du),
+                  ("ddelta", ddelta), ("dz", dz)):
+        setattr(p, f"{nm}_batch_stride", t.stride(0))
+        setattr(p, f"{nm}_d_stride", t.stride(1))
+    p.A_d_stride, p.A_dstate_stride = g["A"].stride()
+    p.dA_d_stride, p.dA_dstate_stride = dA.stride()
+    p.B_batch_stride, p.B_group_stride, p.B_dstate_stride = g["B"].stride()[:3]
+    p.C_batch_stride, p.C_group_stride, p.C_dstate_stride = g["C"].stride()[:3]
+    p.dB_batch_stride, p.dB_group_stride, p.dB_dstate_stride = dB.stride()[:3]
+    p.dC_batch_stride, p.dC_group_stride, p.dC_dstate_stride = dC.stride()[:3]
+    nbytes = lib.mm_scan_bwd_workspace_size(ctypes.byref(p))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+    rc = lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle())
+    assert rc == 0, lib.mm_last_error().decode()
+    torch.cuda.synchronize()
+    exact = selective_scan_bwd_ref(**case, dout=dout, dtype=torch.float64)
+    for name, t in (("du", du), ("ddelta", ddelta), ("dz", dz), ("dA", dA), ("dB", dB), ("dC", dC), ("dD", dD),
+                    ("ddelta_bias", dbias)):
+        _check(t, exact[name], torch.float32, f"capi {name}")
