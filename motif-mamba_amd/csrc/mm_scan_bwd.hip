@@ -14,11 +14,15 @@
 // caller's workspace, and the reverse pass recomputes each tile from its checkpoint (keeping the
 // tile's states and decays in registers) and walks it backwards.
 //
+//   scan_bwd_tiled16<T>   dstate 16, variable B/C (the Mamba shape): 16 channels x 16 states per
+//       128-lane workgroup, sums over states and over the block's channels through LDS, dB/dC
+//       as per-block partials reduced by scan_bwd_reduce_bc (no atomics on them).
 //   scan_bwd_general<T>   any shape: a 256-lane workgroup holds 256/NP rows, one lane per state
 //       (NP = next power of two >= dstate); sums over states go through LDS, sums over rows
 //       (dB, dC, dA, dD, ddelta_bias) are float32 device atomics.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "mm_common.h"
@@ -206,6 +210,305 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
     }
 }
 
+
+// ------------------------------------------------------------------------------------------------
+// dstate-16 backward: a 128-lane workgroup owns 16 channels x 16 states of one (batch, group) --
+// lane (slot rs = lane / 16, channel c = lane % 16) holds states 2 rs and 2 rs + 1 of channel c.
+// Per 16-step tile: the lane owning steps 2 rs, 2 rs + 1 of channel c computes dt', dt'u, u and
+// g = dout silu(z) (and writes dz) into LDS; B and C of the tile are staged in LDS as float32; the
+// tile is recomputed from its checkpoint with states and decays kept in registers, then walked
+// backwards in two halves of 8 steps. Per half, the dB/dC contributions (per state, step and
+// channel) go to LDS and are summed over the 16 channels, the sums written as this channel block's
+// partials (reduced over blocks by scan_bwd_reduce_bc, in a fixed order); the per-slot partial sums
+// over states of gh B and of the delta' derivative go to LDS and the owner of each step adds the 8
+// slots in order and finishes du and ddelta.
+// ------------------------------------------------------------------------------------------------
+constexpr int kFT = 16;          // steps per tile
+constexpr int kFH = 8;           // steps per reduction half
+constexpr int kRS = 20;          // channel stride (floats) of sRed rows: 16 channels, 16-B aligned
+constexpr int kPS = 12;          // step stride (floats) of sPart rows: 8 steps, 16-B aligned
+constexpr int kXS = kFT + 1;     // step stride (float4) of sX rows
+
+template <typename T>
+__device__ __forceinline__ void load2(const T *p, float &a, float &b) {
+    if constexpr (std::is_same_v<T, float>) {
+        const float2 v = *reinterpret_cast<const float2 *>(p);
+        a = v.x; b = v.y;
+    } else if constexpr (std::is_same_v<T, bf16_t>) {
+        unpack_bf16x2(*reinterpret_cast<const uint32_t *>(p), a, b);
+    } else {
+        unpack_f16x2(*reinterpret_cast<const uint32_t *>(p), a, b);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store2(T *p, float a, float b) {
+    if constexpr (std::is_same_v<T, float>) {
+        *reinterpret_cast<float2 *>(p) = make_float2(a, b);
+    } else if constexpr (std::is_same_v<T, bf16_t>) {
+        *reinterpret_cast<uint32_t *>(p) = pack_bf16x2(a, b);
+    } else {
+        *reinterpret_cast<uint32_t *>(p) = pack_f16x2(a, b);
+    }
+}
+
+struct FastWs {
+    float *ck;      // [n_tiles][batch][dim][16]: states before each tile
+    float *partB;   // [block][batch][group][16][L]: dB summed over one 16-channel block
+    float *partC;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(128)
+scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws) {
+    __shared__ __align__(16) float4 sX[16 * kXS];           // [c][t]: (dt', dt'u, u, g)
+    __shared__ __align__(16) float sBC[kFT * 36];            // [t][B 16 | C 16 | pad]
+    __shared__ __align__(16) float sRed[kFH * 16 * 2 * kRS]; // [t][n][dB|dC][c]
+    __shared__ __align__(16) float sPart[8 * 2 * 16 * kPS];  // [slot][gh B | ddt][c][t]
+
+    const int tid = threadIdx.x;
+    const int rs = tid >> 4;               // state slot: states 2 rs, 2 rs + 1; prologue steps 2 rs, 2 rs + 1
+    const int c = tid & 15;                // channel within the block
+    const int n0 = 2 * rs;
+    const int64_t b = blockIdx.y;
+    const int64_t d0 = int64_t(blockIdx.x) * 16;
+    const int64_t d = d0 + c;
+    const int64_t g = d0 / ratio;
+    const int64_t blk = (d0 - g * ratio) / 16;
+    const int64_t L = p.seqlen;
+    const int64_t n_tiles = (L + kFT - 1) / kFT;
+
+    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
+    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
+    const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
+    const T *outp = p.z ? reinterpret_cast<const T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
+    const T *gop = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
+    T *dup = reinterpret_cast<T *>(p.du) + b * p.du_batch_stride + d * p.du_d_stride;
+    T *ddp = reinterpret_cast<T *>(p.ddelta) + b * p.ddelta_batch_stride + d * p.ddelta_d_stride;
+    T *dzp = p.z ? reinterpret_cast<T *>(p.dz) + b * p.dz_batch_stride + d * p.dz_d_stride : nullptr;
+    T *ozp = (p.z && p.out_z) ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
+    // B/C staging: lane -> tensor tid / 64, state (tid / 4) % 16, steps 4 (tid % 4) .. +3 of the tile.
+    const int st_tensor = tid >> 6, st_n = (tid >> 2) & 15, st_q = tid & 3;
+    const T *stp = st_tensor == 0
+        ? reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + st_n * p.B_dstate_stride
+        : reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + st_n * p.C_dstate_stride;
+
+    const float A0 = p.A[d * p.A_d_stride + n0 * p.A_dstate_stride];
+    const float A1 = p.A[d * p.A_d_stride + (n0 + 1) * p.A_dstate_stride];
+    const float A20 = A0 * kLog2e, A21 = A1 * kLog2e;
+    const float Dv = p.D ? p.D[d] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+
+    // Prologue of tile j: this lane's two steps (dt', dt'u, u, g into sX; raw and g kept for the
+    // epilogue; dz and out_z written) and its four B or C values (into sBC). Steps past L are
+    // padding: dt' = g = 0 and B = C = 0 leave every state and gradient unchanged.
+    float e_raw[2], e_dt[2], e_u[2], e_g[2];
+    auto prologue = [&](int64_t j, bool full) {
+        const int64_t t0 = j * kFT;
+        const int64_t te = t0 + 2 * rs;
+        const bool ev = te < L;            // L is a multiple of 8: both steps exist or neither
+        const int64_t tl = ev ? te : L - 2;
+        float dd[2], uu[2];
+        load2(dp + tl, dd[0], dd[1]);
+        load2(up + tl, uu[0], uu[1]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            e_raw[i] = dd[i] + bias;
+            e_dt[i] = ev ? (p.delta_softplus ? softplus_fast(e_raw[i]) : e_raw[i]) : 0.f;
+            e_u[i] = uu[i];
+            e_g[i] = 0.f;
+        }
+        if (full) {
+            float go[2];
+            load2(gop + tl, go[0], go[1]);
+            if (zp) {
+                float zz[2], oo[2], dz[2], oz[2];
+                load2(zp + tl, zz[0], zz[1]);
+                load2(outp + tl, oo[0], oo[1]);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const float sg = 1.f / (1.f + __builtin_amdgcn_exp2f(-zz[i] * kLog2e));
+                    dz[i] = go[i] * oo[i] * sg * (1.f + zz[i] * (1.f - sg));
+                    oz[i] = oo[i] * zz[i] * sg;
+                    go[i] *= zz[i] * sg;
+                }
+                if (ev) {
+                    store2(dzp + te, dz[0], dz[1]);
+                    if (ozp) store2(ozp + te, oz[0], oz[1]);
+                }
+            }
+            e_g[0] = ev ? go[0] : 0.f;
+            e_g[1] = ev ? go[1] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            sX[c * kXS + 2 * rs + i] = make_float4(e_dt[i], e_dt[i] * e_u[i], e_u[i], e_g[i]);
+        // B or C: steps t0 + 4 st_q .. +3 (L is a multiple of 4 here, so the four exist or none do).
+        const int64_t ts = t0 + 4 * st_q;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (ts < L && (full || st_tensor == 0)) {
+            load2(stp + ts, v[0], v[1]);
+            load2(stp + ts + 2, v[2], v[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sBC[(4 * st_q + i) * 36 + st_tensor * 16 + st_n] = v[i];
+    };
+
+    // Pass 1: the states before every tile, into the checkpoint workspace.
+    float h0 = 0.f, h1 = 0.f;
+    for (int64_t j = 0; j < n_tiles; ++j) {
+        *reinterpret_cast<float2 *>(ws.ck + ((j * p.batch + b) * p.dim + d) * 16 + n0) = make_float2(h0, h1);
+        prologue(j, false);
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < kFT; ++t) {
+            const float4 x = sX[c * kXS + t];
+            const float2 bv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + n0]);
+            h0 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A20), h0, x.y * bv.x);
+            h1 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A21), h1, x.y * bv.y);
+        }
+        __syncthreads();
+    }
+
+    // Pass 2: tiles in reverse order.
+    float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f;   // state adjoints, decays of the step after
+    float dA0 = 0.f, dA1 = 0.f, dD_acc = 0.f, dbias_acc = 0.f;
+    for (int64_t j = n_tiles - 1; j >= 0; --j) {
+        const int64_t t0 = j * kFT;
+        prologue(j, true);
+        const float2 hc = *reinterpret_cast<const float2 *>(ws.ck + ((j * p.batch + b) * p.dim + d) * 16 + n0);
+        __syncthreads();
+        float hs0[kFT], hs1[kFT], as0[kFT], as1[kFT];
+        {
+            float x0 = hc.x, x1 = hc.y;
+#pragma unroll
+            for (int t = 0; t < kFT; ++t) {
+                const float4 x = sX[c * kXS + t];
+                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + n0]);
+                as0[t] = __builtin_amdgcn_exp2f(x.x * A20);
+                as1[t] = __builtin_amdgcn_exp2f(x.x * A21);
+                x0 = __builtin_fmaf(as0[t], x0, x.y * bv.x);
+                x1 = __builtin_fmaf(as1[t], x1, x.y * bv.y);
+                hs0[t] = x0;
+                hs1[t] = x1;
+            }
+        }
+#pragma unroll
+        for (int half = 1; half >= 0; --half) {
+            float pu[kFH], pd[kFH];
+            float dA_t0 = 0.f, dA_t1 = 0.f;
+#pragma unroll
+            for (int s = kFH - 1; s >= 0; --s) {
+                const int t = half * kFH + s;
+                const float4 x = sX[c * kXS + t];          // dt', dt'u, u, g
+                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + n0]);
+                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + 16 + n0]);
+                gh0 = __builtin_fmaf(an0, gh0, x.w * cv.x);
+                gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
+                const float ah0 = __builtin_fmaf(-x.y, bv.x, hs0[t]);   // a_t h_{t-1}
+                const float ah1 = __builtin_fmaf(-x.y, bv.y, hs1[t]);
+                float *red = &sRed[(s * 16 + n0) * 2 * kRS + c];
+                red[0] = gh0 * x.y;                        // dB (state n0)
+                red[kRS] = x.w * hs0[t];                   // dC (state n0)
+                red[2 * kRS] = gh1 * x.y;                  // dB (state n0 + 1)
+                red[3 * kRS] = x.w * hs1[t];               // dC (state n0 + 1)
+                pu[s] = __builtin_fmaf(gh1, bv.y, gh0 * bv.x);
+                pd[s] = __builtin_fmaf(gh1, __builtin_fmaf(A1, ah1, x.z * bv.y), gh0 * __builtin_fmaf(A0, ah0, x.z * bv.x));
+                dA_t0 = __builtin_fmaf(gh0 * x.x, ah0, dA_t0);
+                dA_t1 = __builtin_fmaf(gh1 * x.x, ah1, dA_t1);
+                an0 = as0[t];
+                an1 = as1[t];
+            }
+            dA0 += dA_t0;
+            dA1 += dA_t1;
+            float4 *pp = reinterpret_cast<float4 *>(&sPart[((rs * 2 + 0) * 16 + c) * kPS]);
+            pp[0] = make_float4(pu[0], pu[1], pu[2], pu[3]);
+            pp[1] = make_float4(pu[4], pu[5], pu[6], pu[7]);
+            float4 *pq = reinterpret_cast<float4 *>(&sPart[((rs * 2 + 1) * 16 + c) * kPS]);
+            pq[0] = make_float4(pd[0], pd[1], pd[2], pd[3]);
+            pq[1] = make_float4(pd[4], pd[5], pd[6], pd[7]);
+            __syncthreads();
+            // dB / dC of this half summed over the block's 16 channels: lane -> tensor tid / 64,
+            // state (tid / 4) % 16, steps 2 (tid % 4), +1.
+            {
+                const int tn = (tid >> 2) & 15, tt = 2 * (tid & 3), tz = tid >> 6;
+                float sum[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const float4 *rv = reinterpret_cast<const float4 *>(&sRed[((tt + i) * 16 + tn) * 2 * kRS + tz * kRS]);
+                    float acc = 0.f;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v = rv[q];
+                        acc += v.x; acc += v.y; acc += v.z; acc += v.w;
+                    }
+                    sum[i] = acc;
+                }
+                const int64_t ts = t0 + half * kFH + tt;
+                if (ts < L) {
+                    float *dst = (tz == 0 ? ws.partB : ws.partC) +
+                                 (((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * L + ts;
+                    *reinterpret_cast<float2 *>(dst) = make_float2(sum[0], sum[1]);
+                }
+            }
+            // du / ddelta of the steps this lane owns, if they are in this half.
+            if ((rs >> 2) == half) {
+                const int sl = 2 * (rs & 3);               // first owned step within the half
+                const int64_t te = t0 + 2 * rs;
+                float su[2] = {0.f, 0.f}, sd[2] = {0.f, 0.f};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float2 a = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 0) * 16 + c) * kPS + sl]);
+                    const float2 bq = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 1) * 16 + c) * kPS + sl]);
+                    su[0] += a.x; su[1] += a.y;
+                    sd[0] += bq.x; sd[1] += bq.y;
+                }
+                if (te < L) {
+                    float du[2], ddl[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        du[i] = __builtin_fmaf(Dv, e_g[i], e_dt[i] * su[i]);
+                        const float sg = 1.f / (1.f + __builtin_amdgcn_exp2f(-e_raw[i] * kLog2e));
+                        ddl[i] = (p.delta_softplus && e_raw[i] <= 20.f) ? sd[i] * sg : sd[i];
+                        dD_acc = __builtin_fmaf(e_g[i], e_u[i], dD_acc);
+                        dbias_acc += ddl[i];
+                    }
+                    store2(dup + te, du[0], du[1]);
+                    store2(ddp + te, ddl[0], ddl[1]);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    atomicAdd(p.dA + d * p.dA_d_stride + n0 * p.dA_dstate_stride, dA0);
+    atomicAdd(p.dA + d * p.dA_d_stride + (n0 + 1) * p.dA_dstate_stride, dA1);
+    if (p.dD) atomicAdd(p.dD + d, dD_acc);
+    if (p.ddelta_bias) atomicAdd(p.ddelta_bias + d, dbias_acc);
+}
+
+// dB / dC = the sum of the channel blocks' partials, in block order (deterministic).
+__global__ void __launch_bounds__(256)
+scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *part, float *dst, int64_t bs, int64_t gs, int64_t ns,
+                   int64_t n_blocks) {
+    const int64_t L4 = p.seqlen / 4;
+    const int64_t rows = p.batch * p.n_groups * 16;
+    const int64_t total = rows * L4;
+    const int64_t slice = rows * p.seqlen;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t row = i / L4, t4 = i - row * L4;
+        const float4 *src = reinterpret_cast<const float4 *>(part + row * p.seqlen) + t4;
+        float4 acc = src[0];
+        for (int64_t k = 1; k < n_blocks; ++k) {
+            const float4 v = src[k * (slice / 4)];
+            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+        }
+        const int64_t n = row % 16, bg = row / 16;
+        const int64_t gg = bg % p.n_groups, bb = bg / p.n_groups;
+        float *o = dst + bb * bs + gg * gs + n * ns + 4 * t4;
+        o[0] = acc.x; o[1] = acc.y; o[2] = acc.z; o[3] = acc.w;
+    }
+}
+
 template <typename T>
 int launch_general(const mm_scan_bwd_params &p, hipStream_t s) {
     int np_log2 = 0;
@@ -226,23 +529,75 @@ int launch_fill(float *ptr, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int6
     return launch_status("fill_zero4");
 }
 
+// The dstate-16 kernel's requirements: variable B/C, 16-channel blocks inside one group, L a
+// multiple of 8, two-element-aligned activation rows and four-element-aligned B/C rows.
+bool fast_ok(const mm_scan_bwd_params &p) {
+    if (p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
+    if (p.dim % 16 != 0 || (p.dim / p.n_groups) % 16 != 0 || p.seqlen < 8 || p.seqlen % 8 != 0) return false;
+    if (p.batch > 65535 || p.dim / 16 > 0x7fffffff) return false;
+    const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
+    auto al = [](const void *ptr, int64_t bytes) { return (reinterpret_cast<uintptr_t>(ptr) % uintptr_t(bytes)) == 0; };
+    auto row2 = [&](const void *ptr, int64_t s0, int64_t s1) {
+        return ptr == nullptr || (al(ptr, 2 * eb) && s0 % 2 == 0 && s1 % 2 == 0);
+    };
+    bool ok = row2(p.u, p.u_batch_stride, p.u_d_stride) && row2(p.delta, p.delta_batch_stride, p.delta_d_stride) &&
+              row2(p.z, p.z_batch_stride, p.z_d_stride) && row2(p.out, p.out_batch_stride, p.out_d_stride) &&
+              row2(p.dout, p.dout_batch_stride, p.dout_d_stride) && row2(p.du, p.du_batch_stride, p.du_d_stride) &&
+              row2(p.ddelta, p.ddelta_batch_stride, p.ddelta_d_stride) && row2(p.dz, p.dz_batch_stride, p.dz_d_stride) &&
+              row2(p.out_z, p.out_z_batch_stride, p.out_z_d_stride);
+    ok = ok && al(p.B, 2 * eb) && al(p.C, 2 * eb) && p.B_batch_stride % 2 == 0 && p.B_group_stride % 2 == 0 &&
+         p.B_dstate_stride % 2 == 0 && p.C_batch_stride % 2 == 0 && p.C_group_stride % 2 == 0 &&
+         p.C_dstate_stride % 2 == 0;
+    return ok;
+}
+
+int64_t fast_ck_floats(const mm_scan_bwd_params &p) {
+    return ((p.seqlen + kFT - 1) / kFT) * p.batch * p.dim * 16;
+}
+int64_t fast_part_floats(const mm_scan_bwd_params &p) {
+    return (p.dim / 16) * p.batch * 16 * p.seqlen;   // blocks per group x groups = dim / 16
+}
+
+template <typename T>
+int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
+    float *ws = static_cast<float *>(p.workspace);
+    const FastWs fw{ws, ws + fast_ck_floats(p), ws + fast_ck_floats(p) + fast_part_floats(p)};
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / 16), unsigned(p.batch));
+    hipLaunchKernelGGL((scan_bwd_tiled16<T>), grid, dim3(128), 0, s, p, ratio, fw);
+    int rc = launch_status("scan_bwd_tiled16");
+    if (rc != MM_OK) return rc;
+    const int64_t total = p.batch * p.n_groups * 16 * (p.seqlen / 4);
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 8192));
+    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, fw.partB, p.dB, p.dB_batch_stride,
+                       p.dB_group_stride, p.dB_dstate_stride, ratio / 16);
+    rc = launch_status("scan_bwd_reduce_bc");
+    if (rc != MM_OK) return rc;
+    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, fw.partC, p.dC, p.dC_batch_stride,
+                       p.dC_group_stride, p.dC_dstate_stride, ratio / 16);
+    return launch_status("scan_bwd_reduce_bc");
+}
+
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
+    if (bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
     return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));
 }
 
 template <typename T>
 int launch_bwd(const mm_scan_bwd_params &p, hipStream_t s) {
-    // The accumulated gradients start from zero on the launch stream.
+    // The accumulated gradients start from zero on the launch stream (the dstate-16 kernel writes
+    // dB and dC whole and only accumulates dA, dD and ddelta_bias).
+    const bool fast = bwd::fast_ok(p) && p.seqlen > 0;
     int rc = bwd::launch_fill(p.dA, 1, 1, p.dim, p.dstate, 0, 0, p.dA_d_stride, p.dA_dstate_stride, s);
-    if (rc == MM_OK && p.is_variable_B)
+    if (rc == MM_OK && p.is_variable_B && !fast)
         rc = bwd::launch_fill(p.dB, p.batch, p.n_groups, p.dstate, p.seqlen, p.dB_batch_stride, p.dB_group_stride,
                               p.dB_dstate_stride, 1, s);
     if (rc == MM_OK && !p.is_variable_B)
         rc = bwd::launch_fill(p.dB, 1, 1, p.dim, p.dstate, 0, 0, p.dB_d_stride, p.dB_dstate_stride, s);
-    if (rc == MM_OK && p.is_variable_C)
+    if (rc == MM_OK && p.is_variable_C && !fast)
         rc = bwd::launch_fill(p.dC, p.batch, p.n_groups, p.dstate, p.seqlen, p.dC_batch_stride, p.dC_group_stride,
                               p.dC_dstate_stride, 1, s);
     if (rc == MM_OK && !p.is_variable_C)
@@ -251,6 +606,7 @@ int launch_bwd(const mm_scan_bwd_params &p, hipStream_t s) {
     if (rc == MM_OK && p.ddelta_bias) rc = bwd::launch_fill(p.ddelta_bias, 1, 1, 1, p.dim, 0, 0, 0, 1, s);
     if (rc != MM_OK) return rc;
     if (p.seqlen == 0) return MM_OK;
+    if (bwd::fast_ok(p)) return bwd::launch_fast<T>(p, s);
     return bwd::launch_general<T>(p, s);
 }
 

@@ -86,7 +86,7 @@ def test_bwd_options(flags):
     _vs_exact(case, _dout(611, (2, 32, 100), torch.float32), torch.float32, str(flags))
 
 
-@pytest.mark.parametrize("L", [1, 7, 2049, 4100])
+@pytest.mark.parametrize("L", [1, 7, 2049, 4100, 2056, 4096])
 def test_bwd_lengths(L):
     _say(f"bwd L={L}")
     case = _case(620 + L, 1, 16, L, 16, torch.float32)
@@ -199,3 +199,34 @@ def test_bwd_c_abi_direct():
     for name, t in (("du", du), ("ddelta", ddelta), ("dz", dz), ("dA", dA), ("dB", dB), ("dC", dC), ("dD", dD),
                     ("ddelta_bias", dbias)):
         _check(t, exact[name], torch.float32, f"capi {name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("G", [1, 4])
+def test_bwd_dstate16_kernel_medium_shape(dtype, G):
+    """The dstate-16 kernel (16-channel blocks, per-block dB/dC partials) on 2 x 256 channels x L 1024."""
+    _say(f"bwd dstate-16 kernel 2x256x1024 G={G} {dtype}")
+    case = _case(680 + G, 2, 256, 1024, 16, dtype, bkind="4d", G=G)
+    _vs_exact(case, _dout(681, (2, 256, 1024), dtype), dtype, f"G{G}")
+
+
+def test_bwd_dstate16_kernel_matches_general_kernel():
+    """Unaligned u rows send the same request to the general kernel: both agree."""
+    _say("bwd dstate-16 vs general kernel")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(690, 2, 64, 512, 16, torch.float32, bkind="4d", G=2)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    out, x, out_z = ext.fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"],
+                            None, None, None, True)
+    dout = _dout(691, (2, 64, 512), torch.float32).to(DEV)
+    fast = ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None,
+                   dout, x, out, None, None, None, True, False)
+    wide = torch.zeros(2, 64, 513, device=DEV)
+    wide[:, :, 1:] = g["u"]
+    u_odd = wide[:, :, 1:]                     # rows start at odd elements: not 8-byte aligned
+    slow = ext.bwd(u_odd, g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None,
+                   dout, x, out, None, None, None, True, False)
+    for name, a, b in zip(["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"], fast, slow):
+        scale = max(1.0, b.abs().max().item())
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-5 * scale, msg=lambda m: f"{name}: {m}")
