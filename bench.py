@@ -12,8 +12,8 @@ and out_z, last_state written, each once) divided by the measured time per step,
 The JSON line also carries: ``roofline`` for the forward-scan kernel (HBM bound, 8 TB/s peak),
 ``roofline_trans`` (the same kernel against the v_exp_f32 issue rate, which binds it), ``cpu_baseline``
 (the CPU oracle timed on the host on a bounded sample of the same workload), per-config results for
-configs 1 and 3, decode tokens/s for config 4 and the MotifMamba P/Q forward on a Mamba-1.4B layer
-(unless --quick).
+configs 1 and 3, decode tokens/s for config 4, the MotifMamba P/Q forward on a Mamba-1.4B layer and
+the training forward + backward of configs 1 and 2 (unless --quick).
 Only one GPU is used; --gpus N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -136,6 +136,40 @@ def bench_pq(name, steps, warmup, torch):
             "t_floor_us": floor * 1e6, "floor_frac": floor / (ms * 1e-3)}
 
 
+def bench_train(cfg_name, steps, warmup, torch):
+    """Forward in training mode (pre-gate out and chunk states saved, ssi.py:47-61) and the backward
+    (selective_scan_cuda.bwd equivalent) on one configuration: times of each and of the pair."""
+    from motif_mamba_amd import _native
+    from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_inputs
+    ext = _native.ext()
+    c = SCAN_CONFIGS[cfg_name]
+    t = scan_inputs(c, device="cuda")
+    B = t["B"].unsqueeze(1) if t["B"].dim() == 3 else t["B"]
+    C = t["C"].unsqueeze(1) if t["C"].dim() == 3 else t["C"]
+    args = (t["u"], t["delta"], t["A"], B, C, t["D"], t["z"], t["delta_bias"], None, None, None, True)
+    out, x, out_z = ext.fwd(*args)
+    dout = torch.randn(out_z.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(7)).to(out_z.dtype)
+
+    def fwd(i):
+        ext.fwd(*args)
+
+    def bwd(i):
+        ext.bwd(*args[:11], dout, x, out, None, None, None, True, False)
+
+    def both(i):
+        o, xx, oz = ext.fwd(*args)
+        ext.bwd(*args[:11], dout, xx, o, None, None, None, True, False)
+
+    f_ms = _time_loop(fwd, steps, warmup, torch)
+    b_ms = _time_loop(bwd, steps, warmup, torch)
+    s_ms = _time_loop(both, steps, warmup, torch)
+    elems = c.batch * c.dim * c.seqlen
+    del t, out, x, out_z, dout
+    torch.cuda.empty_cache()
+    return {"shape": [c.batch, c.dim, c.seqlen, c.dstate], "dtype": c.dtype, "fwd_train_ms": f_ms, "bwd_ms": b_ms,
+            "fwd_bwd_ms": s_ms, "elements_per_s": elems / (s_ms * 1e-3)}
+
+
 def cpu_baseline(torch, seconds_target=15.0):
     """The CPU oracle (torch restatement of selective_scan_ref) on a bounded sample of config 2:
     one batch row and a slice of channels at the full L = 4096, scaled to GB/s of the config's
@@ -183,7 +217,8 @@ def main():
                     help="also run three 1 GiB device-to-device copies: the reference that scales the "
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
-                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b) "
+                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, "
+                         "cfg1_train, cfg2_train) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -203,6 +238,8 @@ def main():
             res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
         elif name.startswith("pq_"):
             res = bench_pq(name, args.steps, args.warmup, torch)
+        elif name.endswith("_train"):
+            res = bench_train(name[: -len("_train")], args.steps, args.warmup, torch)
         else:
             res = bench_scan(name, args.steps, args.warmup, torch, rotate=2 if name == "cfg1" else 1)
         print(json.dumps({"config": name, **res}), flush=True)
@@ -230,6 +267,9 @@ def main():
             extra[f"cfg4_b{b}"] = bench_decode(b, 1024, 16, torch)
         _log("MotifMamba P/Q forward (Mamba-1.4B layer, rank 2, per-channel P/Q)")
         extra["pq_1p4b"] = bench_pq("pq_1p4b", max(5, args.steps), 2, torch)
+        for name in ("cfg1", "cfg2"):
+            _log(f"training forward + backward ({name})")
+            extra[f"{name}_train"] = bench_train(name, max(5, args.steps // 2), 2, torch)
     cpu = None
     if not args.no_cpu:
         _log("CPU baseline (oracle on a bounded sample)")

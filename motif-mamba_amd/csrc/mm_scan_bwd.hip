@@ -225,31 +225,34 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
 // ------------------------------------------------------------------------------------------------
 constexpr int kFT = 16;          // steps per tile
 constexpr int kFH = 8;           // steps per reduction half
-constexpr int kRS = 20;          // channel stride (floats) of sRed rows: 16 channels, 16-B aligned
-constexpr int kPS = 12;          // step stride (floats) of sPart rows: 8 steps, 16-B aligned
+constexpr int kPS = 8;           // step stride (floats) of sPart rows
 constexpr int kXS = kFT + 1;     // step stride (float4) of sX rows
+constexpr int kBufs = 1;         // sX / sBC buffers (one: 4 workgroups fit a CU's LDS)
+
+// sRed address of (tensor, state n, step t of the half, channel c): a block of 8 rows of 16
+// channels per (tensor, state), rows 20 floats apart so that 8 consecutive steps of one state (the
+// reduction reads, 16 bytes per lane) fall in distinct banks; blocks 168 floats apart (8 mod 16
+// banks) so that the 4 state pairs of a wave (the per-step writes) split over both bank halves.
+constexpr int kRedRow = 20;
+constexpr int kRedBlock = 168;
+__device__ __forceinline__ int red_at(int tensor, int n, int t, int c) {
+    return (tensor * 16 + n) * kRedBlock + t * kRedRow + c;
+}
+constexpr int kRedFloats = 32 * kRedBlock;
+static_assert((kFH - 1) * kRedRow + 16 <= kRedBlock, "sRed rows overlap");
 
 template <typename T>
-__device__ __forceinline__ void load2(const T *p, float &a, float &b) {
-    if constexpr (std::is_same_v<T, float>) {
-        const float2 v = *reinterpret_cast<const float2 *>(p);
-        a = v.x; b = v.y;
-    } else if constexpr (std::is_same_v<T, bf16_t>) {
-        unpack_bf16x2(*reinterpret_cast<const uint32_t *>(p), a, b);
-    } else {
-        unpack_f16x2(*reinterpret_cast<const uint32_t *>(p), a, b);
-    }
+__device__ __forceinline__ void unpack2(const RawVec<T, 2> &r, float &a, float &b) {
+    float o[2];
+    unpack_raw<T, 2>(r, o);
+    a = o[0];
+    b = o[1];
 }
 
 template <typename T>
 __device__ __forceinline__ void store2(T *p, float a, float b) {
-    if constexpr (std::is_same_v<T, float>) {
-        *reinterpret_cast<float2 *>(p) = make_float2(a, b);
-    } else if constexpr (std::is_same_v<T, bf16_t>) {
-        *reinterpret_cast<uint32_t *>(p) = pack_bf16x2(a, b);
-    } else {
-        *reinterpret_cast<uint32_t *>(p) = pack_f16x2(a, b);
-    }
+    const float x[2] = {a, b};
+    store_vec<T, 2>(p, x);
 }
 
 struct FastWs {
@@ -258,12 +261,20 @@ struct FastWs {
     float *partC;
 };
 
+// Global data of one tile for one lane, loaded a tile ahead of its use.
+template <typename T>
+struct TileRaw {
+    RawVec<T, 2> d, u, go, z, o;   // this lane's two steps of one channel
+    RawVec<T, 2> bc0, bc1;         // four B or C values of one state
+    float2 hc;                     // checkpoint of the lane's two states (pass 2)
+};
+
 template <typename T>
 __global__ void __launch_bounds__(128)
 scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws) {
-    __shared__ __align__(16) float4 sX[16 * kXS];           // [c][t]: (dt', dt'u, u, g)
-    __shared__ __align__(16) float sBC[kFT * 36];            // [t][B 16 | C 16 | pad]
-    __shared__ __align__(16) float sRed[kFH * 16 * 2 * kRS]; // [t][n][dB|dC][c]
+    __shared__ __align__(16) float4 sX[kBufs][16 * kXS];    // [buf][c][t]: (dt', dt'u, u, g)
+    __shared__ __align__(16) float sBC[kBufs][kFT * 36];     // [buf][t][B 16 | C 16 | pad]
+    __shared__ __align__(16) float sRed[kRedFloats];         // red_at(tensor, n, t, c)
     __shared__ __align__(16) float sPart[8 * 2 * 16 * kPS];  // [slot][gh B | ddt][c][t]
 
     const int tid = threadIdx.x;
@@ -292,6 +303,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const T *stp = st_tensor == 0
         ? reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + st_n * p.B_dstate_stride
         : reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + st_n * p.C_dstate_stride;
+    float *ckp = ws.ck + (b * p.dim + d) * 16 + n0;
+    const int64_t ck_tile = p.batch * p.dim * 16;
 
     const float A0 = p.A[d * p.A_d_stride + n0 * p.A_dstate_stride];
     const float A1 = p.A[d * p.A_d_stride + (n0 + 1) * p.A_dstate_stride];
@@ -299,35 +312,54 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
 
-    // Prologue of tile j: this lane's two steps (dt', dt'u, u, g into sX; raw and g kept for the
-    // epilogue; dz and out_z written) and its four B or C values (into sBC). Steps past L are
-    // padding: dt' = g = 0 and B = C = 0 leave every state and gradient unchanged.
-    float e_raw[2], e_dt[2], e_u[2], e_g[2];
-    auto prologue = [&](int64_t j, bool full) {
-        const int64_t t0 = j * kFT;
-        const int64_t te = t0 + 2 * rs;
-        const bool ev = te < L;            // L is a multiple of 8: both steps exist or neither
-        const int64_t tl = ev ? te : L - 2;
-        float dd[2], uu[2];
-        load2(dp + tl, dd[0], dd[1]);
-        load2(up + tl, uu[0], uu[1]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            e_raw[i] = dd[i] + bias;
-            e_dt[i] = ev ? (p.delta_softplus ? softplus_fast(e_raw[i]) : e_raw[i]) : 0.f;
-            e_u[i] = uu[i];
-            e_g[i] = 0.f;
-        }
+    // Loads of tile j (clamped into the row: always in bounds). Steps past L are padding, made
+    // inert in commit(): dt' = g = 0 and B = C = 0 leave every state and gradient unchanged.
+    auto load = [&](int64_t j, bool full) {
+        TileRaw<T> r;
+        const int64_t jj = j < 0 ? 0 : (j >= n_tiles ? n_tiles - 1 : j);
+        const int64_t te = jj * kFT + 2 * rs;
+        const int64_t tl = te < L ? te : L - 2;
+        r.d = load_raw<T, 2>(dp + tl);
+        r.u = load_raw<T, 2>(up + tl);
+        r.go = {};
+        r.z = {};
+        r.o = {};
         if (full) {
-            float go[2];
-            load2(gop + tl, go[0], go[1]);
+            r.go = load_raw<T, 2>(gop + tl);
+            if (zp) {
+                r.z = load_raw<T, 2>(zp + tl);
+                r.o = load_raw<T, 2>(outp + tl);
+            }
+        }
+        const int64_t ts0 = jj * kFT + 4 * st_q;
+        const int64_t ts = ts0 < L ? ts0 : L - 4;
+        r.bc0 = {};
+        r.bc1 = {};
+        if (full || st_tensor == 0) {
+            r.bc0 = load_raw<T, 2>(stp + ts);
+            r.bc1 = load_raw<T, 2>(stp + ts + 2);
+        }
+        r.hc = full ? *reinterpret_cast<const float2 *>(ckp + jj * ck_tile) : make_float2(0.f, 0.f);
+        return r;
+    };
+    // Tile j's per-step values into LDS buffer `buf`; the lane's own steps kept for the epilogue;
+    // dz (and out_z) written.
+    float e_raw[2], e_dt[2], e_u[2], e_g[2];
+    auto commit = [&](const TileRaw<T> &r, int64_t j, int buf, bool full) {
+        const int64_t te = j * kFT + 2 * rs;
+        const bool ev = te < L;            // L is a multiple of 8: both steps exist or neither
+        float dd[2], go[2] = {0.f, 0.f};
+        unpack2<T>(r.d, dd[0], dd[1]);
+        unpack2<T>(r.u, e_u[0], e_u[1]);
+        if (full) {
+            unpack2<T>(r.go, go[0], go[1]);
             if (zp) {
                 float zz[2], oo[2], dz[2], oz[2];
-                load2(zp + tl, zz[0], zz[1]);
-                load2(outp + tl, oo[0], oo[1]);
+                unpack2<T>(r.z, zz[0], zz[1]);
+                unpack2<T>(r.o, oo[0], oo[1]);
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    const float sg = 1.f / (1.f + __builtin_amdgcn_exp2f(-zz[i] * kLog2e));
+                    const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zz[i] * kLog2e));
                     dz[i] = go[i] * oo[i] * sg * (1.f + zz[i] * (1.f - sg));
                     oz[i] = oo[i] * zz[i] * sg;
                     go[i] *= zz[i] * sg;
@@ -337,54 +369,60 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                     if (ozp) store2(ozp + te, oz[0], oz[1]);
                 }
             }
-            e_g[0] = ev ? go[0] : 0.f;
-            e_g[1] = ev ? go[1] : 0.f;
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            sX[c * kXS + 2 * rs + i] = make_float4(e_dt[i], e_dt[i] * e_u[i], e_u[i], e_g[i]);
-        // B or C: steps t0 + 4 st_q .. +3 (L is a multiple of 4 here, so the four exist or none do).
-        const int64_t ts = t0 + 4 * st_q;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        if (ts < L && (full || st_tensor == 0)) {
-            load2(stp + ts, v[0], v[1]);
-            load2(stp + ts + 2, v[2], v[3]);
+        for (int i = 0; i < 2; ++i) {
+            e_raw[i] = dd[i] + bias;
+            e_dt[i] = ev ? (p.delta_softplus ? softplus_fast(e_raw[i]) : e_raw[i]) : 0.f;
+            e_g[i] = ev ? go[i] : 0.f;
+            sX[buf][c * kXS + 2 * rs + i] = make_float4(e_dt[i], e_dt[i] * e_u[i], e_u[i], e_g[i]);
         }
+        const bool bv_ok = j * kFT + 4 * st_q < L;   // L is a multiple of 4: the four exist or none do
+        float v[4];
+        unpack2<T>(r.bc0, v[0], v[1]);
+        unpack2<T>(r.bc1, v[2], v[3]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sBC[(4 * st_q + i) * 36 + st_tensor * 16 + st_n] = v[i];
+        for (int i = 0; i < 4; ++i) sBC[buf][(4 * st_q + i) * 36 + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
     };
 
     // Pass 1: the states before every tile, into the checkpoint workspace.
     float h0 = 0.f, h1 = 0.f;
+    TileRaw<T> nxt = load(0, false);
     for (int64_t j = 0; j < n_tiles; ++j) {
-        *reinterpret_cast<float2 *>(ws.ck + ((j * p.batch + b) * p.dim + d) * 16 + n0) = make_float2(h0, h1);
-        prologue(j, false);
+        const int buf = int(j % kBufs);
+        *reinterpret_cast<float2 *>(ckp + j * ck_tile) = make_float2(h0, h1);
+        commit(nxt, j, buf, false);
+        nxt = load(j + 1, false);
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < kFT; ++t) {
-            const float4 x = sX[c * kXS + t];
-            const float2 bv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + n0]);
+            const float4 x = sX[buf][c * kXS + t];
+            const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + n0]);
             h0 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A20), h0, x.y * bv.x);
             h1 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A21), h1, x.y * bv.y);
         }
-        __syncthreads();
+        if (kBufs == 1) __syncthreads();   // reads done before the next commit rewrites the buffer
     }
+    __syncthreads();   // the checkpoints stored above are read back by this lane only
 
     // Pass 2: tiles in reverse order.
     float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f;   // state adjoints, decays of the step after
     float dA0 = 0.f, dA1 = 0.f, dD_acc = 0.f, dbias_acc = 0.f;
+    nxt = load(n_tiles - 1, true);
     for (int64_t j = n_tiles - 1; j >= 0; --j) {
         const int64_t t0 = j * kFT;
-        prologue(j, true);
-        const float2 hc = *reinterpret_cast<const float2 *>(ws.ck + ((j * p.batch + b) * p.dim + d) * 16 + n0);
+        const int buf = int(j % kBufs);
+        const float2 hc = nxt.hc;
+        commit(nxt, j, buf, true);
+        nxt = load(j - 1, true);
         __syncthreads();
         float hs0[kFT], hs1[kFT], as0[kFT], as1[kFT];
         {
             float x0 = hc.x, x1 = hc.y;
 #pragma unroll
             for (int t = 0; t < kFT; ++t) {
-                const float4 x = sX[c * kXS + t];
-                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + n0]);
+                const float4 x = sX[buf][c * kXS + t];
+                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + n0]);
                 as0[t] = __builtin_amdgcn_exp2f(x.x * A20);
                 as1[t] = __builtin_amdgcn_exp2f(x.x * A21);
                 x0 = __builtin_fmaf(as0[t], x0, x.y * bv.x);
@@ -400,18 +438,17 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 #pragma unroll
             for (int s = kFH - 1; s >= 0; --s) {
                 const int t = half * kFH + s;
-                const float4 x = sX[c * kXS + t];          // dt', dt'u, u, g
-                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + n0]);
-                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[t * 36 + 16 + n0]);
+                const float4 x = sX[buf][c * kXS + t];     // dt', dt'u, u, g
+                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + n0]);
+                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + 16 + n0]);
                 gh0 = __builtin_fmaf(an0, gh0, x.w * cv.x);
                 gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
                 const float ah0 = __builtin_fmaf(-x.y, bv.x, hs0[t]);   // a_t h_{t-1}
                 const float ah1 = __builtin_fmaf(-x.y, bv.y, hs1[t]);
-                float *red = &sRed[(s * 16 + n0) * 2 * kRS + c];
-                red[0] = gh0 * x.y;                        // dB (state n0)
-                red[kRS] = x.w * hs0[t];                   // dC (state n0)
-                red[2 * kRS] = gh1 * x.y;                  // dB (state n0 + 1)
-                red[3 * kRS] = x.w * hs1[t];               // dC (state n0 + 1)
+                sRed[red_at(0, n0, s, c)] = gh0 * x.y;          // dB contributions
+                sRed[red_at(0, n0 + 1, s, c)] = gh1 * x.y;
+                sRed[red_at(1, n0, s, c)] = x.w * hs0[t];       // dC contributions
+                sRed[red_at(1, n0 + 1, s, c)] = x.w * hs1[t];
                 pu[s] = __builtin_fmaf(gh1, bv.y, gh0 * bv.x);
                 pd[s] = __builtin_fmaf(gh1, __builtin_fmaf(A1, ah1, x.z * bv.y), gh0 * __builtin_fmaf(A0, ah0, x.z * bv.x));
                 dA_t0 = __builtin_fmaf(gh0 * x.x, ah0, dA_t0);
@@ -428,30 +465,26 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             pq[0] = make_float4(pd[0], pd[1], pd[2], pd[3]);
             pq[1] = make_float4(pd[4], pd[5], pd[6], pd[7]);
             __syncthreads();
-            // dB / dC of this half summed over the block's 16 channels: lane -> tensor tid / 64,
-            // state (tid / 4) % 16, steps 2 (tid % 4), +1.
-            {
-                const int tn = (tid >> 2) & 15, tt = 2 * (tid & 3), tz = tid >> 6;
-                float sum[2];
+            // dB / dC of this half summed over the block's 16 channels: rows (tensor, state, step)
+            // tid and tid + 128, step fastest, so consecutive lanes read consecutive steps.
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const float4 *rv = reinterpret_cast<const float4 *>(&sRed[((tt + i) * 16 + tn) * 2 * kRS + tz * kRS]);
-                    float acc = 0.f;
+            for (int k = 0; k < 2; ++k) {
+                const int row = tid + 128 * k;
+                const int tz = row >> 7, tn = (row >> 3) & 15, tt = row & 7;
+                const float4 *rv = reinterpret_cast<const float4 *>(&sRed[red_at(tz, tn, tt, 0)]);
+                float q4[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float4 v = rv[q];
-                        acc += v.x; acc += v.y; acc += v.z; acc += v.w;
-                    }
-                    sum[i] = acc;
+                for (int q = 0; q < 4; ++q) {   // pairwise: short dependency chains, fixed order
+                    const float4 v = rv[q];
+                    q4[q] = (v.x + v.y) + (v.z + v.w);
                 }
+                const float acc = (q4[0] + q4[1]) + (q4[2] + q4[3]);
                 const int64_t ts = t0 + half * kFH + tt;
-                if (ts < L) {
-                    float *dst = (tz == 0 ? ws.partB : ws.partC) +
-                                 (((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * L + ts;
-                    *reinterpret_cast<float2 *>(dst) = make_float2(sum[0], sum[1]);
-                }
+                if (ts < L)
+                    (tz == 0 ? ws.partB : ws.partC)[(((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * L + ts] = acc;
             }
-            // du / ddelta of the steps this lane owns, if they are in this half.
+            // du / ddelta of the steps this lane owns, if they are in this half: the 8 slots' partial
+            // sums over states, added in slot order.
             if ((rs >> 2) == half) {
                 const int sl = 2 * (rs & 3);               // first owned step within the half
                 const int64_t te = t0 + 2 * rs;
@@ -468,7 +501,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
                         du[i] = __builtin_fmaf(Dv, e_g[i], e_dt[i] * su[i]);
-                        const float sg = 1.f / (1.f + __builtin_amdgcn_exp2f(-e_raw[i] * kLog2e));
+                        const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-e_raw[i] * kLog2e));
                         ddl[i] = (p.delta_softplus && e_raw[i] <= 20.f) ? sd[i] * sg : sd[i];
                         dD_acc = __builtin_fmaf(e_g[i], e_u[i], dD_acc);
                         dbias_acc += ddl[i];
