@@ -1,0 +1,245 @@
+// mm_conv1d.hip -- gfx950 causal depthwise conv1d (forward and decode update), the step before the
+// selective scan in every Mamba block.
+//
+// Reference behaviour: causal_conv1d_fn / causal_conv1d_update of the package causal-conv1d that the
+// reference imports (mamba_simplemotif.py:16-19; pinned >= 1.2.0, not vendored), whose in-tree
+// fallback is mamba_simplemotif.py:298-299 (forward) and :353-358 (update):
+//   out[b,d,t] = act(bias[d] + sum_{k<W} w[d,k] x[b,d,t-(W-1)+k]),  x before t = 0 from
+//   initial_states (or 0); the update appends each new token to the state and takes the dot of the
+//   state's last W entries with w.
+// Both are HBM-bound (2 bytes in, 2 out per element for 16-bit data): the forward gives each lane 8
+// consecutive outputs of one row -- one 16-byte load of its inputs, one of the 8 before them (the
+// halo of W-1 <= 7 inputs), the row's W weights in registers, one 16-byte store; the update gives
+// each lane one (batch, channel) row and keeps the last W-1 inputs in registers.
+#include <hip/hip_runtime.h>
+
+#include <stdio.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "mm_common.h"
+#include "mm_conv1d.h"
+#include "mm_internal.h"
+
+namespace mm {
+namespace conv {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 8;        // outputs per lane
+
+// One element of a tensor whose dtype is known only at run time (weights, bias, states).
+__device__ __forceinline__ float load_any(const void *p, mm_dtype dt, int64_t i) {
+    switch (dt) {
+        case MM_FLOAT32: return reinterpret_cast<const float *>(p)[i];
+        case MM_FLOAT16: return to_f32(reinterpret_cast<const f16_t *>(p)[i]);
+        default: return to_f32(reinterpret_cast<const bf16_t *>(p)[i]);
+    }
+}
+__device__ __forceinline__ void store_any(void *p, mm_dtype dt, int64_t i, float v) {
+    switch (dt) {
+        case MM_FLOAT32: reinterpret_cast<float *>(p)[i] = v; break;
+        case MM_FLOAT16: reinterpret_cast<f16_t *>(p)[i] = from_f32<f16_t>(v); break;
+        default: reinterpret_cast<bf16_t *>(p)[i] = from_f32<bf16_t>(v); break;
+    }
+}
+
+// VEC: rows 16-byte aligned, seqlen a multiple of 8 (every chunk is whole and vector-movable).
+template <typename T, int W, bool VEC>
+__global__ void __launch_bounds__(kThreads)
+conv1d_fwd_kernel(const mm_conv1d_fwd_params p) {
+    const int64_t t0 = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * kChunk;
+    const int64_t d = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int64_t L = p.seqlen;
+    if (t0 >= L) return;
+    const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
+    T *orow = reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride;
+
+    float w[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) w[k] = load_any(p.weight, p.wtype, d * p.weight_d_stride + k * p.weight_w_stride);
+    const float bias = p.bias ? load_any(p.bias, p.wtype, d * p.bias_stride) : 0.f;
+
+    // xs[0..7]: the 8 inputs before the chunk (initial states or 0 before t = 0); xs[8..15]: the chunk.
+    float xs[2 * kChunk];
+    if (VEC) {
+        load8(xr + t0, xs + kChunk);
+        if (t0 >= kChunk) load8(xr + t0 - kChunk, xs);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            xs[kChunk + i] = t0 + i < L ? to_f32(xr[t0 + i]) : 0.f;
+            xs[i] = t0 >= kChunk ? to_f32(xr[t0 - kChunk + i]) : 0.f;
+        }
+    }
+    if (t0 < kChunk) {  // the first chunk of the row: the W - 1 positions before t = 0
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            const int j = i - kChunk + (W - 1);   // index into initial_states
+            xs[i] = (p.initial_states && j >= 0)
+                ? load_any(p.initial_states, p.itype, b * p.init_batch_stride + d * p.init_d_stride + j * p.init_w_stride)
+                : 0.f;
+        }
+    }
+    float o[kChunk];
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+        float acc = bias;
+#pragma unroll
+        for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], xs[kChunk + i - (W - 1) + k], acc);
+        o[i] = p.silu ? acc * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-acc * kLog2e)) : acc;
+    }
+    if (VEC) {
+        store8(orow + t0, o);
+    } else {
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i)
+            if (t0 + i < L) orow[t0 + i] = from_f32<T>(o[i]);
+    }
+    // The last W - 1 inputs (initial states where the row is shorter): written by the lane holding
+    // position L - 1; all of them lie in xs.
+    if (p.final_states && t0 <= L - 1 && L - 1 < t0 + kChunk) {
+#pragma unroll
+        for (int j = 0; j < W - 1; ++j) {
+            const int64_t pos = L - (W - 1) + j;      // position in the row, may be negative
+            const int idx = int(pos - t0) + kChunk;   // index into xs (>= 0: pos >= t0 - 7)
+            store_any(p.final_states, p.itype, b * p.final_batch_stride + d * p.final_d_stride + j * p.final_w_stride,
+                      xs[idx]);
+        }
+    }
+}
+
+// One lane per (batch, channel) row.
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+conv1d_update_kernel(const mm_conv1d_update_params p) {
+    const int64_t row = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (row >= p.batch * p.dim) return;
+    const int64_t b = row / p.dim;
+    const int64_t d = row - b * p.dim;
+    const int W = int(p.width);
+    const int64_t S = p.state_len;
+    const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
+    T *orow = reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride;
+    const int64_t sbase = b * p.state_batch_stride + d * p.state_d_stride;
+
+    float w[MM_CONV1D_MAX_WIDTH], win[MM_CONV1D_MAX_WIDTH];
+#pragma unroll
+    for (int k = 0; k < MM_CONV1D_MAX_WIDTH; ++k) {
+        w[k] = k < W ? load_any(p.weight, p.wtype, d * p.weight_d_stride + k * p.weight_w_stride) : 0.f;
+        // Window slot k holds the input k steps before the current token once the token is shifted
+        // in (slot 0: the token itself); before the first shift slot k holds state[S - 1 - k].
+        win[k] = (k < W - 1) ? load_any(p.conv_state, p.stype, sbase + (S - 1 - k) * p.state_l_stride) : 0.f;
+    }
+    const float bias = p.bias ? load_any(p.bias, p.wtype, d * p.bias_stride) : 0.f;
+    for (int64_t t = 0; t < p.seqlen; ++t) {
+#pragma unroll
+        for (int k = MM_CONV1D_MAX_WIDTH - 1; k >= 1; --k) win[k] = win[k - 1];
+        win[0] = to_f32(xr[t * p.x_l_stride]);
+        float acc = bias;
+#pragma unroll
+        for (int k = 0; k < MM_CONV1D_MAX_WIDTH; ++k)
+            if (k < W) acc = __builtin_fmaf(w[W - 1 - k], win[k], acc);
+        const float o = p.silu ? acc * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-acc * kLog2e)) : acc;
+        orow[t * p.out_l_stride] = from_f32<T>(o);
+    }
+    // New state: the last S entries of (old state ++ new tokens). Ascending j reads position
+    // j + seqlen of the old state before anything at or above it is written.
+    for (int64_t j = 0; j < S; ++j) {
+        const int64_t src = j + p.seqlen;
+        const float v = src < S ? load_any(p.conv_state, p.stype, sbase + src * p.state_l_stride)
+                                : to_f32(xr[(src - S) * p.x_l_stride]);
+        store_any(p.conv_state, p.stype, sbase + j * p.state_l_stride, v);
+    }
+}
+
+bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+template <typename T, int W>
+int launch_fwd_w(const mm_conv1d_fwd_params &p, hipStream_t s) {
+    const int64_t eb = int64_t(sizeof(T));
+    const bool vec = p.seqlen % kChunk == 0 && aligned16(p.x) && aligned16(p.out) && (p.x_batch_stride * eb) % 16 == 0 &&
+                     (p.x_d_stride * eb) % 16 == 0 && (p.out_batch_stride * eb) % 16 == 0 && (p.out_d_stride * eb) % 16 == 0;
+    const int64_t chunks = (p.seqlen + kChunk - 1) / kChunk;
+    dim3 grid(unsigned((chunks + kThreads - 1) / kThreads), unsigned(p.dim), unsigned(p.batch));
+    if (vec)
+        hipLaunchKernelGGL((conv1d_fwd_kernel<T, W, true>), grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((conv1d_fwd_kernel<T, W, false>), grid, dim3(kThreads), 0, s, p);
+    return launch_status("conv1d_fwd");
+}
+
+template <typename T>
+int launch_fwd(const mm_conv1d_fwd_params &p, hipStream_t s) {
+    switch (p.width) {
+        case 1: return launch_fwd_w<T, 1>(p, s);
+        case 2: return launch_fwd_w<T, 2>(p, s);
+        case 3: return launch_fwd_w<T, 3>(p, s);
+        case 4: return launch_fwd_w<T, 4>(p, s);
+        case 5: return launch_fwd_w<T, 5>(p, s);
+        case 6: return launch_fwd_w<T, 6>(p, s);
+        case 7: return launch_fwd_w<T, 7>(p, s);
+        default: return launch_fwd_w<T, 8>(p, s);
+    }
+}
+
+template <typename T>
+int launch_update(const mm_conv1d_update_params &p, hipStream_t s) {
+    const int64_t rows = p.batch * p.dim;
+    hipLaunchKernelGGL((conv1d_update_kernel<T>), dim3(unsigned((rows + kThreads - 1) / kThreads)), dim3(kThreads), 0,
+                       s, p);
+    return launch_status("conv1d_update");
+}
+
+bool dtype_ok(mm_dtype t) { return t == MM_FLOAT32 || t == MM_FLOAT16 || t == MM_BFLOAT16; }
+
+int invalid(const char *msg) { return set_error(MM_ERR_INVALID_ARGUMENT, msg); }
+
+}  // namespace conv
+}  // namespace mm
+
+extern "C" {
+
+int mm_causal_conv1d_fwd(const mm_conv1d_fwd_params *params, void *stream) {
+    using namespace mm::conv;
+    if (!params) return invalid("mm_causal_conv1d_fwd: params is NULL");
+    const mm_conv1d_fwd_params &p = *params;
+    if (!dtype_ok(p.itype) || !dtype_ok(p.wtype)) return invalid("mm_causal_conv1d_fwd: unknown dtype");
+    if (p.batch < 0 || p.dim < 0 || p.seqlen < 0) return invalid("mm_causal_conv1d_fwd: negative size");
+    if (p.width < 1 || p.width > MM_CONV1D_MAX_WIDTH)
+        return invalid("mm_causal_conv1d_fwd: width must be in [1, 8]");
+    if (p.batch > 65535 || p.dim > 65535)
+        return mm::set_error(MM_ERR_UNSUPPORTED, "mm_causal_conv1d_fwd: batch and dim must be <= 65535");
+    if (p.batch == 0 || p.dim == 0 || p.seqlen == 0) return MM_OK;
+    if (!p.x || !p.weight || !p.out) return invalid("mm_causal_conv1d_fwd: x, weight and out are required");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (p.itype) {
+        case MM_FLOAT32: return launch_fwd<float>(p, s);
+        case MM_FLOAT16: return launch_fwd<mm::f16_t>(p, s);
+        default: return launch_fwd<mm::bf16_t>(p, s);
+    }
+}
+
+int mm_causal_conv1d_update(const mm_conv1d_update_params *params, void *stream) {
+    using namespace mm::conv;
+    if (!params) return invalid("mm_causal_conv1d_update: params is NULL");
+    const mm_conv1d_update_params &p = *params;
+    if (!dtype_ok(p.itype) || !dtype_ok(p.wtype) || !dtype_ok(p.stype))
+        return invalid("mm_causal_conv1d_update: unknown dtype");
+    if (p.batch < 0 || p.dim < 0 || p.seqlen < 0) return invalid("mm_causal_conv1d_update: negative size");
+    if (p.width < 1 || p.width > MM_CONV1D_MAX_WIDTH)
+        return invalid("mm_causal_conv1d_update: width must be in [1, 8]");
+    if (p.state_len < p.width - 1) return invalid("mm_causal_conv1d_update: state_len must be >= width - 1");
+    if (p.batch == 0 || p.dim == 0) return MM_OK;
+    if (!p.x || !p.conv_state || !p.weight || !p.out)
+        return invalid("mm_causal_conv1d_update: x, conv_state, weight and out are required");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (p.itype) {
+        case MM_FLOAT32: return launch_update<float>(p, s);
+        case MM_FLOAT16: return launch_update<mm::f16_t>(p, s);
+        default: return launch_update<mm::bf16_t>(p, s);
+    }
+}
+
+}  // extern "C"

@@ -18,6 +18,7 @@
 
 #include <vector>
 
+#include "mm_conv1d.h"
 #include "mm_scan.h"
 
 namespace {
@@ -411,6 +412,103 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
     return result;
 }
 
+
+mm_dtype conv_dtype(const at::Tensor &t, const char *what) {
+    const auto st = t.scalar_type();
+    TORCH_CHECK(st == at::ScalarType::Float || st == at::ScalarType::Half || st == at::ScalarType::BFloat16,
+                what, " must be float32, float16 or bfloat16");
+    return to_mm(st);
+}
+
+// causal_conv1d_fwd (package causal-conv1d; fallback mamba_simplemotif.py:298-299): out, and the
+// last width - 1 inputs into final_states_out when given.
+at::Tensor conv1d_fwd(const at::Tensor &x, const at::Tensor &weight, const c10::optional<at::Tensor> &bias_,
+                      const c10::optional<at::Tensor> &initial_states_, const c10::optional<at::Tensor> &final_states_out_,
+                      bool silu) {
+    TORCH_CHECK(x.is_cuda() && weight.is_cuda(), "x and weight must be on the GPU");
+    TORCH_CHECK(x.dim() == 3, "x must have shape (batch, dim, seqlen)");
+    TORCH_CHECK(x.stride(-1) == 1 || x.size(-1) == 1, "x must be contiguous along seqlen");
+    const int64_t batch = x.size(0), dim = x.size(1), seqlen = x.size(2);
+    TORCH_CHECK(weight.dim() == 2 && weight.size(0) == dim, "weight must have shape (dim, width)");
+    const int64_t width = weight.size(1);
+    TORCH_CHECK(width >= 1 && width <= MM_CONV1D_MAX_WIDTH, "width must be between 1 and 8");
+    at::Tensor out = torch::empty_like(x);
+    mm_conv1d_fwd_params p;
+    std::memset(&p, 0, sizeof(p));
+    p.batch = batch; p.dim = dim; p.seqlen = seqlen; p.width = width;
+    p.itype = conv_dtype(x, "x");
+    p.wtype = conv_dtype(weight, "weight");
+    p.silu = silu;
+    p.x = x.data_ptr(); p.x_batch_stride = x.stride(0); p.x_d_stride = x.stride(1);
+    p.out = out.data_ptr(); p.out_batch_stride = out.stride(0); p.out_d_stride = out.stride(1);
+    p.weight = weight.data_ptr(); p.weight_d_stride = weight.stride(0); p.weight_w_stride = weight.stride(1);
+    if (bias_.has_value()) {
+        const at::Tensor &bias = bias_.value();
+        TORCH_CHECK(bias.is_cuda() && bias.dim() == 1 && bias.size(0) == dim, "bias must have shape (dim,)");
+        TORCH_CHECK(bias.scalar_type() == weight.scalar_type(), "bias must have the dtype of weight");
+        p.bias = bias.data_ptr(); p.bias_stride = bias.stride(0);
+    }
+    if (initial_states_.has_value()) {
+        const at::Tensor &ini = initial_states_.value();
+        TORCH_CHECK(ini.is_cuda() && ini.dim() == 3 && ini.size(0) == batch && ini.size(1) == dim && ini.size(2) == width - 1,
+                    "initial_states must have shape (batch, dim, width - 1)");
+        TORCH_CHECK(ini.scalar_type() == x.scalar_type(), "initial_states must have the dtype of x");
+        p.initial_states = ini.data_ptr();
+        p.init_batch_stride = ini.stride(0); p.init_d_stride = ini.stride(1); p.init_w_stride = ini.stride(2);
+    }
+    if (final_states_out_.has_value()) {
+        const at::Tensor &fin = final_states_out_.value();
+        TORCH_CHECK(fin.is_cuda() && fin.dim() == 3 && fin.size(0) == batch && fin.size(1) == dim && fin.size(2) == width - 1,
+                    "final_states_out must have shape (batch, dim, width - 1)");
+        TORCH_CHECK(fin.scalar_type() == x.scalar_type(), "final_states_out must have the dtype of x");
+        p.final_states = fin.data_ptr();
+        p.final_batch_stride = fin.stride(0); p.final_d_stride = fin.stride(1); p.final_w_stride = fin.stride(2);
+    }
+    const c10::DeviceGuard device_guard{x.device()};
+    check_rc(mm_causal_conv1d_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_causal_conv1d_fwd");
+    return out;
+}
+
+// causal_conv1d_update (package causal-conv1d; fallback mamba_simplemotif.py:353-358): x (batch, dim)
+// or (batch, dim, seqlen), conv_state (batch, dim, state_len) updated in place.
+at::Tensor conv1d_update(const at::Tensor &x, const at::Tensor &conv_state, const at::Tensor &weight,
+                         const c10::optional<at::Tensor> &bias_, bool silu) {
+    TORCH_CHECK(x.is_cuda() && conv_state.is_cuda() && weight.is_cuda(), "x, conv_state and weight must be on the GPU");
+    TORCH_CHECK(x.dim() == 2 || x.dim() == 3, "x must have shape (batch, dim) or (batch, dim, seqlen)");
+    const at::Tensor x3 = x.dim() == 2 ? x.unsqueeze(-1) : x;
+    const int64_t batch = x3.size(0), dim = x3.size(1), seqlen = x3.size(2);
+    TORCH_CHECK(weight.dim() == 2 && weight.size(0) == dim, "weight must have shape (dim, width)");
+    const int64_t width = weight.size(1);
+    TORCH_CHECK(width >= 1 && width <= MM_CONV1D_MAX_WIDTH, "width must be between 1 and 8");
+    TORCH_CHECK(conv_state.dim() == 3 && conv_state.size(0) == batch && conv_state.size(1) == dim,
+                "conv_state must have shape (batch, dim, state_len)");
+    TORCH_CHECK(conv_state.size(2) >= width - 1, "conv_state must hold at least width - 1 steps");
+    at::Tensor out = torch::empty_like(x3);
+    mm_conv1d_update_params p;
+    std::memset(&p, 0, sizeof(p));
+    p.batch = batch; p.dim = dim; p.seqlen = seqlen; p.width = width; p.state_len = conv_state.size(2);
+    p.itype = conv_dtype(x, "x");
+    p.wtype = conv_dtype(weight, "weight");
+    p.stype = conv_dtype(conv_state, "conv_state");
+    p.silu = silu;
+    p.x = x3.data_ptr(); p.x_batch_stride = x3.stride(0); p.x_d_stride = x3.stride(1); p.x_l_stride = x3.stride(2);
+    p.conv_state = conv_state.data_ptr();
+    p.state_batch_stride = conv_state.stride(0); p.state_d_stride = conv_state.stride(1);
+    p.state_l_stride = conv_state.stride(2);
+    p.out = out.data_ptr(); p.out_batch_stride = out.stride(0); p.out_d_stride = out.stride(1);
+    p.out_l_stride = out.stride(2);
+    p.weight = weight.data_ptr(); p.weight_d_stride = weight.stride(0); p.weight_w_stride = weight.stride(1);
+    if (bias_.has_value()) {
+        const at::Tensor &bias = bias_.value();
+        TORCH_CHECK(bias.is_cuda() && bias.dim() == 1 && bias.size(0) == dim, "bias must have shape (dim,)");
+        TORCH_CHECK(bias.scalar_type() == weight.scalar_type(), "bias must have the dtype of weight");
+        p.bias = bias.data_ptr(); p.bias_stride = bias.stride(0);
+    }
+    const c10::DeviceGuard device_guard{x.device()};
+    check_rc(mm_causal_conv1d_update(&p, c10::hip::getCurrentHIPStream().stream()), "mm_causal_conv1d_update");
+    return x.dim() == 2 ? out.squeeze(-1) : out;
+}
+
 at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::Tensor &dt, const at::Tensor &A,
                         const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                         const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &dt_bias_,
@@ -532,5 +630,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           pybind11::arg("state"), pybind11::arg("x"), pybind11::arg("dt"), pybind11::arg("A"), pybind11::arg("B"),
           pybind11::arg("C"), pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
           pybind11::arg("dt_bias") = pybind11::none(), pybind11::arg("dt_softplus") = false);
+    m.def("conv1d_fwd", &conv1d_fwd, "Causal depthwise conv1d forward",
+          pybind11::arg("x"), pybind11::arg("weight"), pybind11::arg("bias") = pybind11::none(),
+          pybind11::arg("initial_states") = pybind11::none(), pybind11::arg("final_states_out") = pybind11::none(),
+          pybind11::arg("silu") = false);
+    m.def("conv1d_update", &conv1d_update, "Causal depthwise conv1d decode update (in place on conv_state)",
+          pybind11::arg("x"), pybind11::arg("conv_state"), pybind11::arg("weight"),
+          pybind11::arg("bias") = pybind11::none(), pybind11::arg("silu") = false);
     m.def("abi_version", []() { return mm_abi_version(); });
 }

@@ -4,8 +4,11 @@ Public API (drop-in for the reference's):
   selective_scan_fn, SelectiveScanFn   (mamba_ssm/ops/selective_scan_interface.py:24-61, 237-259)
   SelectiveScanPQFn                    (selective_scan_interface.py:93-150, forward; with z too)
   selective_state_update               (upstream mamba_ssm.ops.triton.selective_state_update)
+  causal_conv1d_fn, causal_conv1d_update (package causal-conv1d, mamba_simplemotif.py:16-19)
 """
 from .selective_scan import SelectiveScanFn, SelectiveScanPQFn, selective_scan_fn
+from .causal_conv1d import causal_conv1d_fn, causal_conv1d_update
 from .state_update import selective_state_update
 
-__all__ = ["SelectiveScanFn", "SelectiveScanPQFn", "selective_scan_fn", "selective_state_update"]
+__all__ = ["SelectiveScanFn", "SelectiveScanPQFn", "selective_scan_fn", "selective_state_update",
+           "causal_conv1d_fn", "causal_conv1d_update"]

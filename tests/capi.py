@@ -10,6 +10,7 @@ import torch
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(REPO, "include", "mm_scan.h")
+HEADERS = [os.path.join(REPO, "include", h) for h in ("mm_scan.h", "mm_conv1d.h")]
 
 i64, i32, vp = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
 
@@ -62,6 +63,26 @@ class ScanBwdParams(ctypes.Structure):
                 ("workspace", vp), ("workspace_bytes", i64)]
 
 
+class Conv1dFwdParams(ctypes.Structure):
+    _fields_ = [("batch", i64), ("dim", i64), ("seqlen", i64), ("width", i64),
+                ("itype", i32), ("wtype", i32), ("silu", i32),
+                ("x", vp), ("weight", vp), ("bias", vp), ("initial_states", vp), ("out", vp), ("final_states", vp),
+                ("x_batch_stride", i64), ("x_d_stride", i64), ("out_batch_stride", i64), ("out_d_stride", i64),
+                ("weight_d_stride", i64), ("weight_w_stride", i64), ("bias_stride", i64),
+                ("init_batch_stride", i64), ("init_d_stride", i64), ("init_w_stride", i64),
+                ("final_batch_stride", i64), ("final_d_stride", i64), ("final_w_stride", i64)]
+
+
+class Conv1dUpdateParams(ctypes.Structure):
+    _fields_ = [("batch", i64), ("dim", i64), ("seqlen", i64), ("width", i64), ("state_len", i64),
+                ("itype", i32), ("wtype", i32), ("stype", i32), ("silu", i32),
+                ("x", vp), ("conv_state", vp), ("weight", vp), ("bias", vp), ("out", vp),
+                ("x_batch_stride", i64), ("x_d_stride", i64), ("x_l_stride", i64),
+                ("state_batch_stride", i64), ("state_d_stride", i64), ("state_l_stride", i64),
+                ("out_batch_stride", i64), ("out_d_stride", i64), ("out_l_stride", i64),
+                ("weight_d_stride", i64), ("weight_w_stride", i64), ("bias_stride", i64)]
+
+
 class StateUpdateParams(ctypes.Structure):
     _fields_ = [("batch", i64), ("dim", i64), ("dstate", i64), ("n_groups", i64),
                 ("itype", i32), ("dt_softplus", i32),
@@ -78,8 +99,8 @@ class StateUpdateParams(ctypes.Structure):
 
 
 def header_functions():
-    """Names of the functions include/mm_scan.h declares."""
-    text = open(HEADER).read()
+    """Names of the functions the headers in include/ declare."""
+    text = "\n".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mm_\w+)\s*\(", text, re.M)))
 
 
@@ -97,6 +118,10 @@ def load():
     lib.mm_scan_bwd.restype = ctypes.c_int
     lib.mm_scan_bwd_workspace_size.argtypes = [ctypes.POINTER(ScanBwdParams)]
     lib.mm_scan_bwd_workspace_size.restype = ctypes.c_int64
+    lib.mm_causal_conv1d_fwd.argtypes = [ctypes.POINTER(Conv1dFwdParams), vp]
+    lib.mm_causal_conv1d_fwd.restype = ctypes.c_int
+    lib.mm_causal_conv1d_update.argtypes = [ctypes.POINTER(Conv1dUpdateParams), vp]
+    lib.mm_causal_conv1d_update.restype = ctypes.c_int
     return lib
 
 

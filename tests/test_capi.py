@@ -15,15 +15,17 @@ def test_library_exports_every_header_function():
     lib = capi.load()
     names = capi.header_functions()
     assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_scan_bwd", "mm_scan_bwd_workspace_size",
-                          "mm_state_update", "mm_last_error", "mm_abi_version"}
+                          "mm_state_update", "mm_last_error", "mm_abi_version", "mm_causal_conv1d_fwd",
+                          "mm_causal_conv1d_update"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 4
+    assert lib.mm_abi_version() == 5
 
 
 def _c_layout(struct, fields, tmp_path):
     src = tmp_path / "layout.c"
-    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mm_scan.h"', 'int main(void) {',
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mm_scan.h"', '#include "mm_conv1d.h"',
+             'int main(void) {',
              f'  printf("%zu\\n", sizeof({struct}));']
     lines += [f'  printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
     lines += ['  return 0;', '}']
@@ -35,6 +37,8 @@ def _c_layout(struct, fields, tmp_path):
 
 @pytest.mark.parametrize("cname,pystruct", [("mm_scan_fwd_params", capi.ScanFwdParams),
                                             ("mm_scan_bwd_params", capi.ScanBwdParams),
+                                            ("mm_conv1d_fwd_params", capi.Conv1dFwdParams),
+                                            ("mm_conv1d_update_params", capi.Conv1dUpdateParams),
                                             ("mm_state_update_params", capi.StateUpdateParams)])
 def test_struct_layout_matches_header(tmp_path, cname, pystruct):
     fields = [f for f, _ in pystruct._fields_]
@@ -205,3 +209,43 @@ def test_scan_bwd_rejects_invalid_params():
     assert lib.mm_scan_bwd_workspace_size(ctypes.byref(p)) == 0
     p.dstate, p.batch = 16, 0   # nothing to do: returns before touching any pointer or the GPU
     assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_OK
+
+
+def test_conv1d_rejects_invalid_params():
+    lib = capi.load()
+    assert lib.mm_causal_conv1d_fwd(None, None) == capi.MM_ERR_INVALID_ARGUMENT
+    p = capi.Conv1dFwdParams()
+    p.batch, p.dim, p.seqlen, p.width, p.itype, p.wtype = 2, 8, 16, 4, 2, 2
+    assert lib.mm_causal_conv1d_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "required" in lib.mm_last_error().decode()
+    p.width = 9
+    assert lib.mm_causal_conv1d_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "width" in lib.mm_last_error().decode()
+    p.width, p.wtype = 4, 7
+    assert lib.mm_causal_conv1d_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    q = capi.Conv1dUpdateParams()
+    q.batch, q.dim, q.seqlen, q.width, q.state_len = 2, 8, 1, 4, 2
+    q.x = q.conv_state = q.weight = q.out = 0x1000
+    assert lib.mm_causal_conv1d_update(ctypes.byref(q), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "state_len" in lib.mm_last_error().decode()
+    q.batch = 0
+    q.state_len = 4
+    assert lib.mm_causal_conv1d_update(ctypes.byref(q), None) == capi.MM_OK
+
+
+def test_causal_conv1d_import_paths_and_argument_errors():
+    import causal_conv1d
+    import causal_conv1d.cpp_functions as cf
+    import motif_mamba_amd
+    assert causal_conv1d.causal_conv1d_fn is motif_mamba_amd.causal_conv1d_fn
+    assert causal_conv1d.causal_conv1d_update is motif_mamba_amd.causal_conv1d_update
+    x = torch.zeros(1, 4, 8)
+    w = torch.zeros(4, 4)
+    with pytest.raises(NotImplementedError):
+        causal_conv1d.causal_conv1d_fn(x, w, activation="relu")
+    with pytest.raises(NotImplementedError):
+        causal_conv1d.causal_conv1d_fn(x, w, seq_idx=torch.zeros(1, 8, dtype=torch.int32))
+    with pytest.raises(NotImplementedError):
+        cf.causal_conv1d_bwd_function()
+    with pytest.raises(RuntimeError):       # CPU tensors are refused by the binding
+        causal_conv1d.causal_conv1d_fn(x, w)

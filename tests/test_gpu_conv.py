@@ -1,0 +1,151 @@
+"""GPU parity of the causal depthwise conv1d (forward and decode update, mm_conv1d.hip) against the
+CPU oracle oracle/conv_ref.py (the Mamba module's torch fallback, mamba_simplemotif.py:298-299 and
+:353-358, and the published semantics of the causal-conv1d API the reference calls).
+Tolerances (north_star): fp32 rtol 1e-4 / atol 1e-5; bf16/fp16 rtol 3e-2 / atol 5e-2.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from oracle.conv_ref import causal_conv1d_ref, causal_conv1d_update_ref
+from tests import capi, fixtures
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg):
+    print(f"\n[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _close(a, b, dtype, what):
+    rtol, atol = fixtures.tolerances(dtype)
+    torch.testing.assert_close(a.float().cpu(), b.float().cpu(), rtol=rtol, atol=atol, msg=lambda m: f"{what}: {m}")
+
+
+def _case(seed, batch, dim, L, W, dtype, wdtype=None, with_bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, dim, L, generator=g).to(dtype)
+    w = (torch.randn(dim, W, generator=g) * 0.5).to(wdtype or dtype)
+    b = (torch.randn(dim, generator=g) * 0.1).to(wdtype or dtype) if with_bias else None
+    return x, w, b
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("W", [2, 3, 4])
+@pytest.mark.parametrize("L", [1, 7, 64, 1000])
+def test_conv_fwd(dtype, W, L):
+    _say(f"conv fwd {dtype} W={W} L={L}")
+    from causal_conv1d import causal_conv1d_fn
+    x, w, b = _case(700 + W + L, 2, 24, L, W, dtype)
+    for act in (None, "silu"):
+        got = causal_conv1d_fn(x.to(DEV), w.to(DEV), b.to(DEV), activation=act)
+        _close(got, causal_conv1d_ref(x, w, b, activation=act), dtype, f"act={act}")
+
+
+@pytest.mark.parametrize("W", [2, 4])
+def test_conv_fwd_initial_and_final_states(W):
+    _say(f"conv fwd initial/final states W={W}")
+    from causal_conv1d import causal_conv1d_fn
+    x, w, b = _case(710 + W, 2, 16, 40, W, torch.float32)
+    ini = torch.randn(2, 16, W - 1, generator=torch.Generator().manual_seed(711))
+    got, fin = causal_conv1d_fn(x.to(DEV), w.to(DEV), b.to(DEV), initial_states=ini.to(DEV),
+                                return_final_states=True, activation="silu")
+    ref, ref_fin = causal_conv1d_ref(x, w, b, initial_states=ini, return_final_states=True, activation="silu")
+    _close(got, ref, torch.float32, "out")
+    torch.testing.assert_close(fin.cpu(), ref_fin)
+    # shorter than width - 1: final states come partly from the initial states
+    got2, fin2 = causal_conv1d_fn(x[..., :1].to(DEV), w.to(DEV), None, initial_states=ini.to(DEV),
+                                  return_final_states=True)
+    ref2, rfin2 = causal_conv1d_ref(x[..., :1], w, None, initial_states=ini, return_final_states=True)
+    _close(got2, ref2, torch.float32, "short out")
+    torch.testing.assert_close(fin2.cpu(), rfin2)
+
+
+def test_conv_fwd_strided_and_mixed_dtypes():
+    """x as the first half of an xz projection (batch stride 2*dim*L), unaligned rows, fp32 weights on
+    bf16 activations (the module's float32 parameters under bf16 activations)."""
+    _say("conv fwd strided / mixed dtypes")
+    from causal_conv1d import causal_conv1d_fn
+    g = torch.Generator().manual_seed(720)
+    xz = torch.randn(2, 64, 256, generator=g).to(torch.bfloat16)
+    w = torch.randn(32, 4, generator=g) * 0.5
+    b = torch.randn(32, generator=g) * 0.1
+    x, _ = xz.to(DEV).chunk(2, dim=1)
+    got = causal_conv1d_fn(x, w.to(DEV), b.to(DEV), activation="silu")
+    _close(got, causal_conv1d_ref(xz[:, :32], w, b, activation="silu"), torch.bfloat16, "xz half")
+    odd = torch.zeros(2, 32, 257, dtype=torch.bfloat16, device=DEV)
+    odd[..., 1:] = xz[:, :32].to(DEV)
+    got2 = causal_conv1d_fn(odd[..., 1:], w.to(DEV), b.to(DEV), activation="silu")
+    _close(got2, causal_conv1d_ref(xz[:, :32], w, b, activation="silu"), torch.bfloat16, "unaligned")
+
+
+@pytest.mark.parametrize("dtype,sdtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                          (torch.float32, torch.float32), (torch.float16, torch.float16)])
+@pytest.mark.parametrize("state_len", [3, 4, 6])
+@pytest.mark.parametrize("seqlen", [1, 3])
+def test_conv_update(dtype, sdtype, state_len, seqlen):
+    _say(f"conv update {dtype} state {sdtype} S={state_len} seqlen={seqlen}")
+    from causal_conv1d import causal_conv1d_update
+    g = torch.Generator().manual_seed(730 + state_len + seqlen)
+    x = torch.randn(3, 40, seqlen, generator=g).to(dtype)
+    w = (torch.randn(40, 4, generator=g) * 0.5).to(dtype)
+    b = (torch.randn(40, generator=g) * 0.1).to(dtype)
+    st = torch.randn(3, 40, state_len, generator=g).to(sdtype)
+    st_ref = st.clone()
+    st_gpu = st.to(DEV)
+    xin = x[..., 0] if seqlen == 1 else x
+    got = causal_conv1d_update(xin.to(DEV), st_gpu, w.to(DEV), b.to(DEV), activation="silu")
+    ref = causal_conv1d_update_ref(xin, st_ref, w, b, activation="silu")
+    assert got.shape == xin.shape
+    _close(got, ref, dtype, "out")
+    _close(st_gpu, st_ref, sdtype, "state")
+
+
+def test_conv_prefill_then_decode_matches_forward():
+    """The module's hand-off (mamba_simplemotif.py:292-293): the state after a prefill is the last
+    d_conv inputs; decoding the following tokens one by one reproduces the forward of the sequence."""
+    _say("conv prefill + decode")
+    from causal_conv1d import causal_conv1d_fn, causal_conv1d_update
+    x, w, b = _case(740, 2, 48, 40, 4, torch.float32)
+    full = causal_conv1d_fn(x.to(DEV), w.to(DEV), b.to(DEV), activation="silu")
+    state = torch.nn.functional.pad(x[..., :32], (4 - 32, 0)).to(DEV).contiguous()   # last 4 inputs
+    for t in range(32, 40):
+        y = causal_conv1d_update(x[:, :, t].to(DEV), state, w.to(DEV), b.to(DEV), activation="silu")
+        torch.testing.assert_close(y, full[:, :, t], rtol=1e-5, atol=1e-6)
+
+
+def test_conv_fwd_benchmark_shape_rows():
+    """The conv before the config-2 scan (batch 4, 5120 channels, L 4096, bf16, width 4): a slice of
+    channels against the oracle."""
+    _say("conv fwd config-2 shape")
+    from causal_conv1d import causal_conv1d_fn
+    g = torch.Generator().manual_seed(750)
+    x = torch.randn(4, 5120, 4096, generator=g).to(torch.bfloat16)
+    w = (torch.randn(5120, 4, generator=g) * 0.5).to(torch.bfloat16)
+    b = (torch.randn(5120, generator=g) * 0.1).to(torch.bfloat16)
+    got = causal_conv1d_fn(x.to(DEV), w.to(DEV), b.to(DEV), activation="silu").cpu()
+    sl = slice(1000, 1064)
+    _close(got[:, sl], causal_conv1d_ref(x[:, sl], w[sl], b[sl], activation="silu"), torch.bfloat16, "rows")
+    _close(got[:, -8:], causal_conv1d_ref(x[:, -8:], w[-8:], b[-8:], activation="silu"), torch.bfloat16, "last rows")
+
+
+def test_conv_c_abi_direct():
+    _say("conv C ABI direct")
+    lib = capi.load()
+    x, w, b = _case(760, 2, 16, 128, 4, torch.float32)
+    xg, wg, bg = x.to(DEV), w.to(DEV), b.to(DEV)
+    out = torch.empty_like(xg)
+    p = capi.Conv1dFwdParams()
+    p.batch, p.dim, p.seqlen, p.width, p.itype, p.wtype, p.silu = 2, 16, 128, 4, 0, 0, 1
+    p.x, p.weight, p.bias, p.out = xg.data_ptr(), wg.data_ptr(), bg.data_ptr(), out.data_ptr()
+    p.x_batch_stride, p.x_d_stride = xg.stride(0), xg.stride(1)
+    p.out_batch_stride, p.out_d_stride = out.stride(0), out.stride(1)
+    p.weight_d_stride, p.weight_w_stride, p.bias_stride = wg.stride(0), wg.stride(1), 1
+    rc = lib.mm_causal_conv1d_fwd(ctypes.byref(p), capi.stream_handle())
+    assert rc == 0, lib.mm_last_error().decode()
+    torch.cuda.synchronize()
+    _close(out, causal_conv1d_ref(x, w, b, activation="silu"), torch.float32, "capi fwd")
