@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <type_traits>
@@ -45,10 +46,12 @@ __device__ __forceinline__ void store_any(void *p, mm_dtype dt, int64_t i, float
 }
 
 // VEC: rows 16-byte aligned, seqlen a multiple of 8 (every chunk is whole and vector-movable).
-template <typename T, int W, bool VEC>
+// Each lane computes NC consecutive chunks of 8 outputs: all NC + 1 loads (the 8 inputs before the
+// first chunk carry its halo) are issued before any arithmetic.
+template <typename T, int W, bool VEC, int NC>
 __global__ void __launch_bounds__(kThreads)
 conv1d_fwd_kernel(const mm_conv1d_fwd_params p) {
-    const int64_t t0 = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * kChunk;
+    const int64_t t0 = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * (kChunk * NC);
     const int64_t d = blockIdx.y;
     const int64_t b = blockIdx.z;
     const int64_t L = p.seqlen;
@@ -61,17 +64,22 @@ conv1d_fwd_kernel(const mm_conv1d_fwd_params p) {
     for (int k = 0; k < W; ++k) w[k] = load_any(p.weight, p.wtype, d * p.weight_d_stride + k * p.weight_w_stride);
     const float bias = p.bias ? load_any(p.bias, p.wtype, d * p.bias_stride) : 0.f;
 
-    // xs[0..7]: the 8 inputs before the chunk (initial states or 0 before t = 0); xs[8..15]: the chunk.
-    float xs[2 * kChunk];
+    // xs[0..7]: the 8 inputs before the first chunk (initial states or 0 before t = 0); then the chunks.
+    float xs[kChunk * (NC + 1)];
     if (VEC) {
-        load8(xr + t0, xs + kChunk);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (t0 + c * kChunk < L) load8(xr + t0 + c * kChunk, xs + kChunk * (c + 1));
+            else {
+#pragma unroll
+                for (int i = 0; i < kChunk; ++i) xs[kChunk * (c + 1) + i] = 0.f;
+            }
         if (t0 >= kChunk) load8(xr + t0 - kChunk, xs);
     } else {
 #pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
-            xs[kChunk + i] = t0 + i < L ? to_f32(xr[t0 + i]) : 0.f;
-            xs[i] = t0 >= kChunk ? to_f32(xr[t0 - kChunk + i]) : 0.f;
-        }
+        for (int i = 0; i < kChunk * NC; ++i) xs[kChunk + i] = t0 + i < L ? to_f32(xr[t0 + i]) : 0.f;
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) xs[i] = t0 >= kChunk ? to_f32(xr[t0 - kChunk + i]) : 0.f;
     }
     if (t0 < kChunk) {  // the first chunk of the row: the W - 1 positions before t = 0
 #pragma unroll
@@ -82,30 +90,34 @@ conv1d_fwd_kernel(const mm_conv1d_fwd_params p) {
                 : 0.f;
         }
     }
-    float o[kChunk];
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-        float acc = bias;
+    for (int c = 0; c < NC; ++c) {
+        const int64_t tc = t0 + c * kChunk;
+        float o[kChunk];
 #pragma unroll
-        for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], xs[kChunk + i - (W - 1) + k], acc);
-        o[i] = p.silu ? acc * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-acc * kLog2e)) : acc;
-    }
-    if (VEC) {
-        store8(orow + t0, o);
-    } else {
+        for (int i = 0; i < kChunk; ++i) {
+            float acc = bias;
 #pragma unroll
-        for (int i = 0; i < kChunk; ++i)
-            if (t0 + i < L) orow[t0 + i] = from_f32<T>(o[i]);
-    }
-    // The last W - 1 inputs (initial states where the row is shorter): written by the lane holding
-    // position L - 1; all of them lie in xs.
-    if (p.final_states && t0 <= L - 1 && L - 1 < t0 + kChunk) {
+            for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], xs[kChunk * (c + 1) + i - (W - 1) + k], acc);
+            o[i] = p.silu ? acc * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-acc * kLog2e)) : acc;
+        }
+        if (VEC) {
+            if (tc < L) store8(orow + tc, o);
+        } else {
 #pragma unroll
-        for (int j = 0; j < W - 1; ++j) {
-            const int64_t pos = L - (W - 1) + j;      // position in the row, may be negative
-            const int idx = int(pos - t0) + kChunk;   // index into xs (>= 0: pos >= t0 - 7)
-            store_any(p.final_states, p.itype, b * p.final_batch_stride + d * p.final_d_stride + j * p.final_w_stride,
-                      xs[idx]);
+            for (int i = 0; i < kChunk; ++i)
+                if (tc + i < L) orow[tc + i] = from_f32<T>(o[i]);
+        }
+        // The last W - 1 inputs (initial states where the row is shorter): written by the lane
+        // holding position L - 1; all of them lie in xs.
+        if (p.final_states && tc <= L - 1 && L - 1 < tc + kChunk) {
+#pragma unroll
+            for (int j = 0; j < W - 1; ++j) {
+                const int64_t pos = L - (W - 1) + j;          // position in the row, may be negative
+                const int idx = int(pos - tc) + kChunk * (c + 1);   // index into xs (pos >= tc - 7)
+                store_any(p.final_states, p.itype, b * p.final_batch_stride + d * p.final_d_stride + j * p.final_w_stride,
+                          xs[idx]);
+            }
         }
     }
 }
@@ -161,12 +173,21 @@ int launch_fwd_w(const mm_conv1d_fwd_params &p, hipStream_t s) {
     const int64_t eb = int64_t(sizeof(T));
     const bool vec = p.seqlen % kChunk == 0 && aligned16(p.x) && aligned16(p.out) && (p.x_batch_stride * eb) % 16 == 0 &&
                      (p.x_d_stride * eb) % 16 == 0 && (p.out_batch_stride * eb) % 16 == 0 && (p.out_d_stride * eb) % 16 == 0;
-    const int64_t chunks = (p.seqlen + kChunk - 1) / kChunk;
-    dim3 grid(unsigned((chunks + kThreads - 1) / kThreads), unsigned(p.dim), unsigned(p.batch));
-    if (vec)
-        hipLaunchKernelGGL((conv1d_fwd_kernel<T, W, true>), grid, dim3(kThreads), 0, s, p);
-    else
-        hipLaunchKernelGGL((conv1d_fwd_kernel<T, W, false>), grid, dim3(kThreads), 0, s, p);
+    const char *e = getenv("MM_CONV_NC");
+    const int nc = e ? atoi(e) : 2;
+    auto go = [&](auto ncc) {
+        constexpr int NC = decltype(ncc)::value;
+        const int64_t per_lane = int64_t(kChunk) * NC;
+        const int64_t lanes = (p.seqlen + per_lane - 1) / per_lane;
+        dim3 grid(unsigned((lanes + kThreads - 1) / kThreads), unsigned(p.dim), unsigned(p.batch));
+        if (vec)
+            hipLaunchKernelGGL((conv1d_fwd_kernel<T, W, true, NC>), grid, dim3(kThreads), 0, s, p);
+        else
+            hipLaunchKernelGGL((conv1d_fwd_kernel<T, W, false, NC>), grid, dim3(kThreads), 0, s, p);
+    };
+    if (nc == 1) go(std::integral_constant<int, 1>{});
+    else if (nc == 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 2>{});
     return launch_status("conv1d_fwd");
 }
 
