@@ -122,8 +122,10 @@ conv1d_fwd_kernel(const mm_conv1d_fwd_params p) {
     }
 }
 
-// One lane per (batch, channel) row.
-template <typename T>
+// One lane per (batch, channel) row. VEC4: the state rows are 4 contiguous entries of the input
+// dtype, aligned for one 4-element vector load and store (the module's layout, state_len = d_conv = 4),
+// and the width is at most 5.
+template <typename T, bool VEC4>
 __global__ void __launch_bounds__(kThreads)
 conv1d_update_kernel(const mm_conv1d_update_params p) {
     const int64_t row = int64_t(blockIdx.x) * kThreads + threadIdx.x;
@@ -136,13 +138,21 @@ conv1d_update_kernel(const mm_conv1d_update_params p) {
     T *orow = reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride;
     const int64_t sbase = b * p.state_batch_stride + d * p.state_d_stride;
 
+    float st4[4] = {0.f, 0.f, 0.f, 0.f};
+    if (VEC4) {
+        const RawVec<T, 4> r = load_raw<T, 4>(reinterpret_cast<const T *>(p.conv_state) + sbase);
+        unpack_raw<T, 4>(r, st4);
+    }
     float w[MM_CONV1D_MAX_WIDTH], win[MM_CONV1D_MAX_WIDTH];
 #pragma unroll
     for (int k = 0; k < MM_CONV1D_MAX_WIDTH; ++k) {
         w[k] = k < W ? load_any(p.weight, p.wtype, d * p.weight_d_stride + k * p.weight_w_stride) : 0.f;
         // Window slot k holds the input k steps before the current token once the token is shifted
         // in (slot 0: the token itself); before the first shift slot k holds state[S - 1 - k].
-        win[k] = (k < W - 1) ? load_any(p.conv_state, p.stype, sbase + (S - 1 - k) * p.state_l_stride) : 0.f;
+        if (VEC4)
+            win[k] = (k < W - 1) ? st4[3 - k] : 0.f;
+        else
+            win[k] = (k < W - 1) ? load_any(p.conv_state, p.stype, sbase + (S - 1 - k) * p.state_l_stride) : 0.f;
     }
     const float bias = p.bias ? load_any(p.bias, p.wtype, d * p.bias_stride) : 0.f;
     for (int64_t t = 0; t < p.seqlen; ++t) {
@@ -158,11 +168,21 @@ conv1d_update_kernel(const mm_conv1d_update_params p) {
     }
     // New state: the last S entries of (old state ++ new tokens). Ascending j reads position
     // j + seqlen of the old state before anything at or above it is written.
-    for (int64_t j = 0; j < S; ++j) {
-        const int64_t src = j + p.seqlen;
-        const float v = src < S ? load_any(p.conv_state, p.stype, sbase + src * p.state_l_stride)
-                                : to_f32(xr[(src - S) * p.x_l_stride]);
-        store_any(p.conv_state, p.stype, sbase + j * p.state_l_stride, v);
+    if (VEC4) {
+        float ns[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t src = j + p.seqlen;
+            ns[j] = src < 4 ? st4[src] : to_f32(xr[(src - 4) * p.x_l_stride]);
+        }
+        store_vec<T, 4>(reinterpret_cast<T *>(p.conv_state) + sbase, ns);
+    } else {
+        for (int64_t j = 0; j < S; ++j) {
+            const int64_t src = j + p.seqlen;
+            const float v = src < S ? load_any(p.conv_state, p.stype, sbase + src * p.state_l_stride)
+                                    : to_f32(xr[(src - S) * p.x_l_stride]);
+            store_any(p.conv_state, p.stype, sbase + j * p.state_l_stride, v);
+        }
     }
 }
 
@@ -208,8 +228,15 @@ int launch_fwd(const mm_conv1d_fwd_params &p, hipStream_t s) {
 template <typename T>
 int launch_update(const mm_conv1d_update_params &p, hipStream_t s) {
     const int64_t rows = p.batch * p.dim;
-    hipLaunchKernelGGL((conv1d_update_kernel<T>), dim3(unsigned((rows + kThreads - 1) / kThreads)), dim3(kThreads), 0,
-                       s, p);
+    const int64_t vb = 4 * int64_t(sizeof(T));
+    const bool vec4 = p.state_len == 4 && p.width <= 5 && p.state_l_stride == 1 && p.stype == p.itype &&
+                      reinterpret_cast<uintptr_t>(p.conv_state) % uintptr_t(vb) == 0 && p.state_batch_stride % 4 == 0 &&
+                      p.state_d_stride % 4 == 0;
+    const dim3 grid(unsigned((rows + kThreads - 1) / kThreads));
+    if (vec4)
+        hipLaunchKernelGGL((conv1d_update_kernel<T, true>), grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((conv1d_update_kernel<T, false>), grid, dim3(kThreads), 0, s, p);
     return launch_status("conv1d_update");
 }
 
