@@ -13,7 +13,8 @@ The JSON line also carries: ``roofline`` for the forward-scan kernel (HBM bound,
 ``roofline_trans`` (the same kernel against the v_exp_f32 issue rate, which binds it), ``cpu_baseline``
 (the CPU oracle timed on the host on a bounded sample of the same workload), per-config results for
 configs 1 and 3, decode tokens/s for config 4, the MotifMamba P/Q forward on a Mamba-1.4B layer and
-the training forward + backward of configs 1 and 2 (unless --quick).
+the training forward + backward of configs 1 and 2, and the causal conv1d that precedes the scan
+(forward on the config 1 and 2 shapes, decode update; unless --quick).
 Only one GPU is used; --gpus N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -170,6 +171,39 @@ def bench_train(cfg_name, steps, warmup, torch):
             "fwd_bwd_ms": s_ms, "elements_per_s": elems / (s_ms * 1e-3)}
 
 
+def bench_conv(cfg_name, steps, warmup, torch):
+    """causal_conv1d_fn (width 4, bias, SiLU) on the conv that feeds a scan configuration: HBM
+    throughput of x read and out written once."""
+    from motif_mamba_amd import causal_conv1d_fn
+    from motif_mamba_amd.workloads import SCAN_CONFIGS
+    c = SCAN_CONFIGS[cfg_name]
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[c.dtype]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(c.batch, c.dim, c.seqlen, device="cuda", generator=g).to(dt)
+    w = (torch.randn(c.dim, 4, device="cuda", generator=g) * 0.5).to(dt)
+    b = (torch.randn(c.dim, device="cuda", generator=g) * 0.1).to(dt)
+    ms = _time_loop(lambda i: causal_conv1d_fn(x, w, b, activation="silu"), steps, warmup, torch)
+    nbytes = 2 * x.numel() * x.element_size() + w.numel() * w.element_size() + b.numel() * b.element_size()
+    del x
+    torch.cuda.empty_cache()
+    return {"shape": [c.batch, c.dim, c.seqlen], "width": 4, "dtype": c.dtype, "us": ms * 1e3,
+            "GB_s": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_conv_update(batch, steps, warmup, torch, dim=5120):
+    """causal_conv1d_update of one decode token (state (batch, dim, 4) bf16, width 4, SiLU)."""
+    from motif_mamba_amd import causal_conv1d_update
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x = torch.randn(batch, dim, device="cuda", generator=g).to(torch.bfloat16)
+    st = torch.zeros(batch, dim, 4, device="cuda").to(torch.bfloat16)
+    w = (torch.randn(dim, 4, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+    b = (torch.randn(dim, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+    ms = _time_loop(lambda i: causal_conv1d_update(x, st, w, b, activation="silu"), steps, warmup, torch)
+    nbytes = batch * dim * (2 * 4 * 2 + 2 * 2) + dim * 5 * 2
+    return {"batch": batch, "dim": dim, "us_per_step": ms * 1e3, "tokens_per_s": batch / (ms * 1e-3),
+            "GB_s": nbytes / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(torch, seconds_target=15.0):
     """The CPU oracle (torch restatement of selective_scan_ref) on a bounded sample of config 2:
     one batch row and a slice of channels at the full L = 4096, scaled to GB/s of the config's
@@ -218,7 +252,7 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
                     help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, "
-                         "cfg1_train, cfg2_train) "
+                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_update_b<batch>) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -240,6 +274,10 @@ def main():
             res = bench_pq(name, args.steps, args.warmup, torch)
         elif name.endswith("_train"):
             res = bench_train(name[: -len("_train")], args.steps, args.warmup, torch)
+        elif name.startswith("conv_update_b"):
+            res = bench_conv_update(int(name[len("conv_update_b"):]), max(args.steps, 100), args.warmup, torch)
+        elif name.startswith("conv_"):
+            res = bench_conv(name[len("conv_"):], args.steps, args.warmup, torch)
         else:
             res = bench_scan(name, args.steps, args.warmup, torch, rotate=2 if name == "cfg1" else 1)
         print(json.dumps({"config": name, **res}), flush=True)
@@ -270,6 +308,12 @@ def main():
         for name in ("cfg1", "cfg2"):
             _log(f"training forward + backward ({name})")
             extra[f"{name}_train"] = bench_train(name, max(5, args.steps // 2), 2, torch)
+        for name in ("cfg1", "cfg2"):
+            _log(f"causal_conv1d forward ({name} shape)")
+            extra[f"conv_{name}"] = bench_conv(name, max(10, args.steps), 3, torch)
+        for b in (64, 256):
+            _log(f"causal_conv1d decode update batch {b}")
+            extra[f"conv_update_b{b}"] = bench_conv_update(b, 200, 10, torch)
     cpu = None
     if not args.no_cpu:
         _log("CPU baseline (oracle on a bounded sample)")
