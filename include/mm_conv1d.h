@@ -10,6 +10,8 @@
  *                            vendored), whose in-tree fallback is mamba_simplemotif.py:298-299:
  *                                out[b,d,t] = act(bias[d] + sum_{k<W} weight[d,k] * x[b,d,t-(W-1)+k])
  *                            with x before t = 0 taken from initial_states (or 0).
+ *   mm_causal_conv1d_bwd     replaces causal_conv1d_bwd_function (selective_scan_interface.py:635-637),
+ *                            the backward MambaInnerFn calls.
  *   mm_causal_conv1d_update  replaces `causal_conv1d_update(x, conv_state, weight, bias, activation)`
  *                            (call site mamba_simplemotif.py:352-358; fallback :353-358): each new
  *                            token is appended to conv_state (shifting it left) and the output is the
@@ -74,8 +76,38 @@ typedef struct mm_conv1d_update_params {
     int64_t bias_stride;
 } mm_conv1d_update_params;
 
+/* Backward of the forward above for a gradient `dout` of its output: dx (itype), and dweight,
+ * dbias summed over batch and steps (float32, overwritten: the call clears them first and
+ * accumulates with device atomics). With `silu` the pre-activation is recomputed and dout is taken
+ * through silu'. Replaces causal_conv1d_bwd_function(x, weight, bias, dout, seq_idx=None,
+ * initial_states=None, dfinal_states=None, dx, return_dinitial_states=False, silu_activation)
+ * (call site selective_scan_interface.py:635-637). */
+typedef struct mm_conv1d_bwd_params {
+    int64_t batch, dim, seqlen, width;
+    mm_dtype itype;              /* x, dout, dx */
+    mm_dtype wtype;              /* weight, bias */
+    int32_t silu;
+
+    const void *x;               /* (batch, dim, seqlen) */
+    const void *weight;          /* (dim, width) */
+    const void *bias;            /* (dim,) or NULL */
+    const void *dout;            /* (batch, dim, seqlen) */
+    void *dx;                    /* (batch, dim, seqlen) */
+    float *dweight;              /* (dim, width) contiguous */
+    float *dbias;                /* (dim,) or NULL */
+
+    int64_t x_batch_stride, x_d_stride;
+    int64_t dout_batch_stride, dout_d_stride;
+    int64_t dx_batch_stride, dx_d_stride;
+    int64_t weight_d_stride, weight_w_stride;
+    int64_t bias_stride;
+} mm_conv1d_bwd_params;
+
 /* Causal depthwise conv1d forward. */
 int mm_causal_conv1d_fwd(const mm_conv1d_fwd_params *params, void *stream);
+
+/* Causal depthwise conv1d backward. */
+int mm_causal_conv1d_bwd(const mm_conv1d_bwd_params *params, void *stream);
 
 /* Decode update of the conv state; calls on one state must be ordered (same stream or events). */
 int mm_causal_conv1d_update(const mm_conv1d_update_params *params, void *stream);

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 5
+#define MM_SCAN_ABI_VERSION 6
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)

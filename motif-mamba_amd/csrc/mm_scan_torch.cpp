@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "mm_conv1d.h"
+#include "mm_norm.h"
 #include "mm_scan.h"
 
 namespace {
@@ -251,13 +252,14 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     mm_scan_fwd_params &p = s.p;
     const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
-    // Output layouts follow the reference: out like delta, out_z like z, x contiguous.
+    // Output layouts follow the reference: out like delta, out_z like z (like out when z is a
+    // non-dense view such as half of xz), x contiguous.
     at::Tensor out = torch::empty_like(delta);
     at::Tensor x = torch::empty({p.batch, p.dim, s.n_chunks, p.dstate * 2}, u.options().dtype(A.scalar_type()));
     at::Tensor out_z;
     set_out(p, out);
     if (z_.has_value()) {
-        out_z = torch::empty_like(z_.value());
+        out_z = z_.value().is_non_overlapping_and_dense() ? torch::empty_like(z_.value()) : torch::empty_like(out);
         set_out_z(p, out_z);
     }
     p.chunk_states = x.data_ptr<float>();
@@ -280,7 +282,7 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
     const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
     at::Tensor main;
     if (z_.has_value()) {
-        main = torch::empty_like(z_.value());
+        main = z_.value().is_non_overlapping_and_dense() ? torch::empty_like(z_.value()) : torch::empty_like(delta);
         set_out_z(p, main);
     } else {
         main = torch::empty_like(delta);
@@ -420,11 +422,12 @@ mm_dtype conv_dtype(const at::Tensor &t, const char *what) {
     return to_mm(st);
 }
 
-// causal_conv1d_fwd (package causal-conv1d; fallback mamba_simplemotif.py:298-299): out, and the
-// last width - 1 inputs into final_states_out when given.
+// causal_conv1d_fwd (package causal-conv1d; fallback mamba_simplemotif.py:298-299): out (written into
+// `out` when given, in any layout contiguous along seqlen), and the last width - 1 inputs into
+// final_states_out when given.
 at::Tensor conv1d_fwd(const at::Tensor &x, const at::Tensor &weight, const c10::optional<at::Tensor> &bias_,
                       const c10::optional<at::Tensor> &initial_states_, const c10::optional<at::Tensor> &final_states_out_,
-                      bool silu) {
+                      bool silu, const c10::optional<at::Tensor> &out_) {
     TORCH_CHECK(x.is_cuda() && weight.is_cuda(), "x and weight must be on the GPU");
     TORCH_CHECK(x.dim() == 3, "x must have shape (batch, dim, seqlen)");
     TORCH_CHECK(x.stride(-1) == 1 || x.size(-1) == 1, "x must be contiguous along seqlen");
@@ -432,7 +435,15 @@ at::Tensor conv1d_fwd(const at::Tensor &x, const at::Tensor &weight, const c10::
     TORCH_CHECK(weight.dim() == 2 && weight.size(0) == dim, "weight must have shape (dim, width)");
     const int64_t width = weight.size(1);
     TORCH_CHECK(width >= 1 && width <= MM_CONV1D_MAX_WIDTH, "width must be between 1 and 8");
-    at::Tensor out = torch::empty_like(x);
+    at::Tensor out;
+    if (out_.has_value()) {
+        out = out_.value();
+        CHECK_SHAPE(out, batch, dim, seqlen);
+        TORCH_CHECK(out.is_cuda() && out.scalar_type() == x.scalar_type(), "out must have the dtype of x");
+        TORCH_CHECK(out.stride(-1) == 1 || seqlen == 1, "out must be contiguous along seqlen");
+    } else {
+        out = torch::empty_like(x);
+    }
     mm_conv1d_fwd_params p;
     std::memset(&p, 0, sizeof(p));
     p.batch = batch; p.dim = dim; p.seqlen = seqlen; p.width = width;
@@ -467,6 +478,59 @@ at::Tensor conv1d_fwd(const at::Tensor &x, const at::Tensor &weight, const c10::
     const c10::DeviceGuard device_guard{x.device()};
     check_rc(mm_causal_conv1d_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_causal_conv1d_fwd");
     return out;
+}
+
+// causal_conv1d_bwd (package causal-conv1d, as MambaInnerFn.backward calls it,
+// selective_scan_interface.py:635-637): [dx, dweight, dbias?] for the gradient dout of the forward's
+// output; dx is written into dx_out when given (MambaInnerFn passes a slice of dxz). dweight and dbias
+// are summed in float32 and returned in the dtypes of weight and bias.
+std::vector<at::Tensor> conv1d_bwd(const at::Tensor &x, const at::Tensor &weight, const c10::optional<at::Tensor> &bias_,
+                                   const at::Tensor &dout, const c10::optional<at::Tensor> &dx_out_, bool silu) {
+    TORCH_CHECK(x.is_cuda() && weight.is_cuda() && dout.is_cuda(), "x, weight and dout must be on the GPU");
+    TORCH_CHECK(x.dim() == 3, "x must have shape (batch, dim, seqlen)");
+    TORCH_CHECK(x.stride(-1) == 1 || x.size(-1) == 1, "x must be contiguous along seqlen");
+    const int64_t batch = x.size(0), dim = x.size(1), seqlen = x.size(2);
+    TORCH_CHECK(weight.dim() == 2 && weight.size(0) == dim, "weight must have shape (dim, width)");
+    const int64_t width = weight.size(1);
+    TORCH_CHECK(width >= 1 && width <= MM_CONV1D_MAX_WIDTH, "width must be between 1 and 8");
+    CHECK_SHAPE(dout, batch, dim, seqlen);
+    TORCH_CHECK(dout.scalar_type() == x.scalar_type(), "dout must have the dtype of x");
+    TORCH_CHECK(dout.stride(-1) == 1 || seqlen == 1, "dout must be contiguous along seqlen");
+    at::Tensor dx;
+    if (dx_out_.has_value()) {
+        dx = dx_out_.value();
+        CHECK_SHAPE(dx, batch, dim, seqlen);
+        TORCH_CHECK(dx.is_cuda() && dx.scalar_type() == x.scalar_type(), "dx must have the dtype of x");
+        TORCH_CHECK(dx.stride(-1) == 1 || seqlen == 1, "dx must be contiguous along seqlen");
+    } else {
+        dx = torch::empty_like(x);
+    }
+    at::Tensor dweight = torch::empty({dim, width}, x.options().dtype(at::kFloat));
+    at::Tensor dbias;
+    mm_conv1d_bwd_params p;
+    std::memset(&p, 0, sizeof(p));
+    p.batch = batch; p.dim = dim; p.seqlen = seqlen; p.width = width;
+    p.itype = conv_dtype(x, "x");
+    p.wtype = conv_dtype(weight, "weight");
+    p.silu = silu;
+    p.x = x.data_ptr(); p.x_batch_stride = x.stride(0); p.x_d_stride = x.stride(1);
+    p.dout = dout.data_ptr(); p.dout_batch_stride = dout.stride(0); p.dout_d_stride = dout.stride(1);
+    p.dx = dx.data_ptr(); p.dx_batch_stride = dx.stride(0); p.dx_d_stride = dx.stride(1);
+    p.weight = weight.data_ptr(); p.weight_d_stride = weight.stride(0); p.weight_w_stride = weight.stride(1);
+    p.dweight = dweight.data_ptr<float>();
+    if (bias_.has_value()) {
+        const at::Tensor &bias = bias_.value();
+        TORCH_CHECK(bias.is_cuda() && bias.dim() == 1 && bias.size(0) == dim, "bias must have shape (dim,)");
+        TORCH_CHECK(bias.scalar_type() == weight.scalar_type(), "bias must have the dtype of weight");
+        p.bias = bias.data_ptr(); p.bias_stride = bias.stride(0);
+        dbias = torch::empty({dim}, x.options().dtype(at::kFloat));
+        p.dbias = dbias.data_ptr<float>();
+    }
+    const c10::DeviceGuard device_guard{x.device()};
+    check_rc(mm_causal_conv1d_bwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_causal_conv1d_bwd");
+    std::vector<at::Tensor> res{dx, dweight.to(weight.scalar_type())};
+    if (dbias.defined()) res.push_back(dbias.to(bias_.value().scalar_type()));
+    return res;
 }
 
 // causal_conv1d_update (package causal-conv1d; fallback mamba_simplemotif.py:353-358): x (batch, dim)
@@ -507,6 +571,33 @@ at::Tensor conv1d_update(const at::Tensor &x, const at::Tensor &conv_state, cons
     const c10::DeviceGuard device_guard{x.device()};
     check_rc(mm_causal_conv1d_update(&p, c10::hip::getCurrentHIPStream().stream()), "mm_causal_conv1d_update");
     return x.dim() == 2 ? out.squeeze(-1) : out;
+}
+
+// rms_norm_forward (selective_scan_interface.py:217-234) over dim 1 of a 3-D x (n0, cols, n2), in
+// the layout the scan reads: out[i0, :, i2] = x[i0, :, i2] * weight / rms. out is a new tensor with
+// x's shape and dtype (x's layout when x is dense), or the given `out` (which may be x itself).
+at::Tensor rms_norm_fwd(const at::Tensor &x, const at::Tensor &weight, double eps,
+                        const c10::optional<at::Tensor> &out_) {
+    TORCH_CHECK(x.is_cuda() && weight.is_cuda(), "x and weight must be on the GPU");
+    TORCH_CHECK(x.dim() == 3, "x must have shape (n0, cols, n2)");
+    const int64_t n0 = x.size(0), cols = x.size(1), n2 = x.size(2);
+    CHECK_SHAPE(weight, cols);
+    at::Tensor out = out_.has_value() ? out_.value() : torch::empty_like(x);
+    CHECK_SHAPE(out, n0, cols, n2);
+    TORCH_CHECK(out.is_cuda() && out.scalar_type() == x.scalar_type(), "out must have the dtype of x");
+    mm_rms_norm_params p;
+    std::memset(&p, 0, sizeof(p));
+    p.n0 = n0; p.cols = cols; p.n2 = n2;
+    p.itype = conv_dtype(x, "x");
+    p.wtype = conv_dtype(weight, "weight");
+    p.eps = static_cast<float>(eps);
+    p.x = x.data_ptr(); p.weight = weight.data_ptr(); p.out = out.data_ptr();
+    p.x_stride0 = x.stride(0); p.x_stride_c = x.stride(1); p.x_stride2 = x.stride(2);
+    p.out_stride0 = out.stride(0); p.out_stride_c = out.stride(1); p.out_stride2 = out.stride(2);
+    p.weight_stride = weight.stride(0);
+    const c10::DeviceGuard device_guard{x.device()};
+    check_rc(mm_rms_norm_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_rms_norm_fwd");
+    return out;
 }
 
 at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::Tensor &dt, const at::Tensor &A,
@@ -633,9 +724,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("conv1d_fwd", &conv1d_fwd, "Causal depthwise conv1d forward",
           pybind11::arg("x"), pybind11::arg("weight"), pybind11::arg("bias") = pybind11::none(),
           pybind11::arg("initial_states") = pybind11::none(), pybind11::arg("final_states_out") = pybind11::none(),
-          pybind11::arg("silu") = false);
+          pybind11::arg("silu") = false, pybind11::arg("out") = pybind11::none());
+    m.def("conv1d_bwd", &conv1d_bwd, "Causal depthwise conv1d backward [dx, dweight, dbias?]",
+          pybind11::arg("x"), pybind11::arg("weight"), pybind11::arg("bias"), pybind11::arg("dout"),
+          pybind11::arg("dx") = pybind11::none(), pybind11::arg("silu") = false);
     m.def("conv1d_update", &conv1d_update, "Causal depthwise conv1d decode update (in place on conv_state)",
           pybind11::arg("x"), pybind11::arg("conv_state"), pybind11::arg("weight"),
           pybind11::arg("bias") = pybind11::none(), pybind11::arg("silu") = false);
+    m.def("rms_norm_fwd", &rms_norm_fwd, "Row RMSNorm over dim 1 of a 3-D tensor",
+          pybind11::arg("x"), pybind11::arg("weight"), pybind11::arg("eps") = 1e-6,
+          pybind11::arg("out") = pybind11::none());
     m.def("abi_version", []() { return mm_abi_version(); });
 }

@@ -32,20 +32,24 @@ def _act(y, activation):
     raise NotImplementedError("activation must be None, silu, or swish")
 
 
-def causal_conv1d_ref(x, weight, bias=None, initial_states=None, return_final_states=False, activation=None):
+def causal_conv1d_ref(x, weight, bias=None, initial_states=None, return_final_states=False, activation=None,
+                      compute_dtype=torch.float32):
     """x: (batch, dim, seqlen); weight: (dim, width); bias: (dim,) or None;
     initial_states: (batch, dim, width - 1) or None. Returns out (batch, dim, seqlen) in x's dtype,
-    and with ``return_final_states`` also the last width - 1 inputs (batch, dim, width - 1)."""
+    and with ``return_final_states`` also the last width - 1 inputs (batch, dim, width - 1).
+    ``compute_dtype=torch.float64`` evaluates the same formula in double precision."""
     dtype_in = x.dtype
     dim, width = weight.shape
     seqlen = x.shape[-1]
-    xf = x.float()
+    cd = compute_dtype
+    xf = x.to(cd)
+    wf = weight.to(cd).unsqueeze(1)
+    bf = None if bias is None else bias.to(cd)
     if initial_states is not None:
-        xf = torch.cat([initial_states.float(), xf], dim=-1)
-        y = F.conv1d(xf, weight.float().unsqueeze(1), None if bias is None else bias.float(), padding=0, groups=dim)
+        xf = torch.cat([initial_states.to(cd), xf], dim=-1)
+        y = F.conv1d(xf, wf, bf, padding=0, groups=dim)
     else:
-        y = F.conv1d(xf, weight.float().unsqueeze(1), None if bias is None else bias.float(),
-                     padding=width - 1, groups=dim)
+        y = F.conv1d(xf, wf, bf, padding=width - 1, groups=dim)
     y = _act(y[..., :seqlen], activation).to(dtype_in)
     if not return_final_states:
         return y

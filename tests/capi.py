@@ -10,7 +10,7 @@ import torch
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(REPO, "include", "mm_scan.h")
-HEADERS = [os.path.join(REPO, "include", h) for h in ("mm_scan.h", "mm_conv1d.h")]
+HEADERS = [os.path.join(REPO, "include", h) for h in ("mm_scan.h", "mm_conv1d.h", "mm_norm.h")]
 
 i64, i32, vp = ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p
 
@@ -83,6 +83,22 @@ class Conv1dUpdateParams(ctypes.Structure):
                 ("weight_d_stride", i64), ("weight_w_stride", i64), ("bias_stride", i64)]
 
 
+class Conv1dBwdParams(ctypes.Structure):
+    _fields_ = [("batch", i64), ("dim", i64), ("seqlen", i64), ("width", i64),
+                ("itype", i32), ("wtype", i32), ("silu", i32),
+                ("x", vp), ("weight", vp), ("bias", vp), ("dout", vp), ("dx", vp), ("dweight", vp), ("dbias", vp),
+                ("x_batch_stride", i64), ("x_d_stride", i64), ("dout_batch_stride", i64), ("dout_d_stride", i64),
+                ("dx_batch_stride", i64), ("dx_d_stride", i64),
+                ("weight_d_stride", i64), ("weight_w_stride", i64), ("bias_stride", i64)]
+
+
+class RmsNormParams(ctypes.Structure):
+    _fields_ = [("n0", i64), ("cols", i64), ("n2", i64), ("itype", i32), ("wtype", i32), ("eps", ctypes.c_float),
+                ("x", vp), ("weight", vp), ("out", vp),
+                ("x_stride0", i64), ("x_stride_c", i64), ("x_stride2", i64),
+                ("out_stride0", i64), ("out_stride_c", i64), ("out_stride2", i64), ("weight_stride", i64)]
+
+
 class StateUpdateParams(ctypes.Structure):
     _fields_ = [("batch", i64), ("dim", i64), ("dstate", i64), ("n_groups", i64),
                 ("itype", i32), ("dt_softplus", i32),
@@ -122,6 +138,10 @@ def load():
     lib.mm_causal_conv1d_fwd.restype = ctypes.c_int
     lib.mm_causal_conv1d_update.argtypes = [ctypes.POINTER(Conv1dUpdateParams), vp]
     lib.mm_causal_conv1d_update.restype = ctypes.c_int
+    lib.mm_causal_conv1d_bwd.argtypes = [ctypes.POINTER(Conv1dBwdParams), vp]
+    lib.mm_causal_conv1d_bwd.restype = ctypes.c_int
+    lib.mm_rms_norm_fwd.argtypes = [ctypes.POINTER(RmsNormParams), vp]
+    lib.mm_rms_norm_fwd.restype = ctypes.c_int
     return lib
 
 

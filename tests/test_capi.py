@@ -16,15 +16,15 @@ def test_library_exports_every_header_function():
     names = capi.header_functions()
     assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_scan_bwd", "mm_scan_bwd_workspace_size",
                           "mm_state_update", "mm_last_error", "mm_abi_version", "mm_causal_conv1d_fwd",
-                          "mm_causal_conv1d_update"}
+                          "mm_causal_conv1d_update", "mm_causal_conv1d_bwd", "mm_rms_norm_fwd"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 5
+    assert lib.mm_abi_version() == 6
 
 
 def _c_layout(struct, fields, tmp_path):
     src = tmp_path / "layout.c"
-    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mm_scan.h"', '#include "mm_conv1d.h"',
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "mm_scan.h"', '#include "mm_conv1d.h"', '#include "mm_norm.h"',
              'int main(void) {',
              f'  printf("%zu\\n", sizeof({struct}));']
     lines += [f'  printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
@@ -39,6 +39,8 @@ def _c_layout(struct, fields, tmp_path):
                                             ("mm_scan_bwd_params", capi.ScanBwdParams),
                                             ("mm_conv1d_fwd_params", capi.Conv1dFwdParams),
                                             ("mm_conv1d_update_params", capi.Conv1dUpdateParams),
+                                            ("mm_conv1d_bwd_params", capi.Conv1dBwdParams),
+                                            ("mm_rms_norm_params", capi.RmsNormParams),
                                             ("mm_state_update_params", capi.StateUpdateParams)])
 def test_struct_layout_matches_header(tmp_path, cname, pystruct):
     fields = [f for f, _ in pystruct._fields_]
@@ -231,6 +233,36 @@ def test_conv1d_rejects_invalid_params():
     q.batch = 0
     q.state_len = 4
     assert lib.mm_causal_conv1d_update(ctypes.byref(q), None) == capi.MM_OK
+    assert lib.mm_causal_conv1d_bwd(None, None) == capi.MM_ERR_INVALID_ARGUMENT
+    r = capi.Conv1dBwdParams()
+    r.batch, r.dim, r.seqlen, r.width, r.itype, r.wtype = 2, 8, 16, 4, 2, 2
+    r.x = r.dout = r.dx = r.weight = r.dweight = 0x1000
+    r.bias = 0x1000                      # bias without dbias
+    assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "dbias" in lib.mm_last_error().decode()
+    r.bias, r.x = None, None
+    assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "required" in lib.mm_last_error().decode()
+    r.x, r.width = 0x1000, 0
+    assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_ERR_INVALID_ARGUMENT
+    r.width, r.dim = 4, 0                # nothing to write: returns before any launch
+    assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_OK
+
+
+def test_rms_norm_rejects_invalid_params():
+    lib = capi.load()
+    assert lib.mm_rms_norm_fwd(None, None) == capi.MM_ERR_INVALID_ARGUMENT
+    p = capi.RmsNormParams()
+    p.n0, p.cols, p.n2, p.itype, p.wtype, p.eps = 2, 16, 64, 2, 0, 1e-6
+    assert lib.mm_rms_norm_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    assert "required" in lib.mm_last_error().decode()
+    p.x = p.weight = p.out = 0x1000
+    p.eps = -1.0
+    assert lib.mm_rms_norm_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    p.eps, p.itype = 1e-6, 9
+    assert lib.mm_rms_norm_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+    p.itype, p.n2 = 2, 0
+    assert lib.mm_rms_norm_fwd(ctypes.byref(p), None) == capi.MM_OK
 
 
 def test_causal_conv1d_import_paths_and_argument_errors():
@@ -246,6 +278,7 @@ def test_causal_conv1d_import_paths_and_argument_errors():
     with pytest.raises(NotImplementedError):
         causal_conv1d.causal_conv1d_fn(x, w, seq_idx=torch.zeros(1, 8, dtype=torch.int32))
     with pytest.raises(NotImplementedError):
-        cf.causal_conv1d_bwd_function()
+        cf.causal_conv1d_bwd_function(x, w, None, x, torch.zeros(1, 8, dtype=torch.int32), None, None, None,
+                                      False, True)
     with pytest.raises(RuntimeError):       # CPU tensors are refused by the binding
         causal_conv1d.causal_conv1d_fn(x, w)

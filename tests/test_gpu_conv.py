@@ -1,4 +1,4 @@
-"""GPU parity of the causal depthwise conv1d (forward and decode update, mm_conv1d.hip) against the
+"""GPU parity of the causal depthwise conv1d (forward, backward and decode update, mm_conv1d.hip) against the
 CPU oracle oracle/conv_ref.py (the Mamba module's torch fallback, mamba_simplemotif.py:298-299 and
 :353-358, and the published semantics of the causal-conv1d API the reference calls).
 Tolerances (north_star): fp32 rtol 1e-4 / atol 1e-5; bf16/fp16 rtol 3e-2 / atol 5e-2.
@@ -149,3 +149,109 @@ def test_conv_c_abi_direct():
     assert rc == 0, lib.mm_last_error().decode()
     torch.cuda.synchronize()
     _close(out, causal_conv1d_ref(x, w, b, activation="silu"), torch.float32, "capi fwd")
+
+
+# Backward (mm_causal_conv1d_bwd): gradients of the oracle's float32 forward by autograd, on the same
+# inputs, element-wise |err| <= rtol |exact| + atol max(1, max |exact|) with the forward's (rtol,
+# atol) pair: dweight and dbias are sums over batch and steps whose rounding grows with their scale.
+
+def _gcheck(got, exact, dtype, what):
+    rtol, atol = fixtures.tolerances(dtype)
+    got, exact = got.double().cpu(), exact.double()
+    scale = max(1.0, exact.abs().max().item()) if exact.numel() else 1.0
+    err = (got - exact).abs()
+    bad = err > rtol * exact.abs() + atol * scale
+    assert not bool(bad.any()), f"{what}: {int(bad.sum())}/{err.numel()} beyond tolerance, max err {err.max().item():.3g}"
+
+
+def _ref_grads(x, w, b, dout, act):
+    xr = x.detach().float().clone().requires_grad_(True)
+    wr = w.detach().float().clone().requires_grad_(True)
+    br = b.detach().float().clone().requires_grad_(True) if b is not None else None
+    causal_conv1d_ref(xr, wr, br, activation=act, compute_dtype=torch.float64).float().backward(dout.float())
+    return xr.grad, wr.grad, (br.grad if br is not None else None)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("W", [2, 3, 4])
+@pytest.mark.parametrize("L", [1, 7, 64, 1000])
+def test_conv_bwd(dtype, W, L):
+    _say(f"conv bwd {dtype} W={W} L={L}")
+    from causal_conv1d import causal_conv1d_fn
+    x, w, b = _case(800 + W + L, 2, 24, L, W, dtype)
+    dout = torch.randn(2, 24, L, generator=torch.Generator().manual_seed(801)).to(dtype)
+    for act in (None, "silu"):
+        xg, wg, bg = (t.to(DEV).requires_grad_(True) for t in (x, w, b))
+        causal_conv1d_fn(xg, wg, bg, activation=act).backward(dout.to(DEV))
+        torch.cuda.synchronize()
+        ex, ew, eb = _ref_grads(x, w, b, dout, act)
+        assert xg.grad.dtype == dtype and wg.grad.dtype == w.dtype
+        _gcheck(xg.grad, ex, dtype, f"dx act={act}")
+        _gcheck(wg.grad, ew, dtype, f"dweight act={act}")
+        _gcheck(bg.grad, eb, dtype, f"dbias act={act}")
+
+
+def test_conv_bwd_function_into_dxz_slice_no_bias():
+    """causal_conv1d_bwd_function as MambaInnerFn calls it (ssi.py:635-637): x a half of xz, dout in a
+    channel-major layout, dx written into the matching half of a preallocated dxz, no bias."""
+    _say("conv bwd function into dxz slice")
+    from causal_conv1d.cpp_functions import causal_conv1d_bwd_function
+    g = torch.Generator().manual_seed(810)
+    xz = torch.randn(3, 64, 96, generator=g).to(torch.bfloat16)
+    w = torch.randn(32, 4, generator=g) * 0.5
+    dcm = torch.randn(32, 3, 96, generator=g).to(torch.bfloat16)          # (d, b, l) storage
+    x = xz.to(DEV).chunk(2, dim=1)[0]
+    dout = dcm.to(DEV).transpose(0, 1)                                       # (b, d, l) view
+    dxz = torch.full((3, 64, 96), 7.0, dtype=torch.bfloat16, device=DEV)
+    dx_slot = dxz.chunk(2, dim=1)[0]
+    dx, dw, db, dini = causal_conv1d_bwd_function(x, w.to(DEV), None, dout, None, None, None, dx_slot, False, True)
+    torch.cuda.synchronize()
+    assert db is None and dini is None and dx.data_ptr() == dx_slot.data_ptr()
+    ex, ew, _ = _ref_grads(xz[:, :32], w, None, dcm.transpose(0, 1), "silu")
+    _gcheck(dxz[:, :32], ex, torch.bfloat16, "dx")
+    assert bool((dxz[:, 32:] == 7.0).all()), "the z half of dxz was written"
+    _gcheck(dw, ew, torch.bfloat16, "dweight")
+
+
+def test_conv_bwd_benchmark_shape_rows():
+    """Config-2 conv shape (batch 4, 5120 channels, L 4096, bf16): a slice of channels against the oracle."""
+    _say("conv bwd config-2 shape")
+    from motif_mamba_amd.causal_conv1d import causal_conv1d_bwd
+    g = torch.Generator().manual_seed(820)
+    x = torch.randn(4, 5120, 4096, generator=g).to(torch.bfloat16)
+    w = (torch.randn(5120, 4, generator=g) * 0.5).to(torch.bfloat16)
+    b = (torch.randn(5120, generator=g) * 0.1).to(torch.bfloat16)
+    dout = torch.randn(4, 5120, 4096, generator=g).to(torch.bfloat16)
+    dx, dw, db = causal_conv1d_bwd(x.to(DEV), w.to(DEV), b.to(DEV), dout.to(DEV), None, True)
+    dx, dw, db = dx.cpu(), dw.cpu(), db.cpu()
+    for sl in (slice(1000, 1032), slice(5112, 5120)):
+        ex, ew, eb = _ref_grads(x[:, sl], w[sl], b[sl], dout[:, sl], "silu")
+        _gcheck(dx[:, sl], ex, torch.bfloat16, "dx rows")
+        _gcheck(dw[sl], ew, torch.bfloat16, "dweight rows")
+        _gcheck(db[sl], eb, torch.bfloat16, "dbias rows")
+
+
+def test_conv_bwd_c_abi_direct():
+    _say("conv bwd C ABI direct")
+    lib = capi.load()
+    x, w, b = _case(830, 2, 16, 128, 4, torch.float32)
+    dout = torch.randn(2, 16, 128, generator=torch.Generator().manual_seed(831))
+    xg, wg, bg, dg = x.to(DEV), w.to(DEV), b.to(DEV), dout.to(DEV)
+    dx = torch.empty_like(xg)
+    dw = torch.full((16, 4), 5.0, device=DEV)                                # cleared by the call
+    db = torch.full((16,), 5.0, device=DEV)
+    p = capi.Conv1dBwdParams()
+    p.batch, p.dim, p.seqlen, p.width, p.itype, p.wtype, p.silu = 2, 16, 128, 4, 0, 0, 1
+    p.x, p.weight, p.bias, p.dout = xg.data_ptr(), wg.data_ptr(), bg.data_ptr(), dg.data_ptr()
+    p.dx, p.dweight, p.dbias = dx.data_ptr(), dw.data_ptr(), db.data_ptr()
+    p.x_batch_stride, p.x_d_stride = xg.stride(0), xg.stride(1)
+    p.dout_batch_stride, p.dout_d_stride = dg.stride(0), dg.stride(1)
+    p.dx_batch_stride, p.dx_d_stride = dx.stride(0), dx.stride(1)
+    p.weight_d_stride, p.weight_w_stride, p.bias_stride = wg.stride(0), wg.stride(1), 1
+    rc = lib.mm_causal_conv1d_bwd(ctypes.byref(p), capi.stream_handle())
+    assert rc == 0, lib.mm_last_error().decode()
+    torch.cuda.synchronize()
+    ex, ew, eb = _ref_grads(x, w, b, dout, "silu")
+    _gcheck(dx, ex, torch.float32, "dx")
+    _gcheck(dw, ew, torch.float32, "dweight")
+    _gcheck(db, eb, torch.float32, "dbias")
