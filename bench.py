@@ -13,8 +13,9 @@ The JSON line also carries: ``roofline`` for the forward-scan kernel (HBM bound,
 ``roofline_trans`` (the same kernel against the v_exp_f32 issue rate, which binds it), ``cpu_baseline``
 (the CPU oracle timed on the host on a bounded sample of the same workload), per-config results for
 configs 1 and 3, decode tokens/s for config 4, the MotifMamba P/Q forward on a Mamba-1.4B layer and
-the training forward + backward of configs 1 and 2, and the causal conv1d that precedes the scan
-(forward on the config 1 and 2 shapes, decode update; unless --quick).
+the training forward + backward of configs 1 and 2, the causal conv1d that precedes the scan
+(forward on the config 1 and 2 shapes, decode update) and the fused Mamba block mamba_inner_fn on
+the config-2 tokens of a Mamba-2.8B layer (inference and training; unless --quick).
 Only one GPU is used; --gpus N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -204,6 +205,49 @@ def bench_conv_update(batch, steps, warmup, torch, dim=5120):
             "GB_s": nbytes / (ms * 1e-3) / 1e9}
 
 
+def bench_inner(steps, warmup, torch, batch=4, seqlen=4096, d_model=2560, d_inner=5120, rank=160, d_state=16):
+    """mamba_inner_fn (selective_scan_interface.py:454-656) on a Mamba-2.8B layer (bf16 weights and
+    activations, float32 A / D / dt bias, conv width 4, checkpoint_lvl 1): the inference forward
+    (no gradients), and the training forward + backward with the gradients of every input. The
+    projections' GEMM flops are reported with the achieved rate over the whole block."""
+    from motif_mamba_amd import mamba_inner_fn
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(13)
+
+    def r(*shape, sc=1.0, dt=bf, grad=True):
+        return (torch.randn(*shape, device="cuda", generator=g) * sc).to(dt).requires_grad_(grad)
+    xz = r(batch, 2 * d_inner, seqlen)
+    p = [r(d_inner, 1, 4, sc=0.5), r(d_inner, sc=0.1), r(rank + 2 * d_state, d_inner, sc=d_inner ** -0.5),
+         r(d_inner, rank, sc=rank ** -0.5), r(d_model, d_inner, sc=d_inner ** -0.5), None,
+         (-torch.exp(torch.rand(d_inner, d_state, device="cuda", generator=g) * 2.0)).requires_grad_(True)]
+    D = torch.ones(d_inner, device="cuda", requires_grad=True)
+    dtb = (torch.rand(d_inner, device="cuda", generator=g) * 2.0 - 4.0).requires_grad_(True)
+    dout = torch.randn(batch, seqlen, d_model, device="cuda", generator=g).to(bf)
+
+    def infer(i):
+        with torch.no_grad():
+            mamba_inner_fn(xz, *p, None, None, D, dtb, delta_softplus=True)
+
+    def train(i):
+        for t in [xz, D, dtb] + [q for q in p if q is not None]:
+            t.grad = None
+        mamba_inner_fn(xz, *p, None, None, D, dtb, delta_softplus=True).backward(dout)
+
+    f_ms = _time_loop(infer, steps, warmup, torch)
+    t_ms = _time_loop(train, steps, warmup, torch)
+    tokens = batch * seqlen
+    fwd_flops = 2 * tokens * (d_inner * (rank + 2 * d_state) + rank * d_inner + d_inner * d_model)
+    # backward: two GEMMs per forward projection, and delta recomputed (checkpoint_lvl 1)
+    train_flops = 3 * fwd_flops + 2 * tokens * rank * d_inner
+    del xz, p, dout
+    torch.cuda.empty_cache()
+    return {"shape": {"batch": batch, "seqlen": seqlen, "d_model": d_model, "d_inner": d_inner, "dt_rank": rank,
+                      "d_state": d_state, "d_conv": 4}, "dtype": "bf16",
+            "fwd_ms": f_ms, "fwd_bwd_ms": t_ms, "tokens_per_s_fwd": tokens / (f_ms * 1e-3),
+            "tokens_per_s_fwd_bwd": tokens / (t_ms * 1e-3), "gemm_gflop_fwd": fwd_flops / 1e9,
+            "gemm_gflop_fwd_bwd": train_flops / 1e9}
+
+
 def cpu_baseline(torch, seconds_target=15.0):
     """The CPU oracle (torch restatement of selective_scan_ref) on a bounded sample of config 2:
     one batch row and a slice of channels at the full L = 4096, scaled to GB/s of the config's
@@ -252,7 +296,7 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
                     help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, "
-                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_update_b<batch>) "
+                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_update_b<batch>, inner_2p8b) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -272,6 +316,8 @@ def main():
             res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
         elif name.startswith("pq_"):
             res = bench_pq(name, args.steps, args.warmup, torch)
+        elif name == "inner_2p8b":
+            res = bench_inner(args.steps, args.warmup, torch)
         elif name.endswith("_train"):
             res = bench_train(name[: -len("_train")], args.steps, args.warmup, torch)
         elif name.startswith("conv_update_b"):
@@ -314,6 +360,8 @@ def main():
         for b in (64, 256):
             _log(f"causal_conv1d decode update batch {b}")
             extra[f"conv_update_b{b}"] = bench_conv_update(b, 200, 10, torch)
+        _log("mamba_inner_fn forward and forward + backward (Mamba-2.8B layer, config-2 tokens)")
+        extra["inner_2p8b"] = bench_inner(max(5, args.steps // 2), 2, torch)
     cpu = None
     if not args.no_cpu:
         _log("CPU baseline (oracle on a bounded sample)")
