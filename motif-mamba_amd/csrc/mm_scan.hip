@@ -14,7 +14,7 @@
 //                                 in registers and walks the sequence serially, 8 steps per
 //                                 iteration. Used for every shape the tiled kernel does not take.
 //   state_update<T, SPL>          one decode step; LPR lanes share a row, SPL states per lane.
-//   state_update_vec16<T>         one decode step for dstate 16 with aligned unit-stride rows: four
+//   state_update_rows16<T, U>     one decode step for dstate 16 with aligned unit-stride rows: four
 //                                 lanes per row, four states each as one 16-byte vector.
 // The tiled forward kernel lives in mm_scan_tiled.hip.
 #include <hip/hip_runtime.h>
@@ -239,43 +239,98 @@ __device__ __forceinline__ float4 load4(const T *p) {
     }
 }
 
-// dstate 16 with every row of state, A, B and C contiguous and 4-element aligned (checked on the
-// host): four lanes per (batch, channel) row, each moving four consecutive states as one 16-byte
-// vector, so a wave reads and writes 16 whole state rows (1 KB) per instruction.
+// Loads of one (batch, channel) row's quarter for the dstate-16 decode step, issued before any
+// arithmetic so that a lane has U rows' worth of memory requests in flight.
 template <typename T>
-__global__ void __launch_bounds__(kDecBlock)
-state_update_vec16(const mm_state_update_params p, const int64_t ratio) {
-    const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t row = tid >> 2;
-    const int part = int(tid & 3);
-    if (row >= p.batch * p.dim) return;  // all four lanes of a row leave together
-    const int64_t b = row / p.dim;
-    const int64_t d = row - b * p.dim;
-    const int64_t g = d / ratio;
+struct DecRow {
+    float4 s, a;        // four states and their A entries
+    uint2 bw, cw;       // four B / C values as raw words (16-bit types; fp32 uses bf/cf)
+    float4 bf, cf;
+    T dt, x, z;
+    float D, bias;
+};
 
-    float dt = to_f32(reinterpret_cast<const T *>(p.dt)[b * p.dt_batch_stride + d * p.dt_d_stride]);
-    if (p.dt_bias) dt += p.dt_bias[d];
-    if (p.dt_softplus) dt = softplus_f32(dt);
-    const float x = to_f32(reinterpret_cast<const T *>(p.x)[b * p.x_batch_stride + d * p.x_d_stride]);
-    const float dtx = dt * x;
-    float4 *sp = reinterpret_cast<float4 *>(p.state + b * p.state_batch_stride + d * p.state_d_stride) + part;
-    const float4 a4 = *reinterpret_cast<const float4 *>(p.A + d * p.A_d_stride + 4 * part);
-    const float4 b4 = load4(reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + 4 * part);
-    const float4 c4 = load4(reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + 4 * part);
-    float4 s = *sp;
-    const float dl = dt * kLog2e;
-    s.x = __builtin_fmaf(s.x, fast_exp2(dl * a4.x), dtx * b4.x);
-    s.y = __builtin_fmaf(s.y, fast_exp2(dl * a4.y), dtx * b4.y);
-    s.z = __builtin_fmaf(s.z, fast_exp2(dl * a4.z), dtx * b4.z);
-    s.w = __builtin_fmaf(s.w, fast_exp2(dl * a4.w), dtx * b4.w);
-    *sp = s;
-    float y = __builtin_fmaf(s.x, c4.x, __builtin_fmaf(s.y, c4.y, __builtin_fmaf(s.z, c4.z, s.w * c4.w)));
-    y += __shfl_xor(y, 1, 4);
-    y += __shfl_xor(y, 2, 4);
-    if (part == 0) {
-        if (p.D) y = __builtin_fmaf(p.D[d], x, y);
-        if (p.z) y *= silu_f32(to_f32(reinterpret_cast<const T *>(p.z)[b * p.z_batch_stride + d * p.z_d_stride]));
-        reinterpret_cast<T *>(p.out)[b * p.out_batch_stride + d * p.out_d_stride] = from_f32<T>(y);
+// dstate 16 with every row of state, A, B and C contiguous and 4-element aligned (checked on the
+// host). Four lanes per (batch, channel) row, each moving four consecutive states as one 16-byte
+// vector; a 256-lane workgroup covers 64 consecutive channels of one batch row per pass, U passes
+// (64 U channels). Every load of the U passes is issued before the first state is updated: one
+// 16-byte state load per lane and pass would leave too few bytes in flight to cover HBM latency.
+// The grid is one-dimensional, blockIdx.x = batch row * n_blk + channel block, so that no 64-bit
+// division runs per lane; rows past `dim` load the last channel again and store nothing.
+template <typename T, int U>
+__global__ void __launch_bounds__(kDecBlock)
+state_update_rows16(const mm_state_update_params p, const uint32_t ratio, const uint32_t n_blk) {
+    const uint32_t b = blockIdx.x / n_blk;
+    const uint32_t jb = blockIdx.x - b * n_blk;
+    const int part = int(threadIdx.x & 3);
+    const uint32_t dim = uint32_t(p.dim);
+    const uint32_t d_first = jb * (64u * U) + (threadIdx.x >> 2);
+    const T *xb = reinterpret_cast<const T *>(p.x) + int64_t(b) * p.x_batch_stride;
+    const T *dtb = reinterpret_cast<const T *>(p.dt) + int64_t(b) * p.dt_batch_stride;
+    const T *zb = p.z ? reinterpret_cast<const T *>(p.z) + int64_t(b) * p.z_batch_stride : nullptr;
+    float *stb = p.state + int64_t(b) * p.state_batch_stride;
+    const T *Bb = reinterpret_cast<const T *>(p.B) + int64_t(b) * p.B_batch_stride + 4 * part;
+    const T *Cb = reinterpret_cast<const T *>(p.C) + int64_t(b) * p.C_batch_stride + 4 * part;
+
+    DecRow<T> r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t dr = d_first + 64u * u;
+        const uint32_t d = dr < dim ? dr : dim - 1;
+        const uint32_t g = d / ratio;
+        r[u].s = *reinterpret_cast<const float4 *>(stb + int64_t(d) * p.state_d_stride + 4 * part);
+        r[u].a = *reinterpret_cast<const float4 *>(p.A + int64_t(d) * p.A_d_stride + 4 * part);
+        if constexpr (std::is_same_v<T, float>) {
+            r[u].bf = *reinterpret_cast<const float4 *>(Bb + int64_t(g) * p.B_group_stride);
+            r[u].cf = *reinterpret_cast<const float4 *>(Cb + int64_t(g) * p.C_group_stride);
+        } else {
+            r[u].bw = *reinterpret_cast<const uint2 *>(Bb + int64_t(g) * p.B_group_stride);
+            r[u].cw = *reinterpret_cast<const uint2 *>(Cb + int64_t(g) * p.C_group_stride);
+        }
+        r[u].dt = dtb[int64_t(d) * p.dt_d_stride];
+        r[u].x = xb[int64_t(d) * p.x_d_stride];
+        if (zb) r[u].z = zb[int64_t(d) * p.z_d_stride];
+        r[u].D = p.D ? p.D[d] : 0.f;
+        r[u].bias = p.dt_bias ? p.dt_bias[d] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t dr = d_first + 64u * u;
+        float4 b4, c4;
+        if constexpr (std::is_same_v<T, float>) {
+            b4 = r[u].bf;
+            c4 = r[u].cf;
+        } else if constexpr (std::is_same_v<T, bf16_t>) {
+            unpack_bf16x2(r[u].bw.x, b4.x, b4.y);
+            unpack_bf16x2(r[u].bw.y, b4.z, b4.w);
+            unpack_bf16x2(r[u].cw.x, c4.x, c4.y);
+            unpack_bf16x2(r[u].cw.y, c4.z, c4.w);
+        } else {
+            unpack_f16x2(r[u].bw.x, b4.x, b4.y);
+            unpack_f16x2(r[u].bw.y, b4.z, b4.w);
+            unpack_f16x2(r[u].cw.x, c4.x, c4.y);
+            unpack_f16x2(r[u].cw.y, c4.z, c4.w);
+        }
+        float dt = to_f32(r[u].dt) + r[u].bias;
+        if (p.dt_softplus) dt = softplus_fast(dt);
+        const float x = to_f32(r[u].x);
+        const float dtx = dt * x;
+        const float dl = dt * kLog2e;
+        float4 s = r[u].s;
+        s.x = __builtin_fmaf(s.x, fast_exp2(dl * r[u].a.x), dtx * b4.x);
+        s.y = __builtin_fmaf(s.y, fast_exp2(dl * r[u].a.y), dtx * b4.y);
+        s.z = __builtin_fmaf(s.z, fast_exp2(dl * r[u].a.z), dtx * b4.z);
+        s.w = __builtin_fmaf(s.w, fast_exp2(dl * r[u].a.w), dtx * b4.w);
+        const bool live = dr < dim;
+        if (live) *reinterpret_cast<float4 *>(stb + int64_t(dr) * p.state_d_stride + 4 * part) = s;
+        float y = __builtin_fmaf(s.x, c4.x, __builtin_fmaf(s.y, c4.y, __builtin_fmaf(s.z, c4.z, s.w * c4.w)));
+        y += __shfl_xor(y, 1, 4);
+        y += __shfl_xor(y, 2, 4);
+        if (live && part == 0) {
+            y = __builtin_fmaf(r[u].D, x, y);
+            if (zb) y *= silu_fast(to_f32(r[u].z));
+            reinterpret_cast<T *>(p.out)[int64_t(b) * p.out_batch_stride + int64_t(dr) * p.out_d_stride] = from_f32<T>(y);
+        }
     }
 }
 
@@ -465,13 +520,21 @@ bool su_vec16_ok(const mm_state_update_params &p) {
            p.B_group_stride % 4 == 0 && p.C_batch_stride % 4 == 0 && p.C_group_stride % 4 == 0;
 }
 
+template <typename T, int U>
+int launch_rows16(const mm_state_update_params &p, hipStream_t s) {
+    const int64_t n_blk = (p.dim + 64 * U - 1) / (64 * U);
+    hipLaunchKernelGGL((mm::state_update_rows16<T, U>), dim3(unsigned(p.batch * n_blk)), dim3(mm::kDecBlock), 0, s, p,
+                       uint32_t(p.dim / p.n_groups), uint32_t(n_blk));
+    return mm::launch_status("state_update");
+}
+
 template <typename T>
 int dispatch_su(const mm_state_update_params &p, hipStream_t s) {
-    if (su_vec16_ok(p)) {
-        const int64_t threads = p.batch * p.dim * 4;
-        dim3 grid(unsigned((threads + mm::kDecBlock - 1) / mm::kDecBlock));
-        hipLaunchKernelGGL((mm::state_update_vec16<T>), grid, dim3(mm::kDecBlock), 0, s, p, p.dim / p.n_groups);
-        return mm::launch_status("state_update");
+    if (su_vec16_ok(p) && p.dim < (int64_t(1) << 31) &&
+        p.batch * ((p.dim + 63) / 64) < (int64_t(1) << 31)) {
+        // Four passes per lane once that still leaves about four workgroups per CU of the MI355X.
+        if (p.batch * p.dim >= int64_t(256) * 4 * 256) return launch_rows16<T, 4>(p, s);
+        return launch_rows16<T, 1>(p, s);
     }
     if (p.dstate <= 16) return launch_su<T, 4, 4>(p, s);
     if (p.dstate <= 64) return launch_su<T, 4, 16>(p, s);

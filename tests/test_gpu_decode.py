@@ -43,8 +43,10 @@ def _gpu(d):
     return {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in d.items()}
 
 
+# (96, 2800, 16, 4): enough rows for the four-pass dstate-16 kernel, with a partial last block of
+# channels (2800 = 10 x 256 + 240) and four groups of 700 channels.
 CASES = [(1, 64, 16, 0), (3, 100, 16, 0), (64, 128, 16, 0), (2, 64, 8, 0), (2, 64, 32, 0),
-         (2, 64, 64, 2), (2, 32, 100, 0), (4, 128, 16, 4), (2, 64, 1, 0)]
+         (2, 64, 64, 2), (2, 32, 100, 0), (4, 128, 16, 4), (2, 64, 1, 0), (96, 2800, 16, 4)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
@@ -181,3 +183,43 @@ def test_state_update_c_abi_direct():
     torch.cuda.synchronize()
     torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
     torch.testing.assert_close(g["state"].cpu(), ref_state, rtol=1e-4, atol=1e-5)
+
+
+def test_decode_graph_replay_matches_eager():
+    """Three decode steps captured in one HIP graph (a serving loop's form), replayed four times
+    with fresh inputs and states copied in between: every replay equals the same steps run eagerly,
+    bit for bit (the captured launches are the eager ones)."""
+    from motif_mamba_amd import selective_state_update
+    batch, dim, N = 64, 4096, 16   # the four-pass dstate-16 kernel
+    _say(f"decode graph replay batch {batch} dim {dim}")
+    g = _gpu(_inputs(11, batch, dim, N, torch.bfloat16))
+    state = g["state"].clone()
+
+    def step():
+        return selective_state_update(state, g["x"], g["dt"], g["A"], g["B"], g["C"], g["D"], g["z"],
+                                      g["dt_bias"], dt_softplus=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [step() for _ in range(3)]
+    gen = torch.Generator().manual_seed(12)
+    for rep in range(4):
+        init = (torch.randn(batch, dim, N, generator=gen) * 0.1).to(DEV)
+        for k in ("x", "dt", "z", "B", "C"):
+            g[k].copy_(torch.randn(g[k].shape, generator=gen).to(g[k].dtype).to(DEV))
+        state.copy_(init)
+        graph.replay()
+        torch.cuda.synchronize()
+        got_state, got = state.clone(), [o.clone() for o in outs]
+        ref_state = init.clone()
+        exp = [selective_state_update(ref_state, g["x"], g["dt"], g["A"], g["B"], g["C"], g["D"], g["z"],
+                                      g["dt_bias"], dt_softplus=True) for _ in range(3)]
+        torch.cuda.synchronize()
+        assert torch.equal(got_state, ref_state), f"replay {rep}: state differs from eager"
+        for i, (a, b) in enumerate(zip(got, exp)):
+            assert torch.equal(a, b), f"replay {rep}: output of step {i} differs from eager"
