@@ -55,6 +55,23 @@ def _time_loop(fn, steps, warmup, torch):
     return start.elapsed_time(end) / steps  # ms per step (events on the launch stream)
 
 
+def _graph_ms_per_step(step, n_calls, steps, torch):
+    """step(0 .. n_calls-1) captured once in a HIP graph and replayed steps / n_calls times: the
+    per-call GPU time of a serving loop that does not pay one Python call per token."""
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n_calls):  # warm the allocator and the binding on the capture stream
+            step(i)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        for i in range(n_calls):
+            step(i)
+    reps = max(1, steps // n_calls)
+    return _time_loop(lambda i: graph.replay(), reps, 2, torch) / n_calls
+
+
 def bench_scan(cfg_name, steps, warmup, torch, rotate=1):
     from motif_mamba_amd import selective_scan_fn
     from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_bytes, scan_inputs, scan_transcendentals
@@ -109,20 +126,7 @@ def bench_decode(batch, steps, warmup, torch, sets_max=64):
     ms = _time_loop(step, steps, warmup, torch)
     nbytes = decode_bytes(batch, c.dim, c.dstate)
 
-    # The same S steps captured once in a HIP graph and replayed steps / S times: the per-step GPU
-    # time of a serving loop that does not pay one Python call per token.
-    graph = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(S):  # warm the allocator and the binding on the capture stream
-            step(i)
-    torch.cuda.current_stream().wait_stream(side)
-    with torch.cuda.graph(graph):
-        for i in range(S):
-            step(i)
-    reps = max(1, steps // S)
-    gms = _time_loop(lambda i: graph.replay(), reps, 2, torch) / S
+    gms = _graph_ms_per_step(step, S, steps, torch)
     return {"batch": batch, "dim": c.dim, "dstate": c.dstate, "steps": steps, "us_per_step": ms * 1e3,
             "tokens_per_s": batch / (ms * 1e-3), "GB_s": nbytes / (ms * 1e-3) / 1e9,
             "graph_us_per_step": gms * 1e3, "graph_tokens_per_s": batch / (gms * 1e-3),
@@ -217,10 +221,13 @@ def bench_conv_update(batch, steps, warmup, torch, dim=5120):
     st = torch.zeros(batch, dim, 4, device="cuda").to(torch.bfloat16)
     w = (torch.randn(dim, 4, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
     b = (torch.randn(dim, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
-    ms = _time_loop(lambda i: causal_conv1d_update(x, st, w, b, activation="silu"), steps, warmup, torch)
+    step = lambda i: causal_conv1d_update(x, st, w, b, activation="silu")  # noqa: E731
+    ms = _time_loop(step, steps, warmup, torch)
+    gms = _graph_ms_per_step(step, 64, max(steps, 256), torch)
     nbytes = batch * dim * (2 * 4 * 2 + 2 * 2) + dim * 5 * 2
     return {"batch": batch, "dim": dim, "us_per_step": ms * 1e3, "tokens_per_s": batch / (ms * 1e-3),
-            "GB_s": nbytes / (ms * 1e-3) / 1e9}
+            "GB_s": nbytes / (ms * 1e-3) / 1e9, "graph_us_per_step": gms * 1e3,
+            "graph_GB_s": nbytes / (gms * 1e-3) / 1e9}
 
 
 def bench_inner(steps, warmup, torch, batch=4, seqlen=4096, d_model=2560, d_inner=5120, rank=160, d_state=16):

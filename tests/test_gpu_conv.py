@@ -105,6 +105,26 @@ def test_conv_update(dtype, sdtype, state_len, seqlen):
     _close(st_gpu, st_ref, sdtype, "state")
 
 
+
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32], ids=["w_bf16", "w_fp32"])
+def test_conv_update_decode_many_rows(wdtype):
+    """The decode form at enough rows for the four-pass kernel (224 x 4700 = 1,052,800 rows, a
+    partial last block of channels), bf16 tokens and state with bf16 or float32 weights."""
+    _say(f"conv update 224 x 4700 weight {wdtype}")
+    from causal_conv1d import causal_conv1d_update
+    g = torch.Generator().manual_seed(760)
+    batch, dim = 224, 4700
+    x = torch.randn(batch, dim, generator=g).to(torch.bfloat16)
+    w = (torch.randn(dim, 4, generator=g) * 0.5).to(wdtype)
+    b = (torch.randn(dim, generator=g) * 0.1).to(wdtype)
+    st = torch.randn(batch, dim, 4, generator=g).to(torch.bfloat16)
+    st_ref = st.clone()
+    st_gpu = st.to(DEV)
+    got = causal_conv1d_update(x.to(DEV), st_gpu, w.to(DEV), b.to(DEV), activation="silu")
+    ref = causal_conv1d_update_ref(x, st_ref, w, b, activation="silu")
+    _close(got, ref, torch.bfloat16, "out")
+    assert torch.equal(st_gpu.cpu(), st_ref), "state: the shifted entries must be moved exactly"
+
 def test_conv_prefill_then_decode_matches_forward():
     """The module's hand-off (mamba_simplemotif.py:292-293): the state after a prefill is the last
     d_conv inputs; decoding the following tokens one by one reproduces the forward of the sequence."""
