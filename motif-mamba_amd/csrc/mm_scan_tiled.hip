@@ -601,14 +601,53 @@ int launch_pipe_segmented(const mm_scan_fwd_params &p, hipStream_t stream, const
 // u and z in registers in between. Both waves do the same work in every interval, and the
 // prologue/epilogue instructions sit in the same basic block as the scan, so they fill its latency
 // gaps instead of forming a latency-bound phase of their own.
+//
+// FULL (L a multiple of 32, every tile pair whole): the only clamp left is of the pair index, which
+// is uniform, so every load and store is a buffer instruction whose address is a per-tensor
+// resource (scalar), a byte offset fixed per lane (VGPR) and the pair's byte offset (SGPR) -- no
+// per-lane address arithmetic, compares or selects in the loop (they were about a sixth of its
+// VALU instructions).
 // ---------------------------------------------------------------------------------------------
+// Raw buffer resource over [base, base + 4 GiB): the address of an access is base + the lane's
+// VGPR offset + a scalar offset, range-checked against 2^32 - 1 bytes (gfx9 resource word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, 0x00020000);
+}
+
+// Four consecutive 16-bit elements (8 bytes) through a buffer resource.
+template <typename T>
+__device__ __forceinline__ RawVec<T, 4> buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    static_assert(sizeof(T) == 2, "8-byte buffer accesses move four 16-bit elements");
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+    RawVec<T, 4> x;
+    x.w[0] = v.x;
+    x.w[1] = v.y;
+    return x;
+}
+
+template <typename T>
+__device__ __forceinline__ void buffer_store8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float *x) {
+    static_assert(sizeof(T) == 2, "8-byte buffer accesses move four 16-bit elements");
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 v;
+    if constexpr (std::is_same_v<T, bf16_t>) {
+        v.x = pack_bf16x2(x[0], x[1]);
+        v.y = pack_bf16x2(x[2], x[3]);
+    } else {
+        v.x = pack_f16x2(x[0], x[1]);
+        v.y = pack_f16x2(x[2], x[3]);
+    }
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, soff, 0);
+}
+
 template <typename T>
 struct K2Data {                 // one lane's global data for pair iteration i
     RawVec<T, 4> b, c;          // B, C of one of the lane's row states: 4 steps of tile pair i
     RawVec<T, 4> u, dl, z;      // u, delta, z: 4 steps of this wave's tile of pair i + 1
 };
 
-template <typename T, int PF, bool SOFTPLUS, bool CHUNKS>
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool FULL>
 __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
 scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
@@ -675,17 +714,41 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     // L % 8 == 0); the prologue zeroes delta' of such steps, so they leave the state unchanged.
     const uint32_t last4 = uint32_t(L - E);
     auto clamp4 = [&](int64_t t) { return t < int64_t(last4) ? uint32_t(t) : last4; };
+    // FULL: buffer resources of the group's rows (the host checks that every byte offset of the
+    // group is below 2^32) and this lane's byte offsets from them.
+    constexpr uint32_t SZ = sizeof(T);
+    const uint32_t fo_u = (u_row + kT1 * w + es) * SZ, fo_d = (d_row + kT1 * w + es) * SZ;
+    const uint32_t fo_z = (z_row + kT1 * w + es) * SZ;
+    const uint32_t fo_b = (B_row + sb) * SZ, fo_c = (C_row + sb) * SZ;
+    const uint32_t fo_o = (o_row + es) * SZ, fo_oz = (oz_row + es) * SZ;
+    const __amdgpu_buffer_rsrc_t rs_u = buffer_rsrc(ub), rs_d = buffer_rsrc(db), rs_z = buffer_rsrc(zb);
+    const __amdgpu_buffer_rsrc_t rs_b = buffer_rsrc(Bb), rs_c = buffer_rsrc(Cb);
+    const __amdgpu_buffer_rsrc_t rs_o = buffer_rsrc(ob), rs_oz = buffer_rsrc(ozb);
     auto load_elems = [&](int64_t pair_i, RawVec<T, E> &u, RawVec<T, E> &dl, RawVec<T, E> &z) {
-        const uint32_t te = clamp4(pair_i * (2 * kT1) + kT1 * w + es);
-        u = load_raw<T, E>(ub + (u_row + te));
-        dl = load_raw<T, E>(db + (d_row + te));
-        if (zb) z = load_raw<T, E>(zb + (z_row + te));
-        else z = {};
+        if constexpr (FULL) {
+            const uint32_t sof = uint32_t((pair_i < n_pairs ? pair_i : n_pairs - 1) * (2 * kT1 * SZ));   // uniform
+            u = buffer_load8<T>(rs_u, fo_u, sof);
+            dl = buffer_load8<T>(rs_d, fo_d, sof);
+            if (zb) z = buffer_load8<T>(rs_z, fo_z, sof);
+            else z = {};
+        } else {
+            const uint32_t te = clamp4(pair_i * (2 * kT1) + kT1 * w + es);
+            u = load_raw<T, E>(ub + (u_row + te));
+            dl = load_raw<T, E>(db + (d_row + te));
+            if (zb) z = load_raw<T, E>(zb + (z_row + te));
+            else z = {};
+        }
     };
     auto load_data = [&](int64_t i, K2Data<T> &dst) {
-        const uint32_t tb = clamp4(i * (2 * kT1) + sb);
-        dst.b = load_raw<T, E>(Bb + (B_row + tb));
-        dst.c = load_raw<T, E>(Cb + (C_row + tb));
+        if constexpr (FULL) {
+            const uint32_t sof = uint32_t((i < n_pairs ? i : n_pairs - 1) * (2 * kT1 * SZ));              // uniform
+            dst.b = buffer_load8<T>(rs_b, fo_b, sof);
+            dst.c = buffer_load8<T>(rs_c, fo_c, sof);
+        } else {
+            const uint32_t tb = clamp4(i * (2 * kT1) + sb);
+            dst.b = load_raw<T, E>(Bb + (B_row + tb));
+            dst.c = load_raw<T, E>(Cb + (C_row + tb));
+        }
         load_elems(i + 1, dst.u, dst.dl, dst.z);
     };
 
@@ -707,7 +770,9 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
             const float x = dd[k] + bias;
             dtp[k] = SOFTPLUS ? softplus_fast(x) : x;
         }
-        if (t0 + es >= L) {  // padded steps (L % 8 == 0: all four or none)
+        // Padded steps (L % 8 == 0: all four or none). With FULL only tiles past the last pair are
+        // prepared beyond L, and those are never scanned.
+        if (!FULL && t0 + es >= L) {
 #pragma unroll
             for (int k = 0; k < E; ++k) dtp[k] = 0.f;
         }
@@ -726,15 +791,19 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
             const float4 v = *reinterpret_cast<const float4 *>(&yb[(rr * kCh + ce) * kT1 + ecol]);
             a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
         }
-        if (t0 + es < L) {
+        if (FULL || t0 + es < L) {   // FULL: only whole tiles are finished
             float o[E] = {__builtin_fmaf(Dv, uu[sl][0], a.x), __builtin_fmaf(Dv, uu[sl][1], a.y),
                           __builtin_fmaf(Dv, uu[sl][2], a.z), __builtin_fmaf(Dv, uu[sl][3], a.w)};
             const uint32_t t = uint32_t(t0 + es);
-            if (ob) store_vec<T, E>(ob + (o_row + t), o);
+            if (ob) {
+                if constexpr (FULL) buffer_store8<T>(rs_o, fo_o, uint32_t(t0 * SZ), o);
+                else store_vec<T, E>(ob + (o_row + t), o);
+            }
             if (zb) {
 #pragma unroll
                 for (int k = 0; k < E; ++k) o[k] *= silu_fast(zz[sl][k]);
-                store_vec<T, E>(ozb + (oz_row + t), o);
+                if constexpr (FULL) buffer_store8<T>(rs_oz, fo_oz, uint32_t(t0 * SZ), o);
+                else store_vec<T, E>(ozb + (oz_row + t), o);
             }
         }
     };
@@ -846,15 +915,25 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     }
 }
 
-template <typename T, int PF>
-int launch_k2i(const mm_scan_fwd_params &p, hipStream_t stream) {
+template <typename T, int PF, bool FULL>
+int launch_k2i_full(const mm_scan_fwd_params &p, hipStream_t stream) {
     const int64_t ratio = p.dim / p.n_groups;
     dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
     auto *kern = p.delta_softplus
-                     ? (p.chunk_states ? scan_fwd_k2i<T, PF, true, true> : scan_fwd_k2i<T, PF, true, false>)
-                     : (p.chunk_states ? scan_fwd_k2i<T, PF, false, true> : scan_fwd_k2i<T, PF, false, false>);
+                     ? (p.chunk_states ? scan_fwd_k2i<T, PF, true, true, FULL> : scan_fwd_k2i<T, PF, true, false, FULL>)
+                     : (p.chunk_states ? scan_fwd_k2i<T, PF, false, true, FULL> : scan_fwd_k2i<T, PF, false, false, FULL>);
     hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
     return launch_status("scan_fwd_k2i");
+}
+
+// FULL needs whole tile pairs and byte offsets (span x element size) below 2^32; the callers have
+// checked that the element span is below 2^31 (pipe_offsets_ok) and T is a 16-bit type here.
+template <typename T, int PF>
+int launch_k2i(const mm_scan_fwd_params &p, hipStream_t stream) {
+    static_assert(sizeof(T) == 2, "k2i runs 16-bit inputs");
+    static const bool nofull = getenv("MM_SCAN_NOFULL") != nullptr;
+    if (p.seqlen % (2 * kT1) == 0 && !nofull) return launch_k2i_full<T, PF, true>(p, stream);
+    return launch_k2i_full<T, PF, false>(p, stream);
 }
 
 template <typename T, int NW>
