@@ -201,4 +201,62 @@ __device__ __forceinline__ void store_vec(T *p, const float *x) {
     }
 }
 
+// ---- buffer instructions -----------------------------------------------------------------------
+// Raw buffer resource over [base, base + 4 GiB): the address of an access is base + the lane's
+// VGPR byte offset + a scalar byte offset, range-checked against 2^32 - 1 bytes (gfx9 resource
+// word 3). A kernel that addresses a row group this way keeps one scalar base per tensor and a
+// 32-bit offset per lane instead of a 64-bit pointer per lane and tensor.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, 0x00020000);
+}
+
+// N consecutive elements of T (4, 8 or 16 bytes) through a buffer resource.
+template <typename T, int N>
+__device__ __forceinline__ RawVec<T, N> buffer_load_raw(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    RawVec<T, N> x;
+    constexpr int W = sizeof(x.w) / 4;
+    if constexpr (W == 1) {
+        x.w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    } else if constexpr (W == 2) {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+        x.w[0] = v.x;
+        x.w[1] = v.y;
+    } else {
+        static_assert(W == 4, "buffer_load_raw moves 4, 8 or 16 bytes");
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+        x.w[0] = v.x;
+        x.w[1] = v.y;
+        x.w[2] = v.z;
+        x.w[3] = v.w;
+    }
+    return x;
+}
+
+// N floats converted to T (bf16 round-to-nearest-even) and stored as one 4-, 8- or 16-byte access.
+template <typename T, int N>
+__device__ __forceinline__ void buffer_store_vec(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float *x) {
+    constexpr int W = (N * int(sizeof(T)) + 3) / 4;
+    uint32_t w[W];
+    if constexpr (std::is_same_v<T, float>) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = __float_as_uint(x[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i)
+            w[i] = std::is_same_v<T, bf16_t> ? pack_bf16x2(x[2 * i], x[2 * i + 1]) : pack_f16x2(x[2 * i], x[2 * i + 1]);
+    }
+    if constexpr (W == 1) {
+        __builtin_amdgcn_raw_buffer_store_b32(w[0], r, voff, soff, 0);
+    } else if constexpr (W == 2) {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{w[0], w[1]}, r, voff, soff, 0);
+    } else {
+        static_assert(W == 4, "buffer_store_vec moves 4, 8 or 16 bytes");
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, r, voff, soff, 0);
+    }
+}
+
 }  // namespace mm

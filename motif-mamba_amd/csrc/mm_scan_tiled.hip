@@ -608,39 +608,6 @@ int launch_pipe_segmented(const mm_scan_fwd_params &p, hipStream_t stream, const
 // per-lane address arithmetic, compares or selects in the loop (they were about a sixth of its
 // VALU instructions).
 // ---------------------------------------------------------------------------------------------
-// Raw buffer resource over [base, base + 4 GiB): the address of an access is base + the lane's
-// VGPR offset + a scalar offset, range-checked against 2^32 - 1 bytes (gfx9 resource word 3).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, 0x00020000);
-}
-
-// Four consecutive 16-bit elements (8 bytes) through a buffer resource.
-template <typename T>
-__device__ __forceinline__ RawVec<T, 4> buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    static_assert(sizeof(T) == 2, "8-byte buffer accesses move four 16-bit elements");
-    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
-    RawVec<T, 4> x;
-    x.w[0] = v.x;
-    x.w[1] = v.y;
-    return x;
-}
-
-template <typename T>
-__device__ __forceinline__ void buffer_store8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float *x) {
-    static_assert(sizeof(T) == 2, "8-byte buffer accesses move four 16-bit elements");
-    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-    u32x2 v;
-    if constexpr (std::is_same_v<T, bf16_t>) {
-        v.x = pack_bf16x2(x[0], x[1]);
-        v.y = pack_bf16x2(x[2], x[3]);
-    } else {
-        v.x = pack_f16x2(x[0], x[1]);
-        v.y = pack_f16x2(x[2], x[3]);
-    }
-    __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, soff, 0);
-}
-
 template <typename T>
 struct K2Data {                 // one lane's global data for pair iteration i
     RawVec<T, 4> b, c;          // B, C of one of the lane's row states: 4 steps of tile pair i
@@ -727,9 +694,9 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     auto load_elems = [&](int64_t pair_i, RawVec<T, E> &u, RawVec<T, E> &dl, RawVec<T, E> &z) {
         if constexpr (FULL) {
             const uint32_t sof = uint32_t((pair_i < n_pairs ? pair_i : n_pairs - 1) * (2 * kT1 * SZ));   // uniform
-            u = buffer_load8<T>(rs_u, fo_u, sof);
-            dl = buffer_load8<T>(rs_d, fo_d, sof);
-            if (zb) z = buffer_load8<T>(rs_z, fo_z, sof);
+            u = buffer_load_raw<T, E>(rs_u, fo_u, sof);
+            dl = buffer_load_raw<T, E>(rs_d, fo_d, sof);
+            if (zb) z = buffer_load_raw<T, E>(rs_z, fo_z, sof);
             else z = {};
         } else {
             const uint32_t te = clamp4(pair_i * (2 * kT1) + kT1 * w + es);
@@ -742,8 +709,8 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     auto load_data = [&](int64_t i, K2Data<T> &dst) {
         if constexpr (FULL) {
             const uint32_t sof = uint32_t((i < n_pairs ? i : n_pairs - 1) * (2 * kT1 * SZ));              // uniform
-            dst.b = buffer_load8<T>(rs_b, fo_b, sof);
-            dst.c = buffer_load8<T>(rs_c, fo_c, sof);
+            dst.b = buffer_load_raw<T, E>(rs_b, fo_b, sof);
+            dst.c = buffer_load_raw<T, E>(rs_c, fo_c, sof);
         } else {
             const uint32_t tb = clamp4(i * (2 * kT1) + sb);
             dst.b = load_raw<T, E>(Bb + (B_row + tb));
@@ -796,13 +763,13 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
                           __builtin_fmaf(Dv, uu[sl][2], a.z), __builtin_fmaf(Dv, uu[sl][3], a.w)};
             const uint32_t t = uint32_t(t0 + es);
             if (ob) {
-                if constexpr (FULL) buffer_store8<T>(rs_o, fo_o, uint32_t(t0 * SZ), o);
+                if constexpr (FULL) buffer_store_vec<T, E>(rs_o, fo_o, uint32_t(t0 * SZ), o);
                 else store_vec<T, E>(ob + (o_row + t), o);
             }
             if (zb) {
 #pragma unroll
                 for (int k = 0; k < E; ++k) o[k] *= silu_fast(zz[sl][k]);
-                if constexpr (FULL) buffer_store8<T>(rs_oz, fo_oz, uint32_t(t0 * SZ), o);
+                if constexpr (FULL) buffer_store_vec<T, E>(rs_oz, fo_oz, uint32_t(t0 * SZ), o);
                 else store_vec<T, E>(ozb + (oz_row + t), o);
             }
         }
