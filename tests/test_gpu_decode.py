@@ -43,10 +43,12 @@ def _gpu(d):
     return {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in d.items()}
 
 
-# (96, 2800, 16, 4): enough rows for the four-pass dstate-16 kernel, with a partial last block of
-# channels (2800 = 10 x 256 + 240) and four groups of 700 channels.
+# The dstate-16 kernel takes four batch rows per workgroup from batch 4 on: (96, 2800, 16, 4) has a
+# partial last block of channels (2800 = 43 x 64 + 48) and four groups of 700 channels; (7, 200, 16, 0)
+# and (5, 64, 16, 2) a partial last block of batch rows.
 CASES = [(1, 64, 16, 0), (3, 100, 16, 0), (64, 128, 16, 0), (2, 64, 8, 0), (2, 64, 32, 0),
-         (2, 64, 64, 2), (2, 32, 100, 0), (4, 128, 16, 4), (2, 64, 1, 0), (96, 2800, 16, 4)]
+         (2, 64, 64, 2), (2, 32, 100, 0), (4, 128, 16, 4), (2, 64, 1, 0), (96, 2800, 16, 4),
+         (7, 200, 16, 0), (5, 64, 16, 2)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
