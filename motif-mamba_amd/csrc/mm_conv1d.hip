@@ -188,58 +188,55 @@ conv1d_update_kernel(const mm_conv1d_update_params p) {
 
 
 // The decode form of the Mamba block (one new token, width 4, a contiguous 4-entry state per row,
-// weight rows of 4 contiguous elements): one lane per (batch, channel) row and U rows per lane, 256
-// consecutive channels of one batch row per pass, every load of the U passes issued before any
-// arithmetic. blockIdx.x = batch row * n_blk + channel block (no 64-bit division per lane);
-// channels past `dim` reload the last channel and store nothing.
+// weight rows of 4 contiguous elements): one lane per (batch, channel) row; a workgroup covers 256
+// consecutive channels of U consecutive batch rows, so a lane loads its channel's weights and bias
+// once for U rows, and every load of the U rows is issued before any arithmetic. blockIdx.x = batch
+// block * n_dblk + channel block (no 64-bit division per lane); channels past `dim` and rows past
+// `batch` reload the last one and store nothing.
 template <typename T, typename WT, int U>
 __global__ void __launch_bounds__(kThreads)
-conv1d_update_tok4(const mm_conv1d_update_params p, const uint32_t n_blk) {
-    const uint32_t b = blockIdx.x / n_blk;
-    const uint32_t jb = blockIdx.x - b * n_blk;
-    const uint32_t dim = uint32_t(p.dim);
-    const uint32_t d_first = jb * (uint32_t(kThreads) * U) + threadIdx.x;
-    const T *xb = reinterpret_cast<const T *>(p.x) + int64_t(b) * p.x_batch_stride;
-    T *sb = reinterpret_cast<T *>(p.conv_state) + int64_t(b) * p.state_batch_stride;
-    T *ob = reinterpret_cast<T *>(p.out) + int64_t(b) * p.out_batch_stride;
-    const WT *wb = reinterpret_cast<const WT *>(p.weight);
-    const WT *bb = reinterpret_cast<const WT *>(p.bias);
+conv1d_update_tok4(const mm_conv1d_update_params p, const uint32_t n_dblk) {
+    const uint32_t bb = blockIdx.x / n_dblk;
+    const uint32_t jd = blockIdx.x - bb * n_dblk;
+    const uint32_t dim = uint32_t(p.dim), batch = uint32_t(p.batch);
+    const uint32_t dr = jd * uint32_t(kThreads) + threadIdx.x;
+    const uint32_t d = dr < dim ? dr : dim - 1;
+    const WT *bptr = reinterpret_cast<const WT *>(p.bias);
+    float w4[4];
+    unpack_raw<WT, 4>(load_raw<WT, 4>(reinterpret_cast<const WT *>(p.weight) + int64_t(d) * p.weight_d_stride), w4);
+    const float bias = bptr ? to_f32(bptr[int64_t(d) * p.bias_stride]) : 0.f;
 
     RawVec<T, 4> st[U];
-    RawVec<WT, 4> wr[U];
     T xv[U];
-    WT bv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint32_t dr = d_first + uint32_t(kThreads) * u;
-        const uint32_t d = dr < dim ? dr : dim - 1;
-        st[u] = load_raw<T, 4>(sb + int64_t(d) * p.state_d_stride);
-        wr[u] = load_raw<WT, 4>(wb + int64_t(d) * p.weight_d_stride);
-        xv[u] = xb[int64_t(d) * p.x_d_stride];
-        if (bb) bv[u] = bb[int64_t(d) * p.bias_stride];
+        const uint32_t b0 = bb * U + u;
+        const uint32_t b = b0 < batch ? b0 : batch - 1;
+        st[u] = load_raw<T, 4>(reinterpret_cast<const T *>(p.conv_state) + int64_t(b) * p.state_batch_stride +
+                               int64_t(d) * p.state_d_stride);
+        xv[u] = reinterpret_cast<const T *>(p.x)[int64_t(b) * p.x_batch_stride + int64_t(d) * p.x_d_stride];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint32_t dr = d_first + uint32_t(kThreads) * u;
-        float s4[4], w4[4];
+        const uint32_t b = bb * U + u;
+        float s4[4];
         unpack_raw<T, 4>(st[u], s4);
-        unpack_raw<WT, 4>(wr[u], w4);
         const float x = to_f32(xv[u]);
         // The window after the shift is (s1, s2, s3, x); weight k multiplies window entry k.
-        float acc = bb ? to_f32(bv[u]) : 0.f;
+        float acc = bias;
         acc = __builtin_fmaf(w4[0], s4[1], acc);
         acc = __builtin_fmaf(w4[1], s4[2], acc);
         acc = __builtin_fmaf(w4[2], s4[3], acc);
         acc = __builtin_fmaf(w4[3], x, acc);
         const float o = p.silu ? acc * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-acc * kLog2e)) : acc;
-        if (dr < dim) {
+        if (dr < dim && b < batch) {
             const float ns[4] = {s4[1], s4[2], s4[3], x};
-            store_vec<T, 4>(sb + int64_t(dr) * p.state_d_stride, ns);
-            ob[int64_t(dr) * p.out_d_stride] = from_f32<T>(o);
+            store_vec<T, 4>(reinterpret_cast<T *>(p.conv_state) + int64_t(b) * p.state_batch_stride +
+                                int64_t(dr) * p.state_d_stride, ns);
+            reinterpret_cast<T *>(p.out)[int64_t(b) * p.out_batch_stride + int64_t(dr) * p.out_d_stride] = from_f32<T>(o);
         }
     }
 }
-
 
 // Backward: each lane owns NC chunks of 8 positions of one row. It recomputes the pre-activation y
 // at its positions and the next W - 1 (x from W - 1 before to W - 1 after, as 8-element chunks),
@@ -443,19 +440,20 @@ int launch_update(const mm_conv1d_update_params &p, hipStream_t s) {
     if (vec4 && p.seqlen == 1 && p.width == 4 && p.weight_w_stride == 1 && p.dim < (int64_t(1) << 31)) {
         const int64_t wb = 4 * (p.wtype == MM_FLOAT32 ? 4 : 2);
         const bool w_ok = reinterpret_cast<uintptr_t>(p.weight) % uintptr_t(wb) == 0 && p.weight_d_stride % 4 == 0;
-        if (w_ok && (p.wtype == MM_FLOAT32 || p.wtype == p.itype)) {
-            // Four passes per lane once that still leaves about four workgroups per CU of the MI355X.
-            const int U = rows >= int64_t(kThreads) * 4 * 256 * 4 ? 4 : 1;
-            const int64_t n_blk = (p.dim + int64_t(kThreads) * U - 1) / (int64_t(kThreads) * U);
-            if (p.batch * n_blk < (int64_t(1) << 31)) {
-                const dim3 g1(unsigned(p.batch * n_blk));
+        if (w_ok && (p.wtype == MM_FLOAT32 || p.wtype == p.itype) && p.batch < (int64_t(1) << 31)) {
+            // Four batch rows per workgroup share the weight and bias loads.
+            const int U = p.batch >= 4 ? 4 : 1;
+            const int64_t n_dblk = (p.dim + kThreads - 1) / kThreads;
+            const int64_t n_bblk = (p.batch + U - 1) / U;
+            if (n_bblk * n_dblk < (int64_t(1) << 31)) {
+                const dim3 g1(unsigned(n_bblk * n_dblk));
                 const bool wf = p.wtype == MM_FLOAT32;
                 if (U == 4) {
-                    if (wf) hipLaunchKernelGGL((conv1d_update_tok4<T, float, 4>), g1, dim3(kThreads), 0, s, p, uint32_t(n_blk));
-                    else hipLaunchKernelGGL((conv1d_update_tok4<T, T, 4>), g1, dim3(kThreads), 0, s, p, uint32_t(n_blk));
+                    if (wf) hipLaunchKernelGGL((conv1d_update_tok4<T, float, 4>), g1, dim3(kThreads), 0, s, p, uint32_t(n_dblk));
+                    else hipLaunchKernelGGL((conv1d_update_tok4<T, T, 4>), g1, dim3(kThreads), 0, s, p, uint32_t(n_dblk));
                 } else {
-                    if (wf) hipLaunchKernelGGL((conv1d_update_tok4<T, float, 1>), g1, dim3(kThreads), 0, s, p, uint32_t(n_blk));
-                    else hipLaunchKernelGGL((conv1d_update_tok4<T, T, 1>), g1, dim3(kThreads), 0, s, p, uint32_t(n_blk));
+                    if (wf) hipLaunchKernelGGL((conv1d_update_tok4<T, float, 1>), g1, dim3(kThreads), 0, s, p, uint32_t(n_dblk));
+                    else hipLaunchKernelGGL((conv1d_update_tok4<T, T, 1>), g1, dim3(kThreads), 0, s, p, uint32_t(n_dblk));
                 }
                 return launch_status("conv1d_update");
             }

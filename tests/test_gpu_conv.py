@@ -108,12 +108,13 @@ def test_conv_update(dtype, sdtype, state_len, seqlen):
 
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32], ids=["w_bf16", "w_fp32"])
 def test_conv_update_decode_many_rows(wdtype):
-    """The decode form at enough rows for the four-pass kernel (224 x 4700 = 1,052,800 rows, a
-    partial last block of channels), bf16 tokens and state with bf16 or float32 weights."""
-    _say(f"conv update 224 x 4700 weight {wdtype}")
+    """The decode form with four batch rows per workgroup (222 x 4700: a partial last block of
+    channels, 4700 = 18 x 256 + 92, and of batch rows, 222 = 55 x 4 + 2), bf16 tokens and state with
+    bf16 or float32 weights."""
+    _say(f"conv update 222 x 4700 weight {wdtype}")
     from causal_conv1d import causal_conv1d_update
     g = torch.Generator().manual_seed(760)
-    batch, dim = 224, 4700
+    batch, dim = 222, 4700
     x = torch.randn(batch, dim, generator=g).to(torch.bfloat16)
     w = (torch.randn(dim, 4, generator=g) * 0.5).to(wdtype)
     b = (torch.randn(dim, generator=g) * 0.1).to(wdtype)
