@@ -158,13 +158,15 @@ def test_strided_inputs_like_mamba_block(dtype):
     _close(last.cpu(), exp_last, dtype, "last_state")
 
 
+@pytest.mark.parametrize("L", [4100, 4096])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
-def test_reference_fwd_outputs(dtype):
+def test_reference_fwd_outputs(dtype, L):
     """ext.fwd returns [out, x, out_z] in the layout of selective_scan_cuda.fwd
-    (selective_scan.cpp:383-412): out pre-gate, x = (B, D, ceil(L/2048), 2N) (prod a, h) pairs."""
-    _say(f"reference-format fwd {dtype}")
+    (selective_scan.cpp:383-412): out pre-gate, x = (B, D, ceil(L/2048), 2N) (prod a, h) pairs.
+    L = 4100 runs the general kernel, L = 4096 the dstate-16 kernels (bf16: the buffer-addressed
+    path for L a multiple of 32), both with a partial or whole last 2048-step chunk."""
+    _say(f"reference-format fwd {dtype} L={L}")
     from motif_mamba_amd import _native
-    L = 4100
     case = _case(10, 1, 64, L, 16, dtype, bkind="4d", G=1)
     exp_z, exp_last = selective_scan_ref(**case, return_last_state=True)
     exp_out = selective_scan_ref(**{**case, "z": None})
@@ -172,7 +174,7 @@ def test_reference_fwd_outputs(dtype):
     out, x, out_z = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], D=g["D"], z=g["z"],
                                       delta_bias=g["delta_bias"], delta_softplus=True)
     torch.cuda.synchronize()
-    assert x.shape == (1, 64, 3, 32) and x.dtype == torch.float32
+    assert x.shape == (1, 64, (L + 2047) // 2048, 32) and x.dtype == torch.float32
     _close(out.cpu(), exp_out, dtype, "out")
     _close(out_z.cpu(), exp_z, dtype, "out_z")
     _close(x[:, :, -1, 1::2].cpu(), exp_last, dtype, "x[..., -1, 1::2]")
