@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 6
+#define MM_SCAN_ABI_VERSION 7
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -133,7 +133,7 @@ typedef struct mm_scan_fwd_params {
 
 /* Backward of the diagonal forward scan: the gradients of every input for a given gradient `dout`
  * of the returned output (out_z when z is given, else out), as selective_scan_cuda.bwd computes them
- * (selective_scan.cpp:415-612, selective_scan_bwd_kernel.cuh:405-880), for real A without P/Q:
+ * (selective_scan.cpp:415-612, selective_scan_bwd_kernel.cuh:405-880), for real A (P/Q: below):
  *   g_t   = dout_t * silu(z_t)                      dz_t = dout_t * out_t * silu'(z_t)
  *   gh_t  = C_t g_t + exp(delta'_{t+1} A) gh_{t+1}  (reverse scan per state, gh after L = 0)
  *   du_t  = D g_t + delta'_t sum_n gh_t B_t          ddelta'_t = sum_n gh_t (u_t B_t + A (h_t - delta'_t u_t B_t))
@@ -189,9 +189,30 @@ typedef struct mm_scan_bwd_params {
     int64_t dC_batch_stride, dC_group_stride, dC_dstate_stride, dC_d_stride;
 
     /* Device scratch of mm_scan_bwd_workspace_size() bytes (16-byte aligned), owned by the caller:
-     * the recomputed forward states at every 32-step tile start. Required. */
+     * the recomputed forward states at every 16-step tile start (and, for dstate 16 and for P/Q,
+     * the per-16-channel-block partial sums of dB and dC). Required. */
     void *workspace;
     int64_t workspace_bytes;
+
+    /* MotifMamba low-rank coupling (ABI version 7). With P and Q set (as in mm_scan_fwd_params:
+     * P_d (dstate, pq_rank), Q_d (pq_rank, dstate), float32, d strides 0 for a pair shared by all
+     * channels), the gradients are those of the coupled recurrence
+     *   h_t = exp(delta'_t A) h_{t-1} + delta'_t P (Q h_{t-1}) + delta'_t u_t B_t
+     * -- what torch autograd takes through selective_scan_full_matrix_cuda
+     * (selective_scan_interface.py:262-350), the reference's path for P/Q calls with z -- with the
+     * state adjoint running through the transposed transition matrix exp(delta' A) + delta' P Q,
+     * plus dP and dQ (float32, the shapes of P and Q; overwritten: the call clears them first).
+     * Supported: variable B and C, dstate <= 16, pq_rank 1..4, dim and dim / n_groups multiples of
+     * 16, seqlen a multiple of 8; other requests return MM_ERR_UNSUPPORTED. */
+    const float *P;
+    const float *Q;
+    int64_t pq_rank;
+    int64_t P_d_stride, P_dstate_stride, P_r_stride;
+    int64_t Q_d_stride, Q_r_stride, Q_dstate_stride;
+    float *dP;
+    float *dQ;
+    int64_t dP_d_stride, dP_dstate_stride, dP_r_stride;
+    int64_t dQ_d_stride, dQ_r_stride, dQ_dstate_stride;
 } mm_scan_bwd_params;
 
 /* Single-token decode update, in place on `state`:

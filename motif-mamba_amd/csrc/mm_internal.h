@@ -40,4 +40,11 @@ template <typename T>
 int launch_bwd(const mm_scan_bwd_params &p, hipStream_t stream);
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p);
 
+// Backward with the low-rank P/Q coupling (mm_scan_pq_bwd.hip): pq_bwd_ok() tells whether the
+// request fits the kernel; launch_pq_bwd() runs it with the checkpoint scratch `ck` and the dB / dC
+// partial slabs (the caller clears the accumulated gradients first and reduces the slabs after).
+bool pq_bwd_ok(const mm_scan_bwd_params &p);
+template <typename T>
+int launch_pq_bwd(const mm_scan_bwd_params &p, hipStream_t stream, float *ck, float *partB, float *partC);
+
 }  // namespace mm

@@ -476,6 +476,15 @@ int validate_bwd(const mm_scan_bwd_params *p) {
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: dD is required exactly when D is given");
     if ((p->delta_bias == nullptr) != (p->ddelta_bias == nullptr))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: ddelta_bias is required exactly when delta_bias is given");
+    if ((p->P == nullptr) != (p->Q == nullptr))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: P and Q must both be given or both be NULL");
+    if (p->P && (!p->dP || !p->dQ))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: dP and dQ are required when P and Q are given");
+    if (p->P && (p->pq_rank < 1 || p->pq_rank > 8))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: pq_rank must be in [1, 8] (got %lld)", (long long)p->pq_rank);
+    if (p->P && !mm::pq_bwd_ok(*p))
+        return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, pq_rank <= 4, "
+                                        "dim and dim / n_groups multiples of 16 and seqlen a multiple of 8");
     const int64_t need = mm::bwd_workspace_bytes(*p);
     if (p->seqlen > 0 && (!p->workspace || p->workspace_bytes < need || reinterpret_cast<uintptr_t>(p->workspace) % 16))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: needs a 16-byte aligned workspace of %lld bytes (got %lld)",

@@ -529,6 +529,7 @@ scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *part, float *dst, in
     const int64_t slice = rows * p.seqlen;
     for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
         const int64_t row = i / L4, t4 = i - row * L4;
+        if (row % 16 >= p.dstate) continue;   // slab rows past dstate (P/Q with dstate < 16) are not written
         const float4 *src = reinterpret_cast<const float4 *>(part + row * p.seqlen) + t4;
         float4 acc = src[0];
         for (int64_t k = 1; k < n_blocks; ++k) {
@@ -565,7 +566,7 @@ int launch_fill(float *ptr, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int6
 // The dstate-16 kernel's requirements: variable B/C, 16-channel blocks inside one group, L a
 // multiple of 8, two-element-aligned activation rows and four-element-aligned B/C rows.
 bool fast_ok(const mm_scan_bwd_params &p) {
-    if (p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
+    if (p.P || p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
     if (p.dim % 16 != 0 || (p.dim / p.n_groups) % 16 != 0 || p.seqlen < 8 || p.seqlen % 8 != 0) return false;
     if (p.batch > 65535 || p.dim / 16 > 0x7fffffff) return false;
     const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
@@ -611,10 +612,31 @@ int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
     return launch_status("scan_bwd_reduce_bc");
 }
 
+// The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
+template <typename T>
+int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
+    float *ws = static_cast<float *>(p.workspace);
+    float *partB = ws + fast_ck_floats(p), *partC = partB + fast_part_floats(p);
+    int rc = launch_pq_bwd<T>(p, s, ws, partB, partC);
+    if (rc != MM_OK) return rc;
+    // Slab rows past dstate are never written; the reduction reads only rows n < 16 of each slab
+    // and writes rows n < dstate (dB / dC hold dstate rows).
+    const int64_t ratio = p.dim / p.n_groups;
+    const int64_t total = p.batch * p.n_groups * 16 * (p.seqlen / 4);
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 8192));
+    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partB, p.dB, p.dB_batch_stride,
+                       p.dB_group_stride, p.dB_dstate_stride, ratio / 16);
+    rc = launch_status("scan_bwd_reduce_bc");
+    if (rc != MM_OK) return rc;
+    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partC, p.dC, p.dC_batch_stride,
+                       p.dC_group_stride, p.dC_dstate_stride, ratio / 16);
+    return launch_status("scan_bwd_reduce_bc");
+}
+
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
-    if (bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
+    if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
     return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));
 }
@@ -637,8 +659,14 @@ int launch_bwd(const mm_scan_bwd_params &p, hipStream_t s) {
         rc = bwd::launch_fill(p.dC, 1, 1, p.dim, p.dstate, 0, 0, p.dC_d_stride, p.dC_dstate_stride, s);
     if (rc == MM_OK && p.dD) rc = bwd::launch_fill(p.dD, 1, 1, 1, p.dim, 0, 0, 0, 1, s);
     if (rc == MM_OK && p.ddelta_bias) rc = bwd::launch_fill(p.ddelta_bias, 1, 1, 1, p.dim, 0, 0, 0, 1, s);
+    // dP / dQ: one (dstate, rank) slice per channel unless their d stride is 0 (one shared slice).
+    if (rc == MM_OK && p.P) rc = bwd::launch_fill(p.dP, 1, p.dP_d_stride ? p.dim : 1, p.dstate, p.pq_rank, 0,
+                                                 p.dP_d_stride, p.dP_dstate_stride, p.dP_r_stride, s);
+    if (rc == MM_OK && p.P) rc = bwd::launch_fill(p.dQ, 1, p.dQ_d_stride ? p.dim : 1, p.pq_rank, p.dstate, 0,
+                                                 p.dQ_d_stride, p.dQ_r_stride, p.dQ_dstate_stride, s);
     if (rc != MM_OK) return rc;
     if (p.seqlen == 0) return MM_OK;
+    if (p.P) return bwd::launch_pq<T>(p, s);
     if (bwd::fast_ok(p)) return bwd::launch_fast<T>(p, s);
     return bwd::launch_general<T>(p, s);
 }

@@ -1,0 +1,398 @@
+// mm_scan_pq_bwd.hip -- gfx950 backward of the MotifMamba low-rank coupled scan.
+//
+// Reference behaviour: the gradients torch autograd takes through selective_scan_full_matrix_cuda
+// (mamba_ssm/ops/selective_scan_interface.py:262-350), the path selective_scan_fn takes for P/Q
+// calls with z (selective_scan_interface.py:243-258, the Motif module always passes z), i.e. the
+// exact gradients of
+//
+//     h_t = a_t * h_{t-1} + dt'_t P (Q h_{t-1}) + dt'_t u_t B_t,   a_t = exp(dt'_t A),
+//     y_t = C_t . h_t,   out_t = y_t + D u_t,   out_z_t = out_t * silu(z_t).
+//
+// With g_t = dout_t * silu(z_t) and the state adjoint lam_t = dL / dh_t (a reverse recurrence
+// through the transposed transition matrix M_{t+1} = diag(a_{t+1}) + dt'_{t+1} P Q):
+//
+//     lam_t  = C_t g_t + a_{t+1} * lam_{t+1} + dt'_{t+1} Q^T (P^T lam_{t+1}),     lam_{L-1} = C g
+//     dt'_t  = sum_n lam_t (A a_t h_{t-1} + (P q_t) + u_t B_t),    q_t = Q h_{t-1}
+//     du_t   = D g_t + dt'_t sum_n lam_t B_t
+//     dA    += lam_t dt'_t a_t h_{t-1};  dP += dt'_t lam_t q_t^T;  dQ += dt'_t (P^T lam_t) h_{t-1}^T
+//     dB_t  += lam_t dt'_t u_t;  dC_t += g_t h_t;  dD += g_t u_t;  dz, ddelta_bias as the diagonal case.
+//
+// The design of this file is its own. scan_bwd_pq16<T, S, R>: a workgroup owns 16 channels of one
+// (batch, group) and dstate <= 16 states; the LPR = 16 / S consecutive lanes of a channel hold S
+// states each (S = 2: 8 lanes per channel, two waves per workgroup), and the sums over a channel's
+// states (Q h, P^T lam, and the per-step sums that give du and ddelta) are DPP butterflies inside
+// those lanes, which leave bit-identical totals in all of them. P and Q of the lane's states live
+// in registers. A first pass recomputes the forward and stores the states at every 16-step tile
+// start in the caller's workspace; the second walks the tiles in reverse, recomputes each from its
+// checkpoint into LDS (read back by the same lane) and walks it backwards. The dB / dC contributions are summed over the block's 16 channels through
+// LDS per 8-step half tile and written as the block's partials, which scan_bwd_reduce_bc adds in
+// block order (no atomics on them); dA, dP, dQ, dD and ddelta_bias take float32 atomics once per
+// lane at the end.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "mm_common.h"
+#include "mm_internal.h"
+
+namespace mm {
+namespace pqbwd {
+
+constexpr int kT = 16;           // steps per tile
+constexpr int kH = 8;            // steps per reduction half
+constexpr int kXS = kT + 1;      // sX row stride (float4)
+constexpr int kBCS = 36;         // sBC row stride (floats): B 16 | C 16 | pad 4
+constexpr int kRow = 20;         // sRed row stride (floats): 16 channels + 4
+constexpr int kRed = 2 * kH * 16 * kRow;   // sRed floats: [tensor][step of the half][state][channel]
+
+// x + x[lane permuted by CTRL] as one v_add_f32 with a DPP operand.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false);
+    return x + __builtin_bit_cast(float, o);
+}
+
+// Sum over the LPR consecutive lanes of a channel; every lane ends with the same bits (each step
+// adds the same two partial sums in both lanes of a pair).
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(LPR == 4 || LPR == 8, "LPR");
+    x = dpp_add<0xB1>(x);                           // quad_perm [1,0,3,2]
+    x = dpp_add<0x4E>(x);                           // quad_perm [2,3,0,1]
+    if constexpr (LPR >= 8) x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of 8 lanes
+    return x;
+}
+
+template <typename T, int S, int R>
+__global__ void __launch_bounds__(16 * (16 / S)) __attribute__((amdgpu_waves_per_eu(2)))
+scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, float *const partB,
+              float *const partC) {
+    constexpr int LPR = 16 / S;          // lanes per channel
+    constexpr int NT = 16 * LPR;         // lanes per workgroup
+    constexpr int E = kT / LPR;          // steps per lane of a tile's per-element work
+    __shared__ __align__(16) float4 sX[16 * kXS];       // [c][t]: (dt', dt'u, u, g)
+    __shared__ __align__(16) float sBC[kT * kBCS];       // [t][B 16 | C 16]
+    __shared__ __align__(16) float sRed[kRed];           // [tensor][t][n][c]
+    __shared__ __align__(16) float sHS[kT * 16 * 16];    // [t][c][n]: the tile's states after step t
+    __shared__ __align__(16) float sOwn[2 * 16 * kT];    // [sum of lam B | dt' term][c][t]
+
+    const int tid = threadIdx.x;
+    const int cw = tid / LPR;              // channel of the block
+    const int k = tid % LPR;               // states k S .. k S + S - 1
+    const int64_t b = blockIdx.y;
+    const int64_t d0 = int64_t(blockIdx.x) * 16;
+    const int64_t d = d0 + cw;
+    const int64_t g = d0 / ratio;
+    const int64_t blk = (d0 - g * ratio) / 16;
+    const int64_t L = p.seqlen;
+    const int N = int(p.dstate);
+    const int rank = int(p.pq_rank);
+    const int64_t n_tiles = (L + kT - 1) / kT;
+    const int es = E * k;                  // first step (within a tile) of this lane's elements
+
+    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
+    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
+    const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
+    const T *outp = p.z ? reinterpret_cast<const T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
+    const T *gop = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
+    T *dup = reinterpret_cast<T *>(p.du) + b * p.du_batch_stride + d * p.du_d_stride;
+    T *ddp = reinterpret_cast<T *>(p.ddelta) + b * p.ddelta_batch_stride + d * p.ddelta_d_stride;
+    T *dzp = p.z ? reinterpret_cast<T *>(p.dz) + b * p.dz_batch_stride + d * p.dz_d_stride : nullptr;
+    T *ozp = (p.z && p.out_z) ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
+    const T *Bg = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cg = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+
+    float An[S], A2[S], Pr[S][R], Qr[R][S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int n = k * S + s;
+        const bool on = n < N;
+        An[s] = on ? p.A[d * p.A_d_stride + n * p.A_dstate_stride] : 0.f;
+        A2[s] = An[s] * kLog2e;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool use = on && r < rank;
+            Pr[s][r] = use ? p.P[d * p.P_d_stride + n * p.P_dstate_stride + r * p.P_r_stride] : 0.f;
+            Qr[r][s] = use ? p.Q[d * p.Q_d_stride + r * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
+        }
+    }
+    const float Dv = p.D ? p.D[d] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+    // Checkpoints [tile][batch][dim][16] (states past dstate stay 0).
+    const int64_t ck_tile = p.batch * p.dim * 16;
+    float *const ckp = ck + (b * p.dim + d) * 16 + k * S;
+
+    // B/C staging of one tile (32 rows (tensor, state) of kT steps): NT / 32 lanes per row, SPL
+    // consecutive steps each.
+    constexpr int SPL = kT / (NT / 32);    // steps per staging lane (NT / 32 lanes per row)
+    const int st_row = tid / (NT / 32);    // 0 .. 31: tensor st_row / 16, state st_row % 16
+    const int st_t0 = SPL * (tid % (NT / 32));
+    const int st_n = st_row % 16;
+    const bool st_on = st_n < N;
+    const T *stp = (st_row < 16 ? Bg + int64_t(st_on ? st_n : 0) * p.B_dstate_stride
+                                : Cg + int64_t(st_on ? st_n : 0) * p.C_dstate_stride);
+
+    // Tile j's per-step values into LDS (with B, and C when `full`); this lane's elements kept in
+    // registers; dz and out_z written. Steps past L are padding (dt' = g = 0, B = C = 0: inert).
+    float e_raw[E], e_dt[E], e_u[E], e_g[E];
+    auto commit = [&](int64_t j, bool full) {
+        const int64_t t0 = j * kT;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const int64_t t = t0 + es + i;
+            const bool ev = t < L;
+            const int64_t tc = ev ? t : L - 1;
+            const float dd = to_f32(dp[tc]);
+            const float uu = to_f32(up[tc]);
+            float go = 0.f;
+            if (full) {
+                go = to_f32(gop[tc]);
+                if (zp) {
+                    const float zz = to_f32(zp[tc]);
+                    const float oo = to_f32(outp[tc]);
+                    const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zz * kLog2e));
+                    if (ev) {
+                        dzp[t] = from_f32<T>(go * oo * sg * (1.f + zz * (1.f - sg)));
+                        if (ozp) ozp[t] = from_f32<T>(oo * zz * sg);
+                    }
+                    go *= zz * sg;
+                }
+            }
+            e_raw[i] = dd + bias;
+            e_dt[i] = ev ? (p.delta_softplus ? softplus_fast(e_raw[i]) : e_raw[i]) : 0.f;
+            e_u[i] = uu;
+            e_g[i] = ev ? go : 0.f;
+            sX[cw * kXS + es + i] = make_float4(e_dt[i], e_dt[i] * uu, uu, e_g[i]);
+        }
+        if (full || st_row < 16) {
+#pragma unroll
+            for (int i = 0; i < SPL; ++i) {
+                const int64_t t = t0 + st_t0 + i;
+                const bool on = st_on && t < L;
+                sBC[(st_t0 + i) * kBCS + st_row] = on ? to_f32(stp[t < L ? t : L - 1]) : 0.f;
+            }
+        }
+    };
+
+    // ---- Pass 1: the states before every tile ----
+    {
+        float h[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) h[s] = 0.f;
+        for (int64_t j = 0; j < n_tiles; ++j) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) ckp[j * ck_tile + s] = h[s];
+            commit(j, false);
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < kT; ++t) {
+                const float4 x = sX[cw * kXS + t];
+                float q[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float acc = Qr[r][0] * h[0];
+#pragma unroll
+                    for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
+                    q[r] = group_sum<LPR>(acc) * x.x;
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    float w = x.y * sBC[t * kBCS + k * S + s];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                    h[s] = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A2[s]), h[s], w);
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    // ---- Pass 2: tiles in reverse order ----
+    float carry[S], dA[S], dP[S][R], dQ[R][S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        carry[s] = 0.f;
+        dA[s] = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            dP[s][r] = 0.f;
+            dQ[r][s] = 0.f;
+        }
+    }
+    float dD_acc = 0.f, dbias_acc = 0.f;
+    for (int64_t j = n_tiles - 1; j >= 0; --j) {
+        const int64_t t0 = j * kT;
+        float hck[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) hck[s] = ckp[j * ck_tile + s];
+        commit(j, true);
+        __syncthreads();
+        // Recompute the tile's states from its checkpoint into sHS (read back by this lane only).
+        {
+            float h[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) h[s] = hck[s];
+#pragma unroll 2
+            for (int t = 0; t < kT; ++t) {
+                const float4 x = sX[cw * kXS + t];
+                float q[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float acc = Qr[r][0] * h[0];
+#pragma unroll
+                    for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
+                    q[r] = group_sum<LPR>(acc) * x.x;
+                }
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    float w = x.y * sBC[t * kBCS + k * S + s];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                    h[s] = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A2[s]), h[s], w);
+                    sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
+                }
+            }
+        }
+        for (int t = kT - 1; t >= 0; --t) {
+            const int sh = t % kH;
+            const float4 x = sX[cw * kXS + t];       // dt', dt'u, u, g
+            float Bv[S], Cv[S], lam[S], hp[S], hc[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                Bv[s] = sBC[t * kBCS + k * S + s];
+                Cv[s] = sBC[t * kBCS + 16 + k * S + s];
+                lam[s] = __builtin_fmaf(Cv[s], x.w, carry[s]);
+                hp[s] = t > 0 ? sHS[((t - 1) * 16 + cw) * 16 + k * S + s] : hck[s];   // h_{t-1}
+                hc[s] = sHS[(t * 16 + cw) * 16 + k * S + s];                            // h_t
+            }
+            float q[R], sv[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float aq = Qr[r][0] * hp[0], as = Pr[0][r] * lam[0];
+#pragma unroll
+                for (int s = 1; s < S; ++s) {
+                    aq = __builtin_fmaf(Qr[r][s], hp[s], aq);
+                    as = __builtin_fmaf(Pr[s][r], lam[s], as);
+                }
+                q[r] = group_sum<LPR>(aq);          // (Q h_{t-1})_r
+                sv[r] = group_sum<LPR>(as);         // (P^T lam_t)_r
+            }
+            float pdd = 0.f, pgb = 0.f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const float a = __builtin_amdgcn_exp2f(x.x * A2[s]);
+                const float ah = a * hp[s];
+                float pq = 0.f, qs = 0.f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    pq = __builtin_fmaf(Pr[s][r], q[r], pq);
+                    qs = __builtin_fmaf(Qr[r][s], sv[r], qs);
+                }
+                // dt' term: A a h_{t-1} + P q + u B
+                pdd = __builtin_fmaf(lam[s], __builtin_fmaf(An[s], ah, __builtin_fmaf(x.z, Bv[s], pq)), pdd);
+                pgb = __builtin_fmaf(lam[s], Bv[s], pgb);
+                const float ld = lam[s] * x.x;
+                dA[s] = __builtin_fmaf(ld, ah, dA[s]);
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    dP[s][r] = __builtin_fmaf(ld, q[r], dP[s][r]);
+                    dQ[r][s] = __builtin_fmaf(x.x * sv[r], hp[s], dQ[r][s]);
+                }
+                sRed[((0 * kH + sh) * 16 + k * S + s) * kRow + cw] = lam[s] * x.y;   // dB contribution
+                sRed[((1 * kH + sh) * 16 + k * S + s) * kRow + cw] = x.w * hc[s];    // dC contribution
+                carry[s] = __builtin_fmaf(a, lam[s], x.x * qs);                      // into step t - 1
+            }
+            const float dd_t = group_sum<LPR>(pdd), gb_t = group_sum<LPR>(pgb);
+            if (t / E == k) {                 // this lane owns step t of its channel (and reads it back)
+                sOwn[(0 * 16 + cw) * kT + t] = gb_t;
+                sOwn[(1 * 16 + cw) * kT + t] = dd_t;
+            }
+            if (sh == 0) {
+                __syncthreads();
+                // dB / dC of the half summed over the block's 16 channels, in channel order, written as
+                // this block's partials: 2 x kH x 16 rows (tensor, step, state).
+#pragma unroll
+                for (int rr = 0; rr < (2 * kH * 16) / NT; ++rr) {
+                    const int row = tid + NT * rr;
+                    const int tz = row / (kH * 16), th = (row / 16) % kH, tn = row % 16;
+                    const float4 *rv = reinterpret_cast<const float4 *>(&sRed[((tz * kH + th) * 16 + tn) * kRow]);
+                    float q4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 v = rv[i];
+                        q4[i] = (v.x + v.y) + (v.z + v.w);
+                    }
+                    const float acc = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+                    const int64_t ts = t0 + t + th;
+                    if (ts < L && tn < N)
+                        (tz == 0 ? partB : partC)[(((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * L + ts] = acc;
+                }
+                __syncthreads();
+            }
+        }
+        // du / ddelta of this lane's steps.
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const int64_t te = t0 + es + i;
+            if (te < L) {
+                const float gb = sOwn[(0 * 16 + cw) * kT + es + i], ddt = sOwn[(1 * 16 + cw) * kT + es + i];
+                const float du = __builtin_fmaf(Dv, e_g[i], e_dt[i] * gb);
+                const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-e_raw[i] * kLog2e));
+                const float ddl = (p.delta_softplus && e_raw[i] <= 20.f) ? ddt * sg : ddt;
+                dup[te] = from_f32<T>(du);
+                ddp[te] = from_f32<T>(ddl);
+                dD_acc = __builtin_fmaf(e_g[i], e_u[i], dD_acc);
+                dbias_acc += ddl;
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int n = k * S + s;
+        if (n >= N) continue;
+        atomicAdd(p.dA + d * p.dA_d_stride + n * p.dA_dstate_stride, dA[s]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r >= rank) continue;
+            atomicAdd(p.dP + d * p.dP_d_stride + n * p.dP_dstate_stride + r * p.dP_r_stride, dP[s][r]);
+            atomicAdd(p.dQ + d * p.dQ_d_stride + r * p.dQ_r_stride + n * p.dQ_dstate_stride, dQ[r][s]);
+        }
+    }
+    if (p.dD) atomicAdd(p.dD + d, dD_acc);
+    if (p.ddelta_bias) atomicAdd(p.ddelta_bias + d, dbias_acc);
+}
+
+}  // namespace pqbwd
+
+// The P/Q backward's shape conditions: variable B/C, dstate <= 16, rank 1..4, 16-channel blocks
+// inside one group, L a multiple of 8.
+bool pq_bwd_ok(const mm_scan_bwd_params &p) {
+    return p.is_variable_B && p.is_variable_C && p.dstate >= 1 && p.dstate <= 16 && p.pq_rank >= 1 &&
+           p.pq_rank <= 4 && p.dim % 16 == 0 && (p.dim / p.n_groups) % 16 == 0 && p.seqlen >= 8 &&
+           p.seqlen % 8 == 0 && p.batch <= 65535;
+}
+
+template <typename T, int S>
+static int launch_pq_bwd_s(const mm_scan_bwd_params &p, hipStream_t s, float *ck, float *partB, float *partC) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / 16), unsigned(p.batch));
+    dim3 block(16 * (16 / S));
+    if (p.pq_rank <= 2)
+        hipLaunchKernelGGL((pqbwd::scan_bwd_pq16<T, S, 2>), grid, block, 0, s, p, ratio, ck, partB, partC);
+    else
+        hipLaunchKernelGGL((pqbwd::scan_bwd_pq16<T, S, 4>), grid, block, 0, s, p, ratio, ck, partB, partC);
+    return launch_status("scan_bwd_pq16");
+}
+
+// Two states per lane: 135-157 registers (two or three waves per SIMD); four states per lane would
+// need 187-227 (one wave per SIMD) for fewer butterfly steps.
+template <typename T>
+int launch_pq_bwd(const mm_scan_bwd_params &p, hipStream_t s, float *ck, float *partB, float *partC) {
+    return launch_pq_bwd_s<T, 2>(p, s, ck, partB, partC);
+}
+
+template int launch_pq_bwd<float>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
+template int launch_pq_bwd<f16_t>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
+template int launch_pq_bwd<bf16_t>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
+
+}  // namespace mm

@@ -37,6 +37,11 @@ mm_dtype to_mm(at::ScalarType t) {
 }
 
 void check_rc(int rc, const char *what) {
+    if (rc == MM_ERR_UNSUPPORTED) {
+        // A shape the kernels do not cover: NotImplementedError (a RuntimeError) in Python.
+        throw c10::NotImplementedError({__func__, __FILE__, uint32_t(__LINE__)},
+                                       c10::str(what, " failed (code ", rc, "): ", mm_last_error()));
+    }
     TORCH_CHECK(rc == MM_OK, what, " failed (code ", rc, "): ", mm_last_error());
 }
 
@@ -303,7 +308,9 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
 
 // selective_scan_cuda.bwd (selective_scan.cpp:415-612): [du, ddelta, dA, dB, dC, dD, ddelta_bias,
 // dz?, out_z?]. x (the forward's chunk states) is checked like the reference but not read: the
-// backward recomputes the forward states itself. P/Q are not part of this backward.
+// backward recomputes the forward states itself. With P/Q the exact gradient of the coupled
+// recurrence runs (pq_rank 1..4, dstate <= 16, dim and dim / n_groups multiples of 16; other
+// P/Q shapes raise).
 std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A, const at::Tensor &B,
                             const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                             const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &delta_bias_,
@@ -312,12 +319,14 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
                             const c10::optional<at::Tensor> &x_, const c10::optional<at::Tensor> &out_,
                             c10::optional<at::Tensor> dz_, const c10::optional<at::Tensor> &dP_out_,
                             const c10::optional<at::Tensor> &dQ_out_, bool delta_softplus, bool recompute_out_z) {
-    if (P_.has_value() || Q_.has_value() || gamma_.has_value() || dP_out_.has_value() || dQ_out_.has_value()) {
-        throw c10::NotImplementedError({__func__, __FILE__, uint32_t(__LINE__)},
-                                       "the P/Q backward is not part of the MI355X selective scan");
-    }
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
+    // P/Q (and gamma, validated and not read, as in the forward): the float32 copies stay alive
+    // until the launch is enqueued.
+    const std::vector<at::Tensor> pq_keep = attach_pq(s.p, u, P_, Q_, gamma_);
     const mm_scan_fwd_params &f = s.p;
+    const bool has_pq = f.P != nullptr;
+    TORCH_CHECK(has_pq || (!dP_out_.has_value() && !dQ_out_.has_value()), "dP_out and dQ_out need P and Q");
+    (void)pq_keep;
     TORCH_CHECK(dout.scalar_type() == u.scalar_type());
     TORCH_CHECK(dout.is_cuda());
     TORCH_CHECK(dout.stride(-1) == 1 || dout.size(-1) == 1);
@@ -399,6 +408,36 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
     }
     if (D_.has_value()) p.dD = dD.data_ptr<float>();
     if (delta_bias_.has_value()) p.ddelta_bias = ddelta_bias.data_ptr<float>();
+    // dP / dQ (selective_scan.cpp:580-590): the exact gradients of the coupled recurrence are
+    // added into dP_out / dQ_out (float32, the shapes of P and Q) when given, as the reference
+    // accumulates into them; without them they are computed and dropped, as there, and the
+    // result list is the reference's either way.
+    at::Tensor dP, dQ;
+    if (has_pq) {
+        const at::Tensor &P = P_.value(), &Q = Q_.value();
+        if (dP_out_.has_value() || dQ_out_.has_value()) {
+            TORCH_CHECK(dP_out_.has_value() && dQ_out_.has_value(), "dP_out and dQ_out go together");
+            const at::Tensor &dPo = dP_out_.value(), &dQo = dQ_out_.value();
+            TORCH_CHECK(dPo.is_cuda() && dQo.is_cuda(), "dP_out and dQ_out must be CUDA tensors");
+            TORCH_CHECK(dPo.scalar_type() == at::ScalarType::Float && dQo.scalar_type() == at::ScalarType::Float,
+                        "dP_out and dQ_out must be float32");
+            TORCH_CHECK(dPo.sizes() == P.sizes(), "dP_out shape mismatch");
+            TORCH_CHECK(dQo.sizes() == Q.sizes(), "dQ_out shape mismatch");
+        }
+        dP = torch::empty(P.sizes(), P.options().dtype(at::ScalarType::Float));
+        dQ = torch::empty(Q.sizes(), Q.options().dtype(at::ScalarType::Float));
+        p.P = f.P; p.Q = f.Q; p.pq_rank = f.pq_rank;
+        p.P_d_stride = f.P_d_stride; p.P_dstate_stride = f.P_dstate_stride; p.P_r_stride = f.P_r_stride;
+        p.Q_d_stride = f.Q_d_stride; p.Q_r_stride = f.Q_r_stride; p.Q_dstate_stride = f.Q_dstate_stride;
+        p.dP = dP.data_ptr<float>();
+        p.dQ = dQ.data_ptr<float>();
+        p.dP_d_stride = P.dim() == 3 ? dP.stride(0) : 0;
+        p.dP_dstate_stride = dP.stride(P.dim() - 2);
+        p.dP_r_stride = dP.stride(P.dim() - 1);
+        p.dQ_d_stride = Q.dim() == 3 ? dQ.stride(0) : 0;
+        p.dQ_r_stride = dQ.stride(Q.dim() - 2);
+        p.dQ_dstate_stride = dQ.stride(Q.dim() - 1);
+    }
     const c10::DeviceGuard device_guard{u.device()};
     at::Tensor ws;
     const int64_t ws_bytes = mm_scan_bwd_workspace_size(&p);
@@ -411,6 +450,10 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
     std::vector<at::Tensor> result = {du, ddelta, dA, dB.to(B.scalar_type()), dC.to(C.scalar_type()), dD, ddelta_bias};
     if (has_z) result.push_back(dz);
     if (recompute_out_z) result.push_back(out_z);
+    if (has_pq && dP_out_.has_value()) {
+        dP_out_.value().add_(dP);
+        dQ_out_.value().add_(dQ);
+    }
     return result;
 }
 

@@ -23,7 +23,8 @@ LIB_NAME = "libmm_scan.so"
 EXT_NAME = "mm_scan_torch"
 ARCH = "gfx950"
 
-HIP_SOURCES = ["mm_scan.hip", "mm_scan_tiled.hip", "mm_scan_pq.hip", "mm_scan_bwd.hip", "mm_conv1d.hip", "mm_norm.hip"]
+HIP_SOURCES = ["mm_scan.hip", "mm_scan_tiled.hip", "mm_scan_pq.hip", "mm_scan_bwd.hip", "mm_scan_pq_bwd.hip",
+               "mm_conv1d.hip", "mm_norm.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed fp32 VALU ops are disabled: the compiler would otherwise form v_pk_{add,mul,fma}_f32
 # from scalar float code, and those have given silent wrong results on these GPUs.

@@ -21,8 +21,15 @@ and, as in both reference paths, not used.
 equivalent); with gradients required, the forward saves the reference's tensors (u, delta, A, B,
 C, D, [z], delta_bias, x, [out]); without, it writes only what it returns.
 
-Differences (all raise instead of computing something else): the P/Q backward and complex A are
-not part of this build.
+``SelectiveScanPQFn.backward`` returns the exact gradients of the coupled recurrence (dP and dQ
+included), which is what the reference returns in its default gradient mode: its dense CUDA
+backward (z-less calls) and autograd through its torch loop (calls with z, and dP/dQ always) both
+differentiate the same function. The gfx950 kernel covers pq_rank 1..4, dstate <= 16, dim and
+dim / n_groups multiples of 16 and seqlen a multiple of 8, with variable B and C; other P/Q
+shapes raise NotImplementedError in the backward (the forward covers pq_rank up to 8).
+
+Differences (all raise instead of computing something else): complex A, and the P/Q backward
+outside the shapes above, are not part of this build.
 """
 from __future__ import annotations
 
@@ -121,19 +128,54 @@ class SelectiveScanPQFn(torch.autograd.Function):
             delta_bias = delta_bias.contiguous()
         if B.dim() == 3:
             B = rearrange(B, "b dstate l -> b 1 dstate l")
+            ctx.squeeze_B = True
         if C.dim() == 3:
             C = rearrange(C, "b dstate l -> b 1 dstate l")
-        res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
-                              delta_softplus=delta_softplus, return_last_state=return_last_state,
-                              P=P, Q=Q, gamma=gamma)
-        if return_last_state:
-            return res[0], res[1]
-        return res[0]
+            ctx.squeeze_C = True
+        if not (any(ctx.needs_input_grad[:8]) or any(ctx.needs_input_grad[10:12])):
+            res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
+                                  delta_softplus=delta_softplus, return_last_state=return_last_state,
+                                  P=P, Q=Q, gamma=gamma)
+            if return_last_state:
+                return res[0], res[1]
+            return res[0]
+        # Training: the forward's outputs plus what the backward reads (ssi.py:123-137 saves
+        # u, delta, A, B, C, D, delta_bias, P, Q, gamma, x; out joins them when z is given).
+        out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus)
+        ctx.delta_softplus = delta_softplus
+        ctx.has_z = z is not None
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, x,
+                              out if ctx.has_z else None)
+        last_state = x[:, :, -1, 1::2]
+        result = rest[0] if ctx.has_z else out
+        return result if not return_last_state else (result, last_state)
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(
-            "selective_scan P/Q backward is not implemented by the MI355X build (forward only)")
+    def backward(ctx, dout, *args):
+        """Exact gradients of the coupled recurrence, dP and dQ included: what the reference's
+        default ("exact") mode returns (ssi.py:152-205: its CUDA backward for u, delta, A, B, C,
+        D, delta_bias and autograd through selective_scan_full_matrix_cuda for dP, dQ; with z,
+        autograd through that torch loop for everything). gamma gets no gradient, as there."""
+        u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, x, out = ctx.saved_tensors
+        if dout.stride(-1) != 1:
+            dout = dout.contiguous()
+        dP = torch.zeros(P.shape, dtype=torch.float32, device=P.device)
+        dQ = torch.zeros(Q.shape, dtype=torch.float32, device=Q.device)
+        du, ddelta, dA, dB, dC, dD, ddelta_bias, *rest = ext().bwd(
+            u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, P=P, Q=Q, gamma=gamma, dout=dout,
+            x=x, out=out, dz=None, dP_out=dP, dQ_out=dQ, delta_softplus=ctx.delta_softplus,
+            recompute_out_z=False)
+        dz = rest[0] if ctx.has_z else None
+        dB = dB.squeeze(1) if getattr(ctx, "squeeze_B", False) else dB
+        dC = dC.squeeze(1) if getattr(ctx, "squeeze_C", False) else dC
+        return (du, ddelta, dA, dB, dC,
+                dD if D is not None else None,
+                dz,
+                ddelta_bias if delta_bias is not None else None,
+                None,
+                None,
+                dP.to(P.dtype), dQ.to(Q.dtype),
+                None)
 
 
 def _check_pq(u, delta, A, B, C, P, Q):

@@ -218,7 +218,7 @@ def softplus_f64(x: float) -> float:
 
 
 def selective_scan_pq_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                          return_last_state=False, P=None, Q=None, gamma=None):
+                          return_last_state=False, P=None, Q=None, gamma=None, compute_dtype=torch.float32):
     """CPU restatement of the MotifMamba low-rank coupled scan ``selective_scan_full_matrix_cuda``
     (reference ``mamba_ssm/ops/selective_scan_interface.py:262-350``), op for op:
 
@@ -230,30 +230,32 @@ def selective_scan_pq_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, de
     * per step: ``A_diag = exp(dt * A)``, ``input_term = (dt * u) * B_t``, ``q = einsum('drn,bdn->bdr')``,
       ``pq = einsum('dnr,bdr->bdn')``, ``x = A_diag * x + dt * pq + input_term``, ``y_t = sum(x * C_t)``
       (ssi.py:320-341);
-    * ``out = y + u * D``, ``out *= silu(z.float())``, cast to the input dtype; returns ``(out, x)``
+    * ``out = y + u * D``, ``out *= silu(z.to(compute_dtype))``, cast to the input dtype; returns ``(out, x)``
       with x the float32 state after the last step (ssi.py:343-350).
 
     gamma is accepted and ignored, as in the reference (neither forward path reads it).
     The reference requires CUDA tensors (ssi.py:270-271); this restatement runs on CPU tensors.
+    ``compute_dtype=torch.float64`` evaluates the same op sequence in float64 (exact gradients for
+    precision checks); the default is the reference's float32.
     """
     if P is None or Q is None:
         raise ValueError("P and Q must both be provided for full-matrix path")
     if A.is_complex():
         raise NotImplementedError("Full-matrix P/Q path currently supports real A only")
     dtype_in = u.dtype
-    u_f = u.float()
-    delta_f = delta.float()
-    A_f = A.float()
+    u_f = u.to(compute_dtype)
+    delta_f = delta.to(compute_dtype)
+    A_f = A.to(compute_dtype)
     if delta_bias is not None:
-        delta_f = delta_f + delta_bias[..., None].float()
+        delta_f = delta_f + delta_bias[..., None].to(compute_dtype)
     if delta_softplus:
         delta_f = F.softplus(delta_f)
     batch, dim, seqlen = u.shape
     dstate = A.shape[1]
     var_B = B.dim() >= 3
     var_C = C.dim() >= 3
-    B_f = B.float()
-    C_f = C.float()
+    B_f = B.to(compute_dtype)
+    C_f = C.to(compute_dtype)
     if var_B:
         B_full = (B_f.unsqueeze(1).expand(-1, dim, -1, -1) if B_f.dim() == 3
                   else repeat(B_f, "B G N L -> B (G H) N L", H=dim // B_f.shape[1]))
@@ -263,15 +265,15 @@ def selective_scan_pq_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, de
     if P.dim() == 2 and Q.dim() == 2:
         if P.shape[0] != dstate or Q.shape[1] != dstate or P.shape[1] != Q.shape[0]:
             raise ValueError("Expected P(n, r), Q(r, n) with n=dstate")
-        P_d = P.float().unsqueeze(0).expand(dim, -1, -1)
-        Q_d = Q.float().unsqueeze(0).expand(dim, -1, -1)
+        P_d = P.to(compute_dtype).unsqueeze(0).expand(dim, -1, -1)
+        Q_d = Q.to(compute_dtype).unsqueeze(0).expand(dim, -1, -1)
     elif P.dim() == 3 and Q.dim() == 3:
         if P.shape[0] != dim or Q.shape[0] != dim:
             raise ValueError("Expected P(dim, n, r), Q(dim, r, n)")
         if P.shape[1] != dstate or Q.shape[2] != dstate or P.shape[2] != Q.shape[1]:
             raise ValueError("Expected P(dim, n, r), Q(dim, r, n)")
-        P_d = P.float()
-        Q_d = Q.float()
+        P_d = P.to(compute_dtype)
+        Q_d = Q.to(compute_dtype)
     else:
         raise ValueError("P and Q must both be 2D or both be 3D")
     x = A_f.new_zeros((batch, dim, dstate))
@@ -290,9 +292,9 @@ def selective_scan_pq_ref(u, delta, A, B, C, D=None, z=None, delta_bias=None, de
         else:
             ys.append((x * C_f.unsqueeze(0)).sum(dim=-1))
     y = torch.stack(ys, dim=2)
-    out = y if D is None else y + u_f * D.float().view(1, -1, 1)
+    out = y if D is None else y + u_f * D.to(compute_dtype).view(1, -1, 1)
     if z is not None:
-        out = out * F.silu(z.float())
+        out = out * F.silu(z.to(compute_dtype))
     out = out.to(dtype=dtype_in)
     return out if not return_last_state else (out, x)
 
@@ -345,3 +347,33 @@ def selective_scan_bwd_ref(u, delta, A, B, C, dout, D=None, z=None, delta_bias=N
         "dz": (g["z"].to(z.dtype) if dtype is None else g["z"]) if z is not None else None,
     }
     return res
+
+
+def selective_scan_pq_bwd_ref(u, delta, A, B, C, P, Q, dout, D=None, z=None, delta_bias=None,
+                              delta_softplus=False, dtype=torch.float64):
+    """Gradients of the low-rank coupled scan ``selective_scan_pq_ref`` (the restatement of
+    ssi.py:262-350) with respect to every input, P and Q included, by torch autograd. This is what
+    the reference returns in its default gradient mode (``MOTIFMAMBA_PQ_GRAD_MODE`` "exact",
+    ssi.py:152-205): dP and dQ by autograd through ``selective_scan_full_matrix_cuda``, the other
+    gradients from its dense CUDA backward (selective_scan_bwd_kernel.cuh:166-345, the adjoint of
+    the same recurrence) for z-less calls, or from the same autograd for calls with z.
+
+    ``dtype`` (default float64: the exact gradient) is the precision of the differentiated
+    computation. Returns a dict with du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, dP, dQ (None for
+    absent inputs), all in ``dtype``."""
+    leaves = {}
+
+    def leaf(name, t):
+        if t is None:
+            return None
+        v = t.detach().to(dtype)
+        v.requires_grad_(True)
+        leaves[name] = v
+        return v
+
+    args = {n: leaf(n, t) for n, t in (("u", u), ("delta", delta), ("A", A), ("B", B), ("C", C), ("D", D),
+                                       ("z", z), ("delta_bias", delta_bias), ("P", P), ("Q", Q))}
+    out = selective_scan_pq_ref(**args, delta_softplus=delta_softplus, compute_dtype=dtype)
+    out.backward(dout.to(out.dtype))
+    return {"d" + n: (leaves[n].grad if n in leaves else None)
+            for n in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias", "P", "Q")}

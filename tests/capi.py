@@ -60,7 +60,13 @@ class ScanBwdParams(ctypes.Structure):
                 ("dA_d_stride", i64), ("dA_dstate_stride", i64),
                 ("dB_batch_stride", i64), ("dB_group_stride", i64), ("dB_dstate_stride", i64), ("dB_d_stride", i64),
                 ("dC_batch_stride", i64), ("dC_group_stride", i64), ("dC_dstate_stride", i64), ("dC_d_stride", i64),
-                ("workspace", vp), ("workspace_bytes", i64)]
+                ("workspace", vp), ("workspace_bytes", i64),
+                ("P", vp), ("Q", vp), ("pq_rank", i64),
+                ("P_d_stride", i64), ("P_dstate_stride", i64), ("P_r_stride", i64),
+                ("Q_d_stride", i64), ("Q_r_stride", i64), ("Q_dstate_stride", i64),
+                ("dP", vp), ("dQ", vp),
+                ("dP_d_stride", i64), ("dP_dstate_stride", i64), ("dP_r_stride", i64),
+                ("dQ_d_stride", i64), ("dQ_r_stride", i64), ("dQ_dstate_stride", i64)]
 
 
 class Conv1dFwdParams(ctypes.Structure):

@@ -153,7 +153,7 @@ def test_bwd_native_api_outputs():
     with pytest.raises(RuntimeError):   # x is required past one chunk, as in the reference
         ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None,
                 dout, None, out, None, None, None, True, False)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(NotImplementedError):   # P/Q with 8 channels per group: outside the P/Q backward
         ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"],
                 torch.zeros(16, 2, device=DEV), torch.zeros(2, 16, device=DEV), None,
                 dout, x, out, None, None, None, True, False)

@@ -1,0 +1,240 @@
+"""GPU parity of the low-rank coupled (MotifMamba P/Q) backward (MI355X only).
+
+``selective_scan_fn(..., P=P, Q=Q)`` with gradients runs the forward of mm_scan_pq.hip and the
+backward of mm_scan_pq_bwd.hip through the C ABI. The gradients (dP and dQ included) are compared
+with the exact float64 gradients of the oracle ``selective_scan_pq_ref`` on the same inputs
+(``oracle.ssm_ref.selective_scan_pq_bwd_ref``, pinned in tests/test_oracle_pq_bwd.py): what the
+reference returns in its default gradient mode (ssi.py:152-205).
+
+Tolerances: the forward's (north_star) pair (rtol, atol) = (1e-4, 1e-5) for fp32 and (3e-2, 5e-2)
+for 16-bit inputs, element-wise as |err| <= rtol |exact| + atol max(1, max |exact|), the absolute
+part relative to the tensor's scale as for the diagonal backward (the parameter gradients are sums
+over rows and steps).
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from oracle.ssm_ref import selective_scan_pq_bwd_ref, selective_scan_pq_ref
+from tests import capi
+from tests.test_gpu_pq import _pq_case
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias", "P", "Q"]
+
+
+def _say(msg):
+    print(f"\n[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _tol(dtype):
+    return (1e-4, 1e-5) if dtype == torch.float32 else (3e-2, 5e-2)
+
+
+def _check(got, exact, dtype, what):
+    rtol, atol = _tol(dtype)
+    got = got.double().cpu()
+    exact = exact.double()
+    scale = max(1.0, exact.abs().max().item()) if exact.numel() else 1.0
+    err = (got - exact).abs()
+    bound = rtol * exact.abs() + atol * scale
+    bad = err > bound
+    assert not bool(bad.any()), (f"{what}: {int(bad.sum())}/{err.numel()} beyond tolerance; max err "
+                                 f"{err.max().item():.3g} (scale {scale:.3g})")
+
+
+def _dout(seed, shape, dtype):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)).to(dtype)
+
+
+def _autograd(case, dout):
+    from motif_mamba_amd import selective_scan_fn
+    g = {k: (v.to(DEV).requires_grad_(True) if torch.is_tensor(v) else v) for k, v in case.items()}
+    out = selective_scan_fn(**g)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    return out.detach().cpu(), {n: g[n].grad for n in NAMES if torch.is_tensor(g[n])}
+
+
+def _vs_exact(case, dout, dtype, what):
+    _, grads = _autograd(case, dout)
+    exact = selective_scan_pq_bwd_ref(**case, dout=dout)
+    for n, gr in grads.items():
+        assert gr.dtype == case[n].dtype, (n, gr.dtype)
+        assert gr.shape == case[n].shape, (n, gr.shape)
+        _check(gr, exact["d" + n], dtype, f"{what} d{n}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("per_dim", [True, False])
+def test_pq_bwd_dtypes(dtype, per_dim):
+    _say(f"pq bwd {dtype} per_dim={per_dim}")
+    case = _pq_case(700 + per_dim, batch=2, dim=32, L=136, N=16, R=2, dtype=dtype, per_dim=per_dim)
+    _vs_exact(case, _dout(701, (2, 32, 136), dtype), dtype, f"{dtype}")
+
+
+@pytest.mark.parametrize("R", [1, 3, 4])
+def test_pq_bwd_ranks(R):
+    _say(f"pq bwd rank {R}")
+    case = _pq_case(710 + R, batch=2, dim=32, L=64, N=16, R=R, dtype=torch.float32)
+    _vs_exact(case, _dout(711, (2, 32, 64), torch.float32), torch.float32, f"R{R}")
+
+
+@pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False), dict(with_bias=False),
+                                   dict(softplus=False), dict(bkind="4d", G=2), dict(bkind="4d", G=4)])
+def test_pq_bwd_options(flags):
+    _say(f"pq bwd options {flags}")
+    case = _pq_case(720 + len(str(flags)), batch=2, dim=64, L=72, N=16, R=2, dtype=torch.float32, **flags)
+    _vs_exact(case, _dout(721, (2, 64, 72), torch.float32), torch.float32, str(flags))
+
+
+@pytest.mark.parametrize("N", [1, 4, 12])
+def test_pq_bwd_small_dstate(N):
+    _say(f"pq bwd dstate {N}")
+    case = _pq_case(730 + N, batch=3, dim=16, L=40, N=N, R=min(N, 2), dtype=torch.float32)
+    _vs_exact(case, _dout(731, (3, 16, 40), torch.float32), torch.float32, f"N{N}")
+
+
+@pytest.mark.parametrize("L", [8, 16, 1032])
+def test_pq_bwd_lengths(L):
+    _say(f"pq bwd L={L}")
+    case = _pq_case(740 + L, batch=1, dim=16, L=L, N=16, R=2, dtype=torch.float32)
+    _vs_exact(case, _dout(741, (1, 16, L), torch.float32), torch.float32, f"L{L}")
+
+
+def test_pq_bwd_partial_grads_and_dtypes():
+    """Only some inputs require grad; dP / dQ come back in P's / Q's dtype and shape."""
+    _say("pq bwd partial requires_grad")
+    from motif_mamba_amd import selective_scan_fn
+    case = _pq_case(750, batch=2, dim=16, L=48, N=16, R=2, dtype=torch.bfloat16)
+    dout = _dout(751, (2, 16, 48), torch.bfloat16)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    g["P"] = g["P"].to(torch.bfloat16).requires_grad_(True)
+    g["Q"].requires_grad_(True)
+    out = selective_scan_fn(**g)
+    out.backward(dout.to(DEV))
+    assert g["P"].grad.dtype == torch.bfloat16 and g["P"].grad.shape == (16, 16, 2)
+    assert g["Q"].grad.dtype == torch.float32 and g["Q"].grad.shape == (16, 2, 16)
+    assert g["u"].grad is None and g["A"].grad is None
+    exact = selective_scan_pq_bwd_ref(**dict(case, P=case["P"].to(torch.bfloat16)), dout=dout)
+    _check(g["P"].grad, exact["dP"], torch.bfloat16, "dP")
+    _check(g["Q"].grad, exact["dQ"], torch.bfloat16, "dQ")
+
+
+def test_pq_bwd_training_forward_matches_inference_forward():
+    _say("pq training forward = inference forward")
+    from motif_mamba_amd import selective_scan_fn
+    case = _pq_case(760, batch=2, dim=32, L=256, N=16, R=2, dtype=torch.bfloat16)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    inf, inf_last = selective_scan_fn(**g, return_last_state=True)
+    g["P"] = g["P"].clone().requires_grad_(True)
+    tr, tr_last = selective_scan_fn(**g, return_last_state=True)
+    torch.testing.assert_close(tr.detach(), inf, rtol=0, atol=0)
+    torch.testing.assert_close(tr_last.detach(), inf_last, rtol=1e-6, atol=1e-6)
+
+
+def test_pq_bwd_native_api_accumulates_into_dP_out():
+    """selective_scan_cuda.bwd with P/Q: the reference's output list; dP / dQ are added into
+    dP_out / dQ_out (selective_scan.cpp:580-590 accumulates into them)."""
+    _say("pq bwd native API")
+    from motif_mamba_amd import _native
+    case = _pq_case(770, batch=2, dim=32, L=64, N=16, R=2, dtype=torch.float32)
+    dout = _dout(771, (2, 32, 64), torch.float32)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    B4, C4 = g["B"].unsqueeze(1), g["C"].unsqueeze(1)
+    out, x, out_z = _native.ext().fwd(g["u"], g["delta"], g["A"], B4, C4, g["D"], g["z"], g["delta_bias"],
+                                      g["P"], g["Q"], None, True)
+    dP = torch.ones(32, 16, 2, device=DEV)
+    dQ = torch.full((32, 2, 16), 2.0, device=DEV)
+    res = _native.ext().bwd(g["u"], g["delta"], g["A"], B4, C4, g["D"], g["z"], g["delta_bias"], g["P"], g["Q"],
+                            None, dout.to(DEV), x, out, None, dP, dQ, True, True)
+    assert len(res) == 9      # du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, out_z
+    torch.cuda.synchronize()
+    exact = selective_scan_pq_bwd_ref(**case, dout=dout)
+    _check(dP - 1.0, exact["dP"], torch.float32, "dP_out")
+    _check(dQ - 2.0, exact["dQ"], torch.float32, "dQ_out")
+    _check(res[0], exact["du"], torch.float32, "du")
+    _check(res[7], exact["dz"], torch.float32, "dz")
+    torch.testing.assert_close(res[8], out_z, rtol=1e-6, atol=1e-6)   # recomputed: same math, own rounding
+
+
+def test_pq_bwd_c_abi_direct():
+    _say("pq bwd C ABI direct")
+    lib = capi.load()
+    case = _pq_case(780, batch=2, dim=32, L=96, N=16, R=3, dtype=torch.float32, per_dim=False)
+    dout = _dout(781, (2, 32, 96), torch.float32)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    B4, C4 = g["B"].unsqueeze(1), g["C"].unsqueeze(1)
+    pre = selective_scan_pq_ref(**{**case, "z": None}).to(DEV)   # the forward's pre-gate output
+    do = dout.to(DEV)
+    du, ddelta, dz = torch.empty_like(g["u"]), torch.empty_like(g["delta"]), torch.empty_like(g["z"])
+    dA = torch.full_like(g["A"], 7.0)            # overwritten, not accumulated into
+    dB, dC = torch.full_like(B4, 7.0), torch.full_like(C4, 7.0)
+    dD, dbias = torch.full_like(g["D"], 7.0), torch.full_like(g["delta_bias"], 7.0)
+    dP, dQ = torch.full_like(g["P"], 7.0), torch.full_like(g["Q"], 7.0)
+    p = capi.ScanBwdParams()
+    p.batch, p.dim, p.seqlen, p.dstate, p.n_groups = 2, 32, 96, 16, 1
+    p.itype, p.is_variable_B, p.is_variable_C, p.delta_softplus = 0, 1, 1, 1
+    ptr = lambda t: t.data_ptr()
+    p.u, p.delta, p.A, p.B, p.C, p.D, p.z, p.delta_bias = map(ptr, (g["u"], g["delta"], g["A"], B4, C4, g["D"],
+                                                                  g["z"], g["delta_bias"]))
+    p.dout, p.out = ptr(do), ptr(pre)
+    p.du, p.ddelta, p.dz, p.dA, p.dB, p.dC, p.dD, p.ddelta_bias = map(ptr, (du, ddelta, dz, dA, dB, dC, dD, dbias))
+    for nm, t in (("u", g["u"]), ("delta", g["delta"]), ("z", g["z"]), ("out", pre), ("dout", do), ("du", du),
+                  ("ddelta", ddelta), ("dz", dz)):
+        setattr(p, f"{nm}_batch_stride", t.stride(0))
+        setattr(p, f"{nm}_d_stride", t.stride(1))
+    p.A_d_stride, p.A_dstate_stride = g["A"].stride()
+    p.dA_d_stride, p.dA_dstate_stride = dA.stride()
+    p.B_batch_stride, p.B_group_stride, p.B_dstate_stride = B4.stride()[:3]
+    p.C_batch_stride, p.C_group_stride, p.C_dstate_stride = C4.stride()[:3]
+    p.dB_batch_stride, p.dB_group_stride, p.dB_dstate_stride = dB.stride()[:3]
+    p.dC_batch_stride, p.dC_group_stride, p.dC_dstate_stride = dC.stride()[:3]
+    p.P, p.Q, p.pq_rank = ptr(g["P"]), ptr(g["Q"]), 3
+    p.P_dstate_stride, p.P_r_stride = g["P"].stride()
+    p.Q_r_stride, p.Q_dstate_stride = g["Q"].stride()
+    p.dP, p.dQ = ptr(dP), ptr(dQ)
+    p.dP_dstate_stride, p.dP_r_stride = dP.stride()
+    p.dQ_r_stride, p.dQ_dstate_stride = dQ.stride()
+    nbytes = lib.mm_scan_bwd_workspace_size(ctypes.byref(p))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    p.workspace, p.workspace_bytes = ws.data_ptr(), nbytes
+    rc = lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle())
+    assert rc == 0, lib.mm_last_error().decode()
+    torch.cuda.synchronize()
+    exact = selective_scan_pq_bwd_ref(**case, dout=dout)
+    for name, t in (("du", du), ("ddelta", ddelta), ("dz", dz), ("dA", dA), ("dB", dB.squeeze(1)),
+                    ("dC", dC.squeeze(1)), ("dD", dD), ("ddelta_bias", dbias), ("dP", dP), ("dQ", dQ)):
+        _check(t, exact[name], torch.float32, f"capi {name}")
+    # A rank the kernels do not cover: MM_ERR_UNSUPPORTED with a message, nothing launched.
+    p.pq_rank = 5
+    assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_UNSUPPORTED
+    assert b"pq_rank" in lib.mm_last_error()
+    p.pq_rank, p.dP = 3, None
+    assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("what", ["rank5", "dstate32", "L12", "constB"])
+def test_pq_bwd_unsupported_shapes_raise(what):
+    """Shapes outside the kernel raise NotImplementedError in the backward; the forward runs."""
+    _say(f"pq bwd unsupported {what}")
+    from motif_mamba_amd import selective_scan_fn
+    kw = dict(batch=1, dim=16, L=32, N=16, R=2, dtype=torch.float32)
+    if what == "rank5":
+        kw["R"] = 5
+    elif what == "dstate32":
+        kw["N"] = 32
+    elif what == "L12":
+        kw["L"] = 12
+    case = _pq_case(790, **kw)
+    if what == "constB":
+        case["B"] = torch.randn(16, 16)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    g["u"].requires_grad_(True)
+    out = selective_scan_fn(**g)
+    with pytest.raises(NotImplementedError, match="P/Q backward"):
+        out.backward(torch.ones_like(out))
