@@ -160,6 +160,40 @@ def bench_pq(name, steps, warmup, torch):
             "t_floor_us": floor * 1e6, "floor_frac": floor / (ms * 1e-3)}
 
 
+def bench_pq_train(name, steps, warmup, torch):
+    """Training forward and backward of the low-rank coupled scan (P/Q) on a MotifMamba layer: the
+    forward saving pre-gate out and chunk states, and the backward with dP / dQ."""
+    from motif_mamba_amd import _native
+    from motif_mamba_amd.workloads import PQ_CONFIGS, pq_inputs
+    ext = _native.ext()
+    c = PQ_CONFIGS[name]
+    t = pq_inputs(c, device="cuda")
+    B, C = t["B"].unsqueeze(1), t["C"].unsqueeze(1)
+    args = (t["u"], t["delta"], t["A"], B, C, t["D"], t["z"], t["delta_bias"], t["P"], t["Q"], None, True)
+    out, x, out_z = ext.fwd(*args)
+    dout = torch.randn(out_z.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(7)).to(out_z.dtype)
+    dP, dQ = torch.zeros_like(t["P"]), torch.zeros_like(t["Q"])
+
+    def fwd(i):
+        ext.fwd(*args)
+
+    def bwd(i):
+        ext.bwd(*args[:11], dout, x, out, None, dP, dQ, True, False)
+
+    def both(i):
+        o, xx, oz = ext.fwd(*args)
+        ext.bwd(*args[:11], dout, xx, o, None, dP, dQ, True, False)
+
+    f_ms = _time_loop(fwd, steps, warmup, torch)
+    b_ms = _time_loop(bwd, steps, warmup, torch)
+    s_ms = _time_loop(both, steps, warmup, torch)
+    elems = c.batch * c.dim * c.seqlen
+    del t, out, x, out_z, dout
+    torch.cuda.empty_cache()
+    return {"shape": [c.batch, c.dim, c.seqlen, c.dstate], "rank": c.rank, "per_dim": c.per_dim, "dtype": c.dtype,
+            "fwd_train_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": s_ms, "elements_per_s": elems / (s_ms * 1e-3)}
+
+
 def bench_train(cfg_name, steps, warmup, torch):
     """Forward in training mode (pre-gate out and chunk states saved, ssi.py:47-61) and the backward
     (selective_scan_cuda.bwd equivalent) on one configuration: times of each and of the pair."""
@@ -320,7 +354,7 @@ def main():
                     help="also run three 1 GiB device-to-device copies: the reference that scales the "
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
-                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, "
+                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, pq_1p4b_train, "
                          "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_update_b<batch>, inner_2p8b) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
@@ -339,6 +373,8 @@ def main():
         name = args.only
         if name.startswith("cfg4_b"):
             res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
+        elif name.startswith("pq_") and name.endswith("_train"):
+            res = bench_pq_train(name[: -len("_train")], args.steps, args.warmup, torch)
         elif name.startswith("pq_"):
             res = bench_pq(name, args.steps, args.warmup, torch)
         elif name == "inner_2p8b":
@@ -376,6 +412,8 @@ def main():
             extra[f"cfg4_b{b}"] = bench_decode(b, 1024, 16, torch)
         _log("MotifMamba P/Q forward (Mamba-1.4B layer, rank 2, per-channel P/Q)")
         extra["pq_1p4b"] = bench_pq("pq_1p4b", max(5, args.steps), 2, torch)
+        _log("MotifMamba P/Q training forward + backward (same layer)")
+        extra["pq_1p4b_train"] = bench_pq_train("pq_1p4b", max(5, args.steps // 2), 2, torch)
         for name in ("cfg1", "cfg2"):
             _log(f"training forward + backward ({name})")
             extra[f"{name}_train"] = bench_train(name, max(5, args.steps // 2), 2, torch)

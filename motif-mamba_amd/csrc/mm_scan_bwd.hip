@@ -531,9 +531,21 @@ scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *part, float *dst, in
         const int64_t row = i / L4, t4 = i - row * L4;
         if (row % 16 >= p.dstate) continue;   // slab rows past dstate (P/Q with dstate < 16) are not written
         const float4 *src = reinterpret_cast<const float4 *>(part + row * p.seqlen) + t4;
+        const int64_t st = slice / 4;
         float4 acc = src[0];
-        for (int64_t k = 1; k < n_blocks; ++k) {
-            const float4 v = src[k * (slice / 4)];
+        int64_t k = 1;
+        // Eight loads in flight per lane, added in block order (the sum stays deterministic).
+        for (; k + 8 <= n_blocks; k += 8) {
+            float4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = src[(k + i) * st];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                acc.x += v[i].x; acc.y += v[i].y; acc.z += v[i].z; acc.w += v[i].w;
+            }
+        }
+        for (; k < n_blocks; ++k) {
+            const float4 v = src[k * st];
             acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
         }
         const int64_t n = row % 16, bg = row / 16;

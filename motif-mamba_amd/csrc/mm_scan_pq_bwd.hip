@@ -24,8 +24,11 @@
 // those lanes, which leave bit-identical totals in all of them. P and Q of the lane's states live
 // in registers. A first pass recomputes the forward and stores the states at every 16-step tile
 // start in the caller's workspace; the second walks the tiles in reverse, recomputes each from its
-// checkpoint into LDS (read back by the same lane) and walks it backwards. The dB / dC contributions are summed over the block's 16 channels through
-// LDS per 8-step half tile and written as the block's partials, which scan_bwd_reduce_bc adds in
+// checkpoint into LDS (the states read back by the same lane, Q h_{t-1} by the whole channel) and
+// walks it backwards. The dB / dC
+// contributions are summed over the block's 16 channels through LDS per 4 steps (so that the
+// 35 KB of LDS let four workgroups share a CU) and written as the block's partials, which
+// scan_bwd_reduce_bc adds in
 // block order (no atomics on them); dA, dP, dQ, dD and ddelta_bias take float32 atomics once per
 // lane at the end.
 #include <hip/hip_runtime.h>
@@ -39,7 +42,7 @@ namespace mm {
 namespace pqbwd {
 
 constexpr int kT = 16;           // steps per tile
-constexpr int kH = 8;            // steps per reduction half
+constexpr int kH = 4;            // steps per dB / dC reduction
 constexpr int kXS = kT + 1;      // sX row stride (float4)
 constexpr int kBCS = 36;         // sBC row stride (floats): B 16 | C 16 | pad 4
 constexpr int kRow = 20;         // sRed row stride (floats): 16 channels + 4
@@ -72,9 +75,10 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
     constexpr int E = kT / LPR;          // steps per lane of a tile's per-element work
     __shared__ __align__(16) float4 sX[16 * kXS];       // [c][t]: (dt', dt'u, u, g)
     __shared__ __align__(16) float sBC[kT * kBCS];       // [t][B 16 | C 16]
-    __shared__ __align__(16) float sRed[kRed];           // [tensor][t][n][c]
+    __shared__ __align__(16) float sRed[kRed];           // [tensor][t % kH][n][c]
     __shared__ __align__(16) float sHS[kT * 16 * 16];    // [t][c][n]: the tile's states after step t
     __shared__ __align__(16) float sOwn[2 * 16 * kT];    // [sum of lam B | dt' term][c][t]
+    __shared__ __align__(16) float sQ[kT * 16 * R];      // [t][c][r]: Q h_{t-1} of the tile's steps
 
     const int tid = threadIdx.x;
     const int cw = tid / LPR;              // channel of the block
@@ -235,14 +239,17 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll 2
             for (int t = 0; t < kT; ++t) {
                 const float4 x = sX[cw * kXS + t];
-                float q[R];
+                float q[R], qw = 0.f;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     float acc = Qr[r][0] * h[0];
 #pragma unroll
                     for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
-                    q[r] = group_sum<LPR>(acc) * x.x;
+                    q[r] = group_sum<LPR>(acc);
+                    if (k == r) qw = q[r];
+                    q[r] *= x.x;
                 }
+                if (k < R) sQ[(t * 16 + cw) * R + k] = qw;     // (Q h_{t-1})_k, read by the whole channel
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     float w = x.y * sBC[t * kBCS + k * S + s];
@@ -253,28 +260,31 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                 }
             }
         }
-        for (int t = kT - 1; t >= 0; --t) {
-            const int sh = t % kH;
+        __syncthreads();                             // sQ is read by every lane of the channel
+        float hc[S];                                 // h_t of the step being walked
+#pragma unroll
+        for (int s = 0; s < S; ++s) hc[s] = sHS[((kT - 1) * 16 + cw) * 16 + k * S + s];
+        for (int tg = kT - kH; tg >= 0; tg -= kH) {
+#pragma unroll 2
+        for (int ti = kH - 1; ti >= 0; --ti) {
+            const int t = tg + ti;
+            const int sh = ti;
             const float4 x = sX[cw * kXS + t];       // dt', dt'u, u, g
-            float Bv[S], Cv[S], lam[S], hp[S], hc[S];
+            float Bv[S], Cv[S], lam[S], hp[S];
 #pragma unroll
             for (int s = 0; s < S; ++s) {
                 Bv[s] = sBC[t * kBCS + k * S + s];
                 Cv[s] = sBC[t * kBCS + 16 + k * S + s];
                 lam[s] = __builtin_fmaf(Cv[s], x.w, carry[s]);
                 hp[s] = t > 0 ? sHS[((t - 1) * 16 + cw) * 16 + k * S + s] : hck[s];   // h_{t-1}
-                hc[s] = sHS[(t * 16 + cw) * 16 + k * S + s];                            // h_t
             }
             float q[R], sv[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                float aq = Qr[r][0] * hp[0], as = Pr[0][r] * lam[0];
+                float as = Pr[0][r] * lam[0];
 #pragma unroll
-                for (int s = 1; s < S; ++s) {
-                    aq = __builtin_fmaf(Qr[r][s], hp[s], aq);
-                    as = __builtin_fmaf(Pr[s][r], lam[s], as);
-                }
-                q[r] = group_sum<LPR>(aq);          // (Q h_{t-1})_r
+                for (int s = 1; s < S; ++s) as = __builtin_fmaf(Pr[s][r], lam[s], as);
+                q[r] = sQ[(t * 16 + cw) * R + r];   // (Q h_{t-1})_r
                 sv[r] = group_sum<LPR>(as);         // (P^T lam_t)_r
             }
             float pdd = 0.f, pgb = 0.f;
@@ -301,6 +311,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                 sRed[((0 * kH + sh) * 16 + k * S + s) * kRow + cw] = lam[s] * x.y;   // dB contribution
                 sRed[((1 * kH + sh) * 16 + k * S + s) * kRow + cw] = x.w * hc[s];    // dC contribution
                 carry[s] = __builtin_fmaf(a, lam[s], x.x * qs);                      // into step t - 1
+                hc[s] = hp[s];
             }
             const float dd_t = group_sum<LPR>(pdd), gb_t = group_sum<LPR>(pgb);
             if (t / E == k) {                 // this lane owns step t of its channel (and reads it back)
@@ -309,8 +320,8 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
             }
             if (sh == 0) {
                 __syncthreads();
-                // dB / dC of the half summed over the block's 16 channels, in channel order, written as
-                // this block's partials: 2 x kH x 16 rows (tensor, step, state).
+                // dB / dC of the last kH steps summed over the block's 16 channels, in channel order,
+                // written as this block's partials: 2 x kH x 16 rows (tensor, step, state).
 #pragma unroll
                 for (int rr = 0; rr < (2 * kH * 16) / NT; ++rr) {
                     const int row = tid + NT * rr;
@@ -329,6 +340,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                 }
                 __syncthreads();
             }
+        }
         }
         // du / ddelta of this lane's steps.
 #pragma unroll
