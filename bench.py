@@ -161,8 +161,9 @@ def bench_pq(name, steps, warmup, torch):
 
 
 def bench_pq_train(name, steps, warmup, torch):
-    """Training forward and backward of the low-rank coupled scan (P/Q) on a MotifMamba layer: the
-    forward saving pre-gate out and chunk states, and the backward with dP / dQ."""
+    """Training forward and backward of the low-rank coupled scan (P/Q) on a MotifMamba layer, as
+    SelectiveScanPQFn runs them: the forward saving pre-gate out, chunk states and the 16-step tile
+    states, and the backward (reading those tile states) with dP / dQ."""
     from motif_mamba_amd import _native
     from motif_mamba_amd.workloads import PQ_CONFIGS, pq_inputs
     ext = _native.ext()
@@ -170,28 +171,33 @@ def bench_pq_train(name, steps, warmup, torch):
     t = pq_inputs(c, device="cuda")
     B, C = t["B"].unsqueeze(1), t["C"].unsqueeze(1)
     args = (t["u"], t["delta"], t["A"], B, C, t["D"], t["z"], t["delta_bias"], t["P"], t["Q"], None, True)
-    out, x, out_z = ext.fwd(*args)
+    out, x, out_z, ck = ext.fwd(*args, tile_states=True)
     dout = torch.randn(out_z.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(7)).to(out_z.dtype)
     dP, dQ = torch.zeros_like(t["P"]), torch.zeros_like(t["Q"])
 
     def fwd(i):
-        ext.fwd(*args)
+        ext.fwd(*args, tile_states=True)
 
     def bwd(i):
-        ext.bwd(*args[:11], dout, x, out, None, dP, dQ, True, False)
+        ext.bwd(*args[:11], dout, x, out, None, dP, dQ, True, False, ck)
 
     def both(i):
-        o, xx, oz = ext.fwd(*args)
-        ext.bwd(*args[:11], dout, xx, o, None, dP, dQ, True, False)
+        o, xx, oz, cc = ext.fwd(*args, tile_states=True)
+        ext.bwd(*args[:11], dout, xx, o, None, dP, dQ, True, False, cc)
+
+    def bwd_self(i):                   # without the forward's tile states: the backward recomputes them
+        ext.bwd(*args[:11], dout, x, out, None, dP, dQ, True, False)
 
     f_ms = _time_loop(fwd, steps, warmup, torch)
     b_ms = _time_loop(bwd, steps, warmup, torch)
     s_ms = _time_loop(both, steps, warmup, torch)
+    bs_ms = _time_loop(bwd_self, steps, warmup, torch)
     elems = c.batch * c.dim * c.seqlen
-    del t, out, x, out_z, dout
+    del t, out, x, out_z, dout, ck
     torch.cuda.empty_cache()
     return {"shape": [c.batch, c.dim, c.seqlen, c.dstate], "rank": c.rank, "per_dim": c.per_dim, "dtype": c.dtype,
-            "fwd_train_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": s_ms, "elements_per_s": elems / (s_ms * 1e-3)}
+            "fwd_train_ms": f_ms, "bwd_ms": b_ms, "fwd_bwd_ms": s_ms, "bwd_recompute_ms": bs_ms,
+            "elements_per_s": elems / (s_ms * 1e-3)}
 
 
 def bench_train(cfg_name, steps, warmup, torch):

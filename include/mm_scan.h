@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 7
+#define MM_SCAN_ABI_VERSION 8
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -129,6 +129,13 @@ typedef struct mm_scan_fwd_params {
     int64_t P_d_stride, P_dstate_stride, P_r_stride;
     int64_t Q_d_stride, Q_r_stride, Q_dstate_stride;
     int64_t gamma_d_stride, gamma_dstate_stride;
+
+    /* Checkpoints for the P/Q backward (ABI version 8; no counterpart in the reference, whose
+     * backward keeps only `chunk_states`). When non-NULL (P/Q set, dstate <= 16): the state before
+     * every 16-step tile, float32 [ceil(seqlen / 16)][batch][dim][16], states past dstate written
+     * as 0 -- B * dim * seqlen * 4 bytes, about one float32 copy of u. Passed to mm_scan_bwd as
+     * `tile_states`, they spare it the recompute of the whole forward. NULL: not written. */
+    float *tile_states;
 } mm_scan_fwd_params;
 
 /* Backward of the diagonal forward scan: the gradients of every input for a given gradient `dout`
@@ -213,6 +220,11 @@ typedef struct mm_scan_bwd_params {
     float *dQ;
     int64_t dP_d_stride, dP_dstate_stride, dP_r_stride;
     int64_t dQ_d_stride, dQ_r_stride, dQ_dstate_stride;
+
+    /* Optional with P/Q (ABI version 8): the `tile_states` mm_scan_fwd wrote for the same inputs;
+     * the backward then reads its checkpoints there instead of recomputing them (and needs a
+     * smaller workspace). The contents are trusted: stale states give wrong gradients. */
+    const float *tile_states;
 } mm_scan_bwd_params;
 
 /* Single-token decode update, in place on `state`:

@@ -411,7 +411,7 @@ int validate_fwd(const mm_scan_fwd_params *p) {
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: out_z is required when z is given");
     if (!p->z && p->out_z)
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: out_z given without z");
-    if (!p->out && !p->out_z && !p->last_state && !p->chunk_states)
+    if (!p->out && !p->out_z && !p->last_state && !p->chunk_states && !p->tile_states)
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: no output requested");
     // Low-rank coupling (selective_scan.cpp:342-359): P and Q together, rank <= 8.
     if ((p->P == nullptr) != (p->Q == nullptr))
@@ -419,6 +419,8 @@ int validate_fwd(const mm_scan_fwd_params *p) {
     if (p->P && (p->pq_rank < 0 || p->pq_rank > 8))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: pq_rank must be in [0, 8] (got %lld)",
                     (long long)p->pq_rank);
+    if (p->tile_states && (!p->P || p->dstate > 16))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: tile_states are written only with P/Q and dstate <= 16");
     return MM_OK;
 }
 
@@ -485,6 +487,8 @@ int validate_bwd(const mm_scan_bwd_params *p) {
     if (p->P && !mm::pq_bwd_ok(*p))
         return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, pq_rank <= 4, "
                                         "dim and dim / n_groups multiples of 16 and seqlen a multiple of 8");
+    if (p->tile_states && !p->P)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: tile_states are read only with P/Q");
     const int64_t need = mm::bwd_workspace_bytes(*p);
     if (p->seqlen > 0 && (!p->workspace || p->workspace_bytes < need || reinterpret_cast<uintptr_t>(p->workspace) % 16))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: needs a 16-byte aligned workspace of %lld bytes (got %lld)",

@@ -627,9 +627,11 @@ int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
 // The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
 template <typename T>
 int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
+    // Checkpoints: the forward's tile_states when given, else the head of the workspace.
     float *ws = static_cast<float *>(p.workspace);
-    float *partB = ws + fast_ck_floats(p), *partC = partB + fast_part_floats(p);
-    int rc = launch_pq_bwd<T>(p, s, ws, partB, partC);
+    float *ck = p.tile_states ? const_cast<float *>(p.tile_states) : ws;
+    float *partB = p.tile_states ? ws : ws + fast_ck_floats(p), *partC = partB + fast_part_floats(p);
+    int rc = launch_pq_bwd<T>(p, s, ck, partB, partC);
     if (rc != MM_OK) return rc;
     // Slab rows past dstate are never written; the reduction reads only rows n < 16 of each slab
     // and writes rows n < dstate (dB / dC hold dstate rows).
@@ -648,6 +650,7 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
+    if (p.P && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
     return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));

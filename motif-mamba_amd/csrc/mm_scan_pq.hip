@@ -131,6 +131,13 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     const bool softplus = p.delta_softplus != 0;
     const int es = E * k;                  // first step (within a tile) of this lane's elements
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+    // Checkpoints for the backward: the S states of this lane before every 16-step tile.
+    const int64_t ck_tile = p.batch * p.dim * 16;
+    float *const ckp = (p.tile_states && active) ? p.tile_states + (b * p.dim + d) * 16 + k * S : nullptr;
+    auto put_ck = [&](int64_t j) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) ckp[j * ck_tile + s] = h[s];
+    };
 
     // The B/C half-rows this lane stages: index hr = lane HR + i -> tensor hr / (2 NP) (0: B, 1: C),
     // state (hr % 2NP) / 2, steps 16 (hr % 2) .. +15 of the tile.
@@ -217,12 +224,16 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             *reinterpret_cast<float2 *>(&sDu[cw * kPad + es + i]) = make_float2(dup[i], dup[i + 1]);
         }
         __syncthreads();
+        if (ckp) put_ck(t0 / 16);
 
         // Scan: 32 steps in groups of 4. The decay factors and the input terms of a group do not
         // depend on the state and are formed first; then the coupled updates run in order.
         float yp[kT];
         static_for<0, kT / 4>([&](auto G4) {
             constexpr int s4 = decltype(G4)::value;
+            if constexpr (s4 == 4) {
+                if (ckp && t0 + 16 < L) put_ck(t0 / 16 + 1);
+            }
             const float4 dt4 = *reinterpret_cast<const float4 *>(&sDt[cw * kPad + 4 * s4]);
             const float4 du4 = *reinterpret_cast<const float4 *>(&sDu[cw * kPad + 4 * s4]);
             const float dts[4] = {dt4.x, dt4.y, dt4.z, dt4.w};
@@ -361,6 +372,11 @@ scan_fwd_pq_rowlane(const mm_scan_fwd_params p, const int64_t ratio) {
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
 
     for (int64_t t = 0; t < L; ++t) {
+        if (p.tile_states && active && t % 16 == 0) {
+            // The state before this 16-step tile, for the backward (states past dstate are 0).
+            float *ck = p.tile_states + ((t / 16) * p.batch * p.dim + b * p.dim + d) * 16;
+            for (int n = 0; n < 16; ++n) ck[n] = n < N ? sH[n * kRowBlock + lane] : 0.f;
+        }
         float dt = to_f32(dp[t]) + bias;
         if (p.delta_softplus) dt = softplus_fast(dt);
         const float uu = to_f32(up[t]);

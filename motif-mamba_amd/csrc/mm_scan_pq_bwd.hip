@@ -22,15 +22,14 @@
 // states each (S = 2: 8 lanes per channel, two waves per workgroup), and the sums over a channel's
 // states (Q h, P^T lam, and the per-step sums that give du and ddelta) are DPP butterflies inside
 // those lanes, which leave bit-identical totals in all of them. P and Q of the lane's states live
-// in registers. A first pass recomputes the forward and stores the states at every 16-step tile
-// start in the caller's workspace; the second walks the tiles in reverse, recomputes each from its
-// checkpoint into LDS (the states read back by the same lane, Q h_{t-1} by the whole channel) and
-// walks it backwards. The dB / dC
-// contributions are summed over the block's 16 channels through LDS per 4 steps (so that the
-// 35 KB of LDS let four workgroups share a CU) and written as the block's partials, which
-// scan_bwd_reduce_bc adds in
-// block order (no atomics on them); dA, dP, dQ, dD and ddelta_bias take float32 atomics once per
-// lane at the end.
+// in registers. The states at every 16-step tile start come from the forward (its tile_states) or,
+// without them, from a first pass that recomputes the forward into the caller's workspace. The
+// second pass walks the tiles in reverse: it recomputes each tile from its checkpoint into LDS (the
+// states read back by the same lane, Q h_{t-1} by the whole channel) and walks it backwards. The
+// dB / dC contributions are summed over the block's 16 channels through LDS per 4 steps (so that
+// the 37-39 KB of LDS let four workgroups share a CU) and written as the block's partials, which
+// scan_bwd_reduce_bc adds in block order (no atomics on them); dA, dP, dQ, dD and ddelta_bias take
+// float32 atomics once per lane at the end.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -136,24 +135,61 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
     const T *stp = (st_row < 16 ? Bg + int64_t(st_on ? st_n : 0) * p.B_dstate_stride
                                 : Cg + int64_t(st_on ? st_n : 0) * p.C_dstate_stride);
 
+    // A tile's global inputs, loaded one tile ahead of their use (raw, converted at commit):
+    // delta, u, dout, z, out of this lane's E elements, its SPL staged B or C values and the
+    // checkpoint. Addresses past L are clamped to the row's last element (their steps are padding).
+    struct TileIn {
+        T d[E], u[E], go[E], z[E], o[E], bc[SPL];
+        float hck[S];
+    };
+    auto fetch = [&](int64_t j, bool full, bool with_ck) {
+        TileIn r;
+        const int64_t t0 = j * kT;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const int64_t t = t0 + es + i;
+            const int64_t tc = t < L ? t : L - 1;
+            r.d[i] = dp[tc];
+            r.u[i] = up[tc];
+            if (full) {
+                r.go[i] = gop[tc];
+                if (zp) {
+                    r.z[i] = zp[tc];
+                    r.o[i] = outp[tc];
+                }
+            }
+        }
+        if (full || st_row < 16) {
+#pragma unroll
+            for (int i = 0; i < SPL; ++i) {
+                const int64_t t = t0 + st_t0 + i;
+                r.bc[i] = stp[t < L ? t : L - 1];
+            }
+        }
+        if (with_ck) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) r.hck[s] = ckp[j * ck_tile + s];
+        }
+        return r;
+    };
+
     // Tile j's per-step values into LDS (with B, and C when `full`); this lane's elements kept in
     // registers; dz and out_z written. Steps past L are padding (dt' = g = 0, B = C = 0: inert).
     float e_raw[E], e_dt[E], e_u[E], e_g[E];
-    auto commit = [&](int64_t j, bool full) {
+    auto commit = [&](int64_t j, bool full, const TileIn &r) {
         const int64_t t0 = j * kT;
 #pragma unroll
         for (int i = 0; i < E; ++i) {
             const int64_t t = t0 + es + i;
             const bool ev = t < L;
-            const int64_t tc = ev ? t : L - 1;
-            const float dd = to_f32(dp[tc]);
-            const float uu = to_f32(up[tc]);
+            const float dd = to_f32(r.d[i]);
+            const float uu = to_f32(r.u[i]);
             float go = 0.f;
             if (full) {
-                go = to_f32(gop[tc]);
+                go = to_f32(r.go[i]);
                 if (zp) {
-                    const float zz = to_f32(zp[tc]);
-                    const float oo = to_f32(outp[tc]);
+                    const float zz = to_f32(r.z[i]);
+                    const float oo = to_f32(r.o[i]);
                     const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-zz * kLog2e));
                     if (ev) {
                         dzp[t] = from_f32<T>(go * oo * sg * (1.f + zz * (1.f - sg)));
@@ -173,20 +209,22 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
             for (int i = 0; i < SPL; ++i) {
                 const int64_t t = t0 + st_t0 + i;
                 const bool on = st_on && t < L;
-                sBC[(st_t0 + i) * kBCS + st_row] = on ? to_f32(stp[t < L ? t : L - 1]) : 0.f;
+                sBC[(st_t0 + i) * kBCS + st_row] = on ? to_f32(r.bc[i]) : 0.f;
             }
         }
     };
 
-    // ---- Pass 1: the states before every tile ----
-    {
+    // ---- Pass 1: the states before every tile (skipped when the forward wrote them) ----
+    if (!p.tile_states) {
         float h[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) h[s] = 0.f;
+        TileIn in = fetch(0, false, false);
         for (int64_t j = 0; j < n_tiles; ++j) {
 #pragma unroll
             for (int s = 0; s < S; ++s) ckp[j * ck_tile + s] = h[s];
-            commit(j, false);
+            commit(j, false, in);
+            if (j + 1 < n_tiles) in = fetch(j + 1, false, false);   // in flight during this tile
             __syncthreads();
 #pragma unroll
             for (int t = 0; t < kT; ++t) {
@@ -224,12 +262,14 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
         }
     }
     float dD_acc = 0.f, dbias_acc = 0.f;
+    TileIn in = fetch(n_tiles - 1, true, true);
     for (int64_t j = n_tiles - 1; j >= 0; --j) {
         const int64_t t0 = j * kT;
         float hck[S];
 #pragma unroll
-        for (int s = 0; s < S; ++s) hck[s] = ckp[j * ck_tile + s];
-        commit(j, true);
+        for (int s = 0; s < S; ++s) hck[s] = in.hck[s];
+        commit(j, true, in);
+        if (j > 0) in = fetch(j - 1, true, true);                  // in flight during this tile
         __syncthreads();
         // Recompute the tile's states from its checkpoint into sHS (read back by this lane only).
         {

@@ -253,10 +253,18 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
                             const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                             const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &delta_bias_,
                             const c10::optional<at::Tensor> &P_, const c10::optional<at::Tensor> &Q_,
-                            const c10::optional<at::Tensor> &gamma_, bool delta_softplus) {
+                            const c10::optional<at::Tensor> &gamma_, bool delta_softplus, bool tile_states) {
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     mm_scan_fwd_params &p = s.p;
     const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
+    // tile_states (this build's addition, P/Q and dstate <= 16): the states before every 16-step
+    // tile, appended to the outputs for the backward.
+    at::Tensor ck;
+    if (tile_states) {
+        TORCH_CHECK(p.P != nullptr && p.dstate <= 16, "tile_states need P/Q and dstate <= 16");
+        ck = torch::empty({(p.seqlen + 15) / 16, p.batch, p.dim, 16}, u.options().dtype(at::ScalarType::Float));
+        p.tile_states = ck.data_ptr<float>();
+    }
     // Output layouts follow the reference: out like delta, out_z like z (like out when z is a
     // non-dense view such as half of xz), x contiguous.
     at::Tensor out = torch::empty_like(delta);
@@ -273,6 +281,7 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
     check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
     std::vector<at::Tensor> result = {out, x};
     if (z_.has_value()) result.push_back(out_z);
+    if (tile_states) result.push_back(ck);
     return result;
 }
 
@@ -318,7 +327,8 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
                             const c10::optional<at::Tensor> &gamma_, const at::Tensor &dout,
                             const c10::optional<at::Tensor> &x_, const c10::optional<at::Tensor> &out_,
                             c10::optional<at::Tensor> dz_, const c10::optional<at::Tensor> &dP_out_,
-                            const c10::optional<at::Tensor> &dQ_out_, bool delta_softplus, bool recompute_out_z) {
+                            const c10::optional<at::Tensor> &dQ_out_, bool delta_softplus, bool recompute_out_z,
+                            const c10::optional<at::Tensor> &tile_states_) {
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     // P/Q (and gamma, validated and not read, as in the forward): the float32 copies stay alive
     // until the launch is enqueued.
@@ -437,6 +447,14 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
         p.dQ_d_stride = Q.dim() == 3 ? dQ.stride(0) : 0;
         p.dQ_r_stride = dQ.stride(Q.dim() - 2);
         p.dQ_dstate_stride = dQ.stride(Q.dim() - 1);
+    }
+    if (tile_states_.has_value()) {
+        const at::Tensor &ck = tile_states_.value();
+        TORCH_CHECK(has_pq, "tile_states are read only with P/Q");
+        TORCH_CHECK(ck.is_cuda() && ck.scalar_type() == at::ScalarType::Float && ck.is_contiguous() &&
+                        ck.sizes() == at::IntArrayRef({(f.seqlen + 15) / 16, f.batch, f.dim, 16}),
+                    "tile_states must be the contiguous float32 (ceil(L / 16), batch, dim, 16) tensor of the forward");
+        p.tile_states = ck.data_ptr<float>();
     }
     const c10::DeviceGuard device_guard{u.device()};
     at::Tensor ws;
@@ -745,7 +763,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
           pybind11::arg("delta_bias") = pybind11::none(), pybind11::arg("P") = pybind11::none(),
           pybind11::arg("Q") = pybind11::none(), pybind11::arg("gamma") = pybind11::none(),
-          pybind11::arg("delta_softplus") = false);
+          pybind11::arg("delta_softplus") = false, pybind11::arg("tile_states") = false);
     m.def("bwd", &bwd, "Selective scan backward (reference-compatible outputs)",
           pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
           pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),
@@ -753,7 +771,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           pybind11::arg("Q") = pybind11::none(), pybind11::arg("gamma") = pybind11::none(), pybind11::arg("dout"),
           pybind11::arg("x"), pybind11::arg("out"), pybind11::arg("dz"), pybind11::arg("dP_out") = pybind11::none(),
           pybind11::arg("dQ_out") = pybind11::none(), pybind11::arg("delta_softplus"),
-          pybind11::arg("recompute_out_z"));
+          pybind11::arg("recompute_out_z"), pybind11::arg("tile_states") = pybind11::none());
     m.def("fwd_infer", &fwd_infer, "Selective scan forward, inference outputs [out_z|out, last_state?]",
           pybind11::arg("u"), pybind11::arg("delta"), pybind11::arg("A"), pybind11::arg("B"), pybind11::arg("C"),
           pybind11::arg("D") = pybind11::none(), pybind11::arg("z") = pybind11::none(),

@@ -140,12 +140,17 @@ class SelectiveScanPQFn(torch.autograd.Function):
                 return res[0], res[1]
             return res[0]
         # Training: the forward's outputs plus what the backward reads (ssi.py:123-137 saves
-        # u, delta, A, B, C, D, delta_bias, P, Q, gamma, x; out joins them when z is given).
-        out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus)
+        # u, delta, A, B, C, D, delta_bias, P, Q, gamma, x; out joins them when z is given). With
+        # dstate <= 16 the forward also writes the states before every 16-step tile (B * dim * L
+        # float32, about one float32 copy of u), which spare the backward a recompute of the scan.
+        want_ck = A.shape[1] <= 16
+        out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus,
+                                  tile_states=want_ck)
+        ck = rest.pop() if want_ck else None
         ctx.delta_softplus = delta_softplus
         ctx.has_z = z is not None
         ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, x,
-                              out if ctx.has_z else None)
+                              out if ctx.has_z else None, ck)
         last_state = x[:, :, -1, 1::2]
         result = rest[0] if ctx.has_z else out
         return result if not return_last_state else (result, last_state)
@@ -156,7 +161,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
         default ("exact") mode returns (ssi.py:152-205: its CUDA backward for u, delta, A, B, C,
         D, delta_bias and autograd through selective_scan_full_matrix_cuda for dP, dQ; with z,
         autograd through that torch loop for everything). gamma gets no gradient, as there."""
-        u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, x, out = ctx.saved_tensors
+        u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, x, out, ck = ctx.saved_tensors
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         dP = torch.zeros(P.shape, dtype=torch.float32, device=P.device)
@@ -164,7 +169,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
         du, ddelta, dA, dB, dC, dD, ddelta_bias, *rest = ext().bwd(
             u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, P=P, Q=Q, gamma=gamma, dout=dout,
             x=x, out=out, dz=None, dP_out=dP, dQ_out=dQ, delta_softplus=ctx.delta_softplus,
-            recompute_out_z=False)
+            recompute_out_z=False, tile_states=ck)
         dz = rest[0] if ctx.has_z else None
         dB = dB.squeeze(1) if getattr(ctx, "squeeze_B", False) else dB
         dC = dC.squeeze(1) if getattr(ctx, "squeeze_C", False) else dC

@@ -35,7 +35,8 @@ class ScanFwdParams(ctypes.Structure):
                 ("P", vp), ("Q", vp), ("gamma", vp), ("pq_rank", i64),
                 ("P_d_stride", i64), ("P_dstate_stride", i64), ("P_r_stride", i64),
                 ("Q_d_stride", i64), ("Q_r_stride", i64), ("Q_dstate_stride", i64),
-                ("gamma_d_stride", i64), ("gamma_dstate_stride", i64)]
+                ("gamma_d_stride", i64), ("gamma_dstate_stride", i64),
+                ("tile_states", vp)]
 
 
 class ScanBwdParams(ctypes.Structure):
@@ -66,7 +67,8 @@ class ScanBwdParams(ctypes.Structure):
                 ("Q_d_stride", i64), ("Q_r_stride", i64), ("Q_dstate_stride", i64),
                 ("dP", vp), ("dQ", vp),
                 ("dP_d_stride", i64), ("dP_dstate_stride", i64), ("dP_r_stride", i64),
-                ("dQ_d_stride", i64), ("dQ_r_stride", i64), ("dQ_dstate_stride", i64)]
+                ("dQ_d_stride", i64), ("dQ_r_stride", i64), ("dQ_dstate_stride", i64),
+                ("tile_states", vp)]
 
 
 class Conv1dFwdParams(ctypes.Structure):

@@ -19,7 +19,7 @@ def test_library_exports_every_header_function():
                           "mm_causal_conv1d_update", "mm_causal_conv1d_bwd", "mm_rms_norm_fwd"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 7
+    assert lib.mm_abi_version() == 8
 
 
 def _c_layout(struct, fields, tmp_path):

@@ -12,6 +12,7 @@ part relative to the tensor's scale as for the diagonal backward (the parameter 
 over rows and steps).
 """
 import ctypes
+import os
 import sys
 
 import pytest
@@ -238,3 +239,67 @@ def test_pq_bwd_unsupported_shapes_raise(what):
     out = selective_scan_fn(**g)
     with pytest.raises(NotImplementedError, match="P/Q backward"):
         out.backward(torch.ones_like(out))
+
+
+def test_pq_fwd_tile_states_are_the_prefix_states():
+    """fwd(..., tile_states=True) appends the state before every 16-step tile: ck[j] is the last
+    state of the scan over the first 16 j steps (tiled kernel, and the one-lane-per-row kernel that
+    a strided u selects)."""
+    _say("pq fwd tile_states")
+    from motif_mamba_amd import _native
+    for strided in (False, True):
+        case = _pq_case(800 + strided, batch=2, dim=16, L=72, N=12, R=2, dtype=torch.float32)
+        g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+        if strided:
+            wide = torch.zeros(2, 16, 75, device=DEV)
+            wide[:, :, 1:73] = g["u"]
+            g["u"] = wide[:, :, 1:73]
+        res = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"].unsqueeze(1), g["C"].unsqueeze(1), g["D"], g["z"],
+                                g["delta_bias"], g["P"], g["Q"], None, True, tile_states=True)
+        assert len(res) == 4
+        ck = res[3].cpu()
+        assert ck.shape == (5, 2, 16, 16)
+        assert float(ck[0].abs().max()) == 0.0
+        assert float(ck[:, :, :, 12:].abs().max()) == 0.0       # states past dstate
+        for j in (1, 2, 4):
+            pre = {k: (v[..., : 16 * j] if k in ("u", "delta", "z", "B", "C") else v) for k, v in case.items()}
+            _, last = selective_scan_pq_ref(**pre, return_last_state=True)
+            torch.testing.assert_close(ck[j, :, :, :12], last, rtol=1e-4, atol=1e-5)
+
+
+def test_pq_bwd_with_and_without_tile_states():
+    """The backward reading the forward's tile states equals the one recomputing them (the same
+    recurrence in the same order with 8 lanes per channel in both)."""
+    _say("pq bwd tile_states vs recompute")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _pq_case(810, batch=2, dim=64, L=200, N=16, R=2, dtype=torch.bfloat16)
+    dout = _dout(811, (2, 64, 200), torch.bfloat16).to(DEV)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    B4, C4 = g["B"].unsqueeze(1), g["C"].unsqueeze(1)
+    args = (g["u"], g["delta"], g["A"], B4, C4, g["D"], g["z"], g["delta_bias"], g["P"], g["Q"], None)
+    old = os.environ.get("MM_PQ_LPR")
+    os.environ["MM_PQ_LPR"] = "8"
+    try:
+        out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    finally:
+        if old is None:
+            os.environ.pop("MM_PQ_LPR")
+        else:
+            os.environ["MM_PQ_LPR"] = old
+    grads = []
+    for tiles in (ck, None):
+        dP, dQ = torch.zeros_like(g["P"]), torch.zeros_like(g["Q"])
+        r = ext.bwd(*args, dout, x, out, None, dP, dQ, True, False, tiles)
+        grads.append(list(r) + [dP, dQ])
+    torch.cuda.synchronize()
+    # du, ddelta, dB, dC, dz bit for bit; dA, dD, ddelta_bias, dP, dQ are float32 atomic sums, whose
+    # order (and so last bits) varies from run to run.
+    atomic = {2, 5, 6, 8, 9}
+    for i, (a, b) in enumerate(zip(*grads)):
+        tol = 1e-6 if i in atomic else 0.0
+        torch.testing.assert_close(a, b, rtol=tol, atol=tol)
+    with pytest.raises(RuntimeError, match="tile_states"):
+        ext.bwd(*args, dout, x, out, None, None, None, True, False, ck[:, :1])
+    with pytest.raises(RuntimeError, match="tile_states"):
+        ext.fwd(*args[:8], None, None, None, True, tile_states=True)
