@@ -303,3 +303,30 @@ def test_pq_bwd_with_and_without_tile_states():
         ext.bwd(*args, dout, x, out, None, None, None, True, False, ck[:, :1])
     with pytest.raises(RuntimeError, match="tile_states"):
         ext.fwd(*args[:8], None, None, None, True, tile_states=True)
+
+
+def test_pq_bwd_bench_shape_sampled_channels():
+    """The P/Q training step at the benchmark shape (pq_1p4b: 4 x 4096 x 2048, rank 2, per-channel
+    P/Q, fp16) against the exact float64 gradients of the oracle on sampled channels (independent
+    given B and C): du, ddelta, dz, dA, dD, ddelta_bias, dP and dQ of those channels."""
+    from motif_mamba_amd import selective_scan_fn
+    from motif_mamba_amd.workloads import PQ_CONFIGS, pq_inputs
+    c = PQ_CONFIGS["pq_1p4b"]
+    _say(f"pq bwd bench shape {c}")
+    case = pq_inputs(c)
+    case.pop("return_last_state")
+    dout = _dout(820, case["u"].shape, case["u"].dtype)
+    names = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias", "P", "Q"]
+    g = {k: (v.to(DEV).requires_grad_(True) if k in names else v) for k, v in case.items()}
+    out = selective_scan_fn(**g)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    chans = torch.tensor([0, 1, 2049, c.dim - 1])
+    per_ch = ("A", "D", "delta_bias", "P", "Q")
+    sub = {k: (v[:, chans] if k in ("u", "delta", "z") else v[chans] if k in per_ch else v)
+           for k, v in case.items()}
+    exact = selective_scan_pq_bwd_ref(**sub, dout=dout[:, chans])
+    for n in ("u", "delta", "z"):
+        _check(g[n].grad[:, chans.to(DEV)], exact["d" + n], torch.float16, f"bench d{n}")
+    for n in per_ch:
+        _check(g[n].grad[chans.to(DEV)], exact["d" + n], torch.float16, f"bench d{n}")
