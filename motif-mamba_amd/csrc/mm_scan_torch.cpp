@@ -334,8 +334,10 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
     // until the launch is enqueued.
     const std::vector<at::Tensor> pq_keep = attach_pq(s.p, u, P_, Q_, gamma_);
     const mm_scan_fwd_params &f = s.p;
-    const bool has_pq = f.P != nullptr;
-    TORCH_CHECK(has_pq || (!dP_out_.has_value() && !dQ_out_.has_value()), "dP_out and dQ_out need P and Q");
+    // Rank-0 P/Q couple nothing: their forward is the diagonal scan and so is the backward (dP and
+    // dQ are empty).
+    const bool has_pq = P_.has_value() && f.pq_rank > 0;
+    TORCH_CHECK(P_.has_value() || (!dP_out_.has_value() && !dQ_out_.has_value()), "dP_out and dQ_out need P and Q");
     (void)pq_keep;
     TORCH_CHECK(dout.scalar_type() == u.scalar_type());
     TORCH_CHECK(dout.is_cuda());

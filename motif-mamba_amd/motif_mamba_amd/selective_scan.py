@@ -143,7 +143,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
         # u, delta, A, B, C, D, delta_bias, P, Q, gamma, x; out joins them when z is given). With
         # dstate <= 16 the forward also writes the states before every 16-step tile (B * dim * L
         # float32, about one float32 copy of u), which spare the backward a recompute of the scan.
-        want_ck = A.shape[1] <= 16
+        want_ck = A.shape[1] <= 16 and P.shape[-1] > 0
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus,
                                   tile_states=want_ck)
         ck = rest.pop() if want_ck else None

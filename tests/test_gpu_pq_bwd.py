@@ -330,3 +330,23 @@ def test_pq_bwd_bench_shape_sampled_channels():
         _check(g[n].grad[:, chans.to(DEV)], exact["d" + n], torch.float16, f"bench d{n}")
     for n in per_ch:
         _check(g[n].grad[chans.to(DEV)], exact["d" + n], torch.float16, f"bench d{n}")
+
+
+def test_pq_bwd_rank_zero_is_the_diagonal_backward():
+    """P/Q of rank 0 couple nothing: every gradient is the diagonal scan's, dP and dQ are empty."""
+    _say("pq bwd rank 0")
+    case = _pq_case(830, batch=2, dim=32, L=64, N=16, R=1, dtype=torch.float32)
+    case["P"] = case["P"][..., :0].contiguous()
+    case["Q"] = case["Q"][:, :0, :].contiguous()
+    dout = _dout(831, (2, 32, 64), torch.float32)
+    from motif_mamba_amd import selective_scan_fn
+    g = {k: (v.to(DEV).requires_grad_(True) if torch.is_tensor(v) else v) for k, v in case.items()}
+    out = selective_scan_fn(**g)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    from oracle.ssm_ref import selective_scan_bwd_ref
+    kw = {k: v for k, v in case.items() if k not in ("P", "Q")}
+    exact = selective_scan_bwd_ref(**kw, dout=dout, dtype=torch.float64)
+    for n in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"):
+        _check(g[n].grad, exact["d" + n], torch.float32, f"rank0 d{n}")
+    assert g["P"].grad.shape == (32, 16, 0) and g["Q"].grad.shape == (32, 0, 16)
