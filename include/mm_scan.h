@@ -209,7 +209,7 @@ typedef struct mm_scan_bwd_params {
      * (selective_scan_interface.py:262-350), the reference's path for P/Q calls with z -- with the
      * state adjoint running through the transposed transition matrix exp(delta' A) + delta' P Q,
      * plus dP and dQ (float32, the shapes of P and Q; overwritten: the call clears them first).
-     * Supported: variable B and C, dstate <= 16, pq_rank 1..4, dim and dim / n_groups multiples of
+     * Supported: variable B and C, dstate <= 16, pq_rank 1..8, dim and dim / n_groups multiples of
      * 16, seqlen a multiple of 8; other requests return MM_ERR_UNSUPPORTED. */
     const float *P;
     const float *Q;

@@ -485,7 +485,7 @@ int validate_bwd(const mm_scan_bwd_params *p) {
     if (p->P && (p->pq_rank < 1 || p->pq_rank > 8))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: pq_rank must be in [1, 8] (got %lld)", (long long)p->pq_rank);
     if (p->P && !mm::pq_bwd_ok(*p))
-        return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, pq_rank <= 4, "
+        return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, "
                                         "dim and dim / n_groups multiples of 16 and seqlen a multiple of 8");
     if (p->tile_states && !p->P)
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: tile_states are read only with P/Q");

@@ -416,11 +416,11 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 
 }  // namespace pqbwd
 
-// The P/Q backward's shape conditions: variable B/C, dstate <= 16, rank 1..4, 16-channel blocks
+// The P/Q backward's shape conditions: variable B/C, dstate <= 16, rank 1..8, 16-channel blocks
 // inside one group, L a multiple of 8.
 bool pq_bwd_ok(const mm_scan_bwd_params &p) {
     return p.is_variable_B && p.is_variable_C && p.dstate >= 1 && p.dstate <= 16 && p.pq_rank >= 1 &&
-           p.pq_rank <= 4 && p.dim % 16 == 0 && (p.dim / p.n_groups) % 16 == 0 && p.seqlen >= 8 &&
+           p.pq_rank <= 8 && p.dim % 16 == 0 && (p.dim / p.n_groups) % 16 == 0 && p.seqlen >= 8 &&
            p.seqlen % 8 == 0 && p.batch <= 65535;
 }
 
@@ -431,8 +431,10 @@ static int launch_pq_bwd_s(const mm_scan_bwd_params &p, hipStream_t s, float *ck
     dim3 block(16 * (16 / S));
     if (p.pq_rank <= 2)
         hipLaunchKernelGGL((pqbwd::scan_bwd_pq16<T, S, 2>), grid, block, 0, s, p, ratio, ck, partB, partC);
-    else
+    else if (p.pq_rank <= 4)
         hipLaunchKernelGGL((pqbwd::scan_bwd_pq16<T, S, 4>), grid, block, 0, s, p, ratio, ck, partB, partC);
+    else
+        hipLaunchKernelGGL((pqbwd::scan_bwd_pq16<T, S, 8>), grid, block, 0, s, p, ratio, ck, partB, partC);
     return launch_status("scan_bwd_pq16");
 }
 

@@ -318,7 +318,7 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
 // selective_scan_cuda.bwd (selective_scan.cpp:415-612): [du, ddelta, dA, dB, dC, dD, ddelta_bias,
 // dz?, out_z?]. x (the forward's chunk states) is checked like the reference but not read: the
 // backward recomputes the forward states itself. With P/Q the exact gradient of the coupled
-// recurrence runs (pq_rank 1..4, dstate <= 16, dim and dim / n_groups multiples of 16; other
+// recurrence runs (pq_rank 1..8, dstate <= 16, dim and dim / n_groups multiples of 16; other
 // P/Q shapes raise).
 std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A, const at::Tensor &B,
                             const at::Tensor &C, const c10::optional<at::Tensor> &D_,

@@ -24,9 +24,9 @@ C, D, [z], delta_bias, x, [out]); without, it writes only what it returns.
 ``SelectiveScanPQFn.backward`` returns the exact gradients of the coupled recurrence (dP and dQ
 included), which is what the reference returns in its default gradient mode: its dense CUDA
 backward (z-less calls) and autograd through its torch loop (calls with z, and dP/dQ always) both
-differentiate the same function. The gfx950 kernel covers pq_rank 1..4, dstate <= 16, dim and
+differentiate the same function. The gfx950 kernel covers pq_rank 1..8, dstate <= 16, dim and
 dim / n_groups multiples of 16 and seqlen a multiple of 8, with variable B and C; other P/Q
-shapes raise NotImplementedError in the backward (the forward covers pq_rank up to 8).
+shapes raise NotImplementedError in the backward.
 
 Differences (all raise instead of computing something else): complex A, and the P/Q backward
 outside the shapes above, are not part of this build.

@@ -78,7 +78,7 @@ def test_pq_bwd_dtypes(dtype, per_dim):
     _vs_exact(case, _dout(701, (2, 32, 136), dtype), dtype, f"{dtype}")
 
 
-@pytest.mark.parametrize("R", [1, 3, 4])
+@pytest.mark.parametrize("R", [1, 3, 4, 5, 8])
 def test_pq_bwd_ranks(R):
     _say(f"pq bwd rank {R}")
     case = _pq_case(710 + R, batch=2, dim=32, L=64, N=16, R=R, dtype=torch.float32)
@@ -211,23 +211,25 @@ def test_pq_bwd_c_abi_direct():
     for name, t in (("du", du), ("ddelta", ddelta), ("dz", dz), ("dA", dA), ("dB", dB.squeeze(1)),
                     ("dC", dC.squeeze(1)), ("dD", dD), ("ddelta_bias", dbias), ("dP", dP), ("dQ", dQ)):
         _check(t, exact[name], torch.float32, f"capi {name}")
-    # A rank the kernels do not cover: MM_ERR_UNSUPPORTED with a message, nothing launched.
-    p.pq_rank = 5
-    assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_UNSUPPORTED
+    # Refusals, nothing launched: a rank past the reference's limit of 8 (invalid), a length the
+    # kernel does not cover (unsupported), missing dP.
+    p.pq_rank = 9
+    assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_INVALID_ARGUMENT
     assert b"pq_rank" in lib.mm_last_error()
-    p.pq_rank, p.dP = 3, None
+    p.pq_rank, p.seqlen = 3, 92
+    assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_UNSUPPORTED
+    assert b"P/Q backward" in lib.mm_last_error()
+    p.seqlen, p.dP = 96, None
     assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_INVALID_ARGUMENT
 
 
-@pytest.mark.parametrize("what", ["rank5", "dstate32", "L12", "constB"])
+@pytest.mark.parametrize("what", ["dstate32", "L12", "constB"])
 def test_pq_bwd_unsupported_shapes_raise(what):
     """Shapes outside the kernel raise NotImplementedError in the backward; the forward runs."""
     _say(f"pq bwd unsupported {what}")
     from motif_mamba_amd import selective_scan_fn
     kw = dict(batch=1, dim=16, L=32, N=16, R=2, dtype=torch.float32)
-    if what == "rank5":
-        kw["R"] = 5
-    elif what == "dstate32":
+    if what == "dstate32":
         kw["N"] = 32
     elif what == "L12":
         kw["L"] = 12
