@@ -15,7 +15,9 @@
  *
  *   mm_scan_bwd      replaces `selective_scan_cuda.bwd(u, delta, A, B, C, D, z, delta_bias, P, Q,
  *                    gamma, dout, x, out, dz, dP_out, dQ_out, delta_softplus, recompute_out_z)`
- *                    (selective_scan.cpp:415-612, pybind :628-637) for real A without P/Q.
+ *                    (selective_scan.cpp:415-612, pybind :628-637) for real A, with the exact
+ *                    gradients of the P/Q coupling (dense kernel selective_scan_bwd_kernel.cuh:
+ *                    166-345; autograd through selective_scan_interface.py:262-350 for dP/dQ).
  *
  *   mm_state_update  replaces `selective_state_update(state, x, dt, A, B, C, D, z, dt_bias,
  *                    dt_softplus)` as called at mamba_ssm/modules/mamba_simplemotif.py:397-399
@@ -205,9 +207,9 @@ typedef struct mm_scan_bwd_params {
      * P_d (dstate, pq_rank), Q_d (pq_rank, dstate), float32, d strides 0 for a pair shared by all
      * channels), the gradients are those of the coupled recurrence
      *   h_t = exp(delta'_t A) h_{t-1} + delta'_t P (Q h_{t-1}) + delta'_t u_t B_t
-     * -- what torch autograd takes through selective_scan_full_matrix_cuda
-     * (selective_scan_interface.py:262-350), the reference's path for P/Q calls with z -- with the
-     * state adjoint running through the transposed transition matrix exp(delta' A) + delta' P Q,
+     * -- what the reference's dense backward kernel (selective_scan_bwd_kernel.cuh:166-345) and
+     * torch autograd through selective_scan_full_matrix_cuda (selective_scan_interface.py:262-350,
+     * its path for P/Q calls with z and for dP/dQ) both compute -- with the state adjoint running through the transposed transition matrix exp(delta' A) + delta' P Q,
      * plus dP and dQ (float32, the shapes of P and Q; overwritten: the call clears them first).
      * Supported: variable B and C, dstate <= 16, pq_rank 1..8, dim and dim / n_groups multiples of
      * 16, seqlen a multiple of 8; other requests return MM_ERR_UNSUPPORTED. */
