@@ -201,8 +201,10 @@ def bench_pq_train(name, steps, warmup, torch):
 
 
 def bench_train(cfg_name, steps, warmup, torch):
-    """Forward in training mode (pre-gate out and chunk states saved, ssi.py:47-61) and the backward
-    (selective_scan_cuda.bwd equivalent) on one configuration: times of each and of the pair."""
+    """Forward in training mode (pre-gate out and chunk states saved, ssi.py:47-61, plus the 16-step
+    tile states SelectiveScanFn keeps) and the backward (selective_scan_cuda.bwd equivalent, reading
+    those tile states) on one configuration: times of each and of the pair, and of the backward that
+    recomputes the tile states itself."""
     from motif_mamba_amd import _native
     from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_inputs
     ext = _native.ext()
@@ -211,27 +213,33 @@ def bench_train(cfg_name, steps, warmup, torch):
     B = t["B"].unsqueeze(1) if t["B"].dim() == 3 else t["B"]
     C = t["C"].unsqueeze(1) if t["C"].dim() == 3 else t["C"]
     args = (t["u"], t["delta"], t["A"], B, C, t["D"], t["z"], t["delta_bias"], None, None, None, True)
-    out, x, out_z = ext.fwd(*args)
+    out, x, out_z, ck = ext.fwd(*args, tile_states=True)
+    ck_ok = ck is not None
     dout = torch.randn(out_z.shape, device="cuda", generator=torch.Generator(device="cuda").manual_seed(7)).to(out_z.dtype)
 
     def fwd(i):
-        ext.fwd(*args)
+        ext.fwd(*args, tile_states=True)
 
     def bwd(i):
-        ext.bwd(*args[:11], dout, x, out, None, None, None, True, False)
+        ext.bwd(*args[:11], dout, x, out, None, None, None, True, False, ck)
 
     def both(i):
-        o, xx, oz = ext.fwd(*args)
-        ext.bwd(*args[:11], dout, xx, o, None, None, None, True, False)
+        o, xx, oz, cc = ext.fwd(*args, tile_states=True)
+        ext.bwd(*args[:11], dout, xx, o, None, None, None, True, False, cc)
+
+    def bwd_self(i):                   # without the forward's tile states: the backward recomputes them
+        ext.bwd(*args[:11], dout, x, out, None, None, None, True, False)
 
     f_ms = _time_loop(fwd, steps, warmup, torch)
     b_ms = _time_loop(bwd, steps, warmup, torch)
     s_ms = _time_loop(both, steps, warmup, torch)
+    bs_ms = _time_loop(bwd_self, steps, warmup, torch)
     elems = c.batch * c.dim * c.seqlen
-    del t, out, x, out_z, dout
+    del t, out, x, out_z, dout, ck
     torch.cuda.empty_cache()
     return {"shape": [c.batch, c.dim, c.seqlen, c.dstate], "dtype": c.dtype, "fwd_train_ms": f_ms, "bwd_ms": b_ms,
-            "fwd_bwd_ms": s_ms, "elements_per_s": elems / (s_ms * 1e-3)}
+            "fwd_bwd_ms": s_ms, "bwd_recompute_ms": bs_ms, "tile_states": ck_ok,
+            "elements_per_s": elems / (s_ms * 1e-3)}
 
 
 def bench_conv(cfg_name, steps, warmup, torch):

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 8
+#define MM_SCAN_ABI_VERSION 9
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -132,11 +132,13 @@ typedef struct mm_scan_fwd_params {
     int64_t Q_d_stride, Q_r_stride, Q_dstate_stride;
     int64_t gamma_d_stride, gamma_dstate_stride;
 
-    /* Checkpoints for the P/Q backward (ABI version 8; no counterpart in the reference, whose
-     * backward keeps only `chunk_states`). When non-NULL (P/Q set, dstate <= 16): the state before
-     * every 16-step tile, float32 [ceil(seqlen / 16)][batch][dim][16], states past dstate written
-     * as 0 -- B * dim * seqlen * 4 bytes, about one float32 copy of u. Passed to mm_scan_bwd as
-     * `tile_states`, they spare it the recompute of the whole forward. NULL: not written. */
+    /* Checkpoints for the backward (ABI version 8, 9 without P/Q; no counterpart in the reference,
+     * whose backward keeps only `chunk_states`). When non-NULL: the state before every 16-step
+     * tile, float32 [ceil(seqlen / 16)][batch][dim][16], states past dstate written as 0 --
+     * B * dim * seqlen * 4 bytes, about one float32 copy of u. Passed to mm_scan_bwd as
+     * `tile_states`, they spare it the recompute of the whole forward. Written with P/Q and
+     * dstate <= 16, and without P/Q by the dstate-16 kernels (mm_scan_fwd_tile_states_size() is
+     * non-zero exactly when this request can write them). NULL: not written. */
     float *tile_states;
 } mm_scan_fwd_params;
 
@@ -223,9 +225,10 @@ typedef struct mm_scan_bwd_params {
     int64_t dP_d_stride, dP_dstate_stride, dP_r_stride;
     int64_t dQ_d_stride, dQ_r_stride, dQ_dstate_stride;
 
-    /* Optional with P/Q (ABI version 8): the `tile_states` mm_scan_fwd wrote for the same inputs;
-     * the backward then reads its checkpoints there instead of recomputing them (and needs a
-     * smaller workspace). The contents are trusted: stale states give wrong gradients. */
+    /* Optional (ABI version 8, 9 without P/Q): the `tile_states` mm_scan_fwd wrote for the same
+     * inputs; the P/Q backward and the dstate-16 backward then read their checkpoints there
+     * instead of recomputing them (and need a smaller workspace); the general backward ignores
+     * them. The contents are trusted: stale states give wrong gradients. */
     const float *tile_states;
 } mm_scan_bwd_params;
 
@@ -269,6 +272,10 @@ int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream);
  * returns 0 for a request mm_scan_fwd would reject. No counterpart in the reference (its forward
  * allocates nothing beyond the outputs, selective_scan.cpp:383-389). */
 int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params);
+
+/* Bytes of `tile_states` mm_scan_fwd writes for this request, 0 when it cannot write them (no
+ * counterpart in the reference: the checkpoints the backward would otherwise recompute). */
+int64_t mm_scan_fwd_tile_states_size(const mm_scan_fwd_params *params);
 
 /* Backward scan. Replaces selective_scan_cuda.bwd (selective_scan.cpp:415-612, pybind :628-637). */
 int mm_scan_bwd(const mm_scan_bwd_params *params, void *stream);

@@ -25,6 +25,7 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream);
 // Number of sequence segments the dstate-16 kernels use for `p` (1: a single pass), and the
 // workspace bytes that takes (mm_scan_tiled.hip).
 int64_t segment_count(const mm_scan_fwd_params &p);
+bool tile_states_ok(const mm_scan_fwd_params &p);
 int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg);
 
 // Forward scan with the low-rank P/Q coupling (mm_scan_pq.hip): the tiled kernel when the request

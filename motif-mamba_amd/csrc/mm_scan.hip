@@ -419,8 +419,12 @@ int validate_fwd(const mm_scan_fwd_params *p) {
     if (p->P && (p->pq_rank < 0 || p->pq_rank > 8))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: pq_rank must be in [0, 8] (got %lld)",
                     (long long)p->pq_rank);
-    if (p->tile_states && (!p->P || p->dstate > 16))
-        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: tile_states are written only with P/Q and dstate <= 16");
+    if (p->tile_states && p->dstate > 16)
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: tile_states need dstate <= 16");
+    if (p->tile_states && !p->P && !mm::tile_states_ok(*p))
+        return fail(MM_ERR_UNSUPPORTED, "mm_scan_fwd: without P/Q, tile_states are written by the dstate-16 kernels "
+                                        "(variable B/C, dim and dim / n_groups multiples of 16, L a multiple of 8, "
+                                        "aligned rows); mm_scan_fwd_tile_states_size tells");
     return MM_OK;
 }
 
@@ -450,7 +454,7 @@ template <typename T>
 int dispatch_fwd(const mm_scan_fwd_params &p, hipStream_t s) {
     if (p.P) return mm::launch_pq<T>(p, s);
     int rc = mm::try_launch_tiled<T>(p, s);
-    if (rc != MM_ERR_UNSUPPORTED) return rc;
+    if (rc != MM_ERR_UNSUPPORTED || p.tile_states) return rc;   // the general kernel writes no tile states
     return launch_rowlane<T>(p, s);
 }
 
@@ -487,8 +491,7 @@ int validate_bwd(const mm_scan_bwd_params *p) {
     if (p->P && !mm::pq_bwd_ok(*p))
         return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, "
                                         "dim and dim / n_groups multiples of 16 and seqlen a multiple of 8");
-    if (p->tile_states && !p->P)
-        return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: tile_states are read only with P/Q");
+
     const int64_t need = mm::bwd_workspace_bytes(*p);
     if (p->seqlen > 0 && (!p->workspace || p->workspace_bytes < need || reinterpret_cast<uintptr_t>(p->workspace) % 16))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: needs a 16-byte aligned workspace of %lld bytes (got %lld)",
@@ -602,6 +605,15 @@ int64_t mm_scan_bwd_workspace_size(const mm_scan_bwd_params *params) {
         params->dstate > MM_SCAN_MAX_DSTATE)
         return 0;
     return mm::bwd_workspace_bytes(*params);
+}
+
+int64_t mm_scan_fwd_tile_states_size(const mm_scan_fwd_params *params) {
+    if (!params || params->batch < 0 || params->dim < 0 || params->seqlen < 0 || params->dstate < 1 ||
+        params->dstate > 16 || params->n_groups < 1 || (params->dim > 0 && params->dim % params->n_groups))
+        return 0;
+    const mm_scan_fwd_params &p = *params;
+    if (!p.P && !mm::tile_states_ok(p)) return 0;
+    return ((p.seqlen + 15) / 16) * p.batch * p.dim * 16 * int64_t(sizeof(float));
 }
 
 int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params) {

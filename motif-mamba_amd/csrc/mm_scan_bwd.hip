@@ -385,10 +385,11 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
         for (int i = 0; i < 4; ++i) sBC[buf][(4 * st_q + i) * 36 + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
     };
 
-    // Pass 1: the states before every tile, into the checkpoint workspace.
+    // Pass 1: the states before every tile, into the checkpoint workspace (skipped when the
+    // forward wrote them: ws.ck then points at its tile_states).
     float h0 = 0.f, h1 = 0.f;
     TileRaw<T> nxt = load(0, false);
-    for (int64_t j = 0; j < n_tiles; ++j) {
+    for (int64_t j = 0; j < (p.tile_states ? 0 : n_tiles); ++j) {
         const int buf = int(j % kBufs);
         *reinterpret_cast<float2 *>(ckp + j * ck_tile) = make_float2(h0, h1);
         commit(nxt, j, buf, false);
@@ -607,7 +608,10 @@ int64_t fast_part_floats(const mm_scan_bwd_params &p) {
 template <typename T>
 int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
     float *ws = static_cast<float *>(p.workspace);
-    const FastWs fw{ws, ws + fast_ck_floats(p), ws + fast_ck_floats(p) + fast_part_floats(p)};
+    const bool own_ck = p.tile_states == nullptr;
+    float *ck = own_ck ? ws : const_cast<float *>(p.tile_states);
+    float *partB = own_ck ? ws + fast_ck_floats(p) : ws;
+    const FastWs fw{ck, partB, partB + fast_part_floats(p)};
     const int64_t ratio = p.dim / p.n_groups;
     dim3 grid(unsigned(p.dim / 16), unsigned(p.batch));
     hipLaunchKernelGGL((scan_bwd_tiled16<T>), grid, dim3(128), 0, s, p, ratio, fw);
@@ -650,7 +654,7 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
-    if (p.P && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
+    if ((p.P || bwd::fast_ok(p)) && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
     return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));

@@ -484,8 +484,18 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
                 }
             }
         }
+        // The state after this tile = the checkpoint before the next one, for the backward.
+        if (MODE == 0 && p.tile_states && t0 + kT1 < L) {
+            float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + r * K;
+#pragma unroll
+            for (int k = 0; k < K; ++k) ck[k] = h[k];
+        }
     };
 
+    if (MODE == 0 && p.tile_states) {    // the checkpoint before the first tile: zero
+#pragma unroll
+        for (int k = 0; k < K; ++k) p.tile_states[(b * p.dim + d0 + c) * 16 + r * K + k] = 0.f;
+    }
     PairData<T, K> ring[PF];
 #pragma unroll
     for (int s = 0; s < PF; ++s) load_pair(pb + s, ring[s]);
@@ -820,10 +830,17 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
                 csp[3] = h[1];
             }
         }
+        // The state after this tile = the checkpoint before the next one, for the backward.
+        if (p.tile_states && t0 + kT1 < L) {
+            float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + 2 * r;
+            *reinterpret_cast<float2 *>(ck) = make_float2(h[0], h[1]);
+        }
     };
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
+    if (p.tile_states)                     // the checkpoint before the first tile: zero
+        *reinterpret_cast<float2 *>(p.tile_states + (b * p.dim + d0 + c) * 16 + 2 * r) = make_float2(0.f, 0.f);
     K2Data<T> ring[PF];
     {
         RawVec<T, E> u0, d0v, z0;
@@ -971,7 +988,7 @@ static bool pipe_offsets_ok(const mm_scan_fwd_params &p) {
 // (two waves per group): enough segments for ~3 waves per SIMD, each at least 512 steps. The
 // segmented scan does ~1.75x the work of one pass, which pays only at such low occupancy.
 int64_t segment_count(const mm_scan_fwd_params &p) {
-    if (!tiled_shape_ok(p) || !pipe_offsets_ok(p)) return 1;
+    if (!tiled_shape_ok(p) || !pipe_offsets_ok(p) || p.tile_states) return 1;
     const int64_t waves = 2 * p.batch * (p.dim / tiled::kCh);
     if (waves >= 1024) return 1;
     const int64_t n_pairs = (p.seqlen + 2 * tiled::kT1 - 1) / (2 * tiled::kT1);
@@ -990,6 +1007,12 @@ template <typename T>
 int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (!tiled_shape_ok(p) || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
     const bool pipe_ok = pipe_offsets_ok(p);
+    if (p.tile_states) {
+        // The backward's checkpoints are written by the default kernels only (one pass, no segments).
+        if (!pipe_ok) return MM_ERR_UNSUPPORTED;
+        if constexpr (std::is_same_v<T, float>) return launch_pipe_pf<T, 2>(p, stream);
+        else return tiled::launch_k2i<T, 2>(p, stream);
+    }
     const int64_t n_seg = pipe_ok ? segment_count(p) : 1;
     if (n_seg > 1 && p.workspace && p.workspace_bytes >= segment_workspace_bytes(p, n_seg) &&
         (reinterpret_cast<uintptr_t>(p.workspace) & 15u) == 0) {
@@ -1011,6 +1034,11 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
             if constexpr (std::is_same_v<T, float>) return launch_pipe_pf<T, 2>(p, stream);
             else return tiled::launch_k2i<T, 2>(p, stream);
     }
+}
+
+// Whether the diagonal forward can write tile_states for this request (the kernels above).
+bool tile_states_ok(const mm_scan_fwd_params &p) {
+    return tiled_shape_ok(p) && fwd_vector_ok(&p) && pipe_offsets_ok(p);
 }
 
 template int try_launch_tiled<float>(const mm_scan_fwd_params &, hipStream_t);

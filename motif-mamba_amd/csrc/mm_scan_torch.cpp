@@ -257,14 +257,6 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     mm_scan_fwd_params &p = s.p;
     const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
-    // tile_states (this build's addition, P/Q and dstate <= 16): the states before every 16-step
-    // tile, appended to the outputs for the backward.
-    at::Tensor ck;
-    if (tile_states) {
-        TORCH_CHECK(p.P != nullptr && p.dstate <= 16, "tile_states need P/Q and dstate <= 16");
-        ck = torch::empty({(p.seqlen + 15) / 16, p.batch, p.dim, 16}, u.options().dtype(at::ScalarType::Float));
-        p.tile_states = ck.data_ptr<float>();
-    }
     // Output layouts follow the reference: out like delta, out_z like z (like out when z is a
     // non-dense view such as half of xz), x contiguous.
     at::Tensor out = torch::empty_like(delta);
@@ -276,6 +268,14 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
         set_out_z(p, out_z);
     }
     p.chunk_states = x.data_ptr<float>();
+    // tile_states (this build's addition): the states before every 16-step tile, appended to the
+    // outputs for the backward -- None when the kernels cannot write them for this request (the
+    // query sees the final parameter block, outputs included).
+    at::Tensor ck;
+    if (tile_states && mm_scan_fwd_tile_states_size(&p) > 0) {
+        ck = torch::empty({(p.seqlen + 15) / 16, p.batch, p.dim, 16}, u.options().dtype(at::ScalarType::Float));
+        p.tile_states = ck.data_ptr<float>();
+    }
     const c10::DeviceGuard device_guard{u.device()};
     const at::Tensor ws = attach_workspace(p, u);
     check_rc(mm_scan_fwd(&p, c10::hip::getCurrentHIPStream().stream()), "mm_scan_fwd");
@@ -452,7 +452,6 @@ std::vector<at::Tensor> bwd(const at::Tensor &u, const at::Tensor &delta, const 
     }
     if (tile_states_.has_value()) {
         const at::Tensor &ck = tile_states_.value();
-        TORCH_CHECK(has_pq, "tile_states are read only with P/Q");
         TORCH_CHECK(ck.is_cuda() && ck.scalar_type() == at::ScalarType::Float && ck.is_contiguous() &&
                         ck.sizes() == at::IntArrayRef({(f.seqlen + 15) / 16, f.batch, f.dim, 16}),
                     "tile_states must be the contiguous float32 (ceil(L / 16), batch, dim, 16) tensor of the forward");

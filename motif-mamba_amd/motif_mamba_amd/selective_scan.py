@@ -33,10 +33,19 @@ outside the shapes above, are not part of this build.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 from einops import rearrange
 
 from ._native import ext
+
+
+def _save_tile_states():
+    """Whether training forwards keep the 16-step tile states for the backward (default on;
+    MM_TILE_STATES=0 trades the B * dim * L float32 of saved activations for the backward's recompute
+    of the scan)."""
+    return os.environ.get("MM_TILE_STATES", "1") != "0"
 
 
 class SelectiveScanFn(torch.autograd.Function):
@@ -69,15 +78,20 @@ class SelectiveScanFn(torch.autograd.Function):
             if return_last_state:
                 return res[0], res[1]
             return res[0]
-        # Training: the reference's outputs and saved tensors (ssi.py:47-61).
-        out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, None, None, None, delta_softplus)
+        # Training: the reference's outputs and saved tensors (ssi.py:47-61), plus, for dstate 16,
+        # the states before every 16-step tile (None where the kernels do not write them), which
+        # spare the backward its recompute of the scan.
+        want_ck = A.shape[1] == 16 and _save_tile_states()
+        out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, None, None, None, delta_softplus,
+                                  tile_states=want_ck)
+        ck = rest.pop() if want_ck else None
         ctx.delta_softplus = delta_softplus
         ctx.has_z = z is not None
         last_state = x[:, :, -1, 1::2]
         if not ctx.has_z:
-            ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, x)
+            ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, x, ck)
             return out if not return_last_state else (out, last_state)
-        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, x, out)
+        ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, x, out, ck)
         out_z = rest[0]
         return out_z if not return_last_state else (out_z, last_state)
 
@@ -85,16 +99,16 @@ class SelectiveScanFn(torch.autograd.Function):
     def backward(ctx, dout, *args):
         """ssi.py:63-91: the gradient of last_state is not propagated, as in the reference."""
         if not ctx.has_z:
-            u, delta, A, B, C, D, delta_bias, x = ctx.saved_tensors
+            u, delta, A, B, C, D, delta_bias, x, ck = ctx.saved_tensors
             z = None
             out = None
         else:
-            u, delta, A, B, C, D, z, delta_bias, x, out = ctx.saved_tensors
+            u, delta, A, B, C, D, z, delta_bias, x, out, ck = ctx.saved_tensors
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
         du, ddelta, dA, dB, dC, dD, ddelta_bias, *rest = ext().bwd(
             u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, dout=dout, x=x, out=out, dz=None,
-            delta_softplus=ctx.delta_softplus, recompute_out_z=False)
+            delta_softplus=ctx.delta_softplus, recompute_out_z=False, tile_states=ck)
         dz = rest[0] if ctx.has_z else None
         dB = dB.squeeze(1) if getattr(ctx, "squeeze_B", False) else dB
         dC = dC.squeeze(1) if getattr(ctx, "squeeze_C", False) else dC
@@ -143,7 +157,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
         # u, delta, A, B, C, D, delta_bias, P, Q, gamma, x; out joins them when z is given). With
         # dstate <= 16 the forward also writes the states before every 16-step tile (B * dim * L
         # float32, about one float32 copy of u), which spare the backward a recompute of the scan.
-        want_ck = A.shape[1] <= 16 and P.shape[-1] > 0
+        want_ck = A.shape[1] <= 16 and P.shape[-1] > 0 and _save_tile_states()
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus,
                                   tile_states=want_ck)
         ck = rest.pop() if want_ck else None

@@ -138,6 +138,8 @@ def load():
     lib.mm_state_update.restype = ctypes.c_int
     lib.mm_scan_fwd_workspace_size.argtypes = [ctypes.POINTER(ScanFwdParams)]
     lib.mm_scan_fwd_workspace_size.restype = ctypes.c_int64
+    lib.mm_scan_fwd_tile_states_size.argtypes = [ctypes.POINTER(ScanFwdParams)]
+    lib.mm_scan_fwd_tile_states_size.restype = ctypes.c_int64
     lib.mm_scan_bwd.argtypes = [ctypes.POINTER(ScanBwdParams), vp]
     lib.mm_scan_bwd.restype = ctypes.c_int
     lib.mm_scan_bwd_workspace_size.argtypes = [ctypes.POINTER(ScanBwdParams)]

@@ -14,12 +14,13 @@ from tests import capi
 def test_library_exports_every_header_function():
     lib = capi.load()
     names = capi.header_functions()
-    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_scan_bwd", "mm_scan_bwd_workspace_size",
+    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_scan_fwd_tile_states_size",
+                          "mm_scan_bwd", "mm_scan_bwd_workspace_size",
                           "mm_state_update", "mm_last_error", "mm_abi_version", "mm_causal_conv1d_fwd",
                           "mm_causal_conv1d_update", "mm_causal_conv1d_bwd", "mm_rms_norm_fwd"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 8
+    assert lib.mm_abi_version() == 9
 
 
 def _c_layout(struct, fields, tmp_path):

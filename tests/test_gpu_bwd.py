@@ -258,3 +258,40 @@ def test_bwd_full_size_sampled_channels(cfg):
         _check(g[n].grad[:, chans.to(DEV)], exact[GRAD[n]], torch.bfloat16, f"{cfg} {GRAD[n]}")
     for n in ("A", "D", "delta_bias"):
         _check(g[n].grad[chans.to(DEV)], exact[GRAD[n]], torch.bfloat16, f"{cfg} {GRAD[n]}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_bwd_tile_states(dtype):
+    """fwd(..., tile_states=True) on the dstate-16 kernels appends the state before every 16-step
+    tile (ck[j] = the last state of the scan over the first 16 j steps); the backward reading them
+    equals the one recomputing them."""
+    _say(f"bwd tile states {dtype}")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(690, 2, 32, 200, 16, dtype, bkind="4d", G=1)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+    out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    assert ck is not None and ck.shape == (13, 2, 32, 16)
+    ckc = ck.cpu()
+    assert float(ckc[0].abs().max()) == 0.0
+    for j in (1, 5, 12):
+        pre = {k: (v[..., : 16 * j] if k in ("u", "delta", "z", "B", "C") else v) for k, v in case.items()}
+        _, last = selective_scan_ref(**pre, return_last_state=True)
+        torch.testing.assert_close(ckc[j], last, rtol=1e-4 if dtype == torch.float32 else 1e-3,
+                                   atol=1e-5 if dtype == torch.float32 else 1e-4)
+    dout = _dout(691, (2, 32, 200), dtype).to(DEV)
+    a = ext.bwd(*args, dout, x, out, None, None, None, True, False, ck)
+    b = ext.bwd(*args, dout, x, out, None, None, None, True, False)
+    torch.cuda.synchronize()
+    atomic = {2, 5, 6}                 # dA, dD, ddelta_bias: float32 atomic sums
+    for i, (ta, tb) in enumerate(zip(a, b)):
+        tol = 1e-6 if i in atomic else 0.0
+        torch.testing.assert_close(ta, tb, rtol=tol, atol=tol)
+    # A request the dstate-16 kernels do not take (dstate 8): no tile states, and training still runs.
+    c8 = _case(692, 1, 16, 64, 8, dtype)
+    g8 = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in c8.items()}
+    B8, C8 = g8["B"].unsqueeze(1), g8["C"].unsqueeze(1)
+    res = ext.fwd(g8["u"], g8["delta"], g8["A"], B8, C8, g8["D"], g8["z"], g8["delta_bias"], None, None, None, True,
+                  tile_states=True)
+    assert res[-1] is None
