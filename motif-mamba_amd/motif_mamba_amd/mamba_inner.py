@@ -25,7 +25,8 @@ views or GEMM outputs in it, so every projection is a single 2-D GEMM and no act
 transposed in memory (the reference transposes conv1d_out, B, C and out_z through (b l, d) copies).
 
 Checkpointing as the reference: ``checkpoint_lvl=1`` keeps neither conv1d_out nor delta and
-recomputes both in the backward; ``0`` keeps them. Autocast: the projection weights are cast to
+recomputes both in the backward; ``0`` keeps them, and with dstate 16 also the scan's 16-step tile
+states, so that the scan backward need not recompute them (``MM_TILE_STATES=0`` turns that off). Autocast: the projection weights are cast to
 the autocast dtype as the reference does (ssi.py:469-474).
 
 Not provided (raise, as for the other parts of this build): the backward when RMSNorm weights are
@@ -40,6 +41,7 @@ import torch
 import torch.nn.functional as F
 
 from ._native import ext
+from .selective_scan import _save_tile_states
 
 
 def _cm_empty(batch, ch, L, like, dtype=None):
@@ -139,8 +141,12 @@ class MambaInnerFn(torch.autograd.Function):
                                     delta_softplus=delta_softplus, return_last_state=False)[0]
             y = F.linear(_cm_flat(out_z).t(), out_proj_weight, out_proj_bias)
             return y.view(batch, L, -1)
-        out, scan_states, out_z = ext().fwd(conv1d_out, delta, A, B, C, D, z, delta_bias, None, None, None,
-                                            delta_softplus)
+        # checkpoint_lvl 0 keeps activations rather than recomputing them: the scan's 16-step tile
+        # states too (None where the kernels do not write them), which spare the backward a recompute.
+        want_ck = checkpoint_lvl == 0 and A.shape[-1] == 16 and _save_tile_states()
+        out, scan_states, out_z, *ck = ext().fwd(conv1d_out, delta, A, B, C, D, z, delta_bias, None, None, None,
+                                                 delta_softplus, tile_states=want_ck)
+        ck = ck[0] if want_ck else None
         ctx.delta_softplus = delta_softplus
         ctx.out_proj_bias_is_None = out_proj_bias is None
         ctx.checkpoint_lvl = checkpoint_lvl
@@ -150,7 +156,7 @@ class MambaInnerFn(torch.autograd.Function):
         if checkpoint_lvl >= 1:
             conv1d_out, delta = None, None
         ctx.save_for_backward(xz, conv1d_weight, conv1d_bias, x_dbl, x_proj_weight, delta_proj_weight,
-                              out_proj_weight, conv1d_out, delta, A, B, C, D, delta_bias, scan_states, out)
+                              out_proj_weight, conv1d_out, delta, A, B, C, D, delta_bias, scan_states, out, ck)
         y = F.linear(_cm_flat(out_z).t(), out_proj_weight, out_proj_bias)  # (batch * L, d_model)
         return y.view(batch, L, -1)
 
@@ -163,7 +169,7 @@ class MambaInnerFn(torch.autograd.Function):
                 "MambaInnerFn backward with b/c/dt RMSNorm weights is not part of the MI355X build "
                 "(the reference's backward does not differentiate through these norms)")
         (xz, conv1d_weight, conv1d_bias, x_dbl, x_proj_weight, delta_proj_weight, out_proj_weight, conv1d_out,
-         delta, A, B, C, D, delta_bias, scan_states, out) = ctx.saved_tensors
+         delta, A, B, C, D, delta_bias, scan_states, out, ck) = ctx.saved_tensors
         batch, L = xz.shape[0], xz.shape[-1]
         delta_rank = delta_proj_weight.shape[1]
         d_state = A.shape[-1]
@@ -177,7 +183,7 @@ class MambaInnerFn(torch.autograd.Function):
         dout_y = _cm_view(out_proj_weight.t() @ dout2.t(), batch)          # (batch, d_inner, L), channel-major
         du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, out_z = ext().bwd(
             conv1d_out, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, dout=dout_y, x=scan_states, out=out,
-            dz=dz, delta_softplus=ctx.delta_softplus, recompute_out_z=True)
+            dz=dz, delta_softplus=ctx.delta_softplus, recompute_out_z=True, tile_states=ck)
         dout_proj_weight = dout2.t() @ _cm_flat(out_z).t()                 # (d_model, d_inner)
         dout_proj_bias = dout2.sum(dim=0) if not ctx.out_proj_bias_is_None else None
         # Rows of x_dbl that feed nothing (B or C given by the caller) get a zero gradient; the
