@@ -484,15 +484,16 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
                 }
             }
         }
-        // The state after this tile = the checkpoint before the next one, for the backward.
-        if (MODE == 0 && p.tile_states && t0 + kT1 < L) {
+        // The state after this tile = the checkpoint before the next one, for the backward (training
+        // forwards only: those write chunk states; the inference variants carry no such code).
+        if (MODE == 0 && CHUNKS && p.tile_states && t0 + kT1 < L) {
             float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + r * K;
 #pragma unroll
             for (int k = 0; k < K; ++k) ck[k] = h[k];
         }
     };
 
-    if (MODE == 0 && p.tile_states) {    // the checkpoint before the first tile: zero
+    if (MODE == 0 && CHUNKS && p.tile_states) {    // the checkpoint before the first tile: zero
 #pragma unroll
         for (int k = 0; k < K; ++k) p.tile_states[(b * p.dim + d0 + c) * 16 + r * K + k] = 0.f;
     }
@@ -830,8 +831,9 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
                 csp[3] = h[1];
             }
         }
-        // The state after this tile = the checkpoint before the next one, for the backward.
-        if (p.tile_states && t0 + kT1 < L) {
+        // The state after this tile = the checkpoint before the next one, for the backward (training
+        // forwards only: those write chunk states; the inference variants carry no such code).
+        if (CHUNKS && p.tile_states && t0 + kT1 < L) {
             float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + 2 * r;
             *reinterpret_cast<float2 *>(ck) = make_float2(h[0], h[1]);
         }
@@ -839,7 +841,7 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if (p.tile_states)                     // the checkpoint before the first tile: zero
+    if (CHUNKS && p.tile_states)           // the checkpoint before the first tile: zero
         *reinterpret_cast<float2 *>(p.tile_states + (b * p.dim + d0 + c) * 16 + 2 * r) = make_float2(0.f, 0.f);
     K2Data<T> ring[PF];
     {
