@@ -183,6 +183,48 @@ def test_workspace_size_query():
     assert lib.mm_scan_fwd_workspace_size(None) == 0
 
 
+def test_tile_states_size_query():
+    """mm_scan_fwd_tile_states_size (sizes, flags, strides and pointer alignment only; fake pointers
+    are never dereferenced): the training forward of the dstate-16 kernels and every P/Q request
+    with dstate <= 16 write them; other requests do not."""
+    lib = capi.load()
+
+    def params(batch, dim, L, N=16, chunks=True, pq=False):
+        p = capi.ScanFwdParams()
+        p.batch, p.dim, p.seqlen, p.dstate, p.n_groups = batch, dim, L, N, 1
+        p.itype, p.is_variable_B, p.is_variable_C, p.delta_softplus = 2, 1, 1, 1
+        p.u = p.delta = p.A = p.B = p.C = p.z = p.out_z = p.out = 4096
+        p.u_batch_stride = p.delta_batch_stride = p.z_batch_stride = p.out_z_batch_stride = dim * L
+        p.out_batch_stride = dim * L
+        p.u_d_stride = p.delta_d_stride = p.z_d_stride = p.out_z_d_stride = p.out_d_stride = L
+        p.A_d_stride, p.A_dstate_stride = N, 1
+        p.B_batch_stride = p.C_batch_stride = p.B_group_stride = p.C_group_stride = N * L
+        p.B_dstate_stride = p.C_dstate_stride = L
+        if chunks:
+            p.chunk_states = 8192
+        if pq:
+            p.P, p.Q, p.pq_rank = 8192, 16384, 2
+            p.P_dstate_stride, p.P_r_stride, p.Q_r_stride, p.Q_dstate_stride = 2, 1, N, 1
+        return p
+
+    size = lambda p: lib.mm_scan_fwd_tile_states_size(ctypes.byref(p))   # noqa: E731
+    assert size(params(4, 5120, 4096)) == 256 * 4 * 5120 * 16 * 4           # config 2 training forward
+    assert size(params(2, 64, 200)) == 13 * 2 * 64 * 16 * 4                 # ragged last tile
+    assert size(params(4, 5120, 4096, chunks=False)) == 0                  # the inference forward
+    assert size(params(2, 64, 256, N=8)) == 0                              # not the dstate-16 kernels
+    assert size(params(2, 64, 100)) == 0                                   # L % 8 != 0
+    assert size(params(2, 64, 256, N=8, chunks=False, pq=True)) == 16 * 2 * 64 * 16 * 4   # P/Q
+    assert size(params(2, 64, 256, N=32, pq=True)) == 0                    # P/Q, dstate > 16
+    assert lib.mm_scan_fwd_tile_states_size(None) == 0
+    # A diagonal request the kernels cannot serve is refused when tile states are asked for.
+    p = params(2, 64, 256, N=8)
+    p.tile_states = 32768
+    assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_ERR_UNSUPPORTED
+    p = params(2, 64, 256, chunks=False)
+    p.tile_states = 32768
+    assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+
+
 def test_scan_bwd_rejects_invalid_params():
     """Validation of mm_scan_bwd happens before anything is launched (fake pointers)."""
     lib = capi.load()
