@@ -353,3 +353,30 @@ def test_pq_bwd_rank_zero_is_the_diagonal_backward():
     for n in ("u", "delta", "A", "B", "C", "D", "z", "delta_bias"):
         _check(g[n].grad, exact["d" + n], torch.float32, f"rank0 d{n}")
     assert g["P"].grad.shape == (32, 16, 0) and g["Q"].grad.shape == (32, 0, 16)
+
+
+def test_pq_bwd_xz_chunk_views():
+    """The Motif module's call form (mamba_simplemotif.py:314-332): u and z are the two halves of
+    one (batch, 2 dim, L) activation, strided views, and delta is a (b, d, l) view of a
+    channel-major matrix; gradients flow back into the shared parent tensors."""
+    _say("pq bwd xz chunk views")
+    from motif_mamba_amd import selective_scan_fn
+    case = _pq_case(840, batch=2, dim=32, L=96, N=16, R=2, dtype=torch.bfloat16)
+    dout = _dout(841, (2, 32, 96), torch.bfloat16)
+    xz = torch.cat([case["u"], case["z"]], dim=1).to(DEV).requires_grad_(True)
+    dl = case["delta"].permute(1, 0, 2).contiguous().to(DEV).requires_grad_(True)   # (dim, batch, L)
+    u, z = xz.chunk(2, dim=1)
+    delta = dl.permute(1, 0, 2)                                                     # (batch, dim, L) view
+    assert u.stride() == (64 * 96, 96, 1) and delta.stride() == (96, 2 * 96, 1)
+    g = {k: (v.to(DEV).requires_grad_(True) if torch.is_tensor(v) else v) for k, v in case.items()
+         if k not in ("u", "z", "delta")}
+    out = selective_scan_fn(u, delta, g["A"], g["B"], g["C"], D=g["D"], z=z, delta_bias=g["delta_bias"],
+                            delta_softplus=True, P=g["P"], Q=g["Q"])
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    exact = selective_scan_pq_bwd_ref(**case, dout=dout)
+    _check(xz.grad[:, :32], exact["du"], torch.bfloat16, "du via xz")
+    _check(xz.grad[:, 32:], exact["dz"], torch.bfloat16, "dz via xz")
+    _check(dl.grad.permute(1, 0, 2), exact["ddelta"], torch.bfloat16, "ddelta via the channel-major view")
+    for n in ("A", "B", "C", "D", "delta_bias", "P", "Q"):
+        _check(g[n].grad, exact["d" + n], torch.bfloat16, f"d{n}")
