@@ -398,11 +398,13 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
             }
         }
     }
+    const bool shared_pq = p.dP_d_stride == 0 && p.dQ_d_stride == 0;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int n = k * S + s;
         if (n >= N) continue;
         atomicAdd(p.dA + d * p.dA_d_stride + n * p.dA_dstate_stride, dA[s]);
+        if (shared_pq) continue;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (r >= rank) continue;
@@ -412,6 +414,32 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
     }
     if (p.dD) atomicAdd(p.dD + d, dD_acc);
     if (p.ddelta_bias) atomicAdd(p.ddelta_bias + d, dbias_acc);
+    if (shared_pq) {
+        // One dP / dQ shared by every channel: the block's 16 channels are summed in LDS first
+        // (sHS is free now), so that each element takes one atomic per block, not one per lane.
+        static_assert(2 * 16 * R * 16 <= kT * 16 * 16, "the shared-P/Q sums fit sHS");
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                sHS[((0 * 16 + k * S + s) * R + r) * 16 + cw] = dP[s][r];
+                sHS[((1 * 16 + k * S + s) * R + r) * 16 + cw] = dQ[r][s];
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < 2 * 16 * R; e += NT) {
+            const int which = e / (16 * R), n = (e / R) % 16, r = e % R;
+            if (n >= N || r >= rank) continue;
+            const float4 *v = reinterpret_cast<const float4 *>(&sHS[e * 16]);
+            float q4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q4[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
+            const float acc = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+            if (which == 0) atomicAdd(p.dP + n * p.dP_dstate_stride + r * p.dP_r_stride, acc);
+            else atomicAdd(p.dQ + r * p.dQ_r_stride + n * p.dQ_dstate_stride, acc);
+        }
+    }
 }
 
 }  // namespace pqbwd
