@@ -295,3 +295,44 @@ def test_bwd_tile_states(dtype):
     res = ext.fwd(g8["u"], g8["delta"], g8["A"], B8, C8, g8["D"], g8["z"], g8["delta_bias"], None, None, None, True,
                   tile_states=True)
     assert res[-1] is None
+
+
+def test_training_step_graph_replay_matches_eager():
+    """The training forward (with tile states) and the backward captured in one HIP graph: the
+    workspace and outputs come from the graph's memory pool and the clears are fill kernels, so
+    replays with fresh inputs equal the eager step (du, ddelta, dz, dB, dC bit for bit; dA, dD and
+    ddelta_bias to float32 atomic-order rounding)."""
+    _say("training step graph replay")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(695, 2, 64, 256, 16, torch.bfloat16, bkind="4d", G=1)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    dout = _dout(696, (2, 64, 256), torch.bfloat16).to(DEV)
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+
+    def step():
+        out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+        return [out_z] + list(ext.bwd(*args, dout, x, out, None, None, None, True, False, ck))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    gen = torch.Generator().manual_seed(697)
+    atomic = {3, 6, 7}                 # dA, dD, ddelta_bias (after out_z at index 0)
+    for rep in range(3):
+        for k in ("u", "delta", "z"):
+            g[k].copy_(torch.randn(g[k].shape, generator=gen).to(g[k].dtype).to(DEV))
+        dout.copy_(torch.randn(dout.shape, generator=gen).to(dout.dtype).to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs]
+        exp = step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(got, exp)):
+            tol = 1e-6 if i in atomic else 0.0
+            torch.testing.assert_close(a, b, rtol=tol, atol=tol, msg=lambda m: f"replay {rep}, output {i}: {m}")
