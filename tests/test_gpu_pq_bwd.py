@@ -380,3 +380,47 @@ def test_pq_bwd_xz_chunk_views():
     _check(dl.grad.permute(1, 0, 2), exact["ddelta"], torch.bfloat16, "ddelta via the channel-major view")
     for n in ("A", "B", "C", "D", "delta_bias", "P", "Q"):
         _check(g[n].grad, exact["d" + n], torch.bfloat16, f"d{n}")
+
+
+def test_pq_training_step_graph_replay_matches_eager():
+    """The P/Q training forward (with tile states) and backward (dP/dQ added into dP_out/dQ_out)
+    captured in one HIP graph; replays with fresh inputs equal the eager step."""
+    _say("pq training step graph replay")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _pq_case(850, batch=2, dim=32, L=128, N=16, R=2, dtype=torch.bfloat16)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    dout = _dout(851, (2, 32, 128), torch.bfloat16).to(DEV)
+    B4, C4 = g["B"].unsqueeze(1), g["C"].unsqueeze(1)
+    args = (g["u"], g["delta"], g["A"], B4, C4, g["D"], g["z"], g["delta_bias"], g["P"], g["Q"], None)
+    dP, dQ = torch.zeros_like(g["P"]), torch.zeros_like(g["Q"])
+
+    def step():
+        dP.zero_()
+        dQ.zero_()
+        out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+        res = ext.bwd(*args, dout, x, out, None, dP, dQ, True, False, ck)
+        return [out_z] + list(res) + [dP.clone(), dQ.clone()]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    gen = torch.Generator().manual_seed(852)
+    atomic = {3, 6, 7, 9, 10}          # dA, dD, ddelta_bias, dP, dQ (after out_z at index 0)
+    for rep in range(3):
+        for k in ("u", "delta", "z"):
+            g[k].copy_(torch.randn(g[k].shape, generator=gen).to(g[k].dtype).to(DEV))
+        dout.copy_(torch.randn(dout.shape, generator=gen).to(dout.dtype).to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs]
+        exp = step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(got, exp)):
+            tol = 1e-5 if i in atomic else 0.0
+            torch.testing.assert_close(a, b, rtol=tol, atol=tol, msg=lambda m: f"replay {rep}, output {i}: {m}")
