@@ -202,7 +202,8 @@ typedef struct mm_scan_bwd_params {
 
     /* Device scratch of mm_scan_bwd_workspace_size() bytes (16-byte aligned), owned by the caller:
      * the recomputed forward states at every 16-step tile start (and, for dstate 16 and for P/Q,
-     * the per-16-channel-block partial sums of dB and dC). Required. */
+     * the per-16-channel-block partial sums of dB and dC; for dstate 16 with tile_states, the
+     * adjoint carries of the sequence segments its last round of workgroups is cut into). Required. */
     void *workspace;
     int64_t workspace_bytes;
 
@@ -282,7 +283,8 @@ int64_t mm_scan_fwd_tile_states_size(const mm_scan_fwd_params *params);
 int mm_scan_bwd(const mm_scan_bwd_params *params, void *stream);
 
 /* Bytes of `workspace` mm_scan_bwd needs for `params` (0 for a request it would reject or that has
- * nothing to do). Reads only sizes. No counterpart in the reference (its backward recomputes each
+ * nothing to do). Reads sizes and, for dstate 16 with tile_states, the current device's compute-unit
+ * count (the size of one round of workgroups). No counterpart in the reference (its backward recomputes each
  * 2048-step chunk inside one thread block). */
 int64_t mm_scan_bwd_workspace_size(const mm_scan_bwd_params *params);
 

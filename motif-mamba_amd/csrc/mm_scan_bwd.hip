@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "mm_common.h"
@@ -261,6 +262,19 @@ struct FastWs {
     float *partC;
 };
 
+// Sequence segments. A launch covers the units (batch row, 16-channel block) unit0, unit0 + 1, ...
+// (unit = b * dim / 16 + d0 / 16), each as n_seg segments of seg_tiles tiles. With n_seg > 1 the
+// CARRY launch walks segments 1 .. n_seg-1 of each unit from a zero adjoint and stores, per channel
+// and state, (a_t0 gh_t0, prod of a over the segment): the adjoint the segment hands to the one
+// before it, and the factor that carries a later adjoint through it. The gradient launch then
+// starts each segment from the combination of those of the segments after it.
+struct BwdSeg {
+    int64_t unit0;
+    int64_t n_seg;
+    int64_t seg_tiles;
+    float2 *carry;      // [unit - unit0][n_seg][16 channels][16 states]
+};
+
 // Global data of one tile for one lane, loaded a tile ahead of its use.
 template <typename T>
 struct TileRaw {
@@ -269,9 +283,9 @@ struct TileRaw {
     float2 hc;                     // checkpoint of the lane's two states (pass 2)
 };
 
-template <typename T>
+template <typename T, bool CARRY>
 __global__ void __launch_bounds__(128)
-scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws) {
+scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws, const BwdSeg sg) {
     __shared__ __align__(16) float4 sX[kBufs][16 * kXS];    // [buf][c][t]: (dt', dt'u, u, g)
     __shared__ __align__(16) float sBC[kBufs][kFT * 36];     // [buf][t][B 16 | C 16 | pad]
     __shared__ __align__(16) float sRed[kRedFloats];         // red_at(tensor, n, t, c)
@@ -281,13 +295,20 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const int rs = tid >> 4;               // state slot: states 2 rs, 2 rs + 1; prologue steps 2 rs, 2 rs + 1
     const int c = tid & 15;                // channel within the block
     const int n0 = 2 * rs;
-    const int64_t b = blockIdx.y;
-    const int64_t d0 = int64_t(blockIdx.x) * 16;
+    // The CARRY launch walks segments 1 .. n_seg-1 (segment 0 hands nothing on).
+    const int64_t nsw = CARRY ? sg.n_seg - 1 : sg.n_seg;
+    const int64_t uo = int64_t(blockIdx.x) / nsw;
+    const int64_t seg = int64_t(blockIdx.x) - uo * nsw + (CARRY ? 1 : 0);
+    const int64_t per_b = p.dim / 16;
+    const int64_t b = (sg.unit0 + uo) / per_b;
+    const int64_t d0 = (sg.unit0 + uo - b * per_b) * 16;
     const int64_t d = d0 + c;
     const int64_t g = d0 / ratio;
     const int64_t blk = (d0 - g * ratio) / 16;
     const int64_t L = p.seqlen;
     const int64_t n_tiles = (L + kFT - 1) / kFT;
+    const int64_t j_lo = seg * sg.seg_tiles;
+    const int64_t j_hi = j_lo + sg.seg_tiles < n_tiles ? j_lo + sg.seg_tiles : n_tiles;
 
     const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
     const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
@@ -364,7 +385,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                     oz[i] = oo[i] * zz[i] * sg;
                     go[i] *= zz[i] * sg;
                 }
-                if (ev) {
+                if (ev && !CARRY) {
                     store2(dzp + te, dz[0], dz[1]);
                     if (ozp) store2(ozp + te, oz[0], oz[1]);
                 }
@@ -385,8 +406,35 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
         for (int i = 0; i < 4; ++i) sBC[buf][(4 * st_q + i) * 36 + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
     };
 
+    if constexpr (CARRY) {
+        // The segment's adjoint from a zero carry, gh_t = C_t g_t + a_{t+1} gh_{t+1}, and the
+        // product of its decays. Steps past L (last segment only) have dt' = g = 0: a = 1, inert.
+        float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f, pa0 = 1.f, pa1 = 1.f;
+        TileRaw<T> nx = load(j_hi - 1, true);
+        for (int64_t j = j_hi - 1; j >= j_lo; --j) {
+            commit(nx, j, 0, true);
+            nx = load(j - 1, true);
+            __syncthreads();
+#pragma unroll
+            for (int t = kFT - 1; t >= 0; --t) {
+                const float4 x = sX[0][c * kXS + t];
+                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[0][t * 36 + 16 + n0]);
+                gh0 = __builtin_fmaf(an0, gh0, x.w * cv.x);
+                gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
+                an0 = __builtin_amdgcn_exp2f(x.x * A20);
+                an1 = __builtin_amdgcn_exp2f(x.x * A21);
+                pa0 *= an0;
+                pa1 *= an1;
+            }
+            __syncthreads();   // reads done before the next commit rewrites the buffer
+        }
+        float4 *cp = reinterpret_cast<float4 *>(sg.carry + ((uo * sg.n_seg + seg) * 16 + c) * 16 + n0);
+        *cp = make_float4(an0 * gh0, pa0, an1 * gh1, pa1);
+        return;
+    }
+
     // Pass 1: the states before every tile, into the checkpoint workspace (skipped when the
-    // forward wrote them: ws.ck then points at its tile_states).
+    // forward wrote them: ws.ck then points at its tile_states; segmented launches always have them).
     float h0 = 0.f, h1 = 0.f;
     TileRaw<T> nxt = load(0, false);
     for (int64_t j = 0; j < (p.tile_states ? 0 : n_tiles); ++j) {
@@ -408,9 +456,23 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 
     // Pass 2: tiles in reverse order.
     float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f;   // state adjoints, decays of the step after
+    if (seg + 1 < sg.n_seg) {
+        // The adjoint entering from the later segments: c_{S-1} = 0, c_{s-1} = e_s + P_s c_s.
+        const float4 *cp = reinterpret_cast<const float4 *>(sg.carry + ((uo * sg.n_seg) * 16 + c) * 16 + n0);
+        float c0 = 0.f, c1 = 0.f;
+        for (int64_t s2 = sg.n_seg - 1; s2 > seg; --s2) {
+            const float4 v = cp[s2 * 128];
+            c0 = __builtin_fmaf(v.y, c0, v.x);
+            c1 = __builtin_fmaf(v.w, c1, v.z);
+        }
+        gh0 = c0;
+        gh1 = c1;
+        an0 = 1.f;
+        an1 = 1.f;
+    }
     float dA0 = 0.f, dA1 = 0.f, dD_acc = 0.f, dbias_acc = 0.f;
-    nxt = load(n_tiles - 1, true);
-    for (int64_t j = n_tiles - 1; j >= 0; --j) {
+    nxt = load(j_hi - 1, true);
+    for (int64_t j = j_hi - 1; j >= j_lo; --j) {
         const int64_t t0 = j * kFT;
         const int buf = int(j % kBufs);
         const float2 hc = nxt.hc;
@@ -605,6 +667,59 @@ int64_t fast_part_floats(const mm_scan_bwd_params &p) {
     return (p.dim / 16) * p.batch * 16 * p.seqlen;   // blocks per group x groups = dim / 16
 }
 
+// Workgroups of scan_bwd_tiled16<T> that the current device runs at once (one round), or 0 when the
+// device cannot be queried. MM_BWD_SLOTS overrides it (tests exercise the segmented tail with it).
+template <typename T>
+int64_t round_slots() {
+    if (const char *e = std::getenv("MM_BWD_SLOTS")) {
+        const long long v = std::atoll(e);
+        if (v > 0) return v;
+    }
+    static int64_t cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cache[dev] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, scan_bwd_tiled16<T, false>, 128, 0) != hipSuccess)
+            return 0;
+        cache[dev] = int64_t(cus) * per_cu;
+    }
+    return cache[dev];
+}
+
+// How the dstate-16 backward covers its units. The kernel is latency-bound, so a last round with
+// few workgroups per CU costs nearly as much as a full one. With the forward's tile states the
+// units of that last round (or all of them, when they fill at most half a round) are instead cut
+// along the sequence into n_seg segments, enough to fill a round, joined by a carry pass.
+struct SegPlan {
+    int64_t main_units, tail_units, n_seg, seg_tiles;
+};
+template <typename T>
+SegPlan seg_plan(const mm_scan_bwd_params &p) {
+    const int64_t units = p.batch * (p.dim / 16);
+    const int64_t n_tiles = (p.seqlen + kFT - 1) / kFT;
+    const SegPlan whole{units, 0, 1, n_tiles};
+    const char *off = std::getenv("MM_BWD_SEGMENTS");
+    if (!p.tile_states || (off && off[0] == '0')) return whole;
+    const int64_t slots = round_slots<T>();
+    if (slots <= 0 || units == 0) return whole;
+    const int64_t tail = units % slots;
+    if (tail == 0) return whole;
+    int64_t n_seg = std::min<int64_t>({slots / tail, 8, n_tiles / 4});
+    if (n_seg < 2) return whole;
+    const int64_t seg_tiles = (n_tiles + n_seg - 1) / n_seg;
+    n_seg = (n_tiles + seg_tiles - 1) / seg_tiles;   // every segment holds at least one tile
+    if (n_seg < 2) return whole;
+    return {units - tail, tail, n_seg, seg_tiles};
+}
+SegPlan seg_plan_for(const mm_scan_bwd_params &p) {
+    if (p.itype == MM_FLOAT32) return seg_plan<float>(p);
+    if (p.itype == MM_FLOAT16) return seg_plan<f16_t>(p);
+    return seg_plan<bf16_t>(p);
+}
+int64_t carry_floats(const SegPlan &pl) { return pl.tail_units * pl.n_seg * 16 * 16 * 2; }
+
 template <typename T>
 int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
     float *ws = static_cast<float *>(p.workspace);
@@ -613,10 +728,29 @@ int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
     float *partB = own_ck ? ws + fast_ck_floats(p) : ws;
     const FastWs fw{ck, partB, partB + fast_part_floats(p)};
     const int64_t ratio = p.dim / p.n_groups;
-    dim3 grid(unsigned(p.dim / 16), unsigned(p.batch));
-    hipLaunchKernelGGL((scan_bwd_tiled16<T>), grid, dim3(128), 0, s, p, ratio, fw);
-    int rc = launch_status("scan_bwd_tiled16");
-    if (rc != MM_OK) return rc;
+    SegPlan pl = seg_plan<T>(p);
+    const int64_t need = (2 * fast_part_floats(p) + carry_floats(pl)) * int64_t(sizeof(float));
+    if (pl.tail_units > 0 && p.workspace_bytes < need)   // a workspace sized without the carries
+        pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT};
+    int rc = MM_OK;
+    if (pl.main_units > 0) {
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, false>), dim3(unsigned(pl.main_units)), dim3(128), 0, s, p, ratio,
+                           fw, BwdSeg{0, 1, (p.seqlen + kFT - 1) / kFT, nullptr});
+        rc = launch_status("scan_bwd_tiled16");
+        if (rc != MM_OK) return rc;
+    }
+    if (pl.tail_units > 0) {
+        const BwdSeg sg{pl.main_units, pl.n_seg, pl.seg_tiles,
+                        reinterpret_cast<float2 *>(partB + 2 * fast_part_floats(p))};
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, true>), dim3(unsigned(pl.tail_units * (pl.n_seg - 1))), dim3(128), 0,
+                           s, p, ratio, fw, sg);
+        rc = launch_status("scan_bwd_tiled16 (carries)");
+        if (rc != MM_OK) return rc;
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, false>), dim3(unsigned(pl.tail_units * pl.n_seg)), dim3(128), 0, s,
+                           p, ratio, fw, sg);
+        rc = launch_status("scan_bwd_tiled16 (segments)");
+        if (rc != MM_OK) return rc;
+    }
     const int64_t total = p.batch * p.n_groups * 16 * (p.seqlen / 4);
     const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 8192));
     hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, fw.partB, p.dB, p.dB_batch_stride,
@@ -654,7 +788,9 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
-    if ((p.P || bwd::fast_ok(p)) && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
+    if (!p.P && bwd::fast_ok(p) && p.tile_states)
+        return (2 * bwd::fast_part_floats(p) + bwd::carry_floats(bwd::seg_plan_for(p))) * int64_t(sizeof(float));
+    if (p.P && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
     return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));
