@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -643,7 +644,7 @@ int launch_fill(float *ptr, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int6
 bool fast_ok(const mm_scan_bwd_params &p) {
     if (p.P || p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
     if (p.dim % 16 != 0 || (p.dim / p.n_groups) % 16 != 0 || p.seqlen < 8 || p.seqlen % 8 != 0) return false;
-    if (p.batch > 65535 || p.dim / 16 > 0x7fffffff) return false;
+    if (p.batch * (p.dim / 16) > 0x7fffffff) return false;   // one workgroup per unit in a 1-D grid
     const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
     auto al = [](const void *ptr, int64_t bytes) { return (reinterpret_cast<uintptr_t>(ptr) % uintptr_t(bytes)) == 0; };
     auto row2 = [&](const void *ptr, int64_t s0, int64_t s1) {
@@ -675,17 +676,19 @@ int64_t round_slots() {
         const long long v = std::atoll(e);
         if (v > 0) return v;
     }
-    static int64_t cache[64] = {};
+    static std::atomic<int64_t> cache[64] = {};   // per device; every thread computes the same value
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cache[dev] == 0) {
+    int64_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, scan_bwd_tiled16<T, false>, 128, 0) != hipSuccess)
             return 0;
-        cache[dev] = int64_t(cus) * per_cu;
+        v = int64_t(cus) * per_cu;
+        cache[dev].store(v, std::memory_order_relaxed);
     }
-    return cache[dev];
+    return v;
 }
 
 // How the dstate-16 backward covers its units. The kernel is latency-bound, so a last round with
