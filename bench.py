@@ -9,9 +9,13 @@ softplus, last state returned), with all inputs resident in HBM before timing st
 is the algorithmic HBM throughput of that step (bytes of u, delta, z, B, C, A, D, delta_bias read
 and out_z, last_state written, each once) divided by the measured time per step, in GB/s.
 
-The JSON line also carries: ``roofline`` for the forward-scan kernel (HBM bound, 8 TB/s peak),
-``roofline_trans`` (the same kernel against the v_exp_f32 issue rate, which binds it), ``cpu_baseline``
-(the CPU oracle timed on the host on a bounded sample of the same workload), per-config results for
+The run starts with the issue-rate probes of libmm_probe.so (csrc/mm_probe.hip), which measure the
+v_exp_f32 and v_fma_f32 rates of this GPU (and bring it to its loaded clock before anything is
+timed). The JSON line carries the forward kernel's rooflines: ``roofline_hbm`` (8 TB/s published
+peak), ``roofline_trans`` (the measured v_exp_f32 rate), ``roofline`` = the binding one of those two
+(north_star: the larger floor), and ``roofline_issue`` (transcendentals plus the 4 VALU operations
+of a state update, at the measured rates); ``cpu_baseline`` (the CPU oracle timed on the host on a
+bounded sample of the same workload, and one per other configuration), per-config results for
 configs 1 and 3, decode tokens/s for config 4, the MotifMamba P/Q forward on a Mamba-1.4B layer and
 the training forward + backward of configs 1 and 2, the causal conv1d that precedes the scan
 (forward on the config 1 and 2 shapes, decode update) and the fused Mamba block mamba_inner_fn on
@@ -31,17 +35,32 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [REPO, os.path.join(REPO, "motif-mamba_amd")]
 
 HBM_PEAK_GBS = 8000.0
-# v_exp_f32 throughput of the whole MI355X, measured with a kernel-time microbenchmark (8 waves per
-# SIMD, independent chains): the transcendental issue roofline of the scan.
-TRANS_PEAK_PER_S = 16.14e12
 METRIC = "selective-scan fwd GB/s & % of binding roofline; decode tokens/s, 1 GPU"
+# Issue rates of this GPU, measured at the start of every run by issue_rates() (libmm_probe.so):
+# "trans_per_s" (v_exp_f32 lane operations per second, chip-wide) and "valu_per_s" (v_fma_f32).
+RATES = {}
 
 
 def _log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+RAMP_S = 0.25
+
+
 def _time_loop(fn, steps, warmup, torch):
+    """ms per step of fn over `steps` timed calls after `warmup` untimed ones. Before those, fn runs
+    untimed for RAMP_S seconds: an idle MI355X takes ~50 ms of sustained load to reach its loaded
+    clocks (config 2 measured 0.88, 0.45, 0.43 then a steady 0.42 ms per step over its first
+    batches of 20 calls, and back to 0.50 after a 1 s pause), and a throughput figure is meant to be
+    the steady-state one."""
+    t0 = time.time()
+    i = 0
+    while time.time() - t0 < RAMP_S:
+        fn(i)
+        i += 1
+        if i % 4 == 0:
+            torch.cuda.synchronize()
     for _ in range(warmup):
         fn(0)
     torch.cuda.synchronize()
@@ -96,10 +115,32 @@ def bench_scan(cfg_name, steps, warmup, torch, rotate=1):
         "ms": ms, "GB_s": nbytes / (ms * 1e-3) / 1e9, "bytes": nbytes,
         "elements_per_s": elems / (ms * 1e-3), "state_updates_per_s": elems * c.dstate / (ms * 1e-3),
         "trans_per_s": trans / (ms * 1e-3), "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "t_floor_us": max(nbytes / (HBM_PEAK_GBS * 1e9), trans / TRANS_PEAK_PER_S) * 1e6,
-        "floor_frac": max(nbytes / (HBM_PEAK_GBS * 1e9), trans / TRANS_PEAK_PER_S) / (ms * 1e-3),
-        "input_rotation": rotate,
+        **scan_floors(nbytes, trans, elems * c.dstate, ms), "input_rotation": rotate,
     }
+
+
+def scan_floors(nbytes, trans, updates, ms):
+    """The scan's rooflines at one shape, from the algorithmic work of one call:
+
+    * HBM: nbytes at the published 8 TB/s;
+    * transcendental issue: trans (N exp2 per element for the decay, exp + log for softplus,
+      exp + rcp for silu) at the v_exp_f32 rate measured on this GPU;
+    * VALU + transcendental issue: the same transcendentals plus 4 VALU operations per state update
+      (the exp argument, B * delta' u, the state FMA, y += C h) at the v_fma_f32 rate measured on
+      this GPU, added because the probes show no co-issue of the two on a SIMD.
+
+    The binding roofline is the larger of the first two (north_star: "HBM bandwidth or exp issue
+    rate"); ``binding_frac`` is its floor over the measured time. The issue floor is reported
+    beside it as the tighter bound this kernel design can reach."""
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    t_trans = trans / RATES["trans_per_s"]
+    t_issue = t_trans + 4 * updates / RATES["valu_per_s"]
+    binding = "hbm" if t_hbm >= t_trans else "trans"
+    t_bind = max(t_hbm, t_trans)
+    t = ms * 1e-3
+    return {"t_hbm_us": t_hbm * 1e6, "t_trans_us": t_trans * 1e6, "t_issue_us": t_issue * 1e6,
+            "binding": binding, "t_floor_us": t_bind * 1e6, "binding_frac": t_bind / t,
+            "issue_frac": t_issue / t}
 
 
 def bench_decode(batch, steps, warmup, torch, sets_max=64):
@@ -151,7 +192,7 @@ def bench_pq(name, steps, warmup, torch):
     trans = scan_transcendentals(c.batch, c.dim, c.seqlen, c.dstate)
     flops = pq_flops(c.batch, c.dim, c.seqlen, c.dstate, c.rank)
     elems = c.batch * c.dim * c.seqlen
-    floor = max(nbytes / (HBM_PEAK_GBS * 1e9), trans / TRANS_PEAK_PER_S)
+    floor = max(nbytes / (HBM_PEAK_GBS * 1e9), trans / RATES["trans_per_s"])
     del inputs
     torch.cuda.empty_cache()
     return {"shape": [c.batch, c.dim, c.seqlen, c.dstate], "rank": c.rank, "per_dim": c.per_dim, "dtype": c.dtype,
@@ -321,40 +362,174 @@ def bench_inner(steps, warmup, torch, batch=4, seqlen=4096, d_model=2560, d_inne
             "gemm_gflop_fwd_bwd": train_flops / 1e9}
 
 
-def cpu_baseline(torch, seconds_target=15.0):
-    """The CPU oracle (torch restatement of selective_scan_ref) on a bounded sample of config 2:
-    one batch row and a slice of channels at the full L = 4096, scaled to GB/s of the config's
-    algorithmic bytes per element."""
-    from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_bytes, scan_inputs
-    from oracle.ssm_ref import selective_scan_ref
-    c = SCAN_CONFIGS["cfg2"]
-    threads = torch.get_num_threads()
-    dims = 64
-    inputs = scan_inputs(c, batch=1, dim=dims)
-    inputs.pop("return_last_state")
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _time_cpu(fn, seconds_target):
     t0 = time.time()
-    selective_scan_ref(**inputs, return_last_state=True)
+    fn()
     t1 = time.time() - t0
     reps = max(1, int(seconds_target / max(t1, 1e-3)))
     t0 = time.time()
     for _ in range(reps):
-        selective_scan_ref(**inputs, return_last_state=True)
-    per = (time.time() - t0) / reps
-    frac = (1 * dims) / (c.batch * c.dim)
-    nbytes = scan_bytes(c.batch, c.dim, c.seqlen, c.dstate, c.n_groups, 2) * frac
-    return {"value": nbytes / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"config 2 shape restricted to batch 1 x {dims} channels x L {c.seqlen} "
-                      f"(1/{int(1 / frac)} of the work), {reps} timed run(s) of {per:.3f}s; "
-                      f"oracle/ssm_ref.selective_scan_ref, torch {torch.__version__} on "
-                      f"{platform.processor() or platform.machine()} with {threads} threads"}
+        fn()
+    return (time.time() - t0) / reps, reps
+
+
+def cpu_scan_sample(torch, cfg_name, batch, dims, seconds_target):
+    """The CPU oracle (oracle.ssm_ref.selective_scan_ref, the torch restatement of the reference's
+    selective_scan_ref, selective_scan_interface.py:353-451) on a bounded sample of one scan
+    configuration: `batch` rows x `dims` channels at the configuration's full L, scaled to the
+    configuration's algorithmic bytes per element (GB/s) and elements per second."""
+    from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_bytes, scan_inputs
+    from oracle.ssm_ref import selective_scan_ref
+    c = SCAN_CONFIGS[cfg_name]
+    inputs = scan_inputs(c, batch=batch, dim=dims)
+    inputs.pop("return_last_state")
+    per, reps = _time_cpu(lambda: selective_scan_ref(**inputs, return_last_state=True), seconds_target)
+    frac = (batch * dims) / (c.batch * c.dim)
+    in_bytes = 2 if c.dtype in ("bf16", "fp16") else 4
+    nbytes = scan_bytes(c.batch, c.dim, c.seqlen, c.dstate, c.n_groups, in_bytes) * frac
+    elems = batch * dims * c.seqlen
+    threads = torch.get_num_threads()
+    return {"value": nbytes / per / 1e9, "unit": "GB/s", "elements_per_s": elems / per, "cores": threads,
+            "kind": "port",
+            "sample": f"{cfg_name} restricted to batch {batch} x {dims} channels x L {c.seqlen} "
+                      f"(1/{round(1 / frac)} of the work), {reps} timed run(s) of {per:.3f}s; "
+                      f"oracle/ssm_ref.selective_scan_ref, torch {torch.__version__}, {threads} threads on "
+                      f"{_cpu_model()} ({os.cpu_count()} logical CPUs visible)"}
+
+
+def cpu_decode_sample(torch, batch, dims, steps, seconds_target):
+    """The CPU restatement of the decode step (oracle.ssm_ref.selective_state_update_ref, the math of
+    mamba_simplemotif.py:369-376 with the upstream kernel's float32 discretisation) over `steps`
+    consecutive steps of config 4 at `batch`, on `dims` of its 5120 channels, scaled to tokens/s
+    of the whole layer."""
+    from oracle.ssm_ref import selective_state_update_ref
+    g = torch.Generator().manual_seed(4)
+    N = 16
+    state0 = torch.randn(batch, dims, N, generator=g) * 0.1
+    bias = torch.rand(dims, generator=g) * 4.6 - 6.9
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(dims, 1)
+    D = torch.ones(dims)
+    S = min(steps, 16)
+    xs = [torch.randn(batch, dims, generator=g).to(torch.bfloat16) for _ in range(3 * S)]
+    BC = [torch.randn(batch, N, generator=g).to(torch.bfloat16) for _ in range(2 * S)]
+
+    def run():
+        st = state0.clone()
+        for i in range(steps):
+            j = i % S
+            selective_state_update_ref(st, xs[3 * j], xs[3 * j + 1], A, BC[2 * j], BC[2 * j + 1], D, xs[3 * j + 2],
+                                       bias, dt_softplus=True)
+    per, reps = _time_cpu(run, seconds_target)
+    frac = dims / 5120
+    threads = torch.get_num_threads()
+    return {"value": batch * steps * frac / per, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"config 4 batch {batch}: {steps} steps on {dims} of 5120 channels (1/{round(1 / frac)} "
+                      f"of the layer), {reps} timed run(s) of {per:.3f}s; oracle/ssm_ref.selective_state_update_ref, "
+                      f"{threads} threads on {_cpu_model()}"}
+
+
+def cpu_baselines(torch):
+    """The headline CPU baseline (config 2) and one per other configuration, each a few seconds."""
+    head = cpu_scan_sample(torch, "cfg2", 1, 64, 10.0)
+    per_cfg = {
+        "cfg1": cpu_scan_sample(torch, "cfg1", 1, 64, 4.0),
+        "cfg3_g1": cpu_scan_sample(torch, "cfg3_g1", 1, 16, 4.0),
+        "cfg3_g4": cpu_scan_sample(torch, "cfg3_g4", 1, 16, 4.0),
+        "cfg4_b1": cpu_decode_sample(torch, 1, 5120, 1024, 2.0),
+        "cfg4_b64": cpu_decode_sample(torch, 64, 320, 1024, 3.0),
+        "cfg4_b256": cpu_decode_sample(torch, 256, 80, 1024, 3.0),
+    }
+    return head, per_cfg
+
+
+# Instructions per round and lane of each probe kind of libmm_probe.so (csrc/mm_probe.hip), as
+# (transcendental, VALU) counts; kind 4 runs kind 1 on even waves and kind 0 on odd waves.
+PROBE_KINDS = {0: ("v_fma_f32", 0, 32), 1: ("v_exp_f32", 32, 0), 2: ("v_mul_f32_dpp row_newbcast", 0, 32),
+               3: ("v_exp_f32 + 4 v_fma_f32 (one wave)", 8, 32), 4: ("v_exp_f32 / v_fma_f32 (alternate waves)", 16, 16),
+               5: ("v_fmac_f32_dpp row_newbcast", 0, 32), 6: ("v_exp_f32 + v_fma_f32 (one wave)", 16, 16)}
+
+
+def issue_rates(torch, waves=(2, 3, 4, 8), iters=2000):
+    """Issue rates of the instructions a state update is made of, measured on this GPU with the
+    probe kernels of libmm_probe.so: for each kind and W waves per SIMD, the SIMD cycles one wave64
+    instruction takes (kernel time x shader clock / instructions per SIMD) and the chip-wide rate in
+    lane operations per second. The shader clock comes from the probes' own s_memtime /
+    s_memrealtime ticks."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(REPO, "motif-mamba_amd", "motif_mamba_amd", "libmm_probe.so"))
+    lib.mm_probe_launch.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    lib.mm_probe_device.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]
+    cus, wall_khz = ctypes.c_int(), ctypes.c_int()
+    if lib.mm_probe_device(ctypes.byref(cus), ctypes.byref(wall_khz)) != 0:
+        raise RuntimeError("mm_probe_device failed")
+    n_simd = cus.value * 4
+    stream = torch.cuda.current_stream()
+    res = {"cus": cus.value, "wall_clock_khz": wall_khz.value, "iters": iters, "kinds": {}}
+    clocks = []
+    for kind, (name, n_trans, n_valu) in PROBE_KINDS.items():
+        rows = []
+        for W in waves:
+            blocks = cus.value * W
+            out = torch.empty(blocks * 256, device="cuda")
+            ticks = torch.zeros(blocks * 8, dtype=torch.int64, device="cuda")
+
+            def launch():
+                rc = lib.mm_probe_launch(kind, blocks, iters, out.data_ptr(), ticks.data_ptr(),
+                                         ctypes.c_void_p(stream.cuda_stream))
+                if rc != 0:
+                    raise RuntimeError(f"mm_probe_launch kind {kind}: hip error {rc}")
+            launch()
+            torch.cuda.synchronize()
+            best = None
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                launch()
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1)
+                best = ms if best is None else min(best, ms)
+            tk = ticks.view(-1, 2).double()
+            clk_hz = (tk[:, 0].sum() / tk[:, 1].sum()).item() * wall_khz.value * 1e3
+            clocks.append(clk_hz)
+            instr_simd = W * iters * (n_trans + n_valu)        # wave64 instructions per SIMD
+            rows.append({"waves_per_simd": W, "ms": round(best, 4), "clock_mhz": round(clk_hz / 1e6, 1),
+                         "simd_cycles_per_instr": round(best * 1e-3 * clk_hz / instr_simd, 3),
+                         "lane_ops_per_s": n_simd * instr_simd * 64 / (best * 1e-3)})
+            del out, ticks
+        res["kinds"][name] = rows
+    res["clock_mhz"] = round(sum(clocks) / len(clocks) / 1e6, 1)
+
+    def best_rate(name):
+        return max(r["lane_ops_per_s"] for r in res["kinds"][name])
+    res["trans_per_s"] = best_rate("v_exp_f32")                 # exp2 lane operations per second, chip
+    res["valu_per_s"] = best_rate("v_fma_f32")
+    res["dpp_valu_per_s"] = best_rate("v_mul_f32_dpp row_newbcast")
+    return res
 
 
 def _traffic():
+    """HBM bytes per launch of the headline kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    recorded in profiles/traffic_cfg2.json (static: counters cannot be read from inside this run)."""
     path = os.path.join(REPO, "profiles", "traffic_cfg2.json")
     if os.path.exists(path):
         with open(path) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
-    return None
+            d = json.load(f)
+        return d.get("hbm_bytes_per_launch"), ("static: profiles/traffic_cfg2.json, rocprofv3 --pmc FETCH_SIZE and "
+                                              "WRITE_SIZE of " + str(d.get("kernel", "the headline kernel")))
+    return None, None
 
 
 def main():
@@ -385,7 +560,13 @@ def main():
 
     if args.only:
         name = args.only
-        if name.startswith("cfg4_b"):
+        RATES.update(issue_rates(torch))
+        if name == "probe":
+            res = RATES
+        elif name == "cpu":
+            head, per_cfg = cpu_baselines(torch)
+            res = {"cfg2": head, **per_cfg}
+        elif name.startswith("cfg4_b"):
             res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
         elif name.startswith("pq_") and name.endswith("_train"):
             res = bench_pq_train(name[: -len("_train")], args.steps, args.warmup, torch)
@@ -404,6 +585,8 @@ def main():
         print(json.dumps({"config": name, **res}), flush=True)
         return
 
+    _log("issue-rate probes (also bring the GPU to its loaded clock before the timed runs)")
+    RATES.update(issue_rates(torch))
     _log("config 2 (headline)")
     head = bench_scan("cfg2", args.steps, args.warmup, torch)
     if args.copy_ref:
@@ -439,26 +622,42 @@ def main():
             extra[f"conv_update_b{b}"] = bench_conv_update(b, 200, 10, torch)
         _log("mamba_inner_fn forward and forward + backward (Mamba-2.8B layer, config-2 tokens)")
         extra["inner_2p8b"] = bench_inner(max(5, args.steps // 2), 2, torch)
-    cpu = None
+    cpu, cpu_cfgs = None, None
     if not args.no_cpu:
-        _log("CPU baseline (oracle on a bounded sample)")
-        cpu = cpu_baseline(torch)
+        _log("CPU baselines (oracle on bounded samples of configs 1-4)")
+        cpu, cpu_cfgs = cpu_baselines(torch)
+        for name, res in cpu_cfgs.items():
+            if name in extra:
+                extra[name]["cpu_baseline"] = res
 
     value = head["GB_s"]
+    t = head["ms"] * 1e-3
+    traffic, traffic_src = _traffic()
+    hbm = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src}
+    trans = {"bound": "trans", "achieved": round(head["trans_per_s"] / 1e12, 3),
+             "peak": round(RATES["trans_per_s"] / 1e12, 3), "unit": "T/s",
+             "frac": round(head["trans_per_s"] / RATES["trans_per_s"], 4), "traffic": traffic,
+             "traffic_source": traffic_src,
+             "peak_source": "v_exp_f32 lane operations per second measured in this run by libmm_probe.so "
+                            "(csrc/mm_probe.hip), the best of 2-8 waves per SIMD"}
+    issue = {"bound": "valu+trans issue", "t_floor_us": round(head["t_issue_us"], 2),
+             "frac": round(head["issue_frac"], 4),
+             "model": "B*D*L*(N+4) transcendentals at the measured v_exp_f32 rate plus 4 VALU operations per "
+                      "state update at the measured v_fma_f32 rate, issued serially (the probes show no co-issue)"}
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(head["ms"], 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "accumulate_dtype": "fp32",
+        "data": "synthetic",
         "config": {"workload": "cfg2: selective_scan_fn fwd, Mamba-2.8B layer (batch 4, d_inner 5120, "
                                "L 4096, dstate 16, bf16, z gate, delta_bias+softplus, last_state)",
                    "batch": 4, "dim": 5120, "seqlen": 4096, "dstate": 16, "n_groups": 1, "io_dtype": "bf16"},
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": _traffic()},
-        "roofline_trans": {"bound": "v_exp_f32 issue", "achieved": round(head["trans_per_s"] / 1e12, 3),
-                           "peak": TRANS_PEAK_PER_S / 1e12, "unit": "T/s",
-                           "frac": round(head["trans_per_s"] / TRANS_PEAK_PER_S, 4),
-                           "t_floor_us": round(head["t_floor_us"], 2), "floor_frac": round(head["floor_frac"], 4)},
+        # The binding roofline of north_star ("HBM bandwidth or exp issue rate", the larger floor).
+        "roofline": trans if head["binding"] == "trans" else hbm,
+        "roofline_hbm": hbm, "roofline_trans": trans, "roofline_issue": issue,
         "cpu_baseline": cpu,
+        "issue_rates": {k: RATES[k] for k in ("clock_mhz", "trans_per_s", "valu_per_s", "dpp_valu_per_s")},
         "headline_detail": head,
         "configs": extra,
     }

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define MM_SCAN_ABI_VERSION 9
+#define MM_SCAN_ABI_VERSION 10
 
 #define MM_OK 0
 #define MM_ERR_INVALID_ARGUMENT (-1)
@@ -203,7 +203,9 @@ typedef struct mm_scan_bwd_params {
     /* Device scratch of mm_scan_bwd_workspace_size() bytes (16-byte aligned), owned by the caller:
      * the recomputed forward states at every 16-step tile start (and, for dstate 16 and for P/Q,
      * the per-16-channel-block partial sums of dB and dC; for dstate 16 with tile_states, the
-     * adjoint carries of the sequence segments its last round of workgroups is cut into). Required. */
+     * adjoint carries of the sequence segments its last round of workgroups is cut into). Required.
+     * With tile_states at dstate 16, a workspace without room for the carries (sized for another
+     * device or round size) is accepted too: the call then scans every row whole, without segments. */
     void *workspace;
     int64_t workspace_bytes;
 
@@ -238,21 +240,28 @@ typedef struct mm_scan_bwd_params {
  *   dt' = softplus(dt + dt_bias) (softplus only when dt_softplus != 0)
  *   state[b,d,n] = state[b,d,n] * exp(dt' * A[d,n]) + dt' * B[b,g(d),n] * x[b,d]
  *   out[b,d] = (sum_n state[b,d,n] * C[b,g(d),n] + D[d] * x[b,d]) * silu(z[b,d])
- * state is float32; x, dt, z, out, B, C are itype; A, D, dt_bias are float32. */
+ * x, dt, z, out, B, C are itype; A is float32. The state is state_type, D and dt_bias are D_type
+ * and dt_bias_type (ABI version 10; all three float32 when left zero): every value is widened to
+ * float32, the arithmetic is float32, the updated state is rounded to state_type (round to nearest
+ * even) when stored, and out is read from the float32 state before that rounding -- the semantics
+ * of the upstream Triton kernel (mamba_ssm 2.2.x selective_state_update), which loads each operand
+ * `.to(tl.float32)` and stores the state back in its own dtype. A bfloat16 or float16 model's
+ * decode passes the state in dt_proj.weight.dtype and D / dt_proj.bias uncast
+ * (mamba_simplemotif.py:397-399, 410-414, 428-435). */
 typedef struct mm_state_update_params {
     int64_t batch, dim, dstate, n_groups;
     mm_dtype itype;
     int32_t dt_softplus;
 
-    float *state;            /* (batch, dim, dstate), updated in place */
+    void *state;             /* (batch, dim, dstate) of state_type, updated in place */
     const void *x;           /* (batch, dim) */
     const void *dt;          /* (batch, dim) */
     const float *A;          /* (dim, dstate) */
     const void *B;           /* (batch, n_groups, dstate) */
     const void *C;           /* (batch, n_groups, dstate) */
-    const float *D;          /* (dim,) or NULL */
+    const void *D;           /* (dim,) contiguous, of D_type, or NULL */
     const void *z;           /* (batch, dim) or NULL */
-    const float *dt_bias;    /* (dim,) or NULL */
+    const void *dt_bias;     /* (dim,) contiguous, of dt_bias_type, or NULL */
     void *out;               /* (batch, dim) */
 
     int64_t state_batch_stride, state_d_stride, state_dstate_stride;
@@ -263,6 +272,9 @@ typedef struct mm_state_update_params {
     int64_t A_d_stride, A_dstate_stride;
     int64_t B_batch_stride, B_group_stride, B_dstate_stride;
     int64_t C_batch_stride, C_group_stride, C_dstate_stride;
+
+    /* ABI version 10: element types of state, D and dt_bias (MM_FLOAT32 = 0 when zeroed). */
+    mm_dtype state_type, D_type, dt_bias_type;
 } mm_state_update_params;
 
 /* Forward scan. Replaces selective_scan_cuda.fwd (selective_scan.cpp:270-413, pybind :620-627),

@@ -36,10 +36,12 @@ int launch_pq(const mm_scan_fwd_params &p, hipStream_t stream);
 int64_t pq_tiled_lanes_per_row(const mm_scan_fwd_params &p);
 
 // Backward (mm_scan_bwd.hip): clears the accumulated gradients and launches the backward kernels
-// on `stream`; bwd_workspace_bytes() is the checkpoint scratch it needs.
+// on `stream`; bwd_workspace_bytes() is the scratch it uses best, bwd_workspace_min_bytes() the
+// least it accepts (with tile states: without the segment carries, every unit then a whole row).
 template <typename T>
 int launch_bwd(const mm_scan_bwd_params &p, hipStream_t stream);
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p);
+int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p);
 
 // Backward with the low-rank P/Q coupling (mm_scan_pq_bwd.hip): pq_bwd_ok() tells whether the
 // request fits the kernel; launch_pq_bwd() runs it with the checkpoint scratch `ck` and the dB / dC

@@ -178,7 +178,14 @@ scan_fwd_rowlane(const mm_scan_fwd_params p, const int64_t ratio, const int32_t 
 // ================================================================================================
 constexpr int kDecBlock = 256;
 
-template <typename T, int SPL, int LPR>
+// A per-channel decode parameter (D, dt_bias) of any float element type, widened to float32.
+__device__ __forceinline__ float load_param(const void *base, mm_dtype t, int64_t i) {
+    if (t == MM_FLOAT16) return to_f32(reinterpret_cast<const f16_t *>(base)[i]);
+    if (t == MM_BFLOAT16) return to_f32(reinterpret_cast<const bf16_t *>(base)[i]);
+    return reinterpret_cast<const float *>(base)[i];
+}
+
+template <typename T, typename S, int SPL, int LPR>
 __global__ void __launch_bounds__(kDecBlock)
 state_update_kernel(const mm_state_update_params p, const int64_t ratio) {
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -193,13 +200,13 @@ state_update_kernel(const mm_state_update_params p, const int64_t ratio) {
     const int N = int(p.dstate);
 
     float dt = to_f32(reinterpret_cast<const T *>(p.dt)[b * p.dt_batch_stride + d * p.dt_d_stride]);
-    if (p.dt_bias) dt += p.dt_bias[d];
+    if (p.dt_bias) dt += load_param(p.dt_bias, p.dt_bias_type, d);
     if (p.dt_softplus) dt = softplus_f32(dt);
     const float x = to_f32(reinterpret_cast<const T *>(p.x)[b * p.x_batch_stride + d * p.x_d_stride]);
     const float dtx = dt * x;
     const T *Bp = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
     const T *Cp = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
-    float *sp = p.state + b * p.state_batch_stride + d * p.state_d_stride;
+    S *sp = reinterpret_cast<S *>(p.state) + b * p.state_batch_stride + d * p.state_d_stride;
 
     float y = 0.f;
 #pragma unroll
@@ -207,16 +214,16 @@ state_update_kernel(const mm_state_update_params p, const int64_t ratio) {
         const int n = part * SPL + k;
         if (n < N) {
             const float a = fast_exp2(dt * p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e);
-            float s = sp[n * p.state_dstate_stride];
+            float s = to_f32(sp[n * p.state_dstate_stride]);
             s = __builtin_fmaf(s, a, dtx * to_f32(Bp[n * p.B_dstate_stride]));
-            if (active) sp[n * p.state_dstate_stride] = s;
-            y = __builtin_fmaf(s, to_f32(Cp[n * p.C_dstate_stride]), y);
+            if (active) sp[n * p.state_dstate_stride] = from_f32<S>(s);
+            y = __builtin_fmaf(s, to_f32(Cp[n * p.C_dstate_stride]), y);   // the float32 state
         }
     }
 #pragma unroll
     for (int off = 1; off < LPR; off <<= 1) y += __shfl_xor(y, off, LPR);
     if (active && part == 0) {
-        if (p.D) y = __builtin_fmaf(p.D[d], x, y);
+        if (p.D) y = __builtin_fmaf(load_param(p.D, p.D_type, d), x, y);
         if (p.z) y *= silu_f32(to_f32(reinterpret_cast<const T *>(p.z)[b * p.z_batch_stride + d * p.z_d_stride]));
         reinterpret_cast<T *>(p.out)[b * p.out_batch_stride + d * p.out_d_stride] = from_f32<T>(y);
     }
@@ -245,12 +252,31 @@ __device__ __forceinline__ float4 load4(const T *p) {
 // arithmetic so that a lane has U rows' worth of memory requests in flight.
 template <typename T>
 struct DecRow {
-    float4 s, a;        // four states and their A entries
+    float4 s;           // four states (float32 state)
+    uint2 sw;           // four states as raw words (16-bit state)
     uint2 bw, cw;       // four B / C values as raw words (16-bit types; fp32 uses bf/cf)
     float4 bf, cf;
     T dt, x, z;
-    float D, bias;
 };
+
+// Four consecutive 16-bit values (two packed words) as float32, and back with round to nearest even.
+template <typename S>
+__device__ __forceinline__ float4 unpack4(uint2 w) {
+    float4 r;
+    if constexpr (std::is_same_v<S, bf16_t>) {
+        unpack_bf16x2(w.x, r.x, r.y);
+        unpack_bf16x2(w.y, r.z, r.w);
+    } else {
+        unpack_f16x2(w.x, r.x, r.y);
+        unpack_f16x2(w.y, r.z, r.w);
+    }
+    return r;
+}
+template <typename S>
+__device__ __forceinline__ uint2 pack4(float4 v) {
+    if constexpr (std::is_same_v<S, bf16_t>) return make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    else return make_uint2(pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w));
+}
 
 // dstate 16 with every row of state, A, B and C contiguous and 4-element aligned (checked on the
 // host). Four lanes per (batch, channel) row, each moving four consecutive states as one 16-byte
@@ -260,7 +286,7 @@ struct DecRow {
 // few bytes in flight to cover HBM latency). The grid is one-dimensional, blockIdx.x = batch block
 // * n_dblk + channel block, so no 64-bit division runs per lane; channels past `dim` and rows past
 // `batch` reload the last one and store nothing.
-template <typename T, int U>
+template <typename T, typename S, int U>
 __global__ void __launch_bounds__(kDecBlock)
 state_update_vec16(const mm_state_update_params p, const uint32_t ratio, const uint32_t n_dblk) {
     const uint32_t bb = blockIdx.x / n_dblk;
@@ -271,14 +297,17 @@ state_update_vec16(const mm_state_update_params p, const uint32_t ratio, const u
     const uint32_t d = dr < dim ? dr : dim - 1;
     const uint32_t g = d / ratio;
     const float4 a4 = *reinterpret_cast<const float4 *>(p.A + int64_t(d) * p.A_d_stride + 4 * part);
-    const float Dv = p.D ? p.D[d] : 0.f;
-    const float bias = p.dt_bias ? p.dt_bias[d] : 0.f;
+    const float Dv = p.D ? load_param(p.D, p.D_type, d) : 0.f;
+    const float bias = p.dt_bias ? load_param(p.dt_bias, p.dt_bias_type, d) : 0.f;
+    S *const state = reinterpret_cast<S *>(p.state);
     DecRow<T> r[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t b0 = bb * U + u;
         const uint32_t b = b0 < uint32_t(p.batch) ? b0 : uint32_t(p.batch) - 1;
-        r[u].s = *reinterpret_cast<const float4 *>(p.state + int64_t(b) * p.state_batch_stride + int64_t(d) * p.state_d_stride + 4 * part);
+        const S *sp = state + int64_t(b) * p.state_batch_stride + int64_t(d) * p.state_d_stride + 4 * part;
+        if constexpr (std::is_same_v<S, float>) r[u].s = *reinterpret_cast<const float4 *>(sp);
+        else r[u].sw = *reinterpret_cast<const uint2 *>(sp);
         const T *Bb = reinterpret_cast<const T *>(p.B) + int64_t(b) * p.B_batch_stride + int64_t(g) * p.B_group_stride + 4 * part;
         const T *Cb = reinterpret_cast<const T *>(p.C) + int64_t(b) * p.C_batch_stride + int64_t(g) * p.C_group_stride + 4 * part;
         if constexpr (std::is_same_v<T, float>) {
@@ -315,13 +344,20 @@ state_update_vec16(const mm_state_update_params p, const uint32_t ratio, const u
         const float x = to_f32(r[u].x);
         const float dtx = dt * x;
         const float dl = dt * kLog2e;
-        float4 s = r[u].s;
+        float4 s;
+        if constexpr (std::is_same_v<S, float>) s = r[u].s;
+        else s = unpack4<S>(r[u].sw);
         s.x = __builtin_fmaf(s.x, fast_exp2(dl * a4.x), dtx * b4.x);
         s.y = __builtin_fmaf(s.y, fast_exp2(dl * a4.y), dtx * b4.y);
         s.z = __builtin_fmaf(s.z, fast_exp2(dl * a4.z), dtx * b4.z);
         s.w = __builtin_fmaf(s.w, fast_exp2(dl * a4.w), dtx * b4.w);
         const bool live = dr < dim && b < uint32_t(p.batch);
-        if (live) *reinterpret_cast<float4 *>(p.state + int64_t(b) * p.state_batch_stride + int64_t(dr) * p.state_d_stride + 4 * part) = s;
+        if (live) {
+            S *sp = state + int64_t(b) * p.state_batch_stride + int64_t(dr) * p.state_d_stride + 4 * part;
+            if constexpr (std::is_same_v<S, float>) *reinterpret_cast<float4 *>(sp) = s;
+            else *reinterpret_cast<uint2 *>(sp) = pack4<S>(s);
+        }
+        // y from the float32 state, before a 16-bit state is rounded.
         float y = __builtin_fmaf(s.x, c4.x, __builtin_fmaf(s.y, c4.y, __builtin_fmaf(s.z, c4.z, s.w * c4.w)));
         y += __shfl_xor(y, 1, 4);
         y += __shfl_xor(y, 2, 4);
@@ -495,7 +531,7 @@ int validate_bwd(const mm_scan_bwd_params *p) {
         return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, "
                                         "dim and dim / n_groups multiples of 16 and seqlen a multiple of 8");
 
-    const int64_t need = mm::bwd_workspace_bytes(*p);
+    const int64_t need = mm::bwd_workspace_min_bytes(*p);
     if (p->seqlen > 0 && (!p->workspace || p->workspace_bytes < need || reinterpret_cast<uintptr_t>(p->workspace) % 16))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: needs a 16-byte aligned workspace of %lld bytes (got %lld)",
                     (long long)need, (long long)p->workspace_bytes);
@@ -505,8 +541,11 @@ int validate_bwd(const mm_scan_bwd_params *p) {
 // ------------------------------------------------------------------------------------------------
 int validate_su(const mm_state_update_params *p) {
     if (!p) return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: params is NULL");
-    if (p->itype != MM_FLOAT32 && p->itype != MM_FLOAT16 && p->itype != MM_BFLOAT16)
+    auto known = [](mm_dtype t) { return t == MM_FLOAT32 || t == MM_FLOAT16 || t == MM_BFLOAT16; };
+    if (!known(p->itype))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: unknown itype %d", int(p->itype));
+    if (!known(p->state_type) || !known(p->D_type) || !known(p->dt_bias_type))
+        return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: unknown state_type, D_type or dt_bias_type");
     if (p->batch < 0 || p->dim < 0)
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_state_update: negative size");
     if (p->dstate < 1 || p->dstate > MM_SCAN_MAX_DSTATE)
@@ -519,11 +558,14 @@ int validate_su(const mm_state_update_params *p) {
     return MM_OK;
 }
 
-template <typename T, int SPL, int LPR>
+template <typename T, typename S, int SPL, int LPR>
 int launch_su(const mm_state_update_params &p, hipStream_t s) {
     const int64_t threads = p.batch * p.dim * LPR;
+    // gridDim.x * blockDim.x must stay below 2^32.
+    if ((threads + mm::kDecBlock - 1) / mm::kDecBlock >= (int64_t(1) << 24))
+        return fail(MM_ERR_UNSUPPORTED, "mm_state_update: batch * dim too large for one launch");
     dim3 grid(unsigned((threads + mm::kDecBlock - 1) / mm::kDecBlock));
-    hipLaunchKernelGGL((mm::state_update_kernel<T, SPL, LPR>), grid, dim3(mm::kDecBlock), 0, s, p, p.dim / p.n_groups);
+    hipLaunchKernelGGL((mm::state_update_kernel<T, S, SPL, LPR>), grid, dim3(mm::kDecBlock), 0, s, p, p.dim / p.n_groups);
     return mm::launch_status("state_update");
 }
 
@@ -533,31 +575,43 @@ bool su_vec16_ok(const mm_state_update_params &p) {
     const int64_t eb = elem_bytes(p.itype);
     auto al = [](const void *ptr, int64_t bytes) { return (reinterpret_cast<uintptr_t>(ptr) % uintptr_t(bytes)) == 0; };
     return p.dstate == 16 && p.state_dstate_stride == 1 && p.A_dstate_stride == 1 && p.B_dstate_stride == 1 &&
-           p.C_dstate_stride == 1 && al(p.state, 16) && p.state_batch_stride % 4 == 0 && p.state_d_stride % 4 == 0 &&
+           p.C_dstate_stride == 1 && al(p.state, 4 * elem_bytes(p.state_type)) && p.state_batch_stride % 4 == 0 &&
+           p.state_d_stride % 4 == 0 &&
            al(p.A, 16) && p.A_d_stride % 4 == 0 && al(p.B, 4 * eb) && al(p.C, 4 * eb) && p.B_batch_stride % 4 == 0 &&
            p.B_group_stride % 4 == 0 && p.C_batch_stride % 4 == 0 && p.C_group_stride % 4 == 0;
 }
 
-template <typename T, int U>
+template <typename T, typename S, int U>
 int launch_vec16(const mm_state_update_params &p, hipStream_t s) {
     const int64_t n_dblk = (p.dim + 63) / 64;
     const int64_t n_bblk = (p.batch + U - 1) / U;
-    hipLaunchKernelGGL((mm::state_update_vec16<T, U>), dim3(unsigned(n_bblk * n_dblk)), dim3(mm::kDecBlock), 0, s, p,
+    hipLaunchKernelGGL((mm::state_update_vec16<T, S, U>), dim3(unsigned(n_bblk * n_dblk)), dim3(mm::kDecBlock), 0, s, p,
                        uint32_t(p.dim / p.n_groups), uint32_t(n_dblk));
     return mm::launch_status("state_update");
 }
 
+template <typename T, typename S>
+int dispatch_su_state(const mm_state_update_params &p, hipStream_t s) {
+    // A 1-D grid of fewer than 2^24 workgroups of 256 lanes keeps gridDim.x * blockDim.x < 2^32.
+    const int64_t U = p.batch >= 4 ? 4 : 1;
+    if (su_vec16_ok(p) && p.dim < (int64_t(1) << 31) && p.batch < (int64_t(1) << 31) &&
+        ((p.batch + U - 1) / U) * ((p.dim + 63) / 64) < (int64_t(1) << 24)) {
+        // Four batch rows per workgroup share the loads of A, D and dt_bias (batch 256: 41 -> 37 us).
+        if (p.batch >= 4) return launch_vec16<T, S, 4>(p, s);
+        return launch_vec16<T, S, 1>(p, s);
+    }
+    if (p.dstate <= 16) return launch_su<T, S, 4, 4>(p, s);
+    if (p.dstate <= 64) return launch_su<T, S, 4, 16>(p, s);
+    return launch_su<T, S, 16, 16>(p, s);
+}
+
 template <typename T>
 int dispatch_su(const mm_state_update_params &p, hipStream_t s) {
-    if (su_vec16_ok(p) && p.dim < (int64_t(1) << 31) && p.batch < (int64_t(1) << 31) &&
-        ((p.batch + 3) / 4) * ((p.dim + 63) / 64) < (int64_t(1) << 31)) {
-        // Four batch rows per workgroup share the loads of A, D and dt_bias (batch 256: 41 -> 37 us).
-        if (p.batch >= 4) return launch_vec16<T, 4>(p, s);
-        return launch_vec16<T, 1>(p, s);
+    switch (p.state_type) {
+        case MM_FLOAT16: return dispatch_su_state<T, mm::f16_t>(p, s);
+        case MM_BFLOAT16: return dispatch_su_state<T, mm::bf16_t>(p, s);
+        default: return dispatch_su_state<T, float>(p, s);
     }
-    if (p.dstate <= 16) return launch_su<T, 4, 4>(p, s);
-    if (p.dstate <= 64) return launch_su<T, 4, 16>(p, s);
-    return launch_su<T, 16, 16>(p, s);
 }
 
 }  // namespace
@@ -605,7 +659,8 @@ int mm_scan_bwd(const mm_scan_bwd_params *params, void *stream) {
 
 int64_t mm_scan_bwd_workspace_size(const mm_scan_bwd_params *params) {
     if (!params || params->batch < 0 || params->dim < 0 || params->seqlen < 0 || params->dstate < 1 ||
-        params->dstate > MM_SCAN_MAX_DSTATE)
+        params->dstate > MM_SCAN_MAX_DSTATE || params->n_groups < 1 ||
+        (params->dim > 0 && params->dim % params->n_groups != 0))
         return 0;
     return mm::bwd_workspace_bytes(*params);
 }

@@ -625,7 +625,10 @@ int launch_general(const mm_scan_bwd_params &p, hipStream_t s) {
     while ((1 << np_log2) < p.dstate) ++np_log2;
     const int64_t rows_per_block = kGenThreads >> np_log2;
     const int64_t rows = p.batch * p.dim;
-    dim3 grid(unsigned((rows + rows_per_block - 1) / rows_per_block));
+    const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
+    if (blocks >= (int64_t(1) << 32) / kGenThreads)   // gridDim.x * blockDim.x must stay below 2^32
+        return set_error(MM_ERR_UNSUPPORTED, "mm_scan_bwd: batch * dim too large for one launch of the general kernel");
+    const dim3 grid(static_cast<unsigned>(blocks));
     hipLaunchKernelGGL((scan_bwd_general<T>), grid, dim3(kGenThreads), 0, s, p, p.dim / p.n_groups, np_log2);
     return launch_status("scan_bwd_general");
 }
@@ -644,7 +647,8 @@ int launch_fill(float *ptr, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int6
 bool fast_ok(const mm_scan_bwd_params &p) {
     if (p.P || p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
     if (p.dim % 16 != 0 || (p.dim / p.n_groups) % 16 != 0 || p.seqlen < 8 || p.seqlen % 8 != 0) return false;
-    if (p.batch * (p.dim / 16) > 0x7fffffff) return false;   // one workgroup per unit in a 1-D grid
+    // One 128-lane workgroup per unit in a 1-D grid: gridDim.x * blockDim.x must stay below 2^32.
+    if (p.batch * (p.dim / 16) >= (int64_t(1) << 25)) return false;
     const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
     auto al = [](const void *ptr, int64_t bytes) { return (reinterpret_cast<uintptr_t>(ptr) % uintptr_t(bytes)) == 0; };
     auto row2 = [&](const void *ptr, int64_t s0, int64_t s1) {
@@ -733,7 +737,9 @@ int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
     const int64_t ratio = p.dim / p.n_groups;
     SegPlan pl = seg_plan<T>(p);
     const int64_t need = (2 * fast_part_floats(p) + carry_floats(pl)) * int64_t(sizeof(float));
-    if (pl.tail_units > 0 && p.workspace_bytes < need)   // a workspace sized without the carries
+    // A workspace without room for the segment carries (sized by bwd_workspace_min_bytes, or queried
+    // under another round size: MM_BWD_SLOTS or another device) runs every unit as a whole row.
+    if (pl.tail_units > 0 && p.workspace_bytes < need)
         pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT};
     int rc = MM_OK;
     if (pl.main_units > 0) {
@@ -797,6 +803,11 @@ int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
     if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
     return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));
+}
+
+int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p) {
+    if (!p.P && bwd::fast_ok(p) && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
+    return bwd_workspace_bytes(p);
 }
 
 template <typename T>

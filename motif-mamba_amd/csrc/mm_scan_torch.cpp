@@ -667,7 +667,10 @@ at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::
                         const c10::optional<at::Tensor> &z_, const c10::optional<at::Tensor> &dt_bias_,
                         bool dt_softplus) {
     TORCH_CHECK(state.dim() == 3, "state must have shape (batch, dim, dstate)");
-    TORCH_CHECK(state.scalar_type() == at::ScalarType::Float, "state must be float32");
+    auto float_type = [](at::ScalarType t) {
+        return t == at::ScalarType::Float || t == at::ScalarType::Half || t == at::ScalarType::BFloat16;
+    };
+    TORCH_CHECK(float_type(state.scalar_type()), "state must be float32, float16 or bfloat16");
     const int64_t batch = state.size(0), dim = state.size(1), dstate = state.size(2);
     const auto itype = x.scalar_type();
     TORCH_CHECK(state.is_cuda() && x.is_cuda() && dt.is_cuda() && A.is_cuda() && B.is_cuda() && C.is_cuda());
@@ -690,12 +693,13 @@ at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::
     TORCH_CHECK(n_groups >= 1 && dim % n_groups == 0, "dim must be a multiple of n_groups");
     if (D_.has_value()) {
         CHECK_SHAPE(D_.value(), dim);
-        TORCH_CHECK(D_.value().scalar_type() == at::ScalarType::Float && D_.value().is_cuda(), "D must be float32 on the GPU");
+        TORCH_CHECK(float_type(D_.value().scalar_type()) && D_.value().is_cuda(),
+                    "D must be float32, float16 or bfloat16 on the GPU");
     }
     if (dt_bias_.has_value()) {
         CHECK_SHAPE(dt_bias_.value(), dim);
-        TORCH_CHECK(dt_bias_.value().scalar_type() == at::ScalarType::Float && dt_bias_.value().is_cuda(),
-                    "dt_bias must be float32 on the GPU");
+        TORCH_CHECK(float_type(dt_bias_.value().scalar_type()) && dt_bias_.value().is_cuda(),
+                    "dt_bias must be float32, float16 or bfloat16 on the GPU");
     }
     if (z_.has_value()) {
         CHECK_SHAPE(z_.value(), batch, dim);
@@ -713,15 +717,18 @@ at::Tensor state_update(const at::Tensor &state, const at::Tensor &x, const at::
     p.n_groups = n_groups;
     p.itype = to_mm(itype);
     p.dt_softplus = dt_softplus;
-    p.state = state.data_ptr<float>();
+    p.state = state.data_ptr();
+    p.state_type = to_mm(state.scalar_type());
     p.x = x.data_ptr();
     p.dt = dt.data_ptr();
     p.A = A.data_ptr<float>();
     p.B = B.data_ptr();
     p.C = C.data_ptr();
-    p.D = Dc.defined() ? Dc.data_ptr<float>() : nullptr;
+    p.D = Dc.defined() ? Dc.data_ptr() : nullptr;
+    p.D_type = Dc.defined() ? to_mm(Dc.scalar_type()) : MM_FLOAT32;
     p.z = z_.has_value() ? z_.value().data_ptr() : nullptr;
-    p.dt_bias = bc.defined() ? bc.data_ptr<float>() : nullptr;
+    p.dt_bias = bc.defined() ? bc.data_ptr() : nullptr;
+    p.dt_bias_type = bc.defined() ? to_mm(bc.scalar_type()) : MM_FLOAT32;
     p.out = out.data_ptr();
     p.state_batch_stride = state.stride(0);
     p.state_d_stride = state.stride(1);

@@ -3,6 +3,9 @@
 * ``libmm_scan.so``      -- the HIP kernels and the C ABI (include/mm_scan.h), built with hipcc.
 * ``mm_scan_torch*.so``  -- the PyTorch-ROCm binding (pybind), built with g++ against torch's
                             headers and linked to ``libmm_scan.so`` through an $ORIGIN rpath.
+* ``libmm_probe.so``     -- instruction-issue probes (csrc/mm_probe.hip) that bench.py runs to
+                            measure the transcendental and VALU issue rates behind its rooflines;
+                            not part of the scan library.
 
 Both land next to this file so they travel with the source tree. ``build()`` always recompiles.
 """
@@ -20,6 +23,7 @@ CSRC = os.path.join(SRC_ROOT, "csrc")
 REPO = os.path.dirname(SRC_ROOT)
 INCLUDE = os.path.join(REPO, "include")
 LIB_NAME = "libmm_scan.so"
+PROBE_NAME = "libmm_probe.so"
 EXT_NAME = "mm_scan_torch"
 ARCH = "gfx950"
 
@@ -68,7 +72,10 @@ def build_library(verbose: bool = True) -> str:
         obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    probe = os.path.join(PKG_DIR, PROBE_NAME)
+    cmds.append([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "mm_probe.hip"), "-o", probe + ".tmp"])
     _run_parallel(cmds, verbose)
+    os.replace(probe + ".tmp", probe)
     out = os.path.join(PKG_DIR, LIB_NAME)
     tmp = out + ".tmp"
     _run_parallel([[HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]], verbose)

@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must precede loading libmm_scan.so, see module docs
 
 from ._build import EXT_NAME, LIB_NAME, PKG_DIR, ext_filename
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib = None
 _ext = None

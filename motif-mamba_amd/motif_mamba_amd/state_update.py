@@ -10,7 +10,11 @@ B/C (batch, dstate) or (batch, n_groups, dstate), D/dt_bias (dim,); and the mult
 state (batch, nheads, headdim, dstate) with x/dt/z (batch, nheads, headdim), A (nheads, headdim,
 dstate), B/C (batch, n_groups, dstate), D/dt_bias (nheads, headdim), flattened to dim =
 nheads * headdim (group of a channel = head // (nheads / n_groups) = channel // (dim / n_groups)).
-The state must be float32.
+The state may be float32, float16 or bfloat16 (a bf16/fp16 model's ``allocate_inference_cache``
+creates it in ``dt_proj.weight.dtype``, ``mamba_simplemotif.py:410-414``), and so may D and
+dt_bias (passed uncast at ``mamba_simplemotif.py:397-399``): everything is widened to float32,
+the state is stored back in its own dtype with round-to-nearest-even, and the output is read
+from the float32 state, as the upstream kernel does.
 """
 from __future__ import annotations
 

@@ -18,8 +18,9 @@ op sequence so that the rounding behaviour is that of the reference on the same 
 un-vendored upstream ``selective_state_update`` (mamba_simplemotif.py:397-399) whose in-tree
 restatement is the torch fallback ``mamba_simplemotif.py:369-376``. The fallback runs the
 discretisation in the activation dtype; the upstream kernel and this restatement run it in
-float32 (dt + dt_bias promotes to float32), which is the behaviour the kernel must match.
-``mamba_step_fallback_ref`` keeps the fallback's literal dtype behaviour for comparison.
+float32 (dt + dt_bias promotes to float32), which is the behaviour the kernel must match. A state
+of a 16-bit dtype (the module allocates it in dt_proj.weight.dtype, mamba_simplemotif.py:410-414)
+is widened, updated in float32 and rounded back to its dtype; the output reads the float32 state.
 
 ``selective_scan_pq_ref`` restates the MotifMamba low-rank coupled scan
 ``selective_scan_full_matrix_cuda`` (ssi.py:262-350): h_t = exp(delta' A) h_{t-1} + delta' P (Q h_{t-1})
@@ -196,20 +197,6 @@ def selective_state_update_ref(state, x, dt, A, B, C, D=None, z=None, dt_bias=No
     if z is not None:
         out = out * F.silu(z.float())
     return out.to(x.dtype)
-
-
-def mamba_step_fallback_ref(state, x, dt, A, B, C, D, z, dt_bias):
-    """Literal dtype behaviour of the reference's torch fallback
-    (mamba_simplemotif.py:369-376): discretisation in dt's dtype, readout of
-    ``state.to(x.dtype)``. Updates ``state`` in place and returns y (x.dtype)."""
-    dtype = x.dtype
-    dtl = F.softplus(dt + dt_bias.to(dtype=dt.dtype))
-    dA = torch.exp(torch.einsum("bd,dn->bdn", dtl, A))
-    dB = torch.einsum("bd,bn->bdn", dtl, B)
-    state.copy_(state * dA + rearrange(x, "b d -> b d 1") * dB)
-    y = torch.einsum("bdn,bn->bd", state.to(dtype), C)
-    y = y + D.to(dtype) * x
-    return y * F.silu(z)
 
 
 def softplus_f64(x: float) -> float:

@@ -119,7 +119,8 @@ class StateUpdateParams(ctypes.Structure):
                 ("out_batch_stride", i64), ("out_d_stride", i64),
                 ("A_d_stride", i64), ("A_dstate_stride", i64),
                 ("B_batch_stride", i64), ("B_group_stride", i64), ("B_dstate_stride", i64),
-                ("C_batch_stride", i64), ("C_group_stride", i64), ("C_dstate_stride", i64)]
+                ("C_batch_stride", i64), ("C_group_stride", i64), ("C_dstate_stride", i64),
+                ("state_type", i32), ("D_type", i32), ("dt_bias_type", i32)]
 
 
 def header_functions():
@@ -219,6 +220,9 @@ def state_update_params(state, x, dt, A, B, C, out, D=None, z=None, dt_bias=None
     p.dt_softplus = int(bool(dt_softplus))
     p.state, p.x, p.dt, p.A, p.B, p.C = map(_ptr, (state, x, dt, A, B, C))
     p.D, p.z, p.dt_bias, p.out = _ptr(D), _ptr(z), _ptr(dt_bias), _ptr(out)
+    p.state_type = DTYPES[state.dtype]
+    p.D_type = DTYPES[D.dtype] if D is not None else 0
+    p.dt_bias_type = DTYPES[dt_bias.dtype] if dt_bias is not None else 0
     p.state_batch_stride, p.state_d_stride, p.state_dstate_stride = state.stride()
     p.x_batch_stride, p.x_d_stride = x.stride()
     p.dt_batch_stride, p.dt_d_stride = dt.stride()

@@ -20,7 +20,7 @@ def test_library_exports_every_header_function():
                           "mm_causal_conv1d_update", "mm_causal_conv1d_bwd", "mm_rms_norm_fwd"}
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.mm_abi_version() == 9
+    assert lib.mm_abi_version() == 10
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -94,6 +94,11 @@ def test_state_update_rejects_invalid_params():
     p.batch, p.dim, p.dstate, p.n_groups, p.itype = 1, 4, 16, 1, 2
     assert lib.mm_state_update(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
     assert "required" in lib.mm_last_error().decode()
+    for field in ("state_type", "D_type", "dt_bias_type"):
+        setattr(p, field, 5)
+        assert lib.mm_state_update(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+        assert "state_type, D_type or dt_bias_type" in lib.mm_last_error().decode()
+        setattr(p, field, 0)
     p.dstate = 300
     assert lib.mm_state_update(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
 
@@ -252,7 +257,14 @@ def test_scan_bwd_rejects_invalid_params():
     p.dstate = 300
     assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
     assert lib.mm_scan_bwd_workspace_size(ctypes.byref(p)) == 0
-    p.dstate, p.batch = 16, 0   # nothing to do: returns before touching any pointer or the GPU
+    p.dstate = 16
+    for groups in (0, -1, 3):   # no groups, or dim (8) not a multiple of them: size 0, call refused
+        p.n_groups = groups
+        assert lib.mm_scan_bwd_workspace_size(ctypes.byref(p)) == 0
+        assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
+        assert "n_groups" in lib.mm_last_error().decode()
+    p.n_groups = 1
+    p.batch = 0   # nothing to do: returns before touching any pointer or the GPU
     assert lib.mm_scan_bwd(ctypes.byref(p), None) == capi.MM_OK
 
 

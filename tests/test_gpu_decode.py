@@ -170,6 +170,147 @@ def test_config4_shapes_steps(batch):
     torch.testing.assert_close(g["state"].cpu(), ref_state, rtol=1e-4, atol=1e-5)
 
 
+def _ulp_tol(dtype):
+    """One unit in the last place of a 16-bit state, relative: the kernel and the oracle round the
+    same float32 value (up to float32 rounding) to the state dtype, so they may differ by one ulp
+    where that value sits on a rounding boundary."""
+    return {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dtype]
+
+
+# (batch, dim, dstate, groups): the vectorised dstate-16 kernel with one and four batch rows per
+# workgroup, groups, and the generic kernel (dstate 8; dstate 16 with a strided state below).
+STATE_CASES = [(3, 100, 16, 0), (4, 128, 16, 4), (64, 512, 16, 2), (2, 64, 8, 0), (5, 96, 32, 0)]
+
+
+@pytest.mark.parametrize("state_dtype", [torch.bfloat16, torch.float16], ids=["bf16state", "fp16state"])
+@pytest.mark.parametrize("param_dtype", ["f32", "model"], ids=["f32params", "modelparams"])
+@pytest.mark.parametrize("case", STATE_CASES, ids=[f"b{c[0]}d{c[1]}N{c[2]}G{c[3]}" for c in STATE_CASES])
+def test_state_update_16bit_state(case, state_dtype, param_dtype):
+    """The state in the model's dtype (mamba_simplemotif.py:410-414, 428-435) and D / dt_bias either
+    float32 or in the model's dtype (passed uncast at :397-399). Widened to float32, computed in
+    float32, the state rounded back to its dtype (round to nearest even), the output read from the
+    float32 state: selective_state_update_ref restates exactly that."""
+    batch, dim, N, G = case
+    _say(f"decode 16-bit state {case} {state_dtype} params {param_dtype}")
+    inp = _inputs(13, batch, dim, N, state_dtype, G)
+    inp["state"] = inp["state"].to(state_dtype)
+    if param_dtype == "model":
+        inp["D"] = inp["D"].to(state_dtype)
+        inp["dt_bias"] = inp["dt_bias"].to(state_dtype)
+    ref_state = inp["state"].clone()
+    exp = selective_state_update_ref(ref_state, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                     inp["z"], inp["dt_bias"], dt_softplus=True)
+    from motif_mamba_amd import selective_state_update
+    g = _gpu(inp)
+    out = selective_state_update(g["state"], g["x"], g["dt"], g["A"], g["B"], g["C"], g["D"], g["z"],
+                                 g["dt_bias"], dt_softplus=True)
+    torch.cuda.synchronize()
+    assert g["state"].dtype == state_dtype
+    torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+    torch.testing.assert_close(g["state"].cpu().float(), ref_state.float(), rtol=_ulp_tol(state_dtype), atol=1e-6)
+    # most elements round identically; a one-ulp split needs a float32 value on a rounding boundary
+    same = (g["state"].cpu() == ref_state).float().mean().item()
+    assert same > 0.98, f"only {same:.3f} of the rounded states agree exactly"
+
+
+@pytest.mark.parametrize("model_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_module_step_call_form(model_dtype):
+    """Mambamotif.step's call in a 16-bit model, as written at mamba_simplemotif.py:360-399: B and C
+    are column slices of x_proj's output (strided views), dt = dt_proj(dt) without its bias, the
+    state from allocate_inference_cache in dt_proj.weight.dtype, D and dt_proj.bias uncast (the
+    model's dtype after model.to(dtype)). Six steps from a zero state."""
+    import torch.nn.functional as F
+    from motif_mamba_amd import selective_state_update
+    _say(f"Mambamotif.step call form {model_dtype}")
+    batch, d_inner, N, R = 4, 256, 16, 8
+    gen = torch.Generator().manual_seed(21)
+    w_x = (torch.randn(R + 2 * N, d_inner, generator=gen) * 0.05).to(model_dtype)
+    w_dt = (torch.randn(d_inner, R, generator=gen) * 0.3).to(model_dtype)
+    lo, hi = math.log(1e-3), math.log(1e-1)
+    dt_bias = (torch.rand(d_inner, generator=gen) * (hi - lo) + lo).to(model_dtype)
+    A = -torch.arange(1, N + 1, dtype=torch.float32).repeat(d_inner, 1)
+    D = torch.ones(d_inner).to(model_dtype)
+    state = torch.zeros(batch, d_inner, N, dtype=model_dtype, device=DEV)
+    ref_state = torch.zeros(batch, d_inner, N, dtype=model_dtype)
+    gA, gD, gbias = A.to(DEV), D.to(DEV), dt_bias.to(DEV)
+    for step in range(6):
+        x = torch.randn(batch, d_inner, generator=gen).to(model_dtype)
+        z = torch.randn(batch, d_inner, generator=gen).to(model_dtype)
+        x_db = F.linear(x.float(), w_x.float()).to(model_dtype)          # (batch, R + 2N)
+        dt, B, C = torch.split(x_db, [R, N, N], dim=-1)
+        dt = F.linear(dt.float(), w_dt.float()).to(model_dtype)
+        gx, gz, gdb = x.to(DEV), z.to(DEV), x_db.to(DEV)
+        gdt, gB, gC = torch.split(gdb, [R, N, N], dim=-1)
+        gdt = dt.to(DEV)
+        assert not gB.is_contiguous()
+        exp = selective_state_update_ref(ref_state, x, dt, A, B, C, D, z, dt_bias, dt_softplus=True)
+        y = selective_state_update(state, gx, gdt, gA, gB, gC, gD, z=gz, dt_bias=gbias, dt_softplus=True)
+        torch.cuda.synchronize()
+        assert y.dtype == model_dtype
+        torch.testing.assert_close(y.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+        torch.testing.assert_close(state.cpu().float(), ref_state.float(), rtol=_ulp_tol(model_dtype), atol=1e-6)
+
+
+def test_16bit_state_strided_and_c_abi():
+    """A bf16 state as a strided cache slice (the generic kernel) through the ctypes C ABI, with
+    bf16 D and dt_bias."""
+    _say("decode bf16 state strided via ctypes")
+    lib = capi.load()
+    inp = _inputs(14, 3, 64, 16, torch.bfloat16)
+    inp["state"] = inp["state"].to(torch.bfloat16)
+    inp["D"] = inp["D"].to(torch.bfloat16)
+    inp["dt_bias"] = inp["dt_bias"].to(torch.bfloat16)
+    ref_state = inp["state"].clone()
+    exp = selective_state_update_ref(ref_state, inp["x"], inp["dt"], inp["A"], inp["B"], inp["C"], inp["D"],
+                                     inp["z"], inp["dt_bias"], dt_softplus=True)
+    g = _gpu(inp)
+    cache = torch.zeros(3, 64, 24, dtype=torch.bfloat16, device=DEV)
+    cache[:, :, 4:20] = g["state"]
+    view = cache[:, :, 4:20]
+    out = torch.empty(3, 64, dtype=torch.bfloat16, device=DEV)
+    p = capi.state_update_params(view, g["x"], g["dt"], g["A"], g["B"], g["C"], out, g["D"], g["z"],
+                                 g["dt_bias"], True)
+    assert lib.mm_state_update(ctypes.byref(p), capi.stream_handle()) == 0, lib.mm_last_error()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
+    torch.testing.assert_close(view.cpu().float(), ref_state.float(), rtol=2.0 ** -7, atol=1e-6)
+    assert torch.count_nonzero(cache[:, :, :4]) == 0 and torch.count_nonzero(cache[:, :, 20:]) == 0
+
+
+@pytest.mark.parametrize("batch", [1, 64, 256])
+def test_config4_full_length(batch):
+    """BASELINE config 4 over its whole length: 1,024 consecutive steps at d_inner 5120 (bf16
+    inputs, float32 state ~ N(0, 0.1), fresh inputs every step, drawn on the GPU from a seeded
+    generator). Channels are independent given B and C, so the oracle follows a fixed subset of
+    channels (every 41st, plus the first and last 16) for every batch row and step; their outputs
+    are compared every 32 steps and their states after the last step."""
+    from motif_mamba_amd import selective_state_update
+    _say(f"config-4 decode batch {batch}: 1024 steps")
+    dim, N, steps = 5120, 16, 1024
+    sub = torch.tensor(sorted(set(range(16)) | set(range(0, dim, 41)) | set(range(dim - 16, dim))))
+    gsub = sub.to(DEV)
+    gen = torch.Generator(device=DEV).manual_seed(40 + batch)
+    state = torch.randn(batch, dim, N, device=DEV, generator=gen) * 0.1
+    lo, hi = math.log(1e-3), math.log(1e-1)
+    dt_bias = torch.rand(dim, device=DEV, generator=gen) * (hi - lo) + lo
+    A = -torch.arange(1, N + 1, dtype=torch.float32, device=DEV).repeat(dim, 1).contiguous()
+    D = torch.ones(dim, device=DEV)
+    ref_state = state[:, gsub].cpu()
+    A_s, D_s, bias_s = A[gsub].cpu(), D[gsub].cpu(), dt_bias[gsub].cpu()
+    for s in range(steps):
+        x, dt, z = (torch.randn(batch, dim, device=DEV, generator=gen).to(torch.bfloat16) for _ in range(3))
+        B, C = (torch.randn(batch, N, device=DEV, generator=gen).to(torch.bfloat16) for _ in range(2))
+        out = selective_state_update(state, x, dt, A, B, C, D, z, dt_bias, dt_softplus=True)
+        exp = selective_state_update_ref(ref_state, x[:, gsub].cpu(), dt[:, gsub].cpu(), A_s, B.cpu(), C.cpu(),
+                                         D_s, z[:, gsub].cpu(), bias_s, dt_softplus=True)
+        if s % 32 == 31:
+            torch.testing.assert_close(out[:, gsub].cpu().float(), exp.float(), rtol=3e-2, atol=5e-2,
+                                       msg=lambda m: f"step {s}: {m}")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(state[:, gsub].cpu(), ref_state, rtol=1e-4, atol=1e-5)
+    assert torch.isfinite(state).all()
+
+
 def test_state_update_c_abi_direct():
     _say("decode C ABI via ctypes")
     lib = capi.load()

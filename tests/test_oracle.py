@@ -240,6 +240,51 @@ def test_decode_grouped_equals_per_group():
         torch.testing.assert_close(s, s_full[:, sl])
 
 
+@pytest.mark.parametrize("state_dtype", [torch.bfloat16, torch.float16])
+def test_decode_16bit_state_known_answer(state_dtype):
+    """Hand-worked step of a 16-bit state (the upstream kernel: widen, update in float32, store with
+    round-to-nearest-even, read y from the float32 state). A = 0 makes the decay 1, so the new state
+    is exactly s + dt' B x. With s = 1 and an increment of a quarter ulp, half an ulp and three
+    quarters of an ulp, RNE stores 1, 1 (tie to even) and 1 + ulp; y = C . state reads the unrounded
+    float32 sums (a y from the rounded state, or truncation instead of RNE, fails here)."""
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[state_dtype]
+    incs = torch.tensor([0.25 * ulp, 0.5 * ulp, 0.75 * ulp, 1.5 * ulp])      # 1.5 ulp: tie from odd
+    state = torch.ones(1, 4, 1, dtype=state_dtype)
+    state[0, 3, 0] = 1.0 + ulp                                               # odd last bit
+    x = incs[None, :].clone()                                                # dt' B x = inc
+    dt = torch.ones(1, 4)
+    A = torch.zeros(4, 1)
+    B = torch.ones(1, 1)
+    C = torch.ones(1, 1)
+    y = selective_state_update_ref(state, x, dt, A, B, C, dt_softplus=False)
+    exact = torch.tensor([1 + 0.25 * ulp, 1 + 0.5 * ulp, 1 + 0.75 * ulp, 1 + 2.5 * ulp])
+    assert torch.equal(y[0].double(), exact.double())
+    stored = torch.tensor([1.0, 1.0, 1.0 + ulp, 1.0 + 2 * ulp], dtype=torch.float64)
+    assert torch.equal(state[0, :, 0].double(), stored)
+    assert state.dtype == state_dtype
+
+
+def test_decode_16bit_state_steps_track_float32_state():
+    """Steps of a bf16 state stay within the accumulated rounding of a float32 run: each step
+    rounds once (at most half an ulp of the largest state seen), and the decay (|a| <= 1) never
+    amplifies earlier errors, so after k steps the difference is at most k/2 such ulps."""
+    g = torch.Generator().manual_seed(38)
+    batch, dim, N, steps = 2, 8, 4, 12
+    s32 = torch.randn(batch, dim, N, generator=g)
+    s16 = s32.to(torch.bfloat16)
+    s32 = s16.float()
+    A = -torch.rand(dim, N, generator=g)
+    peak = s32.abs().max().item()
+    for _ in range(steps):
+        x, dt = (torch.randn(batch, dim, generator=g) for _ in range(2))
+        B, C = (torch.randn(batch, N, generator=g) for _ in range(2))
+        selective_state_update_ref(s32, x, dt, A, B, C, dt_softplus=True)
+        selective_state_update_ref(s16, x, dt, A, B, C, dt_softplus=True)
+        peak = max(peak, s32.abs().max().item(), s16.float().abs().max().item())
+    err = (s16.float() - s32).abs().max().item()
+    assert 0 < err <= steps * 2.0 ** -8 * peak * 1.01
+
+
 def test_chunk_states_prod_a():
     case = _rand_case(37, batch=1, dim=3, L=10, N=2)
     pa = chunk_states_ref(case["delta"], case["A"], case["delta_bias"], True, chunk=4)
