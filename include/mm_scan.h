@@ -291,6 +291,20 @@ int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params);
  * counterpart in the reference: the checkpoints the backward would otherwise recompute). */
 int64_t mm_scan_fwd_tile_states_size(const mm_scan_fwd_params *params);
 
+/* Size of the static device scratch behind mm_scan_fwd_noalloc (4 MiB per GPU, held from the
+ * library's load until the process ends). */
+#define MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+/* mm_scan_fwd for callers that cannot allocate device memory: code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc. No counterpart in the reference. Same results
+ * as mm_scan_fwd with a workspace of mm_scan_fwd_workspace_size() bytes; params->workspace and
+ * workspace_bytes are ignored: the sequence-segment scratch is a static device array of
+ * MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES per GPU (every request the segment heuristic selects needs
+ * less than 2.5 MiB); a request needing more is refused with MM_ERR_INVALID_ARGUMENT. The call
+ * allocates and frees nothing. All calls on one GPU share that GPU's scratch: calls that overlap
+ * in time on one GPU (other streams, other threads) race and must be serialised by the caller. */
+int mm_scan_fwd_noalloc(const mm_scan_fwd_params *params, void *stream);
+
 /* Backward scan. Replaces selective_scan_cuda.bwd (selective_scan.cpp:415-612, pybind :628-637). */
 int mm_scan_bwd(const mm_scan_bwd_params *params, void *stream);
 

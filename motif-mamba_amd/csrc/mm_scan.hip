@@ -20,6 +20,8 @@
 // The tiled forward kernel lives in mm_scan_tiled.hip.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <stdarg.h>
 #include <stdlib.h>
 #include <stdio.h>
@@ -374,6 +376,12 @@ state_update_vec16(const mm_state_update_params p, const uint32_t ratio, const u
 // ================================================================================================
 // Host side: validation, dispatch, error reporting.
 // ================================================================================================
+// Scratch of mm_scan_fwd_noalloc: the sequence-segment carries of the dstate-16 forward. One copy
+// per GPU (a device variable of the code object), held until the process ends. Host code never
+// passes `scratch` itself to a kernel or copy: it is a host-side stand-in whose device address
+// differs per GPU; noalloc_scratch() looks that address up once per device.
+static __device__ __align__(256) float scratch[MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -614,6 +622,31 @@ int dispatch_su(const mm_state_update_params &p, hipStream_t s) {
     }
 }
 
+// The device address of `scratch` on the current GPU, looked up with hipGetSymbolAddress on the
+// first call on each device (with that device current) and kept per device; later calls on the
+// device reuse it. Concurrent first calls may both look it up; they store the same address.
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch_ptr[kMaxDevices];
+
+int noalloc_scratch(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(int(e), "mm_scan_fwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(MM_ERR_UNSUPPORTED, "mm_scan_fwd_noalloc: device index %d out of range", dev);
+    void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (ptr == nullptr) {
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            return fail(e != hipSuccess ? int(e) : MM_ERR_UNSUPPORTED,
+                        "mm_scan_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+    *out = ptr;
+    return MM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -678,6 +711,31 @@ int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params) {
     if (validate_fwd(params) != MM_OK) return 0;
     if (params->batch == 0 || params->dim == 0 || params->P) return 0;
     return mm::segment_workspace_bytes(*params, mm::segment_count(*params));
+}
+
+int mm_scan_fwd_noalloc(const mm_scan_fwd_params *params, void *stream) {
+    int rc = validate_fwd(params);
+    if (rc != MM_OK) return rc;
+    if (params->batch == 0 || params->dim == 0) return MM_OK;
+    mm_scan_fwd_params p = *params;
+    p.workspace = nullptr;
+    p.workspace_bytes = 0;
+    const int64_t need = mm_scan_fwd_workspace_size(params);
+    if (need > int64_t(MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES))
+        return fail(MM_ERR_INVALID_ARGUMENT,
+                    "mm_scan_fwd_noalloc: the request needs %lld bytes of scratch, more than the %d-byte static "
+                    "buffer; use mm_scan_fwd with a workspace", (long long)need, MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES);
+    if (need > 0) {
+        rc = noalloc_scratch(&p.workspace);
+        if (rc != MM_OK) return rc;
+        p.workspace_bytes = MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES;
+    }
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (p.itype) {
+        case MM_FLOAT32: return dispatch_fwd<float>(p, s);
+        case MM_FLOAT16: return dispatch_fwd<mm::f16_t>(p, s);
+        default: return dispatch_fwd<mm::bf16_t>(p, s);
+    }
 }
 
 const char *mm_last_error(void) { return g_err; }

@@ -137,6 +137,8 @@ def load():
     lib.mm_scan_fwd.restype = ctypes.c_int
     lib.mm_state_update.argtypes = [ctypes.POINTER(StateUpdateParams), vp]
     lib.mm_state_update.restype = ctypes.c_int
+    lib.mm_scan_fwd_noalloc.argtypes = [ctypes.POINTER(ScanFwdParams), vp]
+    lib.mm_scan_fwd_noalloc.restype = ctypes.c_int
     lib.mm_scan_fwd_workspace_size.argtypes = [ctypes.POINTER(ScanFwdParams)]
     lib.mm_scan_fwd_workspace_size.restype = ctypes.c_int64
     lib.mm_scan_fwd_tile_states_size.argtypes = [ctypes.POINTER(ScanFwdParams)]

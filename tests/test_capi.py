@@ -14,7 +14,8 @@ from tests import capi
 def test_library_exports_every_header_function():
     lib = capi.load()
     names = capi.header_functions()
-    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_workspace_size", "mm_scan_fwd_tile_states_size",
+    assert set(names) == {"mm_scan_fwd", "mm_scan_fwd_noalloc", "mm_scan_fwd_workspace_size",
+                          "mm_scan_fwd_tile_states_size",
                           "mm_scan_bwd", "mm_scan_bwd_workspace_size",
                           "mm_state_update", "mm_last_error", "mm_abi_version", "mm_causal_conv1d_fwd",
                           "mm_causal_conv1d_update", "mm_causal_conv1d_bwd", "mm_rms_norm_fwd"}
@@ -74,9 +75,10 @@ def test_scan_fwd_rejects_invalid_params(mutate, needle):
     lib = capi.load()
     p = _valid_looking_params()
     mutate(p)
-    rc = lib.mm_scan_fwd(ctypes.byref(p), None)
-    assert rc == capi.MM_ERR_INVALID_ARGUMENT
-    assert needle in lib.mm_last_error().decode()
+    for entry in (lib.mm_scan_fwd, lib.mm_scan_fwd_noalloc):   # same validation, nothing launched
+        rc = entry(ctypes.byref(p), None)
+        assert rc == capi.MM_ERR_INVALID_ARGUMENT
+        assert needle in lib.mm_last_error().decode()
 
 
 def test_scan_fwd_null_params_and_empty_batch():
