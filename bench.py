@@ -457,7 +457,10 @@ def cpu_baselines(torch):
 # (transcendental, VALU) counts; kind 4 runs kind 1 on even waves and kind 0 on odd waves.
 PROBE_KINDS = {0: ("v_fma_f32", 0, 32), 1: ("v_exp_f32", 32, 0), 2: ("v_mul_f32_dpp row_newbcast", 0, 32),
                3: ("v_exp_f32 + 4 v_fma_f32 (one wave)", 8, 32), 4: ("v_exp_f32 / v_fma_f32 (alternate waves)", 16, 16),
-               5: ("v_fmac_f32_dpp row_newbcast", 0, 32), 6: ("v_exp_f32 + v_fma_f32 (one wave)", 16, 16)}
+               5: ("v_fmac_f32_dpp row_newbcast", 0, 32), 6: ("v_exp_f32 + v_fma_f32 (one wave)", 16, 16),
+               7: ("scan core (per state update: exp2, 2 DPP, 2 VALU)", 16, 64),
+               8: ("scan core, plain VALU instead of DPP", 16, 64),
+               9: ("scan core without exp2", 0, 64)}
 
 
 def issue_rates(torch, waves=(2, 3, 4, 8), iters=2000):
@@ -505,9 +508,12 @@ def issue_rates(torch, waves=(2, 3, 4, 8), iters=2000):
             clk_hz = (tk[:, 0].sum() / tk[:, 1].sum()).item() * wall_khz.value * 1e3
             clocks.append(clk_hz)
             instr_simd = W * iters * (n_trans + n_valu)        # wave64 instructions per SIMD
-            rows.append({"waves_per_simd": W, "ms": round(best, 4), "clock_mhz": round(clk_hz / 1e6, 1),
-                         "simd_cycles_per_instr": round(best * 1e-3 * clk_hz / instr_simd, 3),
-                         "lane_ops_per_s": n_simd * instr_simd * 64 / (best * 1e-3)})
+            row = {"waves_per_simd": W, "ms": round(best, 4), "clock_mhz": round(clk_hz / 1e6, 1),
+                   "simd_cycles_per_instr": round(best * 1e-3 * clk_hz / instr_simd, 3),
+                   "lane_ops_per_s": n_simd * instr_simd * 64 / (best * 1e-3)}
+            if kind >= 7:   # the scan-core kinds: 16 state updates per lane and round
+                row["simd_cycles_per_wave_update"] = round(best * 1e-3 * clk_hz / (W * iters * 16), 3)
+            rows.append(row)
             del out, ticks
         res["kinds"][name] = rows
     res["clock_mhz"] = round(sum(clocks) / len(clocks) / 1e6, 1)

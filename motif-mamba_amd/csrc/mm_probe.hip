@@ -18,6 +18,10 @@
 //   4  waves alternate: even waves kind 1, odd waves kind 0 (different waves: do they overlap?)
 //   5  32 x v_fmac_f32_dpp row_newbcast
 //   6  16 x v_exp_f32 + 16 x v_fma_f32, interleaved
+//   7  the dstate-16 forward's scan core, 16 state updates per lane and round as in the kernel:
+//      per step and state exp2(dt' A), B dt'u by DPP row broadcast, the state FMA, y += C h by DPP
+//   8  kind 7 with plain VGPR operands instead of the DPP broadcasts
+//   9  kind 7 without the exp2 (the decay taken as the exp argument itself)
 // Every loop is bounded by `iters`; no kernel waits on another wave.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -28,6 +32,100 @@ namespace {
 #define EXP(a) asm volatile("v_exp_f32 %0, %0" : "+v"(a))
 #define MULDPP(a) asm volatile("v_mul_f32_dpp %0, %1, %0 row_newbcast:3 row_mask:0xf bank_mask:0xf" : "+v"(a) : "v"(src))
 #define FMACDPP(a) asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:5 row_mask:0xf bank_mask:0xf" : "+v"(a) : "v"(src), "v"(m))
+
+template <int LANE>
+__device__ __forceinline__ float row_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + LANE, 0xf, 0xf, false));
+}
+template <int LANE>
+__device__ __forceinline__ void fmac_row_bcast(float &acc, float src, float x) {
+    asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(src), "v"(x), "i"(LANE));
+}
+
+// One round of kind 7/8/9: 4 steps x 2 states. dts/dus are the step's dt' and dt'u (as the scan
+// reads them from LDS), bv/cv hold B and C values that the DPP forms broadcast along the row.
+template <int KIND, int R, int J>
+__device__ __forceinline__ void scan_prep(const float (&At)[2], const float (&dts)[4], const float (&dus)[4],
+                                          const float (&bv)[4], float (&av)[4][2], float (&bbv)[4][2]) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const float arg = dts[J] * At[k];
+        av[J][k] = KIND == 9 ? arg : __builtin_amdgcn_exp2f(arg);
+    }
+    if constexpr (KIND == 8) {
+        bbv[J][0] = bv[J] * dus[J];
+        bbv[J][1] = bv[(J + 1) & 3] * dus[J];
+    } else {
+        bbv[J][0] = row_bcast<(R * 4 + J) & 7>(bv[J]) * dus[J];
+        bbv[J][1] = row_bcast<8 + ((R * 4 + J) & 7)>(bv[J]) * dus[J];
+    }
+}
+
+template <int KIND, int R, int J>
+__device__ __forceinline__ void scan_step(float (&h)[2], const float (&cv)[4], const float (&av)[4][2],
+                                          const float (&bbv)[4][2], float (&pv)[4]) {
+    h[0] = __builtin_fmaf(av[J][0], h[0], bbv[J][0]);
+    h[1] = __builtin_fmaf(av[J][1], h[1], bbv[J][1]);
+    float acc;
+    if constexpr (KIND == 8) {
+        acc = cv[J] * h[0];
+        acc = __builtin_fmaf(cv[(J + 1) & 3], h[1], acc);
+    } else {
+        acc = row_bcast<(R * 4 + J) & 7>(cv[J]) * h[0];
+        fmac_row_bcast<8 + ((R * 4 + J) & 7)>(acc, cv[J], h[1]);
+    }
+    pv[J] = acc;
+}
+
+template <int KIND, int R>
+__device__ __forceinline__ void scan_round(float (&h)[2], const float (&At)[2], const float (&dts)[4], const float (&dus)[4],
+                                           const float (&bv)[4], const float (&cv)[4], float &ysum) {
+    float av[4][2], bbv[4][2], pv[4];
+    scan_prep<KIND, R, 0>(At, dts, dus, bv, av, bbv);
+    scan_prep<KIND, R, 1>(At, dts, dus, bv, av, bbv);
+    scan_prep<KIND, R, 2>(At, dts, dus, bv, av, bbv);
+    scan_prep<KIND, R, 3>(At, dts, dus, bv, av, bbv);
+    scan_step<KIND, R, 0>(h, cv, av, bbv, pv);
+    scan_step<KIND, R, 1>(h, cv, av, bbv, pv);
+    scan_step<KIND, R, 2>(h, cv, av, bbv, pv);
+    scan_step<KIND, R, 3>(h, cv, av, bbv, pv);
+    // the y partials leave the round (the kernel stores them to LDS with one 16-byte write)
+    asm volatile("" ::"v"(pv[0]), "v"(pv[1]), "v"(pv[2]), "v"(pv[3]));
+    ysum = pv[3];
+}
+
+template <int KIND>
+__global__ void __launch_bounds__(256) scan_core_probe(int iters, float *out, uint64_t *ticks) {
+    const int tid = blockIdx.x * 256 + threadIdx.x;
+    const int wave = tid >> 6;
+    const float f = threadIdx.x * 1e-6f;
+    float h[2] = {0.f, 0.f};
+    const float At[2] = {-1.4427f - f, -2.885f + f};
+    float dts[4] = {0.01f + f, 0.02f, 0.03f, 0.04f - f}, dus[4] = {0.1f, 0.2f + f, 0.3f, 0.4f};
+    float bv[4] = {1.f + f, 0.5f, -0.5f, 0.25f}, cv[4] = {0.3f, -0.2f + f, 0.1f, 0.7f};
+    float ysum = 0.f;
+    // Two wait states between the last VALU writes of the DPP sources and their first DPP read.
+#pragma unroll
+    for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+    const uint64_t t0 = __builtin_amdgcn_s_memtime();
+    const uint64_t w0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+        // the step values change every round, as the LDS reads of the kernel make them
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(dts[j]), "+v"(dus[j]));
+        scan_round<KIND, 0>(h, At, dts, dus, bv, cv, ysum);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(dts[j]), "+v"(dus[j]));
+        scan_round<KIND, 1>(h, At, dts, dus, bv, cv, ysum);
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime();
+    const uint64_t w1 = __builtin_amdgcn_s_memrealtime();
+    out[tid] = h[0] + h[1] + ysum;
+    if ((threadIdx.x & 63) == 0) {
+        ticks[2 * wave] = t1 - t0;
+        ticks[2 * wave + 1] = w1 - w0;
+    }
+}
 
 template <int KIND>
 __global__ void __launch_bounds__(256) issue_probe(int iters, float *out, uint64_t *ticks) {
@@ -100,7 +198,7 @@ __global__ void __launch_bounds__(256) issue_probe(int iters, float *out, uint64
 
 extern "C" {
 
-// Launches probe `kind` (0-6) as `blocks` workgroups of 256 lanes for `iters` rounds on `stream`.
+// Launches probe `kind` (0-9) as `blocks` workgroups of 256 lanes for `iters` rounds on `stream`.
 // `out` holds blocks * 256 floats; `ticks` holds 2 x 64-bit counters per wave (blocks * 8 values):
 // shader-clock ticks, then constant-clock ticks, of the wave's loop. Returns 0 or a hipError_t.
 int mm_probe_launch(int kind, int blocks, int iters, float *out, uint64_t *ticks, void *stream) {
@@ -114,6 +212,9 @@ int mm_probe_launch(int kind, int blocks, int iters, float *out, uint64_t *ticks
         case 4: hipLaunchKernelGGL(issue_probe<4>, dim3(blocks), dim3(256), 0, s, iters, out, ticks); break;
         case 5: hipLaunchKernelGGL(issue_probe<5>, dim3(blocks), dim3(256), 0, s, iters, out, ticks); break;
         case 6: hipLaunchKernelGGL(issue_probe<6>, dim3(blocks), dim3(256), 0, s, iters, out, ticks); break;
+        case 7: hipLaunchKernelGGL(scan_core_probe<7>, dim3(blocks), dim3(256), 0, s, iters, out, ticks); break;
+        case 8: hipLaunchKernelGGL(scan_core_probe<8>, dim3(blocks), dim3(256), 0, s, iters, out, ticks); break;
+        case 9: hipLaunchKernelGGL(scan_core_probe<9>, dim3(blocks), dim3(256), 0, s, iters, out, ticks); break;
         default: return int(hipErrorInvalidValue);
     }
     return int(hipGetLastError());

@@ -40,6 +40,10 @@ def _load():
                       dp, i64, i64, i64, dp, i64, i64, i64,
                       dp, dp, ctypes.c_int, dp, dp, dp, i64, dp]
         f.restype = None
+        h = lib.mm_oracle_scan_bwd_rows_f64
+        h.argtypes = [i64, i64, i64, dp, dp, dp, dp, dp, i64, i64, dp, i64, i64,
+                      dp, dp, ctypes.c_int, dp, dp, dp, dp, dp, dp, dp, dp, dp]
+        h.restype = None
         g = lib.mm_oracle_scan_pq_rows_f64
         g.argtypes = [i64, i64, i64, i64, dp, dp, dp, dp,
                       dp, i64, i64, i64, dp, i64, i64, i64,
@@ -135,3 +139,103 @@ def scan_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus
                                     _p(Dr), _p(br), int(bool(delta_softplus)),
                                     _p(out), _p(outz), _p(last), int(chunk), _p(hch))
     return {"out": out, "out_z": outz, "last_state": last, "h_chunks": hch}
+
+
+def scan_all_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False, batches=None):
+    """Float64 scan of every (batch, dim) row of a variable-B/C selective scan, for full-size
+    checks: the rows of one (batch, group) share their B/C slice, so each (batch, group) is one
+    call with a B/C row stride of 0 (no per-row copies of B/C). B/C are (batch, N, L) or
+    (batch, G, N, L). Returns float64 numpy arrays out_z (or out, without z) of shape
+    (len(batches), dim, L) and last_state (len(batches), dim, N) for ``batches`` (all by default).
+    """
+    batch, dim, L = u.shape
+    N = A.shape[1]
+    G = B.shape[1] if B.dim() == 4 else 1
+    gsz = dim // G
+    batches = list(range(batch)) if batches is None else list(batches)
+    ys = np.zeros((len(batches), dim, L))
+    last = np.zeros((len(batches), dim, N))
+
+    def f64(x):
+        return np.ascontiguousarray(x.detach().cpu().double().numpy())
+
+    Ad = f64(A)
+    Dd = f64(D) if D is not None else None
+    bd = f64(delta_bias) if delta_bias is not None else None
+    for i, b in enumerate(batches):
+        for g in range(G):
+            sl = slice(g * gsz, (g + 1) * gsz)
+            ur, dr = f64(u[b, sl]), f64(delta[b, sl])
+            zr = f64(z[b, sl]) if z is not None else None
+            Bg = f64(B[b, g] if B.dim() == 4 else B[b])
+            Cg = f64(C[b, g] if C.dim() == 4 else C[b])
+            out = np.zeros((gsz, L))
+            outz = np.zeros((gsz, L)) if zr is not None else None
+            lst = np.zeros((gsz, N))
+            _load().mm_oracle_scan_rows_f64(gsz, L, N, _p(ur), _p(dr), _p(zr), _p(np.ascontiguousarray(Ad[sl])),
+                                            _p(Bg), 0, L, 1, _p(Cg), 0, L, 1,
+                                            _p(np.ascontiguousarray(Dd[sl]) if Dd is not None else None),
+                                            _p(np.ascontiguousarray(bd[sl]) if bd is not None else None),
+                                            int(bool(delta_softplus)), _p(out), _p(outz), _p(lst), 0, None)
+            ys[i, sl] = outz if outz is not None else out
+            last[i, sl] = lst
+    return ys, last
+
+
+def scan_bwd_all_rows(u, delta, A, B, C, dout, D=None, z=None, delta_bias=None, delta_softplus=False):
+    """Float64 gradients of a variable-B/C selective scan (``mm_oracle_scan_bwd_rows_f64``, the
+    adjoint recurrences of brute.scan_bwd_brute), one call per (batch, group) whose rows share the
+    group's B/C slice. B/C are (batch, N, L) or (batch, G, N, L); dB/dC come back in B's/C's shape.
+    Returns a dict of float64 numpy arrays du, ddelta, dz (None without z), dA, dB, dC, dD,
+    ddelta_bias (None when D / delta_bias are None)."""
+    batch, dim, L = u.shape
+    N = A.shape[1]
+    G = B.shape[1] if B.dim() == 4 else 1
+    gsz = dim // G
+    if N > 256:
+        raise ValueError("dstate <= 256")
+
+    def f64(x):
+        return np.ascontiguousarray(x.detach().cpu().double().numpy())
+
+    Ad = f64(A)
+    Dd = f64(D) if D is not None else None
+    bd = f64(delta_bias) if delta_bias is not None else None
+    res = {"du": np.zeros((batch, dim, L)), "ddelta": np.zeros((batch, dim, L)),
+           "dz": np.zeros((batch, dim, L)) if z is not None else None, "dA": np.zeros((dim, N)),
+           "dB": np.zeros(tuple(B.shape)), "dC": np.zeros(tuple(C.shape)),
+           "dD": np.zeros(dim) if D is not None else None,
+           "ddelta_bias": np.zeros(dim) if delta_bias is not None else None}
+    for b in range(batch):
+        for g in range(G):
+            sl = slice(g * gsz, (g + 1) * gsz)
+            ur, dr, gr = f64(u[b, sl]), f64(delta[b, sl]), f64(dout[b, sl])
+            zr = f64(z[b, sl]) if z is not None else None
+            Bg = f64(B[b, g] if B.dim() == 4 else B[b])
+            Cg = f64(C[b, g] if C.dim() == 4 else C[b])
+            du, dd = np.zeros((gsz, L)), np.zeros((gsz, L))
+            dz = np.zeros((gsz, L)) if zr is not None else None
+            dA, dD, db = np.zeros((gsz, N)), np.zeros(gsz), np.zeros(gsz)
+            dB, dC = np.zeros((N, L)), np.zeros((N, L))
+            _load().mm_oracle_scan_bwd_rows_f64(
+                gsz, L, N, _p(ur), _p(dr), _p(zr), _p(np.ascontiguousarray(Ad[sl])), _p(Bg), L, 1, _p(Cg), L, 1,
+                _p(np.ascontiguousarray(Dd[sl]) if Dd is not None else None),
+                _p(np.ascontiguousarray(bd[sl]) if bd is not None else None), int(bool(delta_softplus)), _p(gr),
+                _p(du), _p(dd), _p(dz), _p(dA), _p(dD), _p(db), _p(dB), _p(dC))
+            res["du"][b, sl], res["ddelta"][b, sl] = du, dd
+            if dz is not None:
+                res["dz"][b, sl] = dz
+            res["dA"][sl] += dA
+            if res["dD"] is not None:
+                res["dD"][sl] += dD
+            if res["ddelta_bias"] is not None:
+                res["ddelta_bias"][sl] += db
+            if B.dim() == 4:
+                res["dB"][b, g] += dB
+            else:
+                res["dB"][b] += dB
+            if C.dim() == 4:
+                res["dC"][b, g] += dC
+            else:
+                res["dC"][b] += dC
+    return res

@@ -6,9 +6,11 @@ are compared with the exact (float64) gradients of the oracle ``selective_scan_r
 inputs (``oracle.ssm_ref.selective_scan_bwd_ref``, pinned in tests/test_oracle_bwd.py).
 
 Tolerances: the forward's (north_star) pair (rtol, atol) = (1e-4, 1e-5) for fp32 and (3e-2, 5e-2)
-for 16-bit inputs, element-wise as |err| <= rtol |exact| + atol max(1, max |exact|): the gradients
-of A, B, C, D and delta_bias are sums over rows and steps, whose rounding grows with the tensor's
-scale, so the absolute part is taken relative to it.
+for 16-bit inputs, element by element: |err| <= rtol |exact| + atol for du, ddelta and dz, and
+|err| <= rtol |exact| + atol max(1, max |exact|) for the reduced gradients dA, dB, dC, dD and
+ddelta_bias (sums over rows and steps, whose rounding grows with the tensor's scale; see _check).
+At the full benchmark shapes every element is compared with the float64 adjoint of
+oracle/scan_f64.c.
 """
 import ctypes
 import sys
@@ -35,15 +37,26 @@ def _tol(dtype):
     return (1e-4, 1e-5) if dtype == torch.float32 else (3e-2, 5e-2)
 
 
+# Gradients with one value per element of an input (du, ddelta, dz) are held element by element
+# to |err| <= rtol |exact| + atol. The reduced gradients (dA, dD, ddelta_bias: sums over batch
+# rows and steps; dB, dC: sums over the channels of a group; dP, dQ: sums over rows and steps)
+# add thousands of terms of both signs: their float32 rounding is relative to the sum of the
+# terms' magnitudes, which the result's own magnitude can fall far below where terms cancel, so
+# the absolute part of their bound is taken relative to the tensor's scale, max(1, max |exact|).
+ELEMENTWISE = {"du", "ddelta", "dz"}
+
+
 def _check(got, exact, dtype, what):
     rtol, atol = _tol(dtype)
     got = got.double().cpu()
-    scale = max(1.0, exact.abs().max().item()) if exact.numel() else 1.0
+    exact = exact.double()
+    elementwise = any(tok in ELEMENTWISE for tok in what.split())
+    scale = 1.0 if elementwise else (max(1.0, exact.abs().max().item()) if exact.numel() else 1.0)
     err = (got - exact).abs()
     bound = rtol * exact.abs() + atol * scale
     bad = err > bound
     assert not bool(bad.any()), (f"{what}: {int(bad.sum())}/{err.numel()} beyond tolerance; max err "
-                                 f"{err.max().item():.3g} (scale {scale:.3g})")
+                                 f"{err.max().item():.3g} (scale {scale:.3g}, elementwise {elementwise})")
 
 
 def _dout(seed, shape, dtype):
@@ -233,14 +246,14 @@ def test_bwd_dstate16_kernel_matches_general_kernel():
 
 
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2"])
-def test_bwd_full_size_sampled_channels(cfg):
+def test_bwd_full_size(cfg):
     """The backward at a benchmark configuration's full shape (config 1: 8 x 1536 x 2048, config 2:
-    4 x 5120 x 4096, bf16), against the exact float64 gradients of the oracle on sampled channels.
-    Channels are independent given B and C, so the oracle on a channel subset gives those channels'
-    du, ddelta, dz, dA, dD and ddelta_bias exactly (dB and dC sum over every channel: covered by the
-    smaller cases)."""
+    4 x 5120 x 4096, bf16), every gradient of every element -- du, ddelta, dz and the sums dA, dB,
+    dC, dD, ddelta_bias -- against the float64 adjoint of oracle/scan_f64.c (pinned against the
+    explicit adjoint brute.scan_bwd_brute in tests/test_oracle_bwd.py), run on the host's threads."""
     from motif_mamba_amd import selective_scan_fn
     from motif_mamba_amd.workloads import SCAN_CONFIGS, scan_inputs
+    from oracle import cscan
     c = SCAN_CONFIGS[cfg]
     _say(f"bwd full size {cfg} {c}")
     case = scan_inputs(c)
@@ -250,14 +263,10 @@ def test_bwd_full_size_sampled_channels(cfg):
     out = selective_scan_fn(**g)
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
-    chans = torch.tensor([0, 1, c.dim // 2 + 7, c.dim - 1])
-    sub = {k: (v[:, chans] if k in ("u", "delta", "z") else v[chans] if k in ("A", "D", "delta_bias") else v)
-           for k, v in case.items()}
-    exact = selective_scan_bwd_ref(**sub, dout=dout[:, chans], dtype=torch.float64)
-    for n in ("u", "delta", "z"):
-        _check(g[n].grad[:, chans.to(DEV)], exact[GRAD[n]], torch.bfloat16, f"{cfg} {GRAD[n]}")
-    for n in ("A", "D", "delta_bias"):
-        _check(g[n].grad[chans.to(DEV)], exact[GRAD[n]], torch.bfloat16, f"{cfg} {GRAD[n]}")
+    exact = cscan.scan_bwd_all_rows(case["u"], case["delta"], case["A"], case["B"], case["C"], dout, D=case["D"],
+                                    z=case["z"], delta_bias=case["delta_bias"], delta_softplus=True)
+    for n in NAMES:
+        _check(g[n].grad, torch.from_numpy(exact[GRAD[n]]), torch.bfloat16, f"{cfg} {GRAD[n]}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

@@ -36,16 +36,26 @@ def _tol(dtype):
     return (1e-4, 1e-5) if dtype == torch.float32 else (3e-2, 5e-2)
 
 
+# Gradients with one value per element of an input (du, ddelta, dz) are held element by element
+# to |err| <= rtol |exact| + atol. The reduced gradients (dA, dD, ddelta_bias: sums over batch
+# rows and steps; dB, dC: sums over the channels of a group; dP, dQ: sums over rows and steps)
+# add thousands of terms of both signs: their float32 rounding is relative to the sum of the
+# terms' magnitudes, which the result's own magnitude can fall far below where terms cancel, so
+# the absolute part of their bound is taken relative to the tensor's scale, max(1, max |exact|).
+ELEMENTWISE = {"du", "ddelta", "dz"}
+
+
 def _check(got, exact, dtype, what):
     rtol, atol = _tol(dtype)
     got = got.double().cpu()
     exact = exact.double()
-    scale = max(1.0, exact.abs().max().item()) if exact.numel() else 1.0
+    elementwise = any(tok in ELEMENTWISE for tok in what.split())
+    scale = 1.0 if elementwise else (max(1.0, exact.abs().max().item()) if exact.numel() else 1.0)
     err = (got - exact).abs()
     bound = rtol * exact.abs() + atol * scale
     bad = err > bound
     assert not bool(bad.any()), (f"{what}: {int(bad.sum())}/{err.numel()} beyond tolerance; max err "
-                                 f"{err.max().item():.3g} (scale {scale:.3g})")
+                                 f"{err.max().item():.3g} (scale {scale:.3g}, elementwise {elementwise})")
 
 
 def _dout(seed, shape, dtype):

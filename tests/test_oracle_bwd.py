@@ -61,6 +61,33 @@ def test_bwd_oracle_matches_explicit_adjoint(bkind, ckind, G, flags):
         np.testing.assert_allclose(got[k].numpy(), np.array(ref[k]), rtol=1e-9, atol=1e-11, err_msg=k)
 
 
+@pytest.mark.parametrize("bkind,G", [("3d", 1), ("4d", 2), ("4d", 1)])
+@pytest.mark.parametrize("flags", [dict(), dict(with_z=False), dict(with_D=False, with_bias=False),
+                                   dict(softplus=False)])
+@pytest.mark.parametrize("L", [1, 37])
+def test_c_adjoint_matches_explicit_adjoint(bkind, G, flags, L):
+    """The float64 C adjoint (oracle/scan_f64.c, mm_oracle_scan_bwd_rows_f64: the full-size
+    checker of the GPU backward) equals the explicit adjoint brute.scan_bwd_brute, every gradient,
+    on each variable-B/C layout and flag combination; softplus past its threshold of 20 is
+    included (delta + bias > 20 on some steps)."""
+    from oracle import cscan
+    case, dout = _case(540 + G + L + len(str(flags)), batch=2, dim=4, L=L, N=3, bkind=bkind, ckind=bkind, G=G,
+                       **flags)
+    if flags.get("softplus", True):
+        case["delta"] = case["delta"].clone()
+        case["delta"][0, 1, ::3] = 25.0        # the softplus threshold: ddelta = ddt' there
+    ref = brute.scan_bwd_brute(_l(case["u"]), _l(case["delta"]), _l(case["A"]), _l(case["B"]), _l(case["C"]),
+                               _l(dout), _l(case["D"]), _l(case["z"]), _l(case["delta_bias"]),
+                               case["delta_softplus"], bkind, bkind)
+    got = cscan.scan_bwd_all_rows(case["u"], case["delta"], case["A"], case["B"], case["C"], dout, D=case["D"],
+                                  z=case["z"], delta_bias=case["delta_bias"], delta_softplus=case["delta_softplus"])
+    for k in ("du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"):
+        if ref[k] is None:
+            assert got[k] is None, k
+            continue
+        np.testing.assert_allclose(got[k], np.array(ref[k]), rtol=1e-10, atol=1e-12, err_msg=k)
+
+
 def test_bwd_oracle_finite_differences():
     case, dout = _case(520, batch=1, dim=2, L=5, N=2, bkind="4d", ckind="4d", G=2)
     names = ["u", "delta", "A", "B", "C", "D", "z", "delta_bias"]
