@@ -26,6 +26,10 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream);
 // workspace bytes that takes (mm_scan_tiled.hip).
 int64_t segment_count(const mm_scan_fwd_params &p);
 bool tile_states_ok(const mm_scan_fwd_params &p);
+// The states before every 16-step tile, alone, into p.tile_states (the backward's checkpoints when
+// the forward did not save them); MM_ERR_UNSUPPORTED without launching when tile_states_ok fails.
+template <typename T>
+int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream);
 int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg);
 
 // Forward scan with the low-rank P/Q coupling (mm_scan_pq.hip): the tiled kernel when the request

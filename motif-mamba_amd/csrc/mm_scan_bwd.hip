@@ -21,6 +21,7 @@
 //       (NP = next power of two >= dstate); sums over states go through LDS, sums over rows
 //       (dB, dC, dA, dD, ddelta_bias) are float32 device atomics.
 #include <hip/hip_runtime.h>
+#include <string.h>
 
 #include <algorithm>
 #include <atomic>
@@ -727,16 +728,67 @@ SegPlan seg_plan_for(const mm_scan_bwd_params &p) {
 }
 int64_t carry_floats(const SegPlan &pl) { return pl.tail_units * pl.n_seg * 16 * 16 * 2; }
 
+// The forward parameter block of the states-only pass the backward runs when no tile states were
+// handed to it: the scan's inputs, no outputs, tile_states = the checkpoint region `ck`.
+mm_scan_fwd_params states_params(const mm_scan_bwd_params &p, float *ck) {
+    mm_scan_fwd_params f;
+    memset(&f, 0, sizeof(f));
+    f.batch = p.batch; f.dim = p.dim; f.seqlen = p.seqlen; f.dstate = p.dstate; f.n_groups = p.n_groups;
+    f.itype = p.itype;
+    f.is_variable_B = p.is_variable_B; f.is_variable_C = p.is_variable_C; f.delta_softplus = p.delta_softplus;
+    f.u = p.u; f.delta = p.delta; f.A = p.A; f.B = p.B; f.C = p.C; f.delta_bias = p.delta_bias;
+    f.u_batch_stride = p.u_batch_stride; f.u_d_stride = p.u_d_stride;
+    f.delta_batch_stride = p.delta_batch_stride; f.delta_d_stride = p.delta_d_stride;
+    f.A_d_stride = p.A_d_stride; f.A_dstate_stride = p.A_dstate_stride;
+    f.B_batch_stride = p.B_batch_stride; f.B_group_stride = p.B_group_stride;
+    f.B_dstate_stride = p.B_dstate_stride; f.B_d_stride = p.B_d_stride;
+    f.C_batch_stride = p.C_batch_stride; f.C_group_stride = p.C_group_stride;
+    f.C_dstate_stride = p.C_dstate_stride; f.C_d_stride = p.C_d_stride;
+    f.tile_states = ck;
+    return f;
+}
+
+
+// Whether `p` (no tile states handed in) is better served by a states-only forward first: only
+// when that forward can write the checkpoints (the dstate-16 pipelined kernel's shape and alignment
+// conditions) and the backward, given them, would cut its last round into sequence segments.
+// Otherwise the backward's own first pass computes the same states at the same cost.
+// MM_BWD_STATES_PASS=0 turns the states pass off (for measurements).
+bool states_pass_ok(const mm_scan_bwd_params &p) {
+    static const bool off = [] {
+        const char *e = std::getenv("MM_BWD_STATES_PASS");
+        return e && e[0] == '0';
+    }();
+    if (off || p.tile_states || p.P) return false;
+    float dummy;
+    if (!tile_states_ok(states_params(p, &dummy))) return false;
+    mm_scan_bwd_params q = p;
+    q.tile_states = &dummy;
+    return seg_plan_for(q).tail_units > 0;
+}
+
 template <typename T>
-int launch_fast(const mm_scan_bwd_params &p, hipStream_t s) {
-    float *ws = static_cast<float *>(p.workspace);
-    const bool own_ck = p.tile_states == nullptr;
-    float *ck = own_ck ? ws : const_cast<float *>(p.tile_states);
-    float *partB = own_ck ? ws + fast_ck_floats(p) : ws;
-    const FastWs fw{ck, partB, partB + fast_part_floats(p)};
-    const int64_t ratio = p.dim / p.n_groups;
+int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
+    float *ws = static_cast<float *>(p_in.workspace);
+    const bool own_ck = p_in.tile_states == nullptr;
+    float *ck = own_ck ? ws : const_cast<float *>(p_in.tile_states);
+    float *partB = own_ck ? ws + fast_ck_floats(p_in) : ws;
+    const FastWs fw{ck, partB, partB + fast_part_floats(p_in)};
+    const int64_t ratio = p_in.dim / p_in.n_groups;
+    // Without the forward's tile states, a states-only forward writes them into the head of the
+    // workspace first (the same states the backward's own first pass would compute, from a kernel
+    // that runs the whole grid at the forward's occupancy); the backward then reads them, as it
+    // reads a training forward's, and may cut its last round into sequence segments.
+    mm_scan_bwd_params p = p_in;
+    if (own_ck && states_pass_ok(p_in)) {
+        const mm_scan_fwd_params f = states_params(p_in, ck);
+        const int rc = launch_states_only<T>(f, s);
+        if (rc != MM_OK) return rc;
+        p.tile_states = ck;
+    }
     SegPlan pl = seg_plan<T>(p);
-    const int64_t need = (2 * fast_part_floats(p) + carry_floats(pl)) * int64_t(sizeof(float));
+    const int64_t need = ((own_ck ? fast_ck_floats(p) : 0) + 2 * fast_part_floats(p) + carry_floats(pl)) *
+                         int64_t(sizeof(float));
     // A workspace without room for the segment carries (sized by bwd_workspace_min_bytes, or queried
     // under another round size: MM_BWD_SLOTS or another device) runs every unit as a whole row.
     if (pl.tail_units > 0 && p.workspace_bytes < need)
@@ -799,6 +851,14 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
     if (!p.P && bwd::fast_ok(p) && p.tile_states)
         return (2 * bwd::fast_part_floats(p) + bwd::carry_floats(bwd::seg_plan_for(p))) * int64_t(sizeof(float));
+    if (!p.P && bwd::fast_ok(p) && bwd::states_pass_ok(p)) {
+        // The states-only forward writes the checkpoints into the workspace; segment carries follow.
+        mm_scan_bwd_params q = p;
+        float dummy;
+        q.tile_states = &dummy;
+        return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p) + bwd::carry_floats(bwd::seg_plan_for(q))) *
+               int64_t(sizeof(float));
+    }
     if (p.P && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
@@ -807,6 +867,7 @@ int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
 
 int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p) {
     if (!p.P && bwd::fast_ok(p) && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
+    if (!p.P && bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     return bwd_workspace_bytes(p);
 }
 

@@ -280,7 +280,8 @@ struct PairData {                  // one lane's global data for one 32-step til
 // Sequence segments of one launch (blockIdx.z = segment): MODE 0 scans whole rows; MODE 1 scans
 // segments 0 .. n_seg-2 from a zero state and writes only their end state (h) and the sum of
 // delta' (sumdt); MODE 2 scans every segment from the carried state h[segment] with the delta'
-// prefix cum[segment] and writes all outputs (last_state from the last segment).
+// prefix cum[segment] and writes all outputs (last_state from the last segment). MODE 3 scans
+// whole rows for the states alone and writes only p.tile_states (the backward's checkpoints).
 struct SegArgs {
     int64_t pairs;   // 32-step tile pairs per segment
     int32_t n_seg;
@@ -317,9 +318,11 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
     const int64_t L = p.seqlen;
     const int64_t n_pairs = (L + 2 * kT1 - 1) / (2 * kT1);
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
-    const int seg = MODE == 0 ? 0 : int(blockIdx.z);
-    const int64_t pb = MODE == 0 ? 0 : seg * sg.pairs;                                      // first pair
-    const int64_t pe = MODE == 0 ? n_pairs : (pb + sg.pairs < n_pairs ? pb + sg.pairs : n_pairs);  // end
+    constexpr bool WHOLE = MODE == 0 || MODE == 3;   // whole rows, no segments
+    constexpr bool YP = MODE == 0 || MODE == 2;      // y partials and outputs
+    const int seg = WHOLE ? 0 : int(blockIdx.z);
+    const int64_t pb = WHOLE ? 0 : seg * sg.pairs;                                          // first pair
+    const int64_t pe = WHOLE ? n_pairs : (pb + sg.pairs < n_pairs ? pb + sg.pairs : n_pairs);  // end
     const int64_t srow = (b * p.dim + d0 + c) * int64_t(sg.n_seg) + seg;                   // segment slot
 
     const int64_t de = d0 + ce;
@@ -392,7 +395,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
 
     // Epilogue of the tile starting at t0 (this lane's slice): rows added in a fixed order.
     auto epilogue = [&](int64_t t0) {
-        if constexpr (MODE == 1) return;  // state-only segments produce no outputs
+        if constexpr (!YP) return;  // state-only scans produce no outputs
         const int ecol = (((es >> 2) ^ (ce >> 2)) << 2) + (es & 3);
         float y[E];
         if constexpr (E == 4) {
@@ -457,22 +460,22 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
                     constexpr int k = decltype(KK)::value;
                     constexpr int src = k * LPS + s / E;
                     h[k] = __builtin_fmaf(av[j][k], h[k], bbv[j][k]);
-                    if constexpr (MODE != 1) {
+                    if constexpr (YP) {
                         if constexpr (k == 0)
                             acc = row_bcast<src>(cv[s % E]) * h[k];
                         else
                             fmac_row_bcast<src>(acc, cv[s % E], h[k]);
                     }
                 });
-                if constexpr (MODE != 1) pv[j] = acc;
+                if constexpr (YP) pv[j] = acc;
             });
-            if constexpr (MODE != 1)
+            if constexpr (YP)
                 *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
             // Without the y-partial chain the scheduler would hoist the exponentials of a whole tile
             // and run out of registers: keep the state-only scan in 4-step groups.
-            if constexpr (MODE == 1) __builtin_amdgcn_sched_barrier(0);
+            if constexpr (!YP) __builtin_amdgcn_sched_barrier(0);
         });
-        if (MODE != 1 && CHUNKS && p.chunk_states) {
+        if (YP && CHUNKS && p.chunk_states) {
             const int64_t tend = t0 + kT1 < L ? t0 + kT1 : L;
             if (t0 < L && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
                 const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
@@ -486,14 +489,14 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
         }
         // The state after this tile = the checkpoint before the next one, for the backward (training
         // forwards only: those write chunk states; the inference variants carry no such code).
-        if (MODE == 0 && CHUNKS && p.tile_states && t0 + kT1 < L) {
+        if (((MODE == 0 && CHUNKS) || MODE == 3) && p.tile_states && t0 + kT1 < L) {
             float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + r * K;
 #pragma unroll
             for (int k = 0; k < K; ++k) ck[k] = h[k];
         }
     };
 
-    if (MODE == 0 && CHUNKS && p.tile_states) {    // the checkpoint before the first tile: zero
+    if (((MODE == 0 && CHUNKS) || MODE == 3) && p.tile_states) {   // the checkpoint before the first tile: zero
 #pragma unroll
         for (int k = 0; k < K; ++k) p.tile_states[(b * p.dim + d0 + c) * 16 + r * K + k] = 0.f;
     }
@@ -535,7 +538,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
 #pragma unroll
         for (int k = 0; k < K; ++k) sg.h[srow * 16 + r * K + k] = h[k];
         if (r == 0) sg.sumdt[srow] = cum_dt;
-    } else {
+    } else if constexpr (MODE != 3) {
         if (p.last_state && (MODE == 0 || seg == sg.n_seg - 1)) {
 #pragma unroll
             for (int k = 0; k < K; ++k) p.last_state[(b * p.dim + d0 + c) * 16 + r * K + k] = h[k];
@@ -582,6 +585,13 @@ int launch_pipe_mode(const mm_scan_fwd_params &p, hipStream_t stream, const SegA
 template <typename T, int K, int PF>
 int launch_pipe(const mm_scan_fwd_params &p, hipStream_t stream) {
     return launch_pipe_mode<T, K, PF, 0>(p, stream, SegArgs{0, 1, nullptr, nullptr, nullptr}, 1);
+}
+
+// The backward's checkpoints alone (MODE 3): the state before every 16-step tile into
+// p.tile_states, nothing else written.
+template <typename T>
+int launch_fwd_states(const mm_scan_fwd_params &p, hipStream_t stream) {
+    return launch_pipe_mode<T, 2, 2, 3>(p, stream, SegArgs{0, 1, nullptr, nullptr, nullptr}, 1);
 }
 
 // Segmented scan: state-only pass over segments 0 .. n_seg-2, carry chain, full pass.
@@ -1042,6 +1052,17 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
 bool tile_states_ok(const mm_scan_fwd_params &p) {
     return tiled_shape_ok(p) && fwd_vector_ok(&p) && pipe_offsets_ok(p);
 }
+
+// The states-only forward the backward runs when no tile states were saved; MM_ERR_UNSUPPORTED
+// (nothing launched) when the request falls outside the dstate-16 pipelined kernel.
+template <typename T>
+int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream) {
+    if (!p.tile_states || !tile_states_ok(p)) return MM_ERR_UNSUPPORTED;
+    return tiled::launch_fwd_states<T>(p, stream);
+}
+template int launch_states_only<float>(const mm_scan_fwd_params &, hipStream_t);
+template int launch_states_only<f16_t>(const mm_scan_fwd_params &, hipStream_t);
+template int launch_states_only<bf16_t>(const mm_scan_fwd_params &, hipStream_t);
 
 template int try_launch_tiled<float>(const mm_scan_fwd_params &, hipStream_t);
 template int try_launch_tiled<f16_t>(const mm_scan_fwd_params &, hipStream_t);

@@ -337,6 +337,37 @@ def test_bwd_segmented_tail(dtype, slots, L, monkeypatch):
                                    msg=lambda m: f"{name}: {m}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("slots,L", [(6, 1000), (64, 200)])
+def test_bwd_states_pass(dtype, slots, L, monkeypatch):
+    """Without the forward's tile states (the callers that recompute, e.g. MambaInnerFn at
+    checkpoint_lvl 1), the backward first runs a states-only forward into its workspace and then
+    takes the segmented path a training forward's tile states would give it (MM_BWD_SLOTS sets the
+    round size so that these small shapes have a partial last round). The gradients match the exact
+    ones, and the backward with the forward's tile states, to float32 rounding."""
+    _say(f"bwd states pass slots={slots} L={L} {dtype}")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(705 + slots, 2, 64, L, 16, dtype, bkind="4d", G=2)
+    dout = _dout(706, (2, 64, L), dtype)
+    monkeypatch.setenv("MM_BWD_SLOTS", str(slots))
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+    out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    assert ck is not None
+    recomputed = ext.bwd(*args, dout.to(DEV), x, out, None, None, None, True, False)       # no tile states
+    saved = ext.bwd(*args, dout.to(DEV), x, out, None, None, None, True, False, ck)
+    torch.cuda.synchronize()
+    exact = selective_scan_bwd_ref(**case, dout=dout, dtype=torch.float64)
+    names = ["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"]
+    for name, a, b in zip(names, recomputed, saved):
+        _check(a, exact[name], dtype, f"states pass {name}")
+        scale = max(1.0, b.abs().max().item())
+        rtol = 1e-5 if dtype == torch.float32 else 1e-2
+        torch.testing.assert_close(a.float(), b.float(), rtol=rtol, atol=rtol * 0.1 * scale,
+                                   msg=lambda m: f"{name}: {m}")
+
+
 def test_training_step_graph_replay_matches_eager():
     """The training forward (with tile states) and the backward captured in one HIP graph: the
     workspace and outputs come from the graph's memory pool and the clears are fill kernels, so
