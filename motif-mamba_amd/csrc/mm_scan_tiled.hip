@@ -798,13 +798,26 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
 
     // Scan of one tile (pair half H) from dt/du into the row partials yb. B/C of state 2r + k at
     // step s of the pair sit in lane 8k + s / 4 of this row, register s % 4.
+    // The tile's dt' / dt'u are read from LDS one 4-step group ahead of their use: groups 1-3 while
+    // the group before computes, and group 0 of the next tile (dtn / dun, prepared two intervals
+    // earlier and published by the last barrier) at the end of this one, so that its LDS latency
+    // passes during the epilogue / prologue work and the barrier instead of stalling the next scan.
     float bv[E], cv[E];
-    auto scan_tile = [&](auto Hc, int64_t t0, const float *dt, const float *du, float *yb) {
+    float4 pre_dt, pre_du;                 // group 0 of the tile about to be scanned
+    auto scan_tile = [&](auto Hc, int64_t t0, const float *dt, const float *du, float *yb, const float *dtn,
+                         const float *dun) {
         constexpr int H = decltype(Hc)::value;
+        float4 dtq = pre_dt, duq = pre_du;
         static_for<0, kT1 / 4>([&](auto S4) {
             constexpr int s4 = decltype(S4)::value;
-            const float4 dtq = *reinterpret_cast<const float4 *>(&dt[c * kP1 + 4 * s4]);
-            const float4 duq = *reinterpret_cast<const float4 *>(&du[c * kP1 + 4 * s4]);
+            float4 ndt, ndu;
+            if constexpr (s4 + 1 < kT1 / 4) {
+                ndt = *reinterpret_cast<const float4 *>(&dt[c * kP1 + 4 * (s4 + 1)]);
+                ndu = *reinterpret_cast<const float4 *>(&du[c * kP1 + 4 * (s4 + 1)]);
+            } else {
+                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kP1]);
+                ndu = *reinterpret_cast<const float4 *>(&dun[c * kP1]);
+            }
             const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
             const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
             float av[4][2], bbv[4][2], pv[4];
@@ -829,7 +842,11 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
             });
             *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) =
                 make_float4(pv[0], pv[1], pv[2], pv[3]);
+            dtq = ndt;
+            duq = ndu;
         });
+        pre_dt = dtq;
+        pre_du = duq;
         if (CHUNKS && p.chunk_states) {
             const int64_t tend = t0 + kT1 < L ? t0 + kT1 : L;
             if (t0 < L && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
@@ -864,6 +881,8 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
         else prologue(u0, d0v, z0, kT1, DT(I1{}), DU(I1{}), I0{});
     }
     __syncthreads();
+    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kP1]);
+    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kP1]);
 
     for (int64_t i0 = 0; i0 < n_pairs; i0 += PF) {
         static_for<0, PF>([&](auto Sc) {
@@ -884,14 +903,16 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
                 load_data(i + PF, ring[S]);
                 // Interval 2i: wave 0 prepares tile 2i+2, wave 1 finishes tile 2i-1.
                 scan_tile(I0{}, t0, DT(std::integral_constant<int, 2 * P>{}), DU(std::integral_constant<int, 2 * P>{}),
-                          YB(I0{}));
+                          YB(I0{}), DT(std::integral_constant<int, 2 * P + 1>{}),
+                          DU(std::integral_constant<int, 2 * P + 1>{}));
                 if (w == 0) prologue(nu, nd, nz, t0 + 2 * kT1, DT(std::integral_constant<int, 2 * P + 2>{}),
                                      DU(std::integral_constant<int, 2 * P + 2>{}), I1P{});
                 else if (i > 0) epilogue(t0 - kT1, YB(I1{}), I1P{});
                 __syncthreads();
                 // Interval 2i+1: wave 1 prepares tile 2i+3, wave 0 finishes tile 2i.
                 scan_tile(I1{}, t0 + kT1, DT(std::integral_constant<int, 2 * P + 1>{}),
-                          DU(std::integral_constant<int, 2 * P + 1>{}), YB(I1{}));
+                          DU(std::integral_constant<int, 2 * P + 1>{}), YB(I1{}),
+                          DT(std::integral_constant<int, 2 * P + 2>{}), DU(std::integral_constant<int, 2 * P + 2>{}));
                 if (w == 1) prologue(nu, nd, nz, t0 + 3 * kT1, DT(std::integral_constant<int, 2 * P + 3>{}),
                                      DU(std::integral_constant<int, 2 * P + 3>{}), I1P{});
                 else epilogue(t0, YB(I0{}), IP{});
@@ -932,6 +953,297 @@ int launch_k2i(const mm_scan_fwd_params &p, hipStream_t stream) {
     return launch_k2i_full<T, PF, false>(p, stream);
 }
 
+// ---------------------------------------------------------------------------------------------
+// scan_fwd_k2s: the scan of k2i with the per-element work split evenly over both waves. Every lane
+// owns 2 consecutive steps of one channel in every tile (lane = 8 x channel + step pair), so in
+// interval j each lane prepares its elements of tile j + 2, scans tile j with its row, and finishes
+// its elements of tile j - 1: the same straight-line code in both waves, with no wave-dependent
+// branch between the scan and the element work, so the scheduler can fill the scan's latency gaps
+// with softplus, the row-partial sums and the gating. Taken when L is a multiple of 32 (whole tile
+// pairs, buffer addressing as k2i's FULL path).
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+struct K2SData {                       // one lane's global data for pair iteration i
+    RawVec<T, 4> b, c;                 // B, C of one of the lane's row states: 4 steps of pair i
+    RawVec<T, 2> u0, d0, z0, u1, d1, z1;   // u, delta, z: 2 steps of tiles 0 and 1 of pair i + 1
+};
+
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
+scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
+    static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
+    constexpr int E = 2, LPS = 8, NR = 8;
+    __shared__ __align__(16) float sDt0[kCh * kP1], sDt1[kCh * kP1], sDt2[kCh * kP1], sDt3[kCh * kP1];
+    __shared__ __align__(16) float sDu0[kCh * kP1], sDu1[kCh * kP1], sDu2[kCh * kP1], sDu3[kCh * kP1];
+    // Row partials of y [row][channel][16 steps], 4-float blocks XOR-swizzled by channel / 4.
+    __shared__ __align__(16) float sY0[NR * kCh * kT1], sY1[NR * kCh * kT1];
+    auto DT = [&](auto I) -> float * {
+        constexpr int i = decltype(I)::value & 3;
+        if constexpr (i == 0) return sDt0; else if constexpr (i == 1) return sDt1;
+        else if constexpr (i == 2) return sDt2; else return sDt3;
+    };
+    auto DU = [&](auto I) -> float * {
+        constexpr int i = decltype(I)::value & 3;
+        if constexpr (i == 0) return sDu0; else if constexpr (i == 1) return sDu1;
+        else if constexpr (i == 2) return sDu2; else return sDu3;
+    };
+    auto YB = [&](auto I) -> float * {
+        if constexpr ((decltype(I)::value & 1) == 0) return sY0; else return sY1;
+    };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int r = tid >> 4;                // row (states 2r, 2r+1) of this lane in the scan
+    const int c = lane & 15;               // channel of this lane in the scan
+    const int ce = tid >> 3;               // channel of this lane's elements
+    const int es = E * (tid & 7);          // first step (within a tile) of its two elements
+    const int64_t b = blockIdx.y;
+    const int64_t d0 = int64_t(blockIdx.x) * kCh;
+    const int64_t g = d0 / ratio;
+    const int64_t L = p.seqlen;
+    const int32_t n_pairs = int32_t(L / (2 * kT1));   // L is a multiple of 32 here
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+
+    const int64_t de = d0 + ce;
+    const T *ub = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d0 * p.u_d_stride;
+    const T *db = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d0 * p.delta_d_stride;
+    const T *zb = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d0 * p.z_d_stride : nullptr;
+    T *ob = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d0 * p.out_d_stride : nullptr;
+    T *ozb = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d0 * p.out_z_d_stride : nullptr;
+    const T *Bb = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cb = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+    const int nl = 2 * r + c / LPS;        // the state whose B/C this lane loads
+    const int sb = 4 * (c % LPS);          // first step (within a pair) of this lane's B/C slice
+
+    float At[2], h[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        At[k] = p.A[(d0 + c) * p.A_d_stride + int64_t(2 * r + k) * p.A_dstate_stride] * kLog2e;
+        h[k] = 0.f;
+    }
+    const float Dv = p.D ? p.D[de] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
+    float cum_dt = 0.f;
+
+    // Buffer resources of the group's rows (the host checks that every byte offset of the group is
+    // below 2^32) and this lane's byte offsets from them; tile and pair offsets are scalar.
+    constexpr uint32_t SZ = sizeof(T);
+    const uint32_t fo_u = uint32_t(ce * p.u_d_stride + es) * SZ, fo_d = uint32_t(ce * p.delta_d_stride + es) * SZ;
+    const uint32_t fo_z = uint32_t(ce * p.z_d_stride + es) * SZ;
+    const uint32_t fo_b = uint32_t(nl * p.B_dstate_stride + sb) * SZ, fo_c = uint32_t(nl * p.C_dstate_stride + sb) * SZ;
+    const uint32_t fo_o = uint32_t(ce * p.out_d_stride + es) * SZ, fo_oz = uint32_t(ce * p.out_z_d_stride + es) * SZ;
+    const __amdgpu_buffer_rsrc_t rs_u = buffer_rsrc(ub), rs_d = buffer_rsrc(db), rs_z = buffer_rsrc(zb);
+    const __amdgpu_buffer_rsrc_t rs_b = buffer_rsrc(Bb), rs_c = buffer_rsrc(Cb);
+    const __amdgpu_buffer_rsrc_t rs_o = buffer_rsrc(ob), rs_oz = buffer_rsrc(ozb);
+    // Pair and tile indices past the end are clamped to the last ones (the data they bring is
+    // never used): every access stays inside the rows.
+    auto pair_off = [&](int32_t i) { return uint32_t(i < n_pairs ? i : n_pairs - 1) * uint32_t(2 * kT1 * SZ); };
+    auto tile_off = [&](int32_t t) { return uint32_t(t < 2 * n_pairs ? t : 2 * n_pairs - 1) * uint32_t(kT1 * SZ); };
+    auto load_tile = [&](int32_t t, RawVec<T, E> &u, RawVec<T, E> &dl, RawVec<T, E> &z) {
+        const uint32_t sof = tile_off(t);
+        u = buffer_load_raw<T, E>(rs_u, fo_u, sof);
+        dl = buffer_load_raw<T, E>(rs_d, fo_d, sof);
+        if constexpr (HAS_Z) z = buffer_load_raw<T, E>(rs_z, fo_z, sof);
+        else z = {};
+    };
+    auto load_data = [&](int32_t i, K2SData<T> &dst) {
+        const uint32_t sof = pair_off(i);
+        dst.b = buffer_load_raw<T, 4>(rs_b, fo_b, sof);
+        dst.c = buffer_load_raw<T, 4>(rs_c, fo_c, sof);
+        load_tile(2 * i + 2, dst.u0, dst.d0, dst.z0);
+        load_tile(2 * i + 3, dst.u1, dst.d1, dst.z1);
+    };
+
+    // u and z of the tiles between their prologue and their epilogue: tile t in slot t % 4.
+    RawVec<T, E> ru[4], rz[4];
+
+    // Prologue of tile t (slot S = t % 4): delta', delta' u of this lane's two elements -> LDS.
+    auto prologue = [&](auto Slot, const RawVec<T, E> &u, const RawVec<T, E> &dl, const RawVec<T, E> &z) {
+        constexpr int sl = decltype(Slot)::value & 3;
+        float uu[E], dd[E], dtp[E];
+        unpack_raw<T, E>(u, uu);
+        unpack_raw<T, E>(dl, dd);
+#pragma unroll
+        for (int k = 0; k < E; ++k) {
+            const float x = dd[k] + bias;
+            dtp[k] = SOFTPLUS ? softplus_fast(x) : x;
+        }
+        *reinterpret_cast<float2 *>(&DT(Slot)[ce * kP1 + es]) = make_float2(dtp[0], dtp[1]);
+        *reinterpret_cast<float2 *>(&DU(Slot)[ce * kP1 + es]) = make_float2(dtp[0] * uu[0], dtp[1] * uu[1]);
+        ru[sl] = u;
+        rz[sl] = z;
+    };
+
+    // Epilogue of tile t (slot S = t % 4, partials in yb): the 8 row partials added in row order,
+    // D u, the silu(z) gate, one 2-element store. The first interval finishes no tile; it runs the
+    // same code on the unused buffers and stores to tile 0, which the lane overwrites with tile 0's
+    // real outputs one interval later (same lane, same addresses, program order), so that no branch
+    // separates the scan from the element work.
+    auto epilogue = [&](auto Slot, const float *yb, int32_t t) {
+        constexpr int sl = decltype(Slot)::value & 3;
+        const int ecol = (((es >> 2) ^ (ce >> 2)) << 2) + (es & 3);
+        float2 a = *reinterpret_cast<const float2 *>(&yb[ce * kT1 + ecol]);
+#pragma unroll
+        for (int rr = 1; rr < NR; ++rr) {
+            const float2 v = *reinterpret_cast<const float2 *>(&yb[(rr * kCh + ce) * kT1 + ecol]);
+            a.x += v.x;
+            a.y += v.y;
+        }
+        float uu[E], zz[E];
+        unpack_raw<T, E>(ru[sl], uu);
+        unpack_raw<T, E>(rz[sl], zz);
+        float o[E] = {__builtin_fmaf(Dv, uu[0], a.x), __builtin_fmaf(Dv, uu[1], a.y)};
+        const uint32_t sof = uint32_t(t) * uint32_t(kT1 * SZ);
+        if constexpr (HAS_OUT) buffer_store_vec<T, E>(rs_o, fo_o, sof, o);
+        if constexpr (HAS_Z) {
+#pragma unroll
+            for (int k = 0; k < E; ++k) o[k] *= silu_fast(zz[k]);
+            buffer_store_vec<T, E>(rs_oz, fo_oz, sof, o);
+        }
+    };
+
+    // Scan of one tile (pair half H) from dt/du into the row partials yb, as k2i's: B/C of state
+    // 2r + k at step s of the pair sit in lane 8k + s / 4 of this row, register s % 4; dt' / dt'u
+    // are read one 4-step group ahead (group 0 of the next tile at the end of this one).
+    float bv[4], cv[4];
+    float4 pre_dt, pre_du;
+    auto scan_tile = [&](auto Hc, int64_t t0, const float *dt, const float *du, float *yb, const float *dtn,
+                         const float *dun) {
+        constexpr int H = decltype(Hc)::value;
+        float4 dtq = pre_dt, duq = pre_du;
+        static_for<0, kT1 / 4>([&](auto S4) {
+            constexpr int s4 = decltype(S4)::value;
+            float4 ndt, ndu;
+            if constexpr (s4 + 1 < kT1 / 4) {
+                ndt = *reinterpret_cast<const float4 *>(&dt[c * kP1 + 4 * (s4 + 1)]);
+                ndu = *reinterpret_cast<const float4 *>(&du[c * kP1 + 4 * (s4 + 1)]);
+            } else {
+                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kP1]);
+                ndu = *reinterpret_cast<const float4 *>(&dun[c * kP1]);
+            }
+            const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
+            const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
+            float av[4][2], bbv[4][2], pv[4];
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                if (CHUNKS) cum_dt += dts[j];
+                static_for<0, 2>([&](auto KK) {
+                    constexpr int k = decltype(KK)::value;
+                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    bbv[j][k] = row_bcast<k * LPS + s / 4>(bv[s % 4]) * dus[j];
+                });
+            });
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                h[0] = __builtin_fmaf(av[j][0], h[0], bbv[j][0]);
+                h[1] = __builtin_fmaf(av[j][1], h[1], bbv[j][1]);
+                float acc = row_bcast<s / 4>(cv[s % 4]) * h[0];
+                fmac_row_bcast<LPS + s / 4>(acc, cv[s % 4], h[1]);
+                pv[j] = acc;
+            });
+            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) =
+                make_float4(pv[0], pv[1], pv[2], pv[3]);
+            dtq = ndt;
+            duq = ndu;
+        });
+        pre_dt = dtq;
+        pre_du = duq;
+        if (CHUNKS && p.chunk_states) {
+            const int64_t tend = t0 + kT1;
+            if (tend % MM_SCAN_CHUNK == 0 || tend == L) {
+                const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
+                float *csp = p.chunk_states + ((b * p.dim + d0 + c) * n_chunks + ci) * 32 + 4 * r;
+                csp[0] = __builtin_amdgcn_exp2f(At[0] * cum_dt);
+                csp[1] = h[0];
+                csp[2] = __builtin_amdgcn_exp2f(At[1] * cum_dt);
+                csp[3] = h[1];
+            }
+        }
+        if (CHUNKS && p.tile_states && t0 + kT1 < L) {
+            float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + 2 * r;
+            *reinterpret_cast<float2 *>(ck) = make_float2(h[0], h[1]);
+        }
+    };
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    if (CHUNKS && p.tile_states)           // the checkpoint before the first tile: zero
+        *reinterpret_cast<float2 *>(p.tile_states + (b * p.dim + d0 + c) * 16 + 2 * r) = make_float2(0.f, 0.f);
+    K2SData<T> ring[PF];
+    {
+        RawVec<T, E> u0, dl0, z0, u1, dl1, z1;
+        load_tile(0, u0, dl0, z0);
+        load_tile(1, u1, dl1, z1);
+#pragma unroll
+        for (int s = 0; s < PF; ++s) load_data(s, ring[s]);
+        prologue(I0{}, u0, dl0, z0);       // tiles 0 and 1, slots 0 and 1
+        prologue(I1{}, u1, dl1, z1);
+    }
+    __syncthreads();
+    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kP1]);
+    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kP1]);
+
+    for (int32_t i0 = 0; i0 < n_pairs; i0 += PF) {
+        static_for<0, PF>([&](auto Sc) {
+            constexpr int S = decltype(Sc)::value;
+            constexpr int P = S & 1;       // parity of the pair index (PF is even)
+            using T2P = std::integral_constant<int, 2 * P>;
+            using T2P1 = std::integral_constant<int, 2 * P + 1>;
+            using T2P2 = std::integral_constant<int, 2 * P + 2>;
+            using T2P3 = std::integral_constant<int, 2 * P + 3>;
+            const int32_t i = i0 + S;
+            if (i < n_pairs) {
+                const int64_t t0 = int64_t(i) * (2 * kT1);
+                unpack_raw<T, 4>(ring[S].b, bv);
+                unpack_raw<T, 4>(ring[S].c, cv);
+                // Two wait states between the VALU writes of the DPP sources and their first DPP
+                // read by the fmac inline asm (the compiler covers its own DPP instructions).
+#pragma unroll
+                for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                const K2SData<T> nxt = ring[S];  // the elements of pair i + 1
+                load_data(i + PF, ring[S]);
+                // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
+                scan_tile(I0{}, t0, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
+                prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
+                epilogue(T2P3{}, YB(I1{}), i > 0 ? 2 * i - 1 : 0);
+                __syncthreads();
+                // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
+                scan_tile(I1{}, t0 + kT1, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
+                prologue(T2P3{}, nxt.u1, nxt.d1, nxt.z1);
+                epilogue(T2P{}, YB(I0{}), 2 * i);
+                __syncthreads();
+            }
+        });
+    }
+    // The last tile, 2 n_pairs - 1 (slot (2 n_pairs - 1) % 4: 1 or 3).
+    if (((n_pairs - 1) & 1) == 0) epilogue(I1{}, YB(I1{}), 2 * n_pairs - 1);
+    else epilogue(std::integral_constant<int, 3>{}, YB(I1{}), 2 * n_pairs - 1);
+    if (p.last_state) {
+        p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r] = h[0];
+        p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r + 1] = h[1];
+    }
+}
+
+template <typename T, int PF, bool HAS_Z, bool HAS_OUT>
+int launch_k2s_io(const mm_scan_fwd_params &p, hipStream_t stream) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
+    auto *kern = p.delta_softplus ? (p.chunk_states ? scan_fwd_k2s<T, PF, true, true, HAS_Z, HAS_OUT>
+                                                    : scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT>)
+                                  : (p.chunk_states ? scan_fwd_k2s<T, PF, false, true, HAS_Z, HAS_OUT>
+                                                    : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT>);
+    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
+    return launch_status("scan_fwd_k2s");
+}
+
+template <typename T, int PF>
+int launch_k2s(const mm_scan_fwd_params &p, hipStream_t stream) {
+    if (p.z) return p.out ? launch_k2s_io<T, PF, true, true>(p, stream) : launch_k2s_io<T, PF, true, false>(p, stream);
+    return launch_k2s_io<T, PF, false, true>(p, stream);   // without z the pre-gate out is the output
+}
+
 template <typename T, int NW>
 int launch_nw(const mm_scan_fwd_params &p, hipStream_t stream) {
     const int64_t ratio = p.dim / p.n_groups;
@@ -945,8 +1257,9 @@ int launch_nw(const mm_scan_fwd_params &p, hipStream_t stream) {
 
 }  // namespace tiled
 
-// Kernel choice for dstate 16: MM_SCAN_KERNEL in the environment selects "k2i" (default: two states
-// per lane, per-element work interleaved with the scan), "k2" / "k1" (two / one state per lane,
+// Kernel choice for dstate 16: by default 16-bit inputs take k2s (L a multiple of 32) or k2i, fp32
+// inputs the pipelined k2. MM_SCAN_KERNEL in the environment selects "k2i" (two states per lane,
+// per-element work alternating between the waves), "k2" / "k1" (two / one state per lane,
 // alternating prologue/epilogue phases), or "nw1" / "nw2" / "nw4" (multi-state-per-lane kernel
 // without pipelining, 1, 2 or 4 waves per group). MM_SCAN_PF (1, 2, 3; default 2) sets the load
 // distance in 32-step tile pairs of k2 / k1 (k2i loads 2 pairs ahead). fp32 inputs use k2 by default.
@@ -956,6 +1269,7 @@ static int tiled_variant() {
         if (!e) return 0;
         if (!strcmp(e, "k1")) return 10;
         if (!strcmp(e, "k2")) return 20;
+        if (!strcmp(e, "k2i")) return 31;
         if (!strcmp(e, "nw1")) return 1;
         if (!strcmp(e, "nw2")) return 2;
         if (!strcmp(e, "nw4")) return 4;
@@ -1015,6 +1329,15 @@ int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg) {
     return n_seg > 1 ? p.batch * p.dim * n_seg * (16 + 2) * int64_t(sizeof(float)) : 0;
 }
 
+// The two-states-per-lane kernels for 16-bit inputs: k2s (symmetric element work) when L is a
+// multiple of 32, else k2i (MM_SCAN_KERNEL=k2i selects k2i always, for comparison).
+template <typename T>
+static int launch_k2x(const mm_scan_fwd_params &p, hipStream_t stream) {
+    static const bool nofull = getenv("MM_SCAN_NOFULL") != nullptr;
+    if (tiled_variant() != 31 && p.seqlen % (2 * tiled::kT1) == 0 && !nofull) return tiled::launch_k2s<T, 2>(p, stream);
+    return tiled::launch_k2i<T, 2>(p, stream);
+}
+
 template <typename T>
 int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (!tiled_shape_ok(p) || !fwd_vector_ok(&p)) return MM_ERR_UNSUPPORTED;
@@ -1023,7 +1346,7 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
         // The backward's checkpoints are written by the default kernels only (one pass, no segments).
         if (!pipe_ok) return MM_ERR_UNSUPPORTED;
         if constexpr (std::is_same_v<T, float>) return launch_pipe_pf<T, 2>(p, stream);
-        else return tiled::launch_k2i<T, 2>(p, stream);
+        else return launch_k2x<T>(p, stream);
     }
     const int64_t n_seg = pipe_ok ? segment_count(p) : 1;
     if (n_seg > 1 && p.workspace && p.workspace_bytes >= segment_workspace_bytes(p, n_seg) &&
@@ -1044,7 +1367,7 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
         default:
             // fp32 rows double the in-flight registers of the interleaved kernel (it would spill).
             if constexpr (std::is_same_v<T, float>) return launch_pipe_pf<T, 2>(p, stream);
-            else return tiled::launch_k2i<T, 2>(p, stream);
+            else return launch_k2x<T>(p, stream);
     }
 }
 
