@@ -269,7 +269,16 @@ scan_fwd_tiled16(const mm_scan_fwd_params p, const int64_t ratio) {
 // writes ~74 B/clk/CU) decides the rate, at the price of 2-3 waves per SIMD.
 // ---------------------------------------------------------------------------------------------
 constexpr int kT1 = 16;   // steps per tile
-constexpr int kP1 = 20;   // LDS row stride (floats) of sDt/sDu: 16 steps + 4, float4 rows stay 16-B aligned
+
+// LDS rows of 16 floats, one per channel (the delta' and delta' u of a tile) or per (state row,
+// channel) (the row partials of y), are stored as four 4-float blocks, block q of channel c at
+// position q ^ swz16(c). The scan accesses them with one lane per channel (c = lane % 16) in
+// 128-bit loads and stores, which the LDS serves 8 lanes per cycle over 32 banks: among the lanes
+// c = 8m .. 8m + 7, c % 2 selects the half of the banks and swz16 takes all four values for either
+// parity, so the 8 lanes hit every bank once. On a 64-bank LDS (16 lanes per cycle) the same holds
+// with c % 4 selecting the quarter and swz16 a bijection of c / 4. The per-element lanes read and
+// write whole rows of adjacent channels, which the permutation inside a row does not change.
+__device__ __forceinline__ int swz16(int c) { return (((c >> 1) ^ (c >> 3)) & 1) | ((c >> 1) & 2); }
 
 template <typename T, int K>
 struct PairData {                  // one lane's global data for one 32-step tile pair
@@ -298,11 +307,9 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
     constexpr int E = 2 * K;               // element steps per lane per tile (and B/C steps per lane per pair)
     constexpr int LPS = 16 / K;            // lanes of a row holding one state's B/C
     constexpr int GL = 32 * NW;            // lanes per role group
-    __shared__ __align__(16) float sDt[2][kCh * kP1];
-    __shared__ __align__(16) float sDu[2][kCh * kP1];
-    // Row partials of y [row][channel][16 steps]; the 4-float blocks of each 16-float row are
-    // XOR-swizzled by channel / 4, so the scan's float4 writes and the epilogue's reads are
-    // free of bank conflicts.
+    __shared__ __align__(16) float sDt[2][kCh * kT1];
+    __shared__ __align__(16) float sDu[2][kCh * kT1];
+    // Row partials of y [row][channel][16 steps], 4-float blocks permuted by swz16(channel).
     __shared__ __align__(16) float sY[NR * kCh * kT1];
 
     const int lane = threadIdx.x & 63;
@@ -312,6 +319,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
     const int gl = int(threadIdx.x) % GL;
     const int ce = gl / (16 / E);          // channel of this lane's element slice
     const int es = E * (gl % (16 / E));    // first step (within a tile) of the slice
+    const int swc = swz16(c), swe = swz16(ce);   // LDS block permutations of the two channels
     const int64_t b = blockIdx.y;
     const int64_t d0 = int64_t(blockIdx.x) * kCh;
     const int64_t g = d0 / ratio;
@@ -360,12 +368,15 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
         const int64_t t0 = i * (2 * kT1);
         const uint32_t tb = clampE(t0 + sb);
         dst.b = load_raw<T, E>(Bb + (B_row + tb));
-        dst.c = load_raw<T, E>(Cb + (C_row + tb));
         const uint32_t te = clampE(t0 + kT1 * grp + es);
         dst.u = load_raw<T, E>(ub + (u_row + te));
         dst.dl = load_raw<T, E>(db + (d_row + te));
-        if (zb) dst.z = load_raw<T, E>(zb + (z_row + te));
-        else dst.z = {};
+        dst.c = {};
+        dst.z = {};
+        if constexpr (YP) {                // C and z feed only the outputs
+            dst.c = load_raw<T, E>(Cb + (C_row + tb));
+            if (zb) dst.z = load_raw<T, E>(zb + (z_row + te));
+        }
     };
 
     // Prologue of the tile starting at t0 (this lane's slice): delta', delta' u -> LDS buffer buf.
@@ -374,7 +385,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
         float dd[E], dtp[E], dup[E];
         unpack_raw<T, E>(src.u, uu);
         unpack_raw<T, E>(src.dl, dd);
-        unpack_raw<T, E>(src.z, zz);
+        if constexpr (YP) unpack_raw<T, E>(src.z, zz);
 #pragma unroll
         for (int k = 0; k < E; ++k) {
             const float x = dd[k] + bias;
@@ -388,15 +399,16 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
         for (int k = 0; k < E; ++k) dup[k] = dtp[k] * uu[k];
 #pragma unroll
         for (int k = 0; k < E; k += 2) {
-            *reinterpret_cast<float2 *>(&sDt[buf][ce * kP1 + es + k]) = make_float2(dtp[k], dtp[k + 1]);
-            *reinterpret_cast<float2 *>(&sDu[buf][ce * kP1 + es + k]) = make_float2(dup[k], dup[k + 1]);
+            const int col = ((((es + k) >> 2) ^ swe) << 2) + ((es + k) & 3);
+            *reinterpret_cast<float2 *>(&sDt[buf][ce * kT1 + col]) = make_float2(dtp[k], dtp[k + 1]);
+            *reinterpret_cast<float2 *>(&sDu[buf][ce * kT1 + col]) = make_float2(dup[k], dup[k + 1]);
         }
     };
 
     // Epilogue of the tile starting at t0 (this lane's slice): rows added in a fixed order.
     auto epilogue = [&](int64_t t0) {
         if constexpr (!YP) return;  // state-only scans produce no outputs
-        const int ecol = (((es >> 2) ^ (ce >> 2)) << 2) + (es & 3);
+        const int ecol = (((es >> 2) ^ swe) << 2) + (es & 3);
         float y[E];
         if constexpr (E == 4) {
             float4 a = *reinterpret_cast<const float4 *>(&sY[ce * kT1 + ecol]);
@@ -434,12 +446,21 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
     float bv[E], cv[E];
     auto scan_tile = [&](auto Hc, int64_t t0, int buf) {
         constexpr int H = decltype(Hc)::value;
+        // The tile's dt' and dt'u: with outputs all read before the scan starts (the y-partial
+        // stores between the 4-step groups would otherwise hold each group's reads back until it
+        // is needed); without them, where registers are short, one group at a time.
+        float4 dtg[kT1 / 4], dug[kT1 / 4];
+        auto read_group = [&](auto S4) {
+            constexpr int s4 = decltype(S4)::value;
+            dtg[s4] = *reinterpret_cast<const float4 *>(&sDt[buf][c * kT1 + ((s4 ^ swc) << 2)]);
+            dug[s4] = *reinterpret_cast<const float4 *>(&sDu[buf][c * kT1 + ((s4 ^ swc) << 2)]);
+        };
+        if constexpr (YP) static_for<0, kT1 / 4>(read_group);
         static_for<0, kT1 / 4>([&](auto S4) {
             constexpr int s4 = decltype(S4)::value;
-            const float4 dtq = *reinterpret_cast<const float4 *>(&sDt[buf][c * kP1 + 4 * s4]);
-            const float4 duq = *reinterpret_cast<const float4 *>(&sDu[buf][c * kP1 + 4 * s4]);
-            const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
-            const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
+            if constexpr (!YP) read_group(S4);
+            const float dts[4] = {dtg[s4].x, dtg[s4].y, dtg[s4].z, dtg[s4].w};
+            const float dus[4] = {dug[s4].x, dug[s4].y, dug[s4].z, dug[s4].w};
             float av[4][K], bbv[4][K], pv[4];
             static_for<0, 4>([&](auto J) {
                 constexpr int j = decltype(J)::value;
@@ -470,7 +491,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
                 if constexpr (YP) pv[j] = acc;
             });
             if constexpr (YP)
-                *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+                *reinterpret_cast<float4 *>(&sY[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
             // Without the y-partial chain the scheduler would hoist the exponentials of a whole tile
             // and run out of registers: keep the state-only scan in 4-step groups.
             if constexpr (!YP) __builtin_amdgcn_sched_barrier(0);
@@ -512,11 +533,16 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
             if (i < pe) {
                 const int64_t t0 = i * (2 * kT1);
                 unpack_raw<T, E>(ring[S].b, bv);
-                unpack_raw<T, E>(ring[S].c, cv);
                 // Two wait states between the VALU writes of the DPP sources and their first DPP
                 // read by the fmac inline asm (the compiler covers its own DPP instructions).
+                if constexpr (YP) {
+                    unpack_raw<T, E>(ring[S].c, cv);
 #pragma unroll
-                for (int k = 0; k < E; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                    for (int k = 0; k < E; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                } else {
+#pragma unroll
+                    for (int k = 0; k < E; ++k) asm volatile("s_nop 1" : "+v"(bv[k]));
+                }
                 PairData<T, K> mine = ring[S];  // group 1's slice of this pair (used below)
                 load_pair(i + PF, ring[S]);
                 // Tile 2i: group 0 finishes it, group 1 prepares tile 2i+1.
@@ -640,9 +666,9 @@ __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))
 scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
     constexpr int E = 4, LPS = 8, NR = 8;
-    __shared__ __align__(16) float sDt0[kCh * kP1], sDt1[kCh * kP1], sDt2[kCh * kP1], sDt3[kCh * kP1];
-    __shared__ __align__(16) float sDu0[kCh * kP1], sDu1[kCh * kP1], sDu2[kCh * kP1], sDu3[kCh * kP1];
-    // Row partials of y [row][channel][16 steps], 4-float blocks XOR-swizzled by channel / 4.
+    __shared__ __align__(16) float sDt0[kCh * kT1], sDt1[kCh * kT1], sDt2[kCh * kT1], sDt3[kCh * kT1];
+    __shared__ __align__(16) float sDu0[kCh * kT1], sDu1[kCh * kT1], sDu2[kCh * kT1], sDu3[kCh * kT1];
+    // Row partials of y [row][channel][16 steps], 4-float blocks permuted by swz16(channel).
     __shared__ __align__(16) float sY0[NR * kCh * kT1], sY1[NR * kCh * kT1];
     auto DT = [&](auto I) -> float * {
         constexpr int i = decltype(I)::value & 3;
@@ -664,6 +690,7 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
     const int c = lane & 15;               // channel of this lane in the scan
     const int ce = lane >> 2;              // channel of this lane's element slice
     const int es = E * (lane & 3);         // first step (within a tile) of the slice
+    const int swc = swz16(c), swe = swz16(ce);   // LDS block permutations of the two channels
     const int64_t b = blockIdx.y;
     const int64_t d0 = int64_t(blockIdx.x) * kCh;
     const int64_t g = d0 / ratio;
@@ -764,15 +791,15 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
 #pragma unroll
             for (int k = 0; k < E; ++k) dtp[k] = 0.f;
         }
-        *reinterpret_cast<float4 *>(&dt[ce * kP1 + es]) = make_float4(dtp[0], dtp[1], dtp[2], dtp[3]);
-        *reinterpret_cast<float4 *>(&du[ce * kP1 + es]) =
+        *reinterpret_cast<float4 *>(&dt[ce * kT1 + (((es >> 2) ^ swe) << 2)]) = make_float4(dtp[0], dtp[1], dtp[2], dtp[3]);
+        *reinterpret_cast<float4 *>(&du[ce * kT1 + (((es >> 2) ^ swe) << 2)]) =
             make_float4(dtp[0] * uu[sl][0], dtp[1] * uu[sl][1], dtp[2] * uu[sl][2], dtp[3] * uu[sl][3]);
     };
 
     // Epilogue of tile t0 / 16 (this lane's slice): the 8 row partials added in row order.
     auto epilogue = [&](int64_t t0, const float *yb, auto Slot) {
         constexpr int sl = decltype(Slot)::value;
-        const int ecol = ((es >> 2) ^ (ce >> 2)) << 2;
+        const int ecol = ((es >> 2) ^ swe) << 2;
         float4 a = *reinterpret_cast<const float4 *>(&yb[ce * kT1 + ecol]);
 #pragma unroll
         for (int rr = 1; rr < NR; ++rr) {
@@ -812,11 +839,11 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
             constexpr int s4 = decltype(S4)::value;
             float4 ndt, ndu;
             if constexpr (s4 + 1 < kT1 / 4) {
-                ndt = *reinterpret_cast<const float4 *>(&dt[c * kP1 + 4 * (s4 + 1)]);
-                ndu = *reinterpret_cast<const float4 *>(&du[c * kP1 + 4 * (s4 + 1)]);
+                ndt = *reinterpret_cast<const float4 *>(&dt[c * kT1 + (((s4 + 1) ^ swc) << 2)]);
+                ndu = *reinterpret_cast<const float4 *>(&du[c * kT1 + (((s4 + 1) ^ swc) << 2)]);
             } else {
-                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kP1]);
-                ndu = *reinterpret_cast<const float4 *>(&dun[c * kP1]);
+                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kT1 + (swc << 2)]);
+                ndu = *reinterpret_cast<const float4 *>(&dun[c * kT1 + (swc << 2)]);
             }
             const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
             const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
@@ -840,7 +867,7 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
                 fmac_row_bcast<LPS + s / E>(acc, cv[s % E], h[1]);
                 pv[j] = acc;
             });
-            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) =
+            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
                 make_float4(pv[0], pv[1], pv[2], pv[3]);
             dtq = ndt;
             duq = ndu;
@@ -881,8 +908,8 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
         else prologue(u0, d0v, z0, kT1, DT(I1{}), DU(I1{}), I0{});
     }
     __syncthreads();
-    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kP1]);
-    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kP1]);
+    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kT1 + (swc << 2)]);
+    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kT1 + (swc << 2)]);
 
     for (int64_t i0 = 0; i0 < n_pairs; i0 += PF) {
         static_for<0, PF>([&](auto Sc) {
@@ -973,9 +1000,9 @@ __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8))
 scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
     constexpr int E = 2, LPS = 8, NR = 8;
-    __shared__ __align__(16) float sDt0[kCh * kP1], sDt1[kCh * kP1], sDt2[kCh * kP1], sDt3[kCh * kP1];
-    __shared__ __align__(16) float sDu0[kCh * kP1], sDu1[kCh * kP1], sDu2[kCh * kP1], sDu3[kCh * kP1];
-    // Row partials of y [row][channel][16 steps], 4-float blocks XOR-swizzled by channel / 4.
+    __shared__ __align__(16) float sDt0[kCh * kT1], sDt1[kCh * kT1], sDt2[kCh * kT1], sDt3[kCh * kT1];
+    __shared__ __align__(16) float sDu0[kCh * kT1], sDu1[kCh * kT1], sDu2[kCh * kT1], sDu3[kCh * kT1];
+    // Row partials of y [row][channel][16 steps], 4-float blocks permuted by swz16(channel).
     __shared__ __align__(16) float sY0[NR * kCh * kT1], sY1[NR * kCh * kT1];
     auto DT = [&](auto I) -> float * {
         constexpr int i = decltype(I)::value & 3;
@@ -997,6 +1024,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     const int c = lane & 15;               // channel of this lane in the scan
     const int ce = tid >> 3;               // channel of this lane's elements
     const int es = E * (tid & 7);          // first step (within a tile) of its two elements
+    const int swc = swz16(c), swe = swz16(ce);   // LDS block permutations of the two channels
     const int64_t b = blockIdx.y;
     const int64_t d0 = int64_t(blockIdx.x) * kCh;
     const int64_t g = d0 / ratio;
@@ -1068,8 +1096,8 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
             const float x = dd[k] + bias;
             dtp[k] = SOFTPLUS ? softplus_fast(x) : x;
         }
-        *reinterpret_cast<float2 *>(&DT(Slot)[ce * kP1 + es]) = make_float2(dtp[0], dtp[1]);
-        *reinterpret_cast<float2 *>(&DU(Slot)[ce * kP1 + es]) = make_float2(dtp[0] * uu[0], dtp[1] * uu[1]);
+        *reinterpret_cast<float2 *>(&DT(Slot)[ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3)]) = make_float2(dtp[0], dtp[1]);
+        *reinterpret_cast<float2 *>(&DU(Slot)[ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3)]) = make_float2(dtp[0] * uu[0], dtp[1] * uu[1]);
         ru[sl] = u;
         rz[sl] = z;
     };
@@ -1081,7 +1109,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     // separates the scan from the element work.
     auto epilogue = [&](auto Slot, const float *yb, int32_t t) {
         constexpr int sl = decltype(Slot)::value & 3;
-        const int ecol = (((es >> 2) ^ (ce >> 2)) << 2) + (es & 3);
+        const int ecol = (((es >> 2) ^ swe) << 2) + (es & 3);
         float2 a = *reinterpret_cast<const float2 *>(&yb[ce * kT1 + ecol]);
 #pragma unroll
         for (int rr = 1; rr < NR; ++rr) {
@@ -1115,11 +1143,11 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
             constexpr int s4 = decltype(S4)::value;
             float4 ndt, ndu;
             if constexpr (s4 + 1 < kT1 / 4) {
-                ndt = *reinterpret_cast<const float4 *>(&dt[c * kP1 + 4 * (s4 + 1)]);
-                ndu = *reinterpret_cast<const float4 *>(&du[c * kP1 + 4 * (s4 + 1)]);
+                ndt = *reinterpret_cast<const float4 *>(&dt[c * kT1 + (((s4 + 1) ^ swc) << 2)]);
+                ndu = *reinterpret_cast<const float4 *>(&du[c * kT1 + (((s4 + 1) ^ swc) << 2)]);
             } else {
-                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kP1]);
-                ndu = *reinterpret_cast<const float4 *>(&dun[c * kP1]);
+                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kT1 + (swc << 2)]);
+                ndu = *reinterpret_cast<const float4 *>(&dun[c * kT1 + (swc << 2)]);
             }
             const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
             const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
@@ -1143,7 +1171,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
                 fmac_row_bcast<LPS + s / 4>(acc, cv[s % 4], h[1]);
                 pv[j] = acc;
             });
-            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ (c >> 2)) << 2)]) =
+            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
                 make_float4(pv[0], pv[1], pv[2], pv[3]);
             dtq = ndt;
             duq = ndu;
@@ -1182,8 +1210,8 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
         prologue(I1{}, u1, dl1, z1);
     }
     __syncthreads();
-    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kP1]);
-    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kP1]);
+    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kT1 + (swc << 2)]);
+    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kT1 + (swc << 2)]);
 
     for (int32_t i0 = 0; i0 < n_pairs; i0 += PF) {
         static_for<0, PF>([&](auto Sc) {
