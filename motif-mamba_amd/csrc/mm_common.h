@@ -234,6 +234,27 @@ __device__ __forceinline__ RawVec<T, N> buffer_load_raw(__amdgpu_buffer_rsrc_t r
     return x;
 }
 
+// N consecutive elements of T of any 4-byte-multiple size, as 16-byte buffer loads and a last,
+// shorter one.
+template <typename T, int N>
+__device__ __forceinline__ RawVec<T, N> buffer_load_rawn(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    constexpr int W = sizeof(RawVec<T, N>) / 4;
+    if constexpr (W <= 4) {
+        return buffer_load_raw<T, N>(r, voff, soff);
+    } else {
+        static_assert(W % 4 == 0, "buffer_load_rawn splits into 16-byte pieces");
+        constexpr int NP = 16 / int(sizeof(T));   // elements per piece
+        RawVec<T, N> x;
+#pragma unroll
+        for (int i = 0; i < W / 4; ++i) {
+            const RawVec<T, NP> v = buffer_load_raw<T, NP>(r, voff + 16 * i, soff);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) x.w[4 * i + k] = v.w[k];
+        }
+        return x;
+    }
+}
+
 // N floats converted to T (bf16 round-to-nearest-even) and stored as one 4-, 8- or 16-byte access.
 template <typename T, int N>
 __device__ __forceinline__ void buffer_store_vec(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float *x) {

@@ -30,6 +30,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 #include "mm_common.h"
@@ -104,8 +106,6 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     const int N = int(p.dstate);
     const int rank = int(p.pq_rank);
 
-    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
-    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
     const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
     T *op = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
     T *ozp = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
@@ -139,6 +139,22 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
         for (int s = 0; s < S; ++s) ckp[j * ck_tile + s] = h[s];
     };
 
+    // The loads of u, delta and z go through buffer resources: the rows of the wave's channels from
+    // its first channel dw, with 32-bit byte offsets per lane (the host checks that every offset of
+    // these rows fits). A whole tile adds its start as a scalar offset; only the last, partial
+    // tile clamps per lane. (B and C, a tensor per lane, keep per-lane pointers: a resource
+    // descriptor must be uniform.)
+    constexpr uint32_t SZ = sizeof(T);
+    const int64_t dw = g * ratio + int64_t(blockIdx.x % blocks_per_group) * CPW;
+    const int64_t dl = d - dw;             // 0 .. CPW - 1 (inactive slots mirror the group's last channel)
+    const __amdgpu_buffer_rsrc_t rs_u = buffer_rsrc(reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + dw * p.u_d_stride);
+    const __amdgpu_buffer_rsrc_t rs_d =
+        buffer_rsrc(reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + dw * p.delta_d_stride);
+    const __amdgpu_buffer_rsrc_t rs_z =    // (p.z, not zp: the condition must be uniform)
+        buffer_rsrc(p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + dw * p.z_d_stride : nullptr);
+    const uint32_t fo_u = uint32_t(dl * p.u_d_stride) * SZ, fo_d = uint32_t(dl * p.delta_d_stride) * SZ;
+    const uint32_t fo_z = uint32_t(dl * p.z_d_stride) * SZ;
+
     // The B/C half-rows this lane stages: index hr = lane HR + i -> tensor hr / (2 NP) (0: B, 1: C),
     // state (hr % 2NP) / 2, steps 16 (hr % 2) .. +15 of the tile.
     const T *bcp[HR];
@@ -152,32 +168,47 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
         bc_half[i] = hr % 2;
         bc_on[i] = n < N;
         const int64_t nn = n < N ? n : 0;
-        bcp[i] = tensor == 0 ? Bg + nn * p.B_dstate_stride : Cg + nn * p.C_dstate_stride;
+        bcp[i] = (tensor == 0 ? Bg + nn * p.B_dstate_stride : Cg + nn * p.C_dstate_stride) + 16 * bc_half[i];
         bc_lds[i] = 16 * bc_half[i] * BCS + tensor * NP + n;
     }
 
     // Loads at or past the end of a row are redirected into the row's last elements (always in
-    // bounds: L is a multiple of 8); the steps they feed are padding with dt' = 0 and B = C = 0.
+    // bounds: L is a multiple of 8); the steps they feed are padding with dt' = 0.
     const int64_t lastE = L - E, last8 = L - 8;
-    auto ce = [&](int64_t i) { return i < lastE ? i : lastE; };
-    auto c8 = [&](int64_t i) { return i < last8 ? i : last8; };
-    RawVec<T, E> ru = load_raw<T, E>(up + ce(es));
-    RawVec<T, E> rd = load_raw<T, E>(dp + ce(es));
-    RawVec<T, E> rz = {};
-    if (zp) rz = load_raw<T, E>(zp + ce(es));
+    RawVec<T, E> ru, rd, rz = {};
+    auto load_elems = [&](int64_t t) {
+        uint32_t eo, so;
+        if (t + kT <= L) {                 // uniform: a whole tile
+            eo = uint32_t(es) * SZ;
+            so = uint32_t(t) * SZ;
+        } else {
+            eo = uint32_t(t + es < lastE ? t + es : lastE) * SZ;
+            so = 0;
+        }
+        ru = buffer_load_rawn<T, E>(rs_u, fo_u + eo, so);
+        rd = buffer_load_rawn<T, E>(rs_d, fo_d + eo, so);
+        if (zp) rz = buffer_load_rawn<T, E>(rs_z, fo_z + eo, so);
+    };
     RawVec<T, 8> rbc[HR][2];
     auto load_bc = [&](int64_t t0) {
+        const bool whole = t0 + kT <= L;   // uniform
 #pragma unroll
         for (int i = 0; i < HR; ++i) {
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
+                // whole tile: t0 (uniform) + a lane constant; else the row's clamped position
+                const int64_t t = t0 + 16 * bc_half[i] + 8 * h2;
+                const T *src = whole ? bcp[i] + t0 + 8 * h2 : bcp[i] - 16 * bc_half[i] + (t < last8 ? t : last8);
                 rbc[i][h2] = {};
-                if (bc_on[i]) rbc[i][h2] = load_raw<T, 8>(bcp[i] + c8(t0 + 16 * bc_half[i] + 8 * h2));
+                if (bc_on[i]) rbc[i][h2] = load_raw<T, 8>(src);
             }
         }
     };
-    // Tile rows [step][B states | C states] as float32; states past dstate and steps past L are 0.
+    // Tile rows [step][B states | C states] as float32; states past dstate are 0 (their loads are
+    // skipped). Steps past L of the last tile are 0 as well, although their dt' = 0 makes B and C
+    // of those steps reach no state and no stored output.
     auto stage_bc = [&](int64_t t0) {
+        const bool whole = t0 + kT <= L;   // uniform
 #pragma unroll
         for (int i = 0; i < HR; ++i) {
             const int64_t first = t0 + 16 * bc_half[i];
@@ -188,11 +219,12 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int64_t t = first + 8 * h2 + e;
-                    sBC[bc_lds[i] + (8 * h2 + e) * BCS] = (bc_on[i] && t < L) ? v[e] : 0.f;
+                    sBC[bc_lds[i] + (8 * h2 + e) * BCS] = (whole || t < L) ? v[e] : 0.f;
                 }
             }
         }
     };
+    load_elems(0);
     load_bc(0);
     stage_bc(0);
 
@@ -204,9 +236,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
         unpack_raw<T, E>(rd, dd);
         unpack_raw<T, E>(rz, zz);
         // Prefetch the next tile (clamped addresses: always in bounds).
-        ru = load_raw<T, E>(up + ce(t1 + es));
-        rd = load_raw<T, E>(dp + ce(t1 + es));
-        if (zp) rz = load_raw<T, E>(zp + ce(t1 + es));
+        load_elems(t1);
         load_bc(t1);
 
         // Prologue: dt' and dt' u of (channel, steps es .. es + E - 1).
@@ -436,10 +466,21 @@ int64_t min_waves() {
     return e ? atoll(e) : 2048;
 }
 
+// The tiled kernel loads u, delta and z with 32-bit byte offsets from the first of a wave's channel
+// rows (up to 16): every offset of those rows must fit.
+static bool offsets_ok(const mm_scan_fwd_params &p) {
+    const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
+    const int64_t ch = 15 * std::max({p.u_d_stride, p.delta_d_stride, p.z ? p.z_d_stride : int64_t(0)});
+    return (ch + p.seqlen) * eb < (int64_t(1) << 32);
+}
+
 // The (S, LPR) of the tiled kernel for this request, or {0, 0} when the request needs the general
-// kernel: variable B and C, dstate <= 64, seqlen >= 8, rows movable as 16-byte vectors.
+// kernel: variable B and C, dstate <= 64, seqlen >= 8, rows movable as 16-byte vectors, offsets
+// that fit in 32 bits.
 TiledShape tiled_shape(const mm_scan_fwd_params &p) {
-    if (!p.is_variable_B || !p.is_variable_C || p.dstate > 64 || p.seqlen < 8 || !fwd_vector_ok(&p)) return {0, 0};
+    if (!p.is_variable_B || !p.is_variable_C || p.dstate > 64 || p.seqlen < 8 || !fwd_vector_ok(&p) ||
+        !offsets_ok(p))
+        return {0, 0};
     const int64_t ratio = p.dim / p.n_groups;
     auto waves = [&](int lpr) { return p.batch * p.n_groups * ((ratio + 64 / lpr - 1) / (64 / lpr)); };
     const char *forced = getenv("MM_PQ_LPR");

@@ -995,7 +995,7 @@ struct K2SData {                       // one lane's global data for pair iterat
     RawVec<T, 2> u0, d0, z0, u1, d1, z1;   // u, delta, z: 2 steps of tiles 0 and 1 of pair i + 1
 };
 
-template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT>
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT, bool YO>
 __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
 scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
@@ -1077,7 +1077,8 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     auto load_data = [&](int32_t i, K2SData<T> &dst) {
         const uint32_t sof = pair_off(i);
         dst.b = buffer_load_raw<T, 4>(rs_b, fo_b, sof);
-        dst.c = buffer_load_raw<T, 4>(rs_c, fo_c, sof);
+        if constexpr (YO) dst.c = buffer_load_raw<T, 4>(rs_c, fo_c, sof);
+        else dst.c = {};
         load_tile(2 * i + 2, dst.u0, dst.d0, dst.z0);
         load_tile(2 * i + 3, dst.u1, dst.d1, dst.z1);
     };
@@ -1098,8 +1099,10 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
         }
         *reinterpret_cast<float2 *>(&DT(Slot)[ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3)]) = make_float2(dtp[0], dtp[1]);
         *reinterpret_cast<float2 *>(&DU(Slot)[ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3)]) = make_float2(dtp[0] * uu[0], dtp[1] * uu[1]);
-        ru[sl] = u;
-        rz[sl] = z;
+        if constexpr (YO) {
+            ru[sl] = u;
+            rz[sl] = z;
+        }
     };
 
     // Epilogue of tile t (slot S = t % 4, partials in yb): the 8 row partials added in row order,
@@ -1167,12 +1170,18 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
                 constexpr int s = kT1 * H + 4 * s4 + j;
                 h[0] = __builtin_fmaf(av[j][0], h[0], bbv[j][0]);
                 h[1] = __builtin_fmaf(av[j][1], h[1], bbv[j][1]);
-                float acc = row_bcast<s / 4>(cv[s % 4]) * h[0];
-                fmac_row_bcast<LPS + s / 4>(acc, cv[s % 4], h[1]);
-                pv[j] = acc;
+                if constexpr (YO) {
+                    float acc = row_bcast<s / 4>(cv[s % 4]) * h[0];
+                    fmac_row_bcast<LPS + s / 4>(acc, cv[s % 4], h[1]);
+                    pv[j] = acc;
+                }
             });
-            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
-                make_float4(pv[0], pv[1], pv[2], pv[3]);
+            if constexpr (YO)
+                *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
+                    make_float4(pv[0], pv[1], pv[2], pv[3]);
+            // Without the y-partial chain the scheduler would hoist the exponentials of a whole
+            // tile and run out of registers: the states-only scan stays in 4-step groups.
+            if constexpr (!YO) __builtin_amdgcn_sched_barrier(0);
             dtq = ndt;
             duq = ndu;
         });
@@ -1189,7 +1198,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
                 csp[3] = h[1];
             }
         }
-        if (CHUNKS && p.tile_states && t0 + kT1 < L) {
+        if ((CHUNKS || !YO) && p.tile_states && t0 + kT1 < L) {
             float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + 2 * r;
             *reinterpret_cast<float2 *>(ck) = make_float2(h[0], h[1]);
         }
@@ -1197,7 +1206,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if (CHUNKS && p.tile_states)           // the checkpoint before the first tile: zero
+    if ((CHUNKS || !YO) && p.tile_states)  // the checkpoint before the first tile: zero
         *reinterpret_cast<float2 *>(p.tile_states + (b * p.dim + d0 + c) * 16 + 2 * r) = make_float2(0.f, 0.f);
     K2SData<T> ring[PF];
     {
@@ -1225,29 +1234,36 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
             if (i < n_pairs) {
                 const int64_t t0 = int64_t(i) * (2 * kT1);
                 unpack_raw<T, 4>(ring[S].b, bv);
-                unpack_raw<T, 4>(ring[S].c, cv);
                 // Two wait states between the VALU writes of the DPP sources and their first DPP
                 // read by the fmac inline asm (the compiler covers its own DPP instructions).
+                if constexpr (YO) {
+                    unpack_raw<T, 4>(ring[S].c, cv);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                    for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]), "+v"(cv[k]));
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]));
+                }
                 const K2SData<T> nxt = ring[S];  // the elements of pair i + 1
                 load_data(i + PF, ring[S]);
                 // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
                 scan_tile(I0{}, t0, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
                 prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
-                epilogue(T2P3{}, YB(I1{}), i > 0 ? 2 * i - 1 : 0);
+                if constexpr (YO) epilogue(T2P3{}, YB(I1{}), i > 0 ? 2 * i - 1 : 0);
                 __syncthreads();
                 // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
                 scan_tile(I1{}, t0 + kT1, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
                 prologue(T2P3{}, nxt.u1, nxt.d1, nxt.z1);
-                epilogue(T2P{}, YB(I0{}), 2 * i);
+                if constexpr (YO) epilogue(T2P{}, YB(I0{}), 2 * i);
                 __syncthreads();
             }
         });
     }
     // The last tile, 2 n_pairs - 1 (slot (2 n_pairs - 1) % 4: 1 or 3).
-    if (((n_pairs - 1) & 1) == 0) epilogue(I1{}, YB(I1{}), 2 * n_pairs - 1);
-    else epilogue(std::integral_constant<int, 3>{}, YB(I1{}), 2 * n_pairs - 1);
+    if constexpr (YO) {
+        if (((n_pairs - 1) & 1) == 0) epilogue(I1{}, YB(I1{}), 2 * n_pairs - 1);
+        else epilogue(std::integral_constant<int, 3>{}, YB(I1{}), 2 * n_pairs - 1);
+    }
     if (p.last_state) {
         p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r] = h[0];
         p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r + 1] = h[1];
@@ -1258,10 +1274,10 @@ template <typename T, int PF, bool HAS_Z, bool HAS_OUT>
 int launch_k2s_io(const mm_scan_fwd_params &p, hipStream_t stream) {
     const int64_t ratio = p.dim / p.n_groups;
     dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
-    auto *kern = p.delta_softplus ? (p.chunk_states ? scan_fwd_k2s<T, PF, true, true, HAS_Z, HAS_OUT>
-                                                    : scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT>)
-                                  : (p.chunk_states ? scan_fwd_k2s<T, PF, false, true, HAS_Z, HAS_OUT>
-                                                    : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT>);
+    auto *kern = p.delta_softplus ? (p.chunk_states ? scan_fwd_k2s<T, PF, true, true, HAS_Z, HAS_OUT, true>
+                                                    : scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT, true>)
+                                  : (p.chunk_states ? scan_fwd_k2s<T, PF, false, true, HAS_Z, HAS_OUT, true>
+                                                    : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT, true>);
     hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
     return launch_status("scan_fwd_k2s");
 }
@@ -1270,6 +1286,17 @@ template <typename T, int PF>
 int launch_k2s(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (p.z) return p.out ? launch_k2s_io<T, PF, true, true>(p, stream) : launch_k2s_io<T, PF, true, false>(p, stream);
     return launch_k2s_io<T, PF, false, true>(p, stream);   // without z the pre-gate out is the output
+}
+
+// The states alone (L a multiple of 32): p.tile_states, and p.last_state when given.
+template <typename T>
+int launch_k2s_states(const mm_scan_fwd_params &p, hipStream_t stream) {
+    const int64_t ratio = p.dim / p.n_groups;
+    dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
+    auto *kern = p.delta_softplus ? scan_fwd_k2s<T, 2, true, false, false, false, false>
+                                  : scan_fwd_k2s<T, 2, false, false, false, false, false>;
+    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
+    return launch_status("scan_fwd_k2s_states");
 }
 
 template <typename T, int NW>
@@ -1405,10 +1432,19 @@ bool tile_states_ok(const mm_scan_fwd_params &p) {
 }
 
 // The states-only forward the backward runs when no tile states were saved; MM_ERR_UNSUPPORTED
-// (nothing launched) when the request falls outside the dstate-16 pipelined kernel.
+// (nothing launched) when the request falls outside the dstate-16 pipelined kernels. 16-bit inputs
+// with L a multiple of 32 take k2s without outputs, others the pipelined kernel's MODE 3
+// (MM_STATES_KERNEL=pipe selects it always, for comparison). Both compute the states with the
+// same operations in the same order.
 template <typename T>
 int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (!p.tile_states || !tile_states_ok(p)) return MM_ERR_UNSUPPORTED;
+    static const bool pipe = [] {
+        const char *e = getenv("MM_STATES_KERNEL");
+        return e && !strcmp(e, "pipe");
+    }();
+    if constexpr (!std::is_same_v<T, float>)
+        if (!pipe && p.seqlen % (2 * tiled::kT1) == 0) return tiled::launch_k2s_states<T>(p, stream);
     return tiled::launch_fwd_states<T>(p, stream);
 }
 template int launch_states_only<float>(const mm_scan_fwd_params &, hipStream_t);

@@ -338,7 +338,7 @@ def test_bwd_segmented_tail(dtype, slots, L, monkeypatch):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("slots,L", [(6, 1000), (64, 200)])
+@pytest.mark.parametrize("slots,L", [(6, 1000), (64, 200), (6, 1024)])   # 1024: k2s states pass (16-bit)
 def test_bwd_states_pass(dtype, slots, L, monkeypatch):
     """Without the forward's tile states (the callers that recompute, e.g. MambaInnerFn at
     checkpoint_lvl 1), the backward first runs a states-only forward into its workspace and then
