@@ -37,16 +37,24 @@ namespace bwd {
 constexpr int kBT = 16;          // steps per checkpoint tile
 constexpr int kGenThreads = 256;
 
-// Zero a float32 tensor of up to 4 dimensions with arbitrary element strides.
-__global__ void __launch_bounds__(256)
-fill_zero4(float *p, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int64_t s0, int64_t s1, int64_t s2, int64_t s3) {
-    const int64_t total = n0 * n1 * n2 * n3;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-        int64_t r = i;
-        const int64_t i3 = r % n3; r /= n3;
-        const int64_t i2 = r % n2; r /= n2;
-        const int64_t i1 = r % n1; r /= n1;
-        p[r * s0 + i1 * s1 + i2 * s2 + i3 * s3] = 0.f;
+// Zero up to 8 float32 tensors of up to 4 dimensions with arbitrary element strides, in one launch
+// (the gradients a backward accumulates into).
+struct FillSet {
+    float *ptr[8];
+    int64_t n[8][4], st[8][4];
+    int count;
+};
+__global__ void __launch_bounds__(256) fill_zero_set(const FillSet fs) {
+    for (int k = 0; k < fs.count; ++k) {
+        const int64_t n1 = fs.n[k][1], n2 = fs.n[k][2], n3 = fs.n[k][3];
+        const int64_t total = fs.n[k][0] * n1 * n2 * n3;
+        for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+            int64_t r = i;
+            const int64_t i3 = r % n3; r /= n3;
+            const int64_t i2 = r % n2; r /= n2;
+            const int64_t i1 = r % n1; r /= n1;
+            fs.ptr[k][r * fs.st[k][0] + i1 * fs.st[k][1] + i2 * fs.st[k][2] + i3 * fs.st[k][3]] = 0.f;
+        }
     }
 }
 
@@ -634,14 +642,30 @@ int launch_general(const mm_scan_bwd_params &p, hipStream_t s) {
     return launch_status("scan_bwd_general");
 }
 
-int launch_fill(float *ptr, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int64_t s0, int64_t s1, int64_t s2,
-                int64_t s3, hipStream_t s) {
-    const int64_t total = n0 * n1 * n2 * n3;
-    if (!ptr || total == 0) return MM_OK;
-    const int64_t blocks = (total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096;
-    hipLaunchKernelGGL(fill_zero4, dim3(unsigned(blocks)), dim3(256), 0, s, ptr, n0, n1, n2, n3, s0, s1, s2, s3);
-    return launch_status("fill_zero4");
-}
+// Tensors to zero, collected and cleared by one launch of fill_zero_set.
+struct Fills {
+    FillSet fs{};
+    int64_t largest = 0;
+    void add(float *ptr, int64_t n0, int64_t n1, int64_t n2, int64_t n3, int64_t s0, int64_t s1, int64_t s2,
+             int64_t s3) {
+        const int64_t total = n0 * n1 * n2 * n3;
+        if (!ptr || total == 0) return;
+        const int k = fs.count++;
+        fs.ptr[k] = ptr;
+        const int64_t n[4] = {n0, n1, n2, n3}, st[4] = {s0, s1, s2, s3};
+        for (int i = 0; i < 4; ++i) {
+            fs.n[k][i] = n[i];
+            fs.st[k][i] = st[i];
+        }
+        largest = std::max(largest, total);
+    }
+    int launch(hipStream_t s) const {
+        if (fs.count == 0) return MM_OK;
+        const int64_t blocks = std::min<int64_t>((largest + 255) / 256, 4096);
+        hipLaunchKernelGGL(fill_zero_set, dim3(unsigned(blocks)), dim3(256), 0, s, fs);
+        return launch_status("fill_zero_set");
+    }
+};
 
 // The dstate-16 kernel's requirements: variable B/C, 16-channel blocks inside one group, L a
 // multiple of 8, two-element-aligned activation rows and four-element-aligned B/C rows.
@@ -876,24 +900,24 @@ int launch_bwd(const mm_scan_bwd_params &p, hipStream_t s) {
     // The accumulated gradients start from zero on the launch stream (the dstate-16 kernel writes
     // dB and dC whole and only accumulates dA, dD and ddelta_bias).
     const bool fast = bwd::fast_ok(p) && p.seqlen > 0;
-    int rc = bwd::launch_fill(p.dA, 1, 1, p.dim, p.dstate, 0, 0, p.dA_d_stride, p.dA_dstate_stride, s);
-    if (rc == MM_OK && p.is_variable_B && !fast)
-        rc = bwd::launch_fill(p.dB, p.batch, p.n_groups, p.dstate, p.seqlen, p.dB_batch_stride, p.dB_group_stride,
-                              p.dB_dstate_stride, 1, s);
-    if (rc == MM_OK && !p.is_variable_B)
-        rc = bwd::launch_fill(p.dB, 1, 1, p.dim, p.dstate, 0, 0, p.dB_d_stride, p.dB_dstate_stride, s);
-    if (rc == MM_OK && p.is_variable_C && !fast)
-        rc = bwd::launch_fill(p.dC, p.batch, p.n_groups, p.dstate, p.seqlen, p.dC_batch_stride, p.dC_group_stride,
-                              p.dC_dstate_stride, 1, s);
-    if (rc == MM_OK && !p.is_variable_C)
-        rc = bwd::launch_fill(p.dC, 1, 1, p.dim, p.dstate, 0, 0, p.dC_d_stride, p.dC_dstate_stride, s);
-    if (rc == MM_OK && p.dD) rc = bwd::launch_fill(p.dD, 1, 1, 1, p.dim, 0, 0, 0, 1, s);
-    if (rc == MM_OK && p.ddelta_bias) rc = bwd::launch_fill(p.ddelta_bias, 1, 1, 1, p.dim, 0, 0, 0, 1, s);
+    bwd::Fills f;
+    f.add(p.dA, 1, 1, p.dim, p.dstate, 0, 0, p.dA_d_stride, p.dA_dstate_stride);
+    if (p.is_variable_B && !fast)
+        f.add(p.dB, p.batch, p.n_groups, p.dstate, p.seqlen, p.dB_batch_stride, p.dB_group_stride, p.dB_dstate_stride, 1);
+    if (!p.is_variable_B) f.add(p.dB, 1, 1, p.dim, p.dstate, 0, 0, p.dB_d_stride, p.dB_dstate_stride);
+    if (p.is_variable_C && !fast)
+        f.add(p.dC, p.batch, p.n_groups, p.dstate, p.seqlen, p.dC_batch_stride, p.dC_group_stride, p.dC_dstate_stride, 1);
+    if (!p.is_variable_C) f.add(p.dC, 1, 1, p.dim, p.dstate, 0, 0, p.dC_d_stride, p.dC_dstate_stride);
+    if (p.dD) f.add(p.dD, 1, 1, 1, p.dim, 0, 0, 0, 1);
+    if (p.ddelta_bias) f.add(p.ddelta_bias, 1, 1, 1, p.dim, 0, 0, 0, 1);
     // dP / dQ: one (dstate, rank) slice per channel unless their d stride is 0 (one shared slice).
-    if (rc == MM_OK && p.P) rc = bwd::launch_fill(p.dP, 1, p.dP_d_stride ? p.dim : 1, p.dstate, p.pq_rank, 0,
-                                                 p.dP_d_stride, p.dP_dstate_stride, p.dP_r_stride, s);
-    if (rc == MM_OK && p.P) rc = bwd::launch_fill(p.dQ, 1, p.dQ_d_stride ? p.dim : 1, p.pq_rank, p.dstate, 0,
-                                                 p.dQ_d_stride, p.dQ_r_stride, p.dQ_dstate_stride, s);
+    if (p.P) {
+        f.add(p.dP, 1, p.dP_d_stride ? p.dim : 1, p.dstate, p.pq_rank, 0, p.dP_d_stride, p.dP_dstate_stride,
+              p.dP_r_stride);
+        f.add(p.dQ, 1, p.dQ_d_stride ? p.dim : 1, p.pq_rank, p.dstate, 0, p.dQ_d_stride, p.dQ_r_stride,
+              p.dQ_dstate_stride);
+    }
+    const int rc = f.launch(s);
     if (rc != MM_OK) return rc;
     if (p.seqlen == 0) return MM_OK;
     if (p.P) return bwd::launch_pq<T>(p, s);
