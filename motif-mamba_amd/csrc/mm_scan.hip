@@ -371,6 +371,108 @@ state_update_vec16(const mm_state_update_params p, const uint32_t ratio, const u
     }
 }
 
+// The raw bits of a 16- or 32-bit value of lane (quad base + Q) of every quad (v_mov_b32_dpp
+// quad_perm [Q,Q,Q,Q]).
+template <int Q>
+__device__ __forceinline__ int quad_bcast(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, Q * 0x55, 0xf, 0xf, false);
+}
+template <typename T>
+__device__ __forceinline__ int raw_bits(T v) {
+    if constexpr (std::is_same_v<T, float>) return __float_as_int(v);
+    else return int(__builtin_bit_cast(uint16_t, v));
+}
+template <typename T>
+__device__ __forceinline__ T from_bits(int v) {
+    if constexpr (std::is_same_v<T, float>) return __int_as_float(v);
+    else return __builtin_bit_cast(T, uint16_t(v));
+}
+
+// state_update_vec16 for four batch rows per workgroup whose 64 channels lie in one group, with
+// the per-row loads shared: the four lanes of a channel row load x, dt and z of four different batch
+// rows (lane part p: row bb * 4 + p) and pass them round the quad with DPP, one load per lane per
+// tensor instead of one per lane per row; B and C of the four rows (2 x 4 x 16 values) come in
+// with one element per lane into LDS; each lane stores the output of batch row p. Per lane that is
+// about half the memory instructions of state_update_vec16<T, S, 4>, whose operations and order it
+// keeps (the results are bit-identical).
+template <typename T, typename S>
+__global__ void __launch_bounds__(kDecBlock)
+state_update_vec16x(const mm_state_update_params p, const uint32_t ratio, const uint32_t n_dblk) {
+    constexpr int U = 4;
+    __shared__ __align__(16) float sBC[U * 2 * 16];   // [row u][B | C][state]
+    const uint32_t bb = blockIdx.x / n_dblk;
+    const uint32_t jd = blockIdx.x - bb * n_dblk;
+    const int tid = int(threadIdx.x);
+    const int part = tid & 3;
+    const uint32_t dim = uint32_t(p.dim), batch = uint32_t(p.batch);
+    const uint32_t dr = jd * 64u + uint32_t(tid >> 2);
+    const uint32_t d = dr < dim ? dr : dim - 1;
+    const uint32_t g = (jd * 64u < dim ? jd * 64u : dim - 1) / ratio;   // one group per workgroup
+    if (tid < U * 2 * 16) {
+        const uint32_t u = uint32_t(tid) >> 5, n = uint32_t(tid) & 15;
+        const uint32_t b = bb * U + u < batch ? bb * U + u : batch - 1;
+        const T *src = (tid & 16) ? reinterpret_cast<const T *>(p.C) + int64_t(b) * p.C_batch_stride + int64_t(g) * p.C_group_stride
+                                  : reinterpret_cast<const T *>(p.B) + int64_t(b) * p.B_batch_stride + int64_t(g) * p.B_group_stride;
+        sBC[tid] = to_f32(src[n]);
+    }
+    const float4 a4 = *reinterpret_cast<const float4 *>(p.A + int64_t(d) * p.A_d_stride + 4 * part);
+    const float Dv = p.D ? load_param(p.D, p.D_type, d) : 0.f;
+    const float bias = p.dt_bias ? load_param(p.dt_bias, p.dt_bias_type, d) : 0.f;
+    S *const state = reinterpret_cast<S *>(p.state);
+    // This lane's batch row for x, dt, z and the output: bb * 4 + part.
+    const uint32_t bp0 = bb * U + uint32_t(part);
+    const uint32_t bp = bp0 < batch ? bp0 : batch - 1;
+    const T xp = reinterpret_cast<const T *>(p.x)[int64_t(bp) * p.x_batch_stride + int64_t(d) * p.x_d_stride];
+    const T dtp = reinterpret_cast<const T *>(p.dt)[int64_t(bp) * p.dt_batch_stride + int64_t(d) * p.dt_d_stride];
+    T zp{};
+    if (p.z) zp = reinterpret_cast<const T *>(p.z)[int64_t(bp) * p.z_batch_stride + int64_t(d) * p.z_d_stride];
+    float4 sv[U];
+    uint2 sw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t b0 = bb * U + u;
+        const uint32_t b = b0 < batch ? b0 : batch - 1;
+        const S *sp = state + int64_t(b) * p.state_batch_stride + int64_t(d) * p.state_d_stride + 4 * part;
+        if constexpr (std::is_same_v<S, float>) sv[u] = *reinterpret_cast<const float4 *>(sp);
+        else sw[u] = *reinterpret_cast<const uint2 *>(sp);
+    }
+    __syncthreads();   // sBC written
+    float y_mine = 0.f;
+    static_for<0, U>([&](auto Uc) {
+        constexpr int u = decltype(Uc)::value;
+        const uint32_t b = bb * U + u;
+        const float4 b4 = *reinterpret_cast<const float4 *>(&sBC[(u * 2 + 0) * 16 + 4 * part]);
+        const float4 c4 = *reinterpret_cast<const float4 *>(&sBC[(u * 2 + 1) * 16 + 4 * part]);
+        float dt = to_f32(from_bits<T>(quad_bcast<u>(raw_bits(dtp)))) + bias;
+        if (p.dt_softplus) dt = softplus_fast(dt);
+        const float x = to_f32(from_bits<T>(quad_bcast<u>(raw_bits(xp))));
+        const float dtx = dt * x;
+        const float dl = dt * kLog2e;
+        float4 st;
+        if constexpr (std::is_same_v<S, float>) st = sv[u];
+        else st = unpack4<S>(sw[u]);
+        st.x = __builtin_fmaf(st.x, fast_exp2(dl * a4.x), dtx * b4.x);
+        st.y = __builtin_fmaf(st.y, fast_exp2(dl * a4.y), dtx * b4.y);
+        st.z = __builtin_fmaf(st.z, fast_exp2(dl * a4.z), dtx * b4.z);
+        st.w = __builtin_fmaf(st.w, fast_exp2(dl * a4.w), dtx * b4.w);
+        if (dr < dim && b < batch) {
+            S *sp = state + int64_t(b) * p.state_batch_stride + int64_t(dr) * p.state_d_stride + 4 * part;
+            if constexpr (std::is_same_v<S, float>) *reinterpret_cast<float4 *>(sp) = st;
+            else *reinterpret_cast<uint2 *>(sp) = pack4<S>(st);
+        }
+        // y from the float32 state, before a 16-bit state is rounded.
+        float y = __builtin_fmaf(st.x, c4.x, __builtin_fmaf(st.y, c4.y, __builtin_fmaf(st.z, c4.z, st.w * c4.w)));
+        y += __shfl_xor(y, 1, 4);
+        y += __shfl_xor(y, 2, 4);
+        if (part == u) y_mine = y;
+    });
+    if (dr < dim && bp0 < batch) {
+        float y = __builtin_fmaf(Dv, to_f32(xp), y_mine);
+        if (p.z) y *= silu_fast(to_f32(zp));
+        reinterpret_cast<T *>(p.out)[int64_t(bp0) * p.out_batch_stride + int64_t(dr) * p.out_d_stride] = from_f32<T>(y);
+    }
+}
+
 }  // namespace mm
 
 // ================================================================================================
@@ -599,12 +701,29 @@ int launch_vec16(const mm_state_update_params &p, hipStream_t s) {
 }
 
 template <typename T, typename S>
+int launch_vec16x(const mm_state_update_params &p, hipStream_t s) {
+    const int64_t n_dblk = (p.dim + 63) / 64;
+    const int64_t n_bblk = (p.batch + 3) / 4;
+    hipLaunchKernelGGL((mm::state_update_vec16x<T, S>), dim3(unsigned(n_bblk * n_dblk)), dim3(mm::kDecBlock), 0, s, p,
+                       uint32_t(p.dim / p.n_groups), uint32_t(n_dblk));
+    return mm::launch_status("state_update");
+}
+
+template <typename T, typename S>
 int dispatch_su_state(const mm_state_update_params &p, hipStream_t s) {
     // A 1-D grid of fewer than 2^24 workgroups of 256 lanes keeps gridDim.x * blockDim.x < 2^32.
     const int64_t U = p.batch >= 4 ? 4 : 1;
     if (su_vec16_ok(p) && p.dim < (int64_t(1) << 31) && p.batch < (int64_t(1) << 31) &&
         ((p.batch + U - 1) / U) * ((p.dim + 63) / 64) < (int64_t(1) << 24)) {
-        // Four batch rows per workgroup share the loads of A, D and dt_bias (batch 256: 41 -> 37 us).
+        // Four batch rows per workgroup share the loads of A, D and dt_bias (batch 256: 41 -> 37 us),
+        // and, when the workgroup's 64 channels lie in one group, those of x, dt, z, B and C
+        // (MM_SU_KERNEL=vec16 keeps the per-row loads, for comparison).
+        static const bool per_row = [] {
+            const char *e = getenv("MM_SU_KERNEL");
+            return e && !strcmp(e, "vec16");
+        }();
+        const int64_t ratio = p.dim / p.n_groups;
+        if (p.batch >= 4 && !per_row && (p.n_groups == 1 || ratio % 64 == 0)) return launch_vec16x<T, S>(p, s);
         if (p.batch >= 4) return launch_vec16<T, S, 4>(p, s);
         return launch_vec16<T, S, 1>(p, s);
     }
