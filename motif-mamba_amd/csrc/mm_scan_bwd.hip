@@ -239,6 +239,9 @@ constexpr int kFH = 8;           // steps per reduction half
 constexpr int kPS = 8;           // step stride (floats) of sPart rows
 constexpr int kXS = kFT + 1;     // step stride (float4) of sX rows
 constexpr int kBufs = 1;         // sX / sBC buffers (one: 4 workgroups fit a CU's LDS)
+// sBC row stride (floats): B 16 | C 16 | 2 pad. 34 (2 mod 32 banks) puts the four step rows that
+// one 32-lane staging store touches on disjoint banks; the 8-byte reads stay aligned.
+constexpr int kBCS = 34;
 
 // sRed address of (tensor, state n, step t of the half, channel c): a block of 8 rows of 16
 // channels per (tensor, state), rows 20 floats apart so that 8 consecutive steps of one state (the
@@ -297,7 +300,7 @@ template <typename T, bool CARRY>
 __global__ void __launch_bounds__(128)
 scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws, const BwdSeg sg) {
     __shared__ __align__(16) float4 sX[kBufs][16 * kXS];    // [buf][c][t]: (dt', dt'u, u, g)
-    __shared__ __align__(16) float sBC[kBufs][kFT * 36];     // [buf][t][B 16 | C 16 | pad]
+    __shared__ __align__(16) float sBC[kBufs][kFT * kBCS];   // [buf][t][B 16 | C 16 | pad]
     __shared__ __align__(16) float sRed[kRedFloats];         // red_at(tensor, n, t, c)
     __shared__ __align__(16) float sPart[8 * 2 * 16 * kPS];  // [slot][gh B | ddt][c][t]
 
@@ -305,6 +308,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const int rs = tid >> 4;               // state slot: states 2 rs, 2 rs + 1; prologue steps 2 rs, 2 rs + 1
     const int c = tid & 15;                // channel within the block
     const int n0 = 2 * rs;
+    const int pswz = (c >> 2) & 3;         // sPart step-pair permutation of this channel
     // The CARRY launch walks segments 1 .. n_seg-1 (segment 0 hands nothing on).
     const int64_t nsw = CARRY ? sg.n_seg - 1 : sg.n_seg;
     const int64_t uo = int64_t(blockIdx.x) / nsw;
@@ -413,7 +417,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
         unpack2<T>(r.bc0, v[0], v[1]);
         unpack2<T>(r.bc1, v[2], v[3]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sBC[buf][(4 * st_q + i) * 36 + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
+        for (int i = 0; i < 4; ++i) sBC[buf][(4 * st_q + i) * kBCS + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
     };
 
     if constexpr (CARRY) {
@@ -428,7 +432,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 #pragma unroll
             for (int t = kFT - 1; t >= 0; --t) {
                 const float4 x = sX[0][c * kXS + t];
-                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[0][t * 36 + 16 + n0]);
+                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[0][t * kBCS + 16 + n0]);
                 gh0 = __builtin_fmaf(an0, gh0, x.w * cv.x);
                 gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
                 an0 = __builtin_amdgcn_exp2f(x.x * A20);
@@ -456,7 +460,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 #pragma unroll
         for (int t = 0; t < kFT; ++t) {
             const float4 x = sX[buf][c * kXS + t];
-            const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + n0]);
+            const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * kBCS + n0]);
             h0 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A20), h0, x.y * bv.x);
             h1 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A21), h1, x.y * bv.y);
         }
@@ -495,7 +499,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 #pragma unroll
             for (int t = 0; t < kFT; ++t) {
                 const float4 x = sX[buf][c * kXS + t];
-                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + n0]);
+                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * kBCS + n0]);
                 as0[t] = __builtin_amdgcn_exp2f(x.x * A20);
                 as1[t] = __builtin_amdgcn_exp2f(x.x * A21);
                 x0 = __builtin_fmaf(as0[t], x0, x.y * bv.x);
@@ -512,8 +516,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             for (int s = kFH - 1; s >= 0; --s) {
                 const int t = half * kFH + s;
                 const float4 x = sX[buf][c * kXS + t];     // dt', dt'u, u, g
-                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + n0]);
-                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[buf][t * 36 + 16 + n0]);
+                const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * kBCS + n0]);
+                const float2 cv = *reinterpret_cast<const float2 *>(&sBC[buf][t * kBCS + 16 + n0]);
                 gh0 = __builtin_fmaf(an0, gh0, x.w * cv.x);
                 gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
                 const float ah0 = __builtin_fmaf(-x.y, bv.x, hs0[t]);   // a_t h_{t-1}
@@ -531,12 +535,16 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             }
             dA0 += dA_t0;
             dA1 += dA_t1;
-            float4 *pp = reinterpret_cast<float4 *>(&sPart[((rs * 2 + 0) * 16 + c) * kPS]);
-            pp[0] = make_float4(pu[0], pu[1], pu[2], pu[3]);
-            pp[1] = make_float4(pu[4], pu[5], pu[6], pu[7]);
-            float4 *pq = reinterpret_cast<float4 *>(&sPart[((rs * 2 + 1) * 16 + c) * kPS]);
-            pq[0] = make_float4(pd[0], pd[1], pd[2], pd[3]);
-            pq[1] = make_float4(pd[4], pd[5], pd[6], pd[7]);
+            // sPart rows hold 4 step pairs; pair q of channel c sits at pair position q ^ pswz, so
+            // that the 16 channels one 64-bit LDS cycle serves hit 16 distinct bank pairs, for these
+            // stores and for the owners' reads below (8-float rows alone put 4 channels on each).
+            float2 *pp = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 0) * 16 + c) * kPS]);
+            float2 *pq = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 1) * 16 + c) * kPS]);
+#pragma unroll
+            for (int q = 0; q < kFH / 2; ++q) {
+                pp[q ^ pswz] = make_float2(pu[2 * q], pu[2 * q + 1]);
+                pq[q ^ pswz] = make_float2(pd[2 * q], pd[2 * q + 1]);
+            }
             __syncthreads();
             // dB / dC of this half summed over the block's 16 channels: rows (tensor, state, step)
             // tid and tid + 128, step fastest, so consecutive lanes read consecutive steps.
@@ -564,8 +572,9 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 float su[2] = {0.f, 0.f}, sd[2] = {0.f, 0.f};
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    const float2 a = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 0) * 16 + c) * kPS + sl]);
-                    const float2 bq = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 1) * 16 + c) * kPS + sl]);
+                    const int pos = 2 * ((sl >> 1) ^ pswz);
+                    const float2 a = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 0) * 16 + c) * kPS + pos]);
+                    const float2 bq = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 1) * 16 + c) * kPS + pos]);
                     su[0] += a.x; su[1] += a.y;
                     sd[0] += bq.x; sd[1] += bq.y;
                 }
