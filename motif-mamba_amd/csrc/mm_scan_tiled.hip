@@ -1270,14 +1270,23 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     }
 }
 
+// fp32 rows: only the instances without chunk states (the training variants' chunk and tile state
+// stores take them past 168 VGPRs, where they spill); the caller routes chunk states elsewhere.
 template <typename T, int PF, bool HAS_Z, bool HAS_OUT>
 int launch_k2s_io(const mm_scan_fwd_params &p, hipStream_t stream) {
     const int64_t ratio = p.dim / p.n_groups;
     dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
-    auto *kern = p.delta_softplus ? (p.chunk_states ? scan_fwd_k2s<T, PF, true, true, HAS_Z, HAS_OUT, true>
-                                                    : scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT, true>)
-                                  : (p.chunk_states ? scan_fwd_k2s<T, PF, false, true, HAS_Z, HAS_OUT, true>
-                                                    : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT, true>);
+    void (*kern)(const mm_scan_fwd_params, const int64_t);
+    if constexpr (sizeof(T) == 4) {
+        if (p.chunk_states || p.tile_states) return MM_ERR_UNSUPPORTED;
+        kern = p.delta_softplus ? scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT, true>
+                                : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT, true>;
+    } else {
+        kern = p.delta_softplus ? (p.chunk_states ? scan_fwd_k2s<T, PF, true, true, HAS_Z, HAS_OUT, true>
+                                                  : scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT, true>)
+                                : (p.chunk_states ? scan_fwd_k2s<T, PF, false, true, HAS_Z, HAS_OUT, true>
+                                                  : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT, true>);
+    }
     hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
     return launch_status("scan_fwd_k2s");
 }
@@ -1312,12 +1321,13 @@ int launch_nw(const mm_scan_fwd_params &p, hipStream_t stream) {
 
 }  // namespace tiled
 
-// Kernel choice for dstate 16: by default 16-bit inputs take k2s (L a multiple of 32) or k2i, fp32
-// inputs the pipelined k2. MM_SCAN_KERNEL in the environment selects "k2i" (two states per lane,
-// per-element work alternating between the waves), "k2" / "k1" (two / one state per lane,
-// alternating prologue/epilogue phases), or "nw1" / "nw2" / "nw4" (multi-state-per-lane kernel
-// without pipelining, 1, 2 or 4 waves per group). MM_SCAN_PF (1, 2, 3; default 2) sets the load
-// distance in 32-step tile pairs of k2 / k1 (k2i loads 2 pairs ahead). fp32 inputs use k2 by default.
+// Kernel choice for dstate 16: by default 16-bit inputs take k2s (L a multiple of 32) or k2i; fp32
+// inputs take k2s for L a multiple of 32 without chunk or tile states (inference), else the
+// pipelined k2. MM_SCAN_KERNEL in the environment selects "k2i" (two states per lane, per-element
+// work alternating between the waves), "k2" / "k1" (two / one state per lane, alternating
+// prologue/epilogue phases), or "nw1" / "nw2" / "nw4" (multi-state-per-lane kernel without
+// pipelining, 1, 2 or 4 waves per group). MM_SCAN_PF (1, 2, 3; default 2) sets the load distance in
+// 32-step tile pairs of k2 / k1 (k2i loads 2 pairs ahead).
 static int tiled_variant() {
     static int v = [] {
         const char *e = getenv("MM_SCAN_KERNEL");
@@ -1389,8 +1399,16 @@ int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg) {
 template <typename T>
 static int launch_k2x(const mm_scan_fwd_params &p, hipStream_t stream) {
     static const bool nofull = getenv("MM_SCAN_NOFULL") != nullptr;
-    if (tiled_variant() != 31 && p.seqlen % (2 * tiled::kT1) == 0 && !nofull) return tiled::launch_k2s<T, 2>(p, stream);
-    return tiled::launch_k2i<T, 2>(p, stream);
+    const bool whole_pairs = p.seqlen % (2 * tiled::kT1) == 0 && !nofull;
+    if constexpr (sizeof(T) == 4) {
+        // fp32: k2s for the inference requests it compiles for (no chunk or tile states), the
+        // pipelined kernel for the rest.
+        if (whole_pairs && !p.chunk_states && !p.tile_states) return tiled::launch_k2s<T, 2>(p, stream);
+        return launch_pipe_pf<T, 2>(p, stream);
+    } else {
+        if (tiled_variant() != 31 && whole_pairs) return tiled::launch_k2s<T, 2>(p, stream);
+        return tiled::launch_k2i<T, 2>(p, stream);
+    }
 }
 
 template <typename T>
@@ -1419,10 +1437,7 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
         case 4: return tiled::launch_nw<T, 4>(p, stream);
         case 10: return launch_pipe_pf<T, 1>(p, stream);
         case 20: return launch_pipe_pf<T, 2>(p, stream);
-        default:
-            // fp32 rows double the in-flight registers of the interleaved kernel (it would spill).
-            if constexpr (std::is_same_v<T, float>) return launch_pipe_pf<T, 2>(p, stream);
-            else return launch_k2x<T>(p, stream);
+        default: return launch_k2x<T>(p, stream);
     }
 }
 

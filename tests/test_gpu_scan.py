@@ -118,9 +118,10 @@ def test_random_shapes(shape, dtype):
                                                               softplus=False)],
                          ids=["noD", "noz", "nobias", "nosoftplus", "bare"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
-def test_optional_inputs(flags, dtype):
-    _say(f"optional inputs {flags} {dtype}")
-    case = _case(8, 2, 64, 80, 16, dtype, **flags)
+@pytest.mark.parametrize("L", [80, 96], ids=["L80", "L96"])  # 96: whole 32-step pairs (k2s)
+def test_optional_inputs(flags, dtype, L):
+    _say(f"optional inputs {flags} {dtype} L={L}")
+    case = _case(8, 2, 64, L, 16, dtype, **flags)
     exp, exp_last = selective_scan_ref(**case, return_last_state=True)
     out, last = _run(case)
     _close(out, exp, dtype, "out")
