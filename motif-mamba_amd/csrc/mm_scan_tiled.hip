@@ -25,6 +25,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "mm_common.h"
@@ -988,6 +989,11 @@ int launch_k2i(const mm_scan_fwd_params &p, hipStream_t stream) {
 // branch between the scan and the element work, so the scheduler can fill the scan's latency gaps
 // with softplus, the row-partial sums and the gating. Taken when L is a multiple of 32 (whole tile
 // pairs, buffer addressing as k2i's FULL path).
+//
+// Sequence segments (SEG, blockIdx.z = segment of sg.pairs tile pairs), as the pipelined kernel's
+// MODE 1 and 2: SEG 1 scans segments 0 .. n_seg-2 from a zero state for the states alone (YO false)
+// and writes each segment's end state and sum of delta'; SEG 2 scans every segment from its carried
+// state (and delta' prefix) and writes the outputs, last_state from the last segment.
 // ---------------------------------------------------------------------------------------------
 template <typename T>
 struct K2SData {                       // one lane's global data for pair iteration i
@@ -995,10 +1001,12 @@ struct K2SData {                       // one lane's global data for pair iterat
     RawVec<T, 2> u0, d0, z0, u1, d1, z1;   // u, delta, z: 2 steps of tiles 0 and 1 of pair i + 1
 };
 
-template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT, bool YO>
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT, bool YO, int SEG = 0>
 __global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
-scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
+scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
+    static_assert(SEG != 1 || !YO, "the first segment pass computes the states alone");
+    static_assert(SEG != 2 || YO, "the second segment pass writes the outputs");
     constexpr int E = 2, LPS = 8, NR = 8;
     __shared__ __align__(16) float sDt0[kCh * kT1], sDt1[kCh * kT1], sDt2[kCh * kT1], sDt3[kCh * kT1];
     __shared__ __align__(16) float sDu0[kCh * kT1], sDu1[kCh * kT1], sDu2[kCh * kT1], sDu3[kCh * kT1];
@@ -1031,6 +1039,10 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
     const int64_t L = p.seqlen;
     const int32_t n_pairs = int32_t(L / (2 * kT1));   // L is a multiple of 32 here
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+    const int seg = SEG ? int(blockIdx.z) : 0;
+    const int32_t pb = SEG ? int32_t(seg * sg.pairs) : 0;                                 // first pair
+    const int32_t pe = SEG ? (pb + int32_t(sg.pairs) < n_pairs ? pb + int32_t(sg.pairs) : n_pairs) : n_pairs;
+    const int64_t srow = (b * p.dim + d0 + c) * int64_t(sg.n_seg) + seg;                 // segment slot
 
     const int64_t de = d0 + ce;
     const T *ub = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d0 * p.u_d_stride;
@@ -1047,11 +1059,11 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         At[k] = p.A[(d0 + c) * p.A_d_stride + int64_t(2 * r + k) * p.A_dstate_stride] * kLog2e;
-        h[k] = 0.f;
+        h[k] = SEG == 2 ? sg.h[srow * 16 + 2 * r + k] : 0.f;
     }
     const float Dv = p.D ? p.D[de] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
-    float cum_dt = 0.f;
+    float cum_dt = (SEG == 2 && CHUNKS) ? sg.cum[srow] : 0.f;
 
     // Buffer resources of the group's rows (the host checks that every byte offset of the group is
     // below 2^32) and this lane's byte offsets from them; tile and pair offsets are scalar.
@@ -1158,7 +1170,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
             static_for<0, 4>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 constexpr int s = kT1 * H + 4 * s4 + j;
-                if (CHUNKS) cum_dt += dts[j];
+                if (CHUNKS || SEG == 1) cum_dt += dts[j];
                 static_for<0, 2>([&](auto KK) {
                     constexpr int k = decltype(KK)::value;
                     av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
@@ -1198,7 +1210,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
                 csp[3] = h[1];
             }
         }
-        if ((CHUNKS || !YO) && p.tile_states && t0 + kT1 < L) {
+        if (SEG == 0 && (CHUNKS || !YO) && p.tile_states && t0 + kT1 < L) {
             float *ck = p.tile_states + ((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + 2 * r;
             *reinterpret_cast<float2 *>(ck) = make_float2(h[0], h[1]);
         }
@@ -1206,32 +1218,34 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if ((CHUNKS || !YO) && p.tile_states)  // the checkpoint before the first tile: zero
+    if (SEG == 0 && (CHUNKS || !YO) && p.tile_states)  // the checkpoint before the first tile: zero
         *reinterpret_cast<float2 *>(p.tile_states + (b * p.dim + d0 + c) * 16 + 2 * r) = make_float2(0.f, 0.f);
+    // Tile t of the segment sits in slot (t - 2 pb) % 4: the slots and buffer parities below count
+    // pairs from pb.
     K2SData<T> ring[PF];
     {
         RawVec<T, E> u0, dl0, z0, u1, dl1, z1;
-        load_tile(0, u0, dl0, z0);
-        load_tile(1, u1, dl1, z1);
+        load_tile(2 * pb, u0, dl0, z0);
+        load_tile(2 * pb + 1, u1, dl1, z1);
 #pragma unroll
-        for (int s = 0; s < PF; ++s) load_data(s, ring[s]);
-        prologue(I0{}, u0, dl0, z0);       // tiles 0 and 1, slots 0 and 1
+        for (int s = 0; s < PF; ++s) load_data(pb + s, ring[s]);
+        prologue(I0{}, u0, dl0, z0);       // tiles 2 pb and 2 pb + 1, slots 0 and 1
         prologue(I1{}, u1, dl1, z1);
     }
     __syncthreads();
     pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kT1 + (swc << 2)]);
     pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kT1 + (swc << 2)]);
 
-    for (int32_t i0 = 0; i0 < n_pairs; i0 += PF) {
+    for (int32_t i0 = pb; i0 < pe; i0 += PF) {
         static_for<0, PF>([&](auto Sc) {
             constexpr int S = decltype(Sc)::value;
-            constexpr int P = S & 1;       // parity of the pair index (PF is even)
+            constexpr int P = S & 1;       // parity of the pair index from pb (PF is even)
             using T2P = std::integral_constant<int, 2 * P>;
             using T2P1 = std::integral_constant<int, 2 * P + 1>;
             using T2P2 = std::integral_constant<int, 2 * P + 2>;
             using T2P3 = std::integral_constant<int, 2 * P + 3>;
             const int32_t i = i0 + S;
-            if (i < n_pairs) {
+            if (i < pe) {
                 const int64_t t0 = int64_t(i) * (2 * kT1);
                 unpack_raw<T, 4>(ring[S].b, bv);
                 // Two wait states between the VALU writes of the DPP sources and their first DPP
@@ -1249,7 +1263,7 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
                 // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
                 scan_tile(I0{}, t0, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
                 prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
-                if constexpr (YO) epilogue(T2P3{}, YB(I1{}), i > 0 ? 2 * i - 1 : 0);
+                if constexpr (YO) epilogue(T2P3{}, YB(I1{}), i > pb ? 2 * i - 1 : 2 * pb);
                 __syncthreads();
                 // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
                 scan_tile(I1{}, t0 + kT1, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
@@ -1259,16 +1273,23 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio) {
             }
         });
     }
-    // The last tile, 2 n_pairs - 1 (slot (2 n_pairs - 1) % 4: 1 or 3).
+    // The last tile, 2 pe - 1 (slot (2 (pe - pb) - 1) % 4: 1 or 3).
     if constexpr (YO) {
-        if (((n_pairs - 1) & 1) == 0) epilogue(I1{}, YB(I1{}), 2 * n_pairs - 1);
-        else epilogue(std::integral_constant<int, 3>{}, YB(I1{}), 2 * n_pairs - 1);
+        if (((pe - 1 - pb) & 1) == 0) epilogue(I1{}, YB(I1{}), 2 * pe - 1);
+        else epilogue(std::integral_constant<int, 3>{}, YB(I1{}), 2 * pe - 1);
     }
-    if (p.last_state) {
+    if constexpr (SEG == 1) {
+        sg.h[srow * 16 + 2 * r] = h[0];
+        sg.h[srow * 16 + 2 * r + 1] = h[1];
+        if (r == 0) sg.sumdt[srow] = cum_dt;
+    } else if (p.last_state && (SEG == 0 || seg == sg.n_seg - 1)) {
         p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r] = h[0];
         p.last_state[(b * p.dim + d0 + c) * 16 + 2 * r + 1] = h[1];
     }
 }
+
+using K2SKernel = void (*)(const mm_scan_fwd_params, const int64_t, const SegArgs);
+constexpr SegArgs kWholeRows{0, 1, nullptr, nullptr, nullptr};
 
 // fp32 rows: only the instances without chunk states (the training variants' chunk and tile state
 // stores take them past 168 VGPRs, where they spill); the caller routes chunk states elsewhere.
@@ -1276,7 +1297,7 @@ template <typename T, int PF, bool HAS_Z, bool HAS_OUT>
 int launch_k2s_io(const mm_scan_fwd_params &p, hipStream_t stream) {
     const int64_t ratio = p.dim / p.n_groups;
     dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
-    void (*kern)(const mm_scan_fwd_params, const int64_t);
+    K2SKernel kern;
     if constexpr (sizeof(T) == 4) {
         if (p.chunk_states || p.tile_states) return MM_ERR_UNSUPPORTED;
         kern = p.delta_softplus ? scan_fwd_k2s<T, PF, true, false, HAS_Z, HAS_OUT, true>
@@ -1287,7 +1308,7 @@ int launch_k2s_io(const mm_scan_fwd_params &p, hipStream_t stream) {
                                 : (p.chunk_states ? scan_fwd_k2s<T, PF, false, true, HAS_Z, HAS_OUT, true>
                                                   : scan_fwd_k2s<T, PF, false, false, HAS_Z, HAS_OUT, true>);
     }
-    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
+    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio, kWholeRows);
     return launch_status("scan_fwd_k2s");
 }
 
@@ -1304,8 +1325,48 @@ int launch_k2s_states(const mm_scan_fwd_params &p, hipStream_t stream) {
     dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
     auto *kern = p.delta_softplus ? scan_fwd_k2s<T, 2, true, false, false, false, false>
                                   : scan_fwd_k2s<T, 2, false, false, false, false, false>;
-    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio);
+    hipLaunchKernelGGL(kern, grid, dim3(128), 0, stream, p, ratio, kWholeRows);
     return launch_status("scan_fwd_k2s_states");
+}
+
+// The full pass of the segmented k2s (SEG 2) for one output set; fp32 has no chunk-state instance.
+template <typename T, bool HAS_Z, bool HAS_OUT>
+K2SKernel k2s_seg_full(bool softplus, bool chunks) {
+    if constexpr (sizeof(T) == 4)
+        return softplus ? scan_fwd_k2s<T, 2, true, false, HAS_Z, HAS_OUT, true, 2>
+                        : scan_fwd_k2s<T, 2, false, false, HAS_Z, HAS_OUT, true, 2>;
+    else
+        return softplus ? (chunks ? scan_fwd_k2s<T, 2, true, true, HAS_Z, HAS_OUT, true, 2>
+                                  : scan_fwd_k2s<T, 2, true, false, HAS_Z, HAS_OUT, true, 2>)
+                        : (chunks ? scan_fwd_k2s<T, 2, false, true, HAS_Z, HAS_OUT, true, 2>
+                                  : scan_fwd_k2s<T, 2, false, false, HAS_Z, HAS_OUT, true, 2>);
+}
+
+// Segmented scan on k2s (L a multiple of 32): the states of segments 0 .. n_seg-2 (SEG 1), the
+// carry chain, every segment with its outputs (SEG 2). Requests that write both out and out_z, and
+// fp32 requests with chunk states, return MM_ERR_UNSUPPORTED before launching anything (the
+// pipelined kernel's segments serve them).
+template <typename T>
+int launch_k2s_segmented(const mm_scan_fwd_params &p, hipStream_t stream, const SegArgs &sg) {
+    const bool chunks = p.chunk_states != nullptr;
+    if ((p.z && p.out) || (sizeof(T) == 4 && chunks) || p.tile_states) return MM_ERR_UNSUPPORTED;
+    const K2SKernel states = p.delta_softplus ? scan_fwd_k2s<T, 2, true, false, false, false, false, 1>
+                                              : scan_fwd_k2s<T, 2, false, false, false, false, false, 1>;
+    const K2SKernel full = p.z ? k2s_seg_full<T, true, false>(p.delta_softplus, chunks)
+                               : k2s_seg_full<T, false, true>(p.delta_softplus, chunks);
+    const int64_t ratio = p.dim / p.n_groups;
+    hipLaunchKernelGGL(states, dim3(unsigned(p.dim / kCh), unsigned(p.batch), unsigned(sg.n_seg - 1)), dim3(128), 0,
+                       stream, p, ratio, sg);
+    int rc = launch_status("scan_fwd_k2s_seg_states");
+    if (rc != MM_OK) return rc;
+    const int64_t rows = p.batch * p.dim;
+    hipLaunchKernelGGL(seg_carry_kernel, dim3(unsigned((rows * 16 + 255) / 256)), dim3(256), 0, stream, p.A,
+                       p.A_d_stride, p.A_dstate_stride, rows, p.dim, sg);
+    rc = launch_status("seg_carry");
+    if (rc != MM_OK) return rc;
+    hipLaunchKernelGGL(full, dim3(unsigned(p.dim / kCh), unsigned(p.batch), unsigned(sg.n_seg)), dim3(128), 0, stream,
+                       p, ratio, sg);
+    return launch_status("scan_fwd_k2s_seg");
 }
 
 template <typename T, int NW>
@@ -1375,19 +1436,52 @@ static bool pipe_offsets_ok(const mm_scan_fwd_params &p) {
     return span < (int64_t(1) << 31);
 }
 
+// Whether a segmented request runs on k2s: every 32-step pair whole, and neither a request that
+// writes both out and out_z nor fp32 with chunk states (the pipelined kernel's segments serve those;
+// MM_SCAN_KERNEL=k2 selects them always).
+static bool k2s_segments_ok(const mm_scan_fwd_params &p) {
+    return p.seqlen % (2 * tiled::kT1) == 0 && tiled_variant() != 20 && !(p.z && p.out) &&
+           !(p.itype == MM_FLOAT32 && p.chunk_states);
+}
+
+// SIMDs of the current device (4 per CU), or 1024 (the MI355X's) when it cannot be queried.
+static int64_t device_simds() {
+    static std::atomic<int64_t> cache[64] = {};   // per device; every thread computes the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
+    int64_t v = cache[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            return 1024;
+        v = 4 * int64_t(cus);
+        cache[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 // Sequence segments for shapes whose (batch, 16-channel) groups give fewer than one wave per SIMD
-// (two waves per group): enough segments for ~3 waves per SIMD, each at least 512 steps. The
-// segmented scan does ~1.75x the work of one pass, which pays only at such low occupancy.
+// (two waves per group): enough segments for ~5 waves per SIMD in the full pass, each at least 512
+// steps. Measured at config 3 (160 groups, L 65,536, fp32, k2s segments): 6, 8, 9, 10, 12, 15, 16,
+// 19, 24 and 32 segments take 1.42, 1.44, 1.31, 1.48, 1.40, 1.29, 1.24, 1.24, 1.25 and 1.25 ms -- a
+// full pass just past one round of workgroups (10, 12) or a few long segments at 2 waves per SIMD
+// (6, 8) cost most, and from ~5 waves per SIMD on the time is flat. MM_SCAN_SEGMENTS=n sets the count
+// (for measurements).
 int64_t segment_count(const mm_scan_fwd_params &p) {
     if (!tiled_shape_ok(p) || !pipe_offsets_ok(p) || p.tile_states) return 1;
     const int64_t waves = 2 * p.batch * (p.dim / tiled::kCh);
-    if (waves >= 1024) return 1;
     const int64_t n_pairs = (p.seqlen + 2 * tiled::kT1 - 1) / (2 * tiled::kT1);
-    int64_t n_seg = (3072 + waves - 1) / waves;
-    n_seg = std::min(n_seg, n_pairs / 16);
+    int64_t n_seg;
+    if (const char *e = std::getenv("MM_SCAN_SEGMENTS"); e && std::atoll(e) >= 1) {
+        n_seg = std::min<int64_t>(std::atoll(e), n_pairs);
+    } else {
+        const int64_t simds = device_simds();
+        if (waves >= simds) return 1;
+        n_seg = std::min((5 * simds + waves - 1) / waves, n_pairs / 16);
+    }
     if (n_seg < 2) return 1;
     const int64_t pairs = (n_pairs + n_seg - 1) / n_seg;
-    return (n_pairs + pairs - 1) / pairs;
+    return (n_pairs + pairs - 1) / pairs;   // every segment holds at least one pair
 }
 
 int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg) {
@@ -1429,6 +1523,10 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
         float *ws = static_cast<float *>(p.workspace);
         const tiled::SegArgs sg{(n_pairs + n_seg - 1) / n_seg, int32_t(n_seg), ws, ws + rows * n_seg * 16,
                                 ws + rows * n_seg * 17};
+        if (k2s_segments_ok(p)) {
+            const int rc = tiled::launch_k2s_segmented<T>(p, stream, sg);
+            if (rc != MM_ERR_UNSUPPORTED) return rc;
+        }
         return tiled::launch_pipe_segmented<T>(p, stream, sg);
     }
     switch (pipe_ok ? tiled_variant() : 2) {
@@ -1447,8 +1545,8 @@ bool tile_states_ok(const mm_scan_fwd_params &p) {
 }
 
 // The states-only forward the backward runs when no tile states were saved; MM_ERR_UNSUPPORTED
-// (nothing launched) when the request falls outside the dstate-16 pipelined kernels. 16-bit inputs
-// with L a multiple of 32 take k2s without outputs, others the pipelined kernel's MODE 3
+// (nothing launched) when the request falls outside the dstate-16 pipelined kernels. Inputs with L
+// a multiple of 32 take k2s without outputs, others the pipelined kernel's MODE 3
 // (MM_STATES_KERNEL=pipe selects it always, for comparison). Both compute the states with the
 // same operations in the same order.
 template <typename T>
@@ -1458,8 +1556,7 @@ int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream) {
         const char *e = getenv("MM_STATES_KERNEL");
         return e && !strcmp(e, "pipe");
     }();
-    if constexpr (!std::is_same_v<T, float>)
-        if (!pipe && p.seqlen % (2 * tiled::kT1) == 0) return tiled::launch_k2s_states<T>(p, stream);
+    if (!pipe && p.seqlen % (2 * tiled::kT1) == 0) return tiled::launch_k2s_states<T>(p, stream);
     return tiled::launch_fwd_states<T>(p, stream);
 }
 template int launch_states_only<float>(const mm_scan_fwd_params &, hipStream_t);

@@ -278,22 +278,39 @@ def _seg_rows(out, last, case, what):
     rows = [(0, d) for d in range(case["u"].shape[1])]
     r = cscan.scan_rows(**case, rows=rows)
     rtol, atol = fixtures.tolerances(case["u"].dtype)
+    exp = r["out_z"] if case["z"] is not None else r["out"]   # without z the pre-gate out is returned
     for i, (b, d) in enumerate(rows):
-        np.testing.assert_allclose(out[b, d].double().numpy(), r["out_z"][i], rtol=rtol, atol=atol,
+        np.testing.assert_allclose(out[b, d].double().numpy(), exp[i], rtol=rtol, atol=atol,
                                    err_msg=f"{what} row {(b, d)} out_z")
         np.testing.assert_allclose(last[b, d].double().numpy(), r["last_state"][i], rtol=rtol, atol=atol,
                                    err_msg=f"{what} row {(b, d)} last_state")
 
 
+# L 8192: 256 tile pairs in 16 segments of 16 pairs (k2s segments). L 8864: 277 pairs in 17
+# segments of 17, the last of 5 (odd pair counts, a short last segment). L 8200: not whole 32-step
+# pairs (the pipelined kernel's segments, a partial last tile).
+@pytest.mark.parametrize("L", [8192, 8864, 8200])
 @pytest.mark.parametrize("G", [1, 2])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
-def test_segmented_scan(dtype, G):
-    """batch 1 x 64 channels x L 8192 is 4 channel groups, so the scan runs in 16 sequence
-    segments (state-only pass, carry chain, full pass); every row against the float64 restatement."""
-    _say(f"segmented scan {dtype} G={G}")
-    case = _case(20 + G, 1, 64, 8192, 16, dtype, bkind="4d", G=G)
+def test_segmented_scan(dtype, G, L):
+    """batch 1 x 64 channels is 4 channel groups, so a long scan runs in sequence segments
+    (state-only pass, carry chain, full pass); every row against the float64 restatement."""
+    _say(f"segmented scan {dtype} G={G} L={L}")
+    case = _case(20 + G, 1, 64, L, 16, dtype, bkind="4d", G=G)
     out, last = _run(case)
-    _seg_rows(out, last, case, f"segmented G={G}")
+    _seg_rows(out, last, case, f"segmented G={G} L={L}")
+
+
+@pytest.mark.parametrize("flags", [dict(with_z=False), dict(softplus=False), dict(with_D=False, with_bias=False)],
+                         ids=["noz", "nosoftplus", "noD_nobias"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_segmented_optional_inputs(dtype, flags):
+    """The segmented kernels without z (the pre-gate out is the output), without softplus, and
+    without D and delta_bias; every row against the float64 restatement."""
+    _say(f"segmented optional inputs {flags} {dtype}")
+    case = _case(26, 1, 64, 4096, 16, dtype, bkind="4d", G=1, **flags)
+    out, last = _run(case)
+    _seg_rows(out, last, case, f"segmented {flags}")
 
 
 def test_segmented_reference_fwd_chunk_states():
@@ -316,6 +333,31 @@ def test_segmented_reference_fwd_chunk_states():
     np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
     exp_out = selective_scan_ref(**{**case, "z": None})
     _close(out.cpu(), exp_out, torch.float32, "out (pre-gate)")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_segmented_reference_fwd_chunk_states_16bit(dtype):
+    """The reference-format fwd without z on a segmented 16-bit shape (k2s segments with chunk
+    states): x's (prod a, h) per 2048-step chunk carry the delta' prefix and the state across
+    segment boundaries; out against the float64 restatement."""
+    _say(f"segmented reference-format fwd, {dtype}, no z")
+    from motif_mamba_amd import _native
+    case = _case(32, 1, 64, 8192 + 96, 16, dtype, bkind="4d", G=1, with_z=False)
+    g = _to(case, DEV)
+    res = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], D=g["D"], z=None,
+                            delta_bias=g["delta_bias"], delta_softplus=True)
+    torch.cuda.synchronize()
+    assert len(res) == 2
+    out, x = res
+    assert x.shape == (1, 64, 5, 32)
+    rows = [(0, d) for d in range(64)]
+    r = cscan.scan_rows(**case, rows=rows, chunk=2048)
+    rtol, atol = fixtures.tolerances(dtype)
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(x[b, d, :, 1::2].cpu().double().numpy(), r["h_chunks"][i], rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(out[b, d].cpu().double().numpy(), r["out"][i], rtol=rtol, atol=atol)
+    pa = chunk_states_ref(case["delta"], case["A"], case["delta_bias"], True)
+    np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
 
 
 def test_segmented_c_abi_with_and_without_workspace():
