@@ -19,6 +19,14 @@
 //  * Global loads for tile i+1 are issued before the scan of tile i.
 // NW trades per-update overhead (smaller K shares the per-step work among fewer updates) for more
 // concurrent waves per SIMD, which gfx950 needs to reach its VALU/transcendental issue rate.
+//
+// The file is compiled three times, in parallel: on its own for fp32 inputs, where it also defines
+// the shape queries (segment_count, segment_workspace_bytes, tile_states_ok), and through
+// mm_scan_tiled_f16.hip / mm_scan_tiled_bf16.hip, which set MM_TILED_TYPE, for the 16-bit instances.
+#ifndef MM_TILED_TYPE
+#define MM_TILED_TYPE float
+#define MM_TILED_COMMON
+#endif
 #include <hip/hip_runtime.h>
 
 #include <stdlib.h>
@@ -576,7 +584,8 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
 // Carries between segments, one thread per (batch, channel, state): the start state of segment s+1
 // is exp2(A log2e sum(delta' of s)) * start(s) + end_from_zero(s); written in place over h, with
 // the delta' prefix of every segment in cum.
-__global__ void __launch_bounds__(256)
+// (static: each of the file's three translation units holds its own copy.)
+static __global__ void __launch_bounds__(256)
 seg_carry_kernel(const float *A, int64_t A_d_stride, int64_t A_dstate_stride, int64_t rows, int64_t dim,
                  const SegArgs sg) {
     const int64_t tid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1444,6 +1453,7 @@ static bool k2s_segments_ok(const mm_scan_fwd_params &p) {
            !(p.itype == MM_FLOAT32 && p.chunk_states);
 }
 
+#ifdef MM_TILED_COMMON
 // SIMDs of the current device (4 per CU), or 1024 (the MI355X's) when it cannot be queried.
 static int64_t device_simds() {
     static std::atomic<int64_t> cache[64] = {};   // per device; every thread computes the same value
@@ -1487,6 +1497,12 @@ int64_t segment_count(const mm_scan_fwd_params &p) {
 int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg) {
     return n_seg > 1 ? p.batch * p.dim * n_seg * (16 + 2) * int64_t(sizeof(float)) : 0;
 }
+
+// Whether the diagonal forward can write tile_states for this request (the kernels below).
+bool tile_states_ok(const mm_scan_fwd_params &p) {
+    return tiled_shape_ok(p) && fwd_vector_ok(&p) && pipe_offsets_ok(p);
+}
+#endif  // MM_TILED_COMMON
 
 // The two-states-per-lane kernels for 16-bit inputs: k2s (symmetric element work) when L is a
 // multiple of 32, else k2i (MM_SCAN_KERNEL=k2i selects k2i always, for comparison).
@@ -1539,10 +1555,6 @@ int try_launch_tiled(const mm_scan_fwd_params &p, hipStream_t stream) {
     }
 }
 
-// Whether the diagonal forward can write tile_states for this request (the kernels above).
-bool tile_states_ok(const mm_scan_fwd_params &p) {
-    return tiled_shape_ok(p) && fwd_vector_ok(&p) && pipe_offsets_ok(p);
-}
 
 // The states-only forward the backward runs when no tile states were saved; MM_ERR_UNSUPPORTED
 // (nothing launched) when the request falls outside the dstate-16 pipelined kernels. Inputs with L
@@ -1559,12 +1571,7 @@ int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream) {
     if (!pipe && p.seqlen % (2 * tiled::kT1) == 0) return tiled::launch_k2s_states<T>(p, stream);
     return tiled::launch_fwd_states<T>(p, stream);
 }
-template int launch_states_only<float>(const mm_scan_fwd_params &, hipStream_t);
-template int launch_states_only<f16_t>(const mm_scan_fwd_params &, hipStream_t);
-template int launch_states_only<bf16_t>(const mm_scan_fwd_params &, hipStream_t);
-
-template int try_launch_tiled<float>(const mm_scan_fwd_params &, hipStream_t);
-template int try_launch_tiled<f16_t>(const mm_scan_fwd_params &, hipStream_t);
-template int try_launch_tiled<bf16_t>(const mm_scan_fwd_params &, hipStream_t);
+template int launch_states_only<MM_TILED_TYPE>(const mm_scan_fwd_params &, hipStream_t);
+template int try_launch_tiled<MM_TILED_TYPE>(const mm_scan_fwd_params &, hipStream_t);
 
 }  // namespace mm

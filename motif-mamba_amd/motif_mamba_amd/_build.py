@@ -27,8 +27,9 @@ PROBE_NAME = "libmm_probe.so"
 EXT_NAME = "mm_scan_torch"
 ARCH = "gfx950"
 
-HIP_SOURCES = ["mm_scan.hip", "mm_scan_tiled.hip", "mm_scan_pq.hip", "mm_scan_bwd.hip", "mm_scan_pq_bwd.hip",
-               "mm_conv1d.hip", "mm_norm.hip"]
+# mm_scan_tiled_{f16,bf16}.hip include mm_scan_tiled.hip for their input type (parallel builds).
+HIP_SOURCES = ["mm_scan.hip", "mm_scan_tiled.hip", "mm_scan_tiled_f16.hip", "mm_scan_tiled_bf16.hip",
+               "mm_scan_pq.hip", "mm_scan_bwd.hip", "mm_scan_pq_bwd.hip", "mm_conv1d.hip", "mm_norm.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # Packed fp32 VALU ops are disabled: the compiler would otherwise form v_pk_{add,mul,fma}_f32
 # from scalar float code, and those have given silent wrong results on these GPUs.
