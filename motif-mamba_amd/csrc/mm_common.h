@@ -45,18 +45,18 @@ __device__ __forceinline__ float softplus_f32(float x) {
 // silu(z) = z / (1 + exp(-z)), in float32.
 __device__ __forceinline__ float silu_f32(float z) { return z / (1.f + expf(-z)); }
 
-// softplus with torch's threshold (x > 20 ? x : log1p(exp(x))) built on v_exp_f32 / v_log_f32.
-// log1p(e) = log(u) + (e - (u - 1)) / u with u = fl(1 + e): the second term restores the part of e
-// lost when rounding 1 + e (exact for e <= 1 by Fast2Sum). 1/u is replaced by max(2 - u, 0): exact
-// at u = 1, and for u >= 2 the term is below 2^-24 relative to log(u) >= 0.69, so dropping it costs
-// under an ulp. Relative error stays at a few ulp for every x, including x << 0 where log1p(e) ~ e.
+// softplus with torch's threshold semantics (x > 20 ? x : log1p(exp(x))) built on v_exp_f32 /
+// v_log_f32, evaluated as max(x, 0) + log1p(e) with e = exp(-|x|): the same function, no overflow,
+// and equal to x in float32 for x > 20 (there e < 2.1e-9 is below half an ulp of x). With e <= 1,
+// u = fl(1 + e) lies in [1, 2] and log1p(e) = log(u) + lost / u + O(lost^2), where lost = e - (u - 1)
+// is exact (Fast2Sum). lost is added without the 1/u: |lost| <= 2^-24 and lost (1 - 1/u) stays
+// below 2^-24 e, so the relative error is a few ulp for every x, including x << 0 where
+// softplus(x) ~ e.
 __device__ __forceinline__ float softplus_fast(float x) {
-    const float e = __builtin_amdgcn_exp2f(x * kLog2e);
+    const float e = __builtin_amdgcn_exp2f(-__builtin_fabsf(x) * kLog2e);
     const float u = 1.f + e;
     const float lost = e - (u - 1.f);
-    const float corr = lost * __builtin_fmaxf(2.f - u, 0.f);
-    const float r = __builtin_fmaf(__builtin_amdgcn_logf(u), kLn2, corr);
-    return x > 20.f ? x : r;
+    return __builtin_fmaxf(x, 0.f) + __builtin_fmaf(__builtin_amdgcn_logf(u), kLn2, lost);
 }
 
 // silu(z) = z * 1 / (1 + 2^(-z log2 e)) with v_exp_f32 and v_rcp_f32 (both ~1 ulp).

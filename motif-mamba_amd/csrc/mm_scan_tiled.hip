@@ -1104,8 +1104,9 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) 
         load_tile(2 * i + 3, dst.u1, dst.d1, dst.z1);
     };
 
-    // u and z of the tiles between their prologue and their epilogue: tile t in slot t % 4.
-    RawVec<T, E> ru[4], rz[4];
+    // u (unpacked) and z of the tiles between their prologue and their epilogue: tile t in slot t % 4.
+    float ru[4][E];
+    RawVec<T, E> rz[4];
 
     // Prologue of tile t (slot S = t % 4): delta', delta' u of this lane's two elements -> LDS.
     auto prologue = [&](auto Slot, const RawVec<T, E> &u, const RawVec<T, E> &dl, const RawVec<T, E> &z) {
@@ -1121,7 +1122,8 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) 
         *reinterpret_cast<float2 *>(&DT(Slot)[ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3)]) = make_float2(dtp[0], dtp[1]);
         *reinterpret_cast<float2 *>(&DU(Slot)[ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3)]) = make_float2(dtp[0] * uu[0], dtp[1] * uu[1]);
         if constexpr (YO) {
-            ru[sl] = u;
+#pragma unroll
+            for (int k = 0; k < E; ++k) ru[sl][k] = uu[k];
             rz[sl] = z;
         }
     };
@@ -1141,10 +1143,9 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) 
             a.x += v.x;
             a.y += v.y;
         }
-        float uu[E], zz[E];
-        unpack_raw<T, E>(ru[sl], uu);
+        float zz[E];
         unpack_raw<T, E>(rz[sl], zz);
-        float o[E] = {__builtin_fmaf(Dv, uu[0], a.x), __builtin_fmaf(Dv, uu[1], a.y)};
+        float o[E] = {__builtin_fmaf(Dv, ru[sl][0], a.x), __builtin_fmaf(Dv, ru[sl][1], a.y)};
         const uint32_t sof = uint32_t(t) * uint32_t(kT1 * SZ);
         if constexpr (HAS_OUT) buffer_store_vec<T, E>(rs_o, fo_o, sof, o);
         if constexpr (HAS_Z) {
@@ -1267,16 +1268,17 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) 
 #pragma unroll
                     for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]));
                 }
-                const K2SData<T> nxt = ring[S];  // the elements of pair i + 1
-                load_data(i + PF, ring[S]);
                 // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
                 scan_tile(I0{}, t0, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
-                prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
+                prologue(T2P2{}, ring[S].u0, ring[S].d0, ring[S].z0);
                 if constexpr (YO) epilogue(T2P3{}, YB(I1{}), i > pb ? 2 * i - 1 : 2 * pb);
                 __syncthreads();
                 // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
                 scan_tile(I1{}, t0 + kT1, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
-                prologue(T2P3{}, nxt.u1, nxt.d1, nxt.z1);
+                prologue(T2P3{}, ring[S].u1, ring[S].d1, ring[S].z1);
+                // The entry is consumed: refill it with pair i + PF (B/C) and the elements of the
+                // pair after it, about one pair (~3 us of this wave's work) before their first use.
+                load_data(i + PF, ring[S]);
                 if constexpr (YO) epilogue(T2P{}, YB(I0{}), 2 * i);
                 __syncthreads();
             }

@@ -218,7 +218,11 @@ def test_module_step_call_form(model_dtype):
     """Mambamotif.step's call in a 16-bit model, as written at mamba_simplemotif.py:360-399: B and C
     are column slices of x_proj's output (strided views), dt = dt_proj(dt) without its bias, the
     state from allocate_inference_cache in dt_proj.weight.dtype, D and dt_proj.bias uncast (the
-    model's dtype after model.to(dtype)). Six steps from a zero state."""
+    model's dtype after model.to(dtype)). Six steps from a zero state. The kernel and the oracle round
+    float32 values that may differ by a few float32 ulps (exp/log/rcp evaluated differently) to the
+    16-bit state every step, so a step can split their states by one 16-bit ulp at that step's
+    magnitude, and the split persists (decayed) through later steps: after k steps they may differ by
+    k ulps of the largest magnitude the element has held."""
     import torch.nn.functional as F
     from motif_mamba_amd import selective_state_update
     _say(f"Mambamotif.step call form {model_dtype}")
@@ -233,6 +237,7 @@ def test_module_step_call_form(model_dtype):
     state = torch.zeros(batch, d_inner, N, dtype=model_dtype, device=DEV)
     ref_state = torch.zeros(batch, d_inner, N, dtype=model_dtype)
     gA, gD, gbias = A.to(DEV), D.to(DEV), dt_bias.to(DEV)
+    peak = torch.zeros(batch, d_inner, N)   # largest |state| each element has held so far
     for step in range(6):
         x = torch.randn(batch, d_inner, generator=gen).to(model_dtype)
         z = torch.randn(batch, d_inner, generator=gen).to(model_dtype)
@@ -248,7 +253,10 @@ def test_module_step_call_form(model_dtype):
         torch.cuda.synchronize()
         assert y.dtype == model_dtype
         torch.testing.assert_close(y.cpu().float(), exp.float(), rtol=3e-2, atol=5e-2)
-        torch.testing.assert_close(state.cpu().float(), ref_state.float(), rtol=_ulp_tol(model_dtype), atol=1e-6)
+        peak = torch.maximum(peak, ref_state.float().abs())
+        diff = (state.cpu().float() - ref_state.float()).abs()
+        bound = (step + 1) * _ulp_tol(model_dtype) * peak + 1e-6
+        assert (diff <= bound).all(), f"step {step}: state differs by {(diff - bound).max().item():.3g} beyond the bound"
 
 
 def test_16bit_state_strided_and_c_abi():
