@@ -282,8 +282,9 @@ typedef struct mm_state_update_params {
 int mm_scan_fwd(const mm_scan_fwd_params *params, void *stream);
 
 /* Bytes of `workspace` that let mm_scan_fwd use sequence-parallel segments for this request
- * (0: the single-pass kernels are used anyway). Reads only sizes, flags and strides of `params`;
- * returns 0 for a request mm_scan_fwd would reject. No counterpart in the reference (its forward
+ * (0: the single-pass kernels are used anyway). Reads only sizes, flags and strides of `params`,
+ * and the current device's compute-unit count (the segment count targets about 5 waves per SIMD):
+ * query it with the call's device current. Returns 0 for a request mm_scan_fwd would reject. No counterpart in the reference (its forward
  * allocates nothing beyond the outputs, selective_scan.cpp:383-389). */
 int64_t mm_scan_fwd_workspace_size(const mm_scan_fwd_params *params);
 
