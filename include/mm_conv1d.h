@@ -77,8 +77,8 @@ typedef struct mm_conv1d_update_params {
 } mm_conv1d_update_params;
 
 /* Backward of the forward above for a gradient `dout` of its output: dx (itype), and dweight,
- * dbias summed over batch and steps (float32, overwritten: the call clears them first and
- * accumulates with device atomics). With `silu` the pre-activation is recomputed and dout is taken
+ * dbias summed over batch and steps (float32, overwritten: one workgroup per channel sums them in a
+ * fixed order and stores them, so repeated calls give the same bits). With `silu` the pre-activation is recomputed and dout is taken
  * through silu'. Replaces causal_conv1d_bwd_function(x, weight, bias, dout, seq_idx=None,
  * initial_states=None, dfinal_states=None, dx, return_dinitial_states=False, silu_activation)
  * (call site selective_scan_interface.py:635-637). */

@@ -238,92 +238,92 @@ conv1d_update_tok4(const mm_conv1d_update_params p, const uint32_t n_dblk) {
     }
 }
 
-// Backward: each lane owns NC chunks of 8 positions of one row. It recomputes the pre-activation y
+// Backward: one workgroup per channel d walks every (batch row, tile of kThreads * 8 * NC steps) of
+// that channel; in each tile a lane owns NC chunks of 8 positions. It recomputes the pre-activation y
 // at its positions and the next W - 1 (x from W - 1 before to W - 1 after, as 8-element chunks),
-// forms dy = dout silu'(y), writes dx[s] = sum_k w[k] dy[s + W - 1 - k], and adds its share of
-// dweight[d, k] = sum dy[t] x[t - (W - 1) + k] and dbias[d] = sum dy[t] into the block's LDS sums,
-// which one lane per (block, k) adds to the float32 outputs.
+// forms dy = dout silu'(y) and writes dx[s] = sum_k w[k] dy[s + W - 1 - k]. Its shares of
+// dweight[d, k] = sum dy[t] x[t - (W - 1) + k] and dbias[d] = sum dy[t] stay in registers over the
+// whole walk; at the end the workgroup adds them (waves by shuffles, then LDS, in a fixed order)
+// and one lane per k stores them: no atomics, no clearing launch, and the same bits on every run.
 template <typename T, int W, bool VEC, int NC>
 __global__ void __launch_bounds__(kThreads)
 conv1d_bwd_kernel(const mm_conv1d_bwd_params p) {
     __shared__ float sRed[kThreads / 64][MM_CONV1D_MAX_WIDTH + 1];
-    const int64_t t0 = (int64_t(blockIdx.x) * kThreads + threadIdx.x) * (kChunk * NC);
-    const int64_t d = blockIdx.y;
-    const int64_t b = blockIdx.z;
+    constexpr int64_t kTile = int64_t(kThreads) * kChunk * NC;   // steps per tile
+    const int64_t d = blockIdx.x;
     const int64_t L = p.seqlen;
-    const bool live = t0 < L;
-    const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
-    const T *gr = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
-    T *dxr = reinterpret_cast<T *>(p.dx) + b * p.dx_batch_stride + d * p.dx_d_stride;
+    const int64_t n_tiles = (L + kTile - 1) / kTile;
 
     float w[W];
 #pragma unroll
     for (int k = 0; k < W; ++k) w[k] = load_any(p.weight, p.wtype, d * p.weight_d_stride + k * p.weight_w_stride);
     const float bias = p.bias ? load_any(p.bias, p.wtype, d * p.bias_stride) : 0.f;
 
-    // xs: chunk before, the NC chunks, chunk after; gs: dout of the NC chunks and the chunk after.
-    constexpr int NX = kChunk * (NC + 2), NG = kChunk * (NC + 1);
-    float xs[NX], gs[NG];
-    auto ld = [&](const T *row, int64_t t, float *dst) {   // 8 elements at t (zeros outside [0, L))
-        if (VEC && t >= 0 && t + kChunk <= L) {
-            load8(row + t, dst);
-        } else {
-#pragma unroll
-            for (int i = 0; i < kChunk; ++i) dst[i] = (t + i >= 0 && t + i < L) ? to_f32(row[t + i]) : 0.f;
-        }
-    };
-    if (live) {
-#pragma unroll
-        for (int c = 0; c < NC + 2; ++c) ld(xr, t0 + (c - 1) * kChunk, xs + c * kChunk);
-#pragma unroll
-        for (int c = 0; c < NC + 1; ++c) ld(gr, t0 + c * kChunk, gs + c * kChunk);
-    } else {
-#pragma unroll
-        for (int i = 0; i < NX; ++i) xs[i] = 0.f;
-#pragma unroll
-        for (int i = 0; i < NG; ++i) gs[i] = 0.f;
-    }
-    // dy at positions t0 .. t0 + 8 (NC + 1) - 1 (0 past L).
-    float dy[NG];
-#pragma unroll
-    for (int i = 0; i < NG; ++i) {
-        float y = bias;
-#pragma unroll
-        for (int k = 0; k < W; ++k) y = __builtin_fmaf(w[k], xs[kChunk + i - (W - 1) + k], y);
-        float g = gs[i];
-        if (p.silu) {
-            const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * kLog2e));
-            g *= sg * (1.f + y * (1.f - sg));
-        }
-        dy[i] = (t0 + i < L) ? g : 0.f;
-    }
     float dw[W], db = 0.f;
 #pragma unroll
     for (int k = 0; k < W; ++k) dw[k] = 0.f;
+    for (int64_t b = 0; b < p.batch; ++b) {
+        const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
+        const T *gr = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
+        T *dxr = reinterpret_cast<T *>(p.dx) + b * p.dx_batch_stride + d * p.dx_d_stride;
+        for (int64_t tile = 0; tile < n_tiles; ++tile) {
+            const int64_t t0 = tile * kTile + int64_t(threadIdx.x) * (kChunk * NC);
+            if (t0 >= L) continue;   // lanes past the row's end (last tile only)
+            // xs: chunk before, the NC chunks, chunk after; gs: dout of the NC chunks and the chunk after.
+            constexpr int NX = kChunk * (NC + 2), NG = kChunk * (NC + 1);
+            float xs[NX], gs[NG];
+            auto ld = [&](const T *row, int64_t t, float *dst) {   // 8 elements at t (zeros outside [0, L))
+                if (VEC && t >= 0 && t + kChunk <= L) {
+                    load8(row + t, dst);
+                } else {
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        float o[kChunk];
+                    for (int i = 0; i < kChunk; ++i) dst[i] = (t + i >= 0 && t + i < L) ? to_f32(row[t + i]) : 0.f;
+                }
+            };
 #pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
-            const int s = c * kChunk + i;
-            float acc = 0.f;
+            for (int c = 0; c < NC + 2; ++c) ld(xr, t0 + (c - 1) * kChunk, xs + c * kChunk);
 #pragma unroll
-            for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], dy[s + W - 1 - k], acc);
-            o[i] = acc;
-            db += dy[s];
+            for (int c = 0; c < NC + 1; ++c) ld(gr, t0 + c * kChunk, gs + c * kChunk);
+            // dy at positions t0 .. t0 + 8 (NC + 1) - 1 (0 past L).
+            float dy[NG];
 #pragma unroll
-            for (int k = 0; k < W; ++k) dw[k] = __builtin_fmaf(dy[s], xs[kChunk + s - (W - 1) + k], dw[k]);
-        }
-        const int64_t tc = t0 + c * kChunk;
-        if (VEC && tc + kChunk <= L) {
-            store8(dxr + tc, o);
-        } else {
+            for (int i = 0; i < NG; ++i) {
+                float y = bias;
 #pragma unroll
-            for (int i = 0; i < kChunk; ++i)
-                if (tc + i < L) dxr[tc + i] = from_f32<T>(o[i]);
+                for (int k = 0; k < W; ++k) y = __builtin_fmaf(w[k], xs[kChunk + i - (W - 1) + k], y);
+                float g = gs[i];
+                if (p.silu) {
+                    const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * kLog2e));
+                    g *= sg * (1.f + y * (1.f - sg));
+                }
+                dy[i] = (t0 + i < L) ? g : 0.f;
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                float o[kChunk];
+#pragma unroll
+                for (int i = 0; i < kChunk; ++i) {
+                    const int s = c * kChunk + i;
+                    float acc = 0.f;
+#pragma unroll
+                    for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], dy[s + W - 1 - k], acc);
+                    o[i] = acc;
+                    db += dy[s];
+#pragma unroll
+                    for (int k = 0; k < W; ++k) dw[k] = __builtin_fmaf(dy[s], xs[kChunk + s - (W - 1) + k], dw[k]);
+                }
+                const int64_t tc = t0 + c * kChunk;
+                if (VEC && tc + kChunk <= L) {
+                    store8(dxr + tc, o);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kChunk; ++i)
+                        if (tc + i < L) dxr[tc + i] = from_f32<T>(o[i]);
+                }
+            }
         }
     }
-    // Block sums of dweight / dbias: waves by DPP-free shuffles, then LDS, then one atomic per k.
+    // Workgroup sums of dweight / dbias: waves by shuffles, then the waves in order through LDS.
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
     for (int k = 0; k <= W; ++k) {
@@ -338,17 +338,13 @@ conv1d_bwd_kernel(const mm_conv1d_bwd_params p) {
         float v = 0.f;
 #pragma unroll
         for (int i = 0; i < kThreads / 64; ++i) v += sRed[i][k];
-        if (k < W) atomicAdd(p.dweight + d * W + k, v);
-        else if (p.dbias) atomicAdd(p.dbias + d, v);
+        if (k < W) p.dweight[d * W + k] = v;
+        else if (p.dbias) p.dbias[d] = v;
     }
 }
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-__global__ void fill_zero(float *p, int64_t n) {
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0.f;
-}
 
 template <typename T, int W>
 int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
@@ -359,9 +355,7 @@ int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
     };
     const bool vec = p.seqlen % kChunk == 0 && row_ok(p.x, p.x_batch_stride, p.x_d_stride) &&
                      row_ok(p.dout, p.dout_batch_stride, p.dout_d_stride) && row_ok(p.dx, p.dx_batch_stride, p.dx_d_stride);
-    const int64_t per_lane = int64_t(kChunk) * NC;
-    const int64_t lanes = (p.seqlen + per_lane - 1) / per_lane;
-    dim3 grid(unsigned((lanes + kThreads - 1) / kThreads), unsigned(p.dim), unsigned(p.batch));
+    const dim3 grid(unsigned(p.dim));   // one workgroup per channel (dim < 2^31, checked on entry)
     if (vec)
         hipLaunchKernelGGL((conv1d_bwd_kernel<T, W, true, NC>), grid, dim3(kThreads), 0, s, p);
     else
@@ -369,18 +363,11 @@ int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
     return launch_status("conv1d_bwd");
 }
 
+// dweight and dbias are written (not accumulated) by the one workgroup of each channel, also for
+// an empty batch or sequence (zero sums).
 template <typename T>
 int launch_bwd(const mm_conv1d_bwd_params &p, hipStream_t s) {
-    const int64_t nw = p.dim * p.width;
-    hipLaunchKernelGGL(fill_zero, dim3(unsigned((nw + 255) / 256)), dim3(256), 0, s, p.dweight, nw);
-    int rc = launch_status("conv1d_bwd clear");
-    if (rc != MM_OK) return rc;
-    if (p.dbias) {
-        hipLaunchKernelGGL(fill_zero, dim3(unsigned((p.dim + 255) / 256)), dim3(256), 0, s, p.dbias, p.dim);
-        rc = launch_status("conv1d_bwd clear");
-        if (rc != MM_OK) return rc;
-    }
-    if (p.seqlen == 0) return MM_OK;
+    if (p.dim == 0) return MM_OK;
     switch (p.width) {
         case 1: return launch_bwd_w<T, 1>(p, s);
         case 2: return launch_bwd_w<T, 2>(p, s);
@@ -504,15 +491,15 @@ int mm_causal_conv1d_bwd(const mm_conv1d_bwd_params *params, void *stream) {
     if (p.batch < 0 || p.dim < 0 || p.seqlen < 0) return invalid("mm_causal_conv1d_bwd: negative size");
     if (p.width < 1 || p.width > MM_CONV1D_MAX_WIDTH)
         return invalid("mm_causal_conv1d_bwd: width must be in [1, 8]");
-    if (p.batch > 65535 || p.dim > 65535)
-        return mm::set_error(MM_ERR_UNSUPPORTED, "mm_causal_conv1d_bwd: batch and dim must be <= 65535");
+    if (p.dim > 0x7fffffff)   // one workgroup per channel on a one-dimensional grid
+        return mm::set_error(MM_ERR_UNSUPPORTED, "mm_causal_conv1d_bwd: dim must be < 2^31");
     if (p.dim == 0) return MM_OK;
     if (!p.weight || !p.dweight || (p.bias && !p.dbias))
         return invalid("mm_causal_conv1d_bwd: weight and dweight (and dbias with bias) are required");
     if (p.batch > 0 && p.seqlen > 0 && (!p.x || !p.dout || !p.dx))
         return invalid("mm_causal_conv1d_bwd: x, dout and dx are required");
     mm_conv1d_bwd_params q = p;
-    if (q.batch == 0) q.seqlen = 0;   // nothing to add: the sums are just cleared
+    if (q.batch == 0) q.seqlen = 0;   // nothing to add: the sums are written as zeros
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     switch (q.itype) {
         case MM_FLOAT32: return launch_bwd<float>(q, s);
