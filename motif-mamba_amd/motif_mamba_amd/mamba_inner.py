@@ -96,8 +96,10 @@ class MambaInnerFn(torch.autograd.Function):
     def forward(ctx, xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
                 out_proj_bias, A, B=None, C=None, D=None, delta_bias=None, B_proj_bias=None, C_proj_bias=None,
                 delta_softplus=True, checkpoint_lvl=1, b_rms_weight=None, c_rms_weight=None, dt_rms_weight=None,
-                b_c_dt_rms_eps=1e-6):
-        """xz: (batch, 2 d_inner, seqlen) -> (batch, seqlen, d_model)."""
+                b_c_dt_rms_eps=1e-6, grad_enabled=True):
+        """xz: (batch, 2 d_inner, seqlen) -> (batch, seqlen, d_model). grad_enabled: the caller's grad
+        mode (mamba_inner_fn passes it): under torch.no_grad() the inference path runs even when the
+        weights require grad."""
         assert checkpoint_lvl in (0, 1), "checkpoint_lvl must be 0 or 1"
         if A.is_complex():
             raise NotImplementedError("complex A is not supported by the MI355X build")
@@ -135,7 +137,7 @@ class MambaInnerFn(torch.autograd.Function):
             C = C.contiguous()
         if D is not None:
             D = D.contiguous()
-        if not any(ctx.needs_input_grad):
+        if not grad_enabled or not any(ctx.needs_input_grad):
             # Inference: the scan writes only the gated output; nothing is kept for a backward.
             out_z = ext().fwd_infer(conv1d_out, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
                                     delta_softplus=delta_softplus, return_last_state=False)[0]
@@ -224,7 +226,7 @@ class MambaInnerFn(torch.autograd.Function):
                 dout_proj_weight, dout_proj_bias,
                 dA, dB, dC, dD if D is not None else None,
                 ddelta_bias if delta_bias is not None else None,
-                dB_proj_bias, dC_proj_bias, None, None, None, None, None, None)
+                dB_proj_bias, dC_proj_bias, None, None, None, None, None, None, None)
 
 
 def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
@@ -234,4 +236,5 @@ def mamba_inner_fn(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_wei
     """ssi.py:648-656."""
     return MambaInnerFn.apply(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
                               out_proj_bias, A, B, C, D, delta_bias, B_proj_bias, C_proj_bias, delta_softplus,
-                              checkpoint_lvl, b_rms_weight, c_rms_weight, dt_rms_weight, b_c_dt_rms_eps)
+                              checkpoint_lvl, b_rms_weight, c_rms_weight, dt_rms_weight, b_c_dt_rms_eps,
+                              torch.is_grad_enabled())

@@ -52,7 +52,10 @@ class SelectiveScanFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                return_last_state=False):
+                return_last_state=False, grad_enabled=True):
+        # grad_enabled: the grad mode of the caller (selective_scan_fn passes it; forward itself runs
+        # with grad disabled, and needs_input_grad reflects requires_grad alone, so a module called
+        # under torch.no_grad() with parameters that require grad would otherwise take the training path).
         if u.stride(-1) != 1:
             u = u.contiguous()
         if delta.stride(-1) != 1:
@@ -71,7 +74,7 @@ class SelectiveScanFn(torch.autograd.Function):
         if C.dim() == 3:
             C = rearrange(C, "b dstate l -> b 1 dstate l")
             ctx.squeeze_C = True
-        if not any(ctx.needs_input_grad[:8]):
+        if not grad_enabled or not any(ctx.needs_input_grad[:8]):
             # Inference: only what is returned is written (no pre-gate out, no chunk states).
             res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
                                   delta_softplus=delta_softplus, return_last_state=return_last_state)
@@ -117,6 +120,7 @@ class SelectiveScanFn(torch.autograd.Function):
                 dz,
                 ddelta_bias if delta_bias is not None else None,
                 None,
+                None,
                 None)
 
 
@@ -125,7 +129,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False,
-                return_last_state=False, P=None, Q=None, gamma=None):
+                return_last_state=False, P=None, Q=None, gamma=None, grad_enabled=True):
         if u.stride(-1) != 1:
             u = u.contiguous()
         if delta.stride(-1) != 1:
@@ -146,7 +150,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
         if C.dim() == 3:
             C = rearrange(C, "b dstate l -> b 1 dstate l")
             ctx.squeeze_C = True
-        if not (any(ctx.needs_input_grad[:8]) or any(ctx.needs_input_grad[10:12])):
+        if not grad_enabled or not (any(ctx.needs_input_grad[:8]) or any(ctx.needs_input_grad[10:12])):
             res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
                                   delta_softplus=delta_softplus, return_last_state=return_last_state,
                                   P=P, Q=Q, gamma=gamma)
@@ -194,6 +198,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
                 None,
                 None,
                 dP.to(P.dtype), dQ.to(Q.dtype),
+                None,
                 None)
 
 
@@ -229,5 +234,6 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
     if P is not None or Q is not None or gamma is not None:
         _check_pq(u, delta, A, B, C, P, Q)
         return SelectiveScanPQFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
-                                       return_last_state, P, Q, gamma)
-    return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state)
+                                       return_last_state, P, Q, gamma, torch.is_grad_enabled())
+    return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state,
+                                 torch.is_grad_enabled())

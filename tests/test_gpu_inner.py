@@ -153,6 +153,22 @@ def test_checkpoint_levels_agree_and_inference_path():
         torch.testing.assert_close(g0[k], g1[k], rtol=1e-2, atol=1e-2, msg=lambda m: f"d{k}: {m}")
 
 
+def test_no_grad_with_weights_requiring_grad_takes_inference_path():
+    """A module evaluated under torch.no_grad() passes weights that require grad: mamba_inner_fn
+    takes the inference path then too (the caller's grad mode is passed in), so its output has the
+    same bits as with weights that do not require grad, and carries no graph."""
+    _say("mamba_inner no_grad with weights requiring grad")
+    from mamba_ssm.ops.selective_scan_interface import mamba_inner_fn
+    c = _case(940, L=256, dtype=torch.bfloat16)
+    yi, _ = _run(c)
+    g = _dev(c, True)
+    with torch.no_grad():
+        y = mamba_inner_fn(*[g[k] for k in ARGS])
+    torch.cuda.synchronize()
+    assert not y.requires_grad
+    assert torch.equal(y.cpu(), yi)
+
+
 def test_given_B_C():
     """B and C passed in (not projected): variable (batch, 1, N, L) and constant (d, N) forms; the
     x_proj rows that would have produced them get a zero gradient."""

@@ -216,6 +216,31 @@ def test_deterministic():
     assert torch.equal(a, b) and torch.equal(la, lb)
 
 
+def test_no_grad_with_inputs_requiring_grad_takes_inference_path():
+    """Under torch.no_grad() with inputs that require grad (a module's A, D and delta_bias
+    parameters), selective_scan_fn runs the inference forward: the output has the bits of the
+    training forward's, carries no graph, and nothing for a backward is allocated (the training
+    forward would add the pre-gate out, the chunk states and the tile states: about 3x the output)."""
+    _say("selective_scan_fn no_grad with inputs requiring grad")
+    from motif_mamba_amd import selective_scan_fn
+    case = _case(40, 2, 64, 1024, 16, torch.bfloat16)
+    g = _to(case, DEV)
+    for k in ("A", "D", "delta_bias"):
+        g[k].requires_grad_(True)
+    out_train = selective_scan_fn(**g)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    with torch.no_grad():
+        out = selective_scan_fn(**g)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - base
+    assert not out.requires_grad and out_train.requires_grad
+    assert torch.equal(out, out_train.detach())
+    out_bytes = out.numel() * out.element_size()
+    assert peak < 2 * out_bytes, f"peak {peak} bytes for a {out_bytes}-byte output"
+
+
 # ---------------------------------------------------------------------------------------------
 # Full benchmark shapes: every row against the float64 C restatement.
 # ---------------------------------------------------------------------------------------------
