@@ -1268,27 +1268,21 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) 
 #pragma unroll
                     for (int k = 0; k < 4; ++k) asm volatile("s_nop 1" : "+v"(bv[k]));
                 }
-                // Refill of the ring entry with pair i + PF (B/C) and the elements of the pair after
-                // it. The inference instances refill it once its elements are consumed (after the
-                // second prologue below), about one pair (~3 us of this wave's work) before first
-                // use, which spares copying the entry; the training instances, whose chunk and tile
-                // state stores add memory traffic, take the copy and load it here, a pair earlier.
-                constexpr bool late_refill = !CHUNKS;
-                K2SData<T> early;
-                if constexpr (!late_refill) {
-                    early = ring[S];
-                    load_data(i + PF, ring[S]);
-                }
-                const K2SData<T> &el = late_refill ? ring[S] : early;   // the elements of pair i + 1
+                // The ring entry is refilled with pair i + PF (B/C) and the elements of the pair
+                // after it before this pair's scan starts, about two pairs ahead of their use; its
+                // elements of pair i + 1 are kept in `nxt` for the two prologues below. Refilling
+                // the entry after the second prologue instead (no copy, fewer registers) left only
+                // one pair of distance and cost 2.3 % at config 2.
+                const K2SData<T> nxt = ring[S];
+                load_data(i + PF, ring[S]);
                 // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
                 scan_tile(I0{}, t0, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
-                prologue(T2P2{}, el.u0, el.d0, el.z0);
+                prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
                 if constexpr (YO) epilogue(T2P3{}, YB(I1{}), i > pb ? 2 * i - 1 : 2 * pb);
                 __syncthreads();
                 // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
                 scan_tile(I1{}, t0 + kT1, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
-                prologue(T2P3{}, el.u1, el.d1, el.z1);
-                if constexpr (late_refill) load_data(i + PF, ring[S]);
+                prologue(T2P3{}, nxt.u1, nxt.d1, nxt.z1);
                 if constexpr (YO) epilogue(T2P{}, YB(I0{}), 2 * i);
                 __syncthreads();
             }
