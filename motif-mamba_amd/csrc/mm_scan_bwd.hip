@@ -485,13 +485,16 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
         an1 = 1.f;
     }
     float dA0 = 0.f, dA1 = 0.f, dD_acc = 0.f, dbias_acc = 0.f;
-    nxt = load(j_hi - 1, true);
-    for (int64_t j = j_hi - 1; j >= j_lo; --j) {
+    // Two tiles in flight: the loads of tile j - 2 are issued once tile j is committed. The two ring
+    // entries keep their registers (the loop is unrolled by two below): a copy of an entry whose
+    // loads are still in flight would wait for them.
+    TileRaw<T> ra = load(j_hi - 1, true), rb = load(j_hi - 2, true);
+    auto tile = [&](const int64_t j, TileRaw<T> &cur) {
         const int64_t t0 = j * kFT;
         const int buf = int(j % kBufs);
-        const float2 hc = nxt.hc;
-        commit(nxt, j, buf, true);
-        nxt = load(j - 1, true);
+        const float2 hc = cur.hc;
+        commit(cur, j, buf, true);
+        cur = load(j - 2, true);
         __syncthreads();
         float hs0[kFT], hs1[kFT], as0[kFT], as1[kFT];
         {
@@ -594,6 +597,10 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             }
             __syncthreads();
         }
+    };
+    for (int64_t j = j_hi - 1; j >= j_lo; j -= 2) {
+        tile(j, ra);
+        if (j - 1 >= j_lo) tile(j - 1, rb);
     }
     atomicAdd(p.dA + d * p.dA_d_stride + n0 * p.dA_dstate_stride, dA0);
     atomicAdd(p.dA + d * p.dA_d_stride + (n0 + 1) * p.dA_dstate_stride, dA1);
