@@ -175,8 +175,14 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     // Loads at or past the end of a row are redirected into the row's last elements (always in
     // bounds: L is a multiple of 8); the steps they feed are padding with dt' = 0.
     const int64_t lastE = L - E, last8 = L - 8;
-    RawVec<T, E> ru, rd, rz = {};
-    auto load_elems = [&](int64_t t) {
+    // Loads run D tiles ahead: rings of D entries (elements, B/C) whose registers stay fixed (the
+    // tile loop is unrolled by D below; copying an entry whose loads are in flight would wait for
+    // them). D = 2 where the second entry fits in registers (S <= 2); at S = 4 it would spill.
+    constexpr int D = S <= 2 ? 2 : 1;
+    struct Elems {
+        RawVec<T, E> u, d, z;
+    };
+    auto load_elems = [&](int64_t t, Elems &e) {
         uint32_t eo, so;
         if (t + kT <= L) {                 // uniform: a whole tile
             eo = uint32_t(es) * SZ;
@@ -185,12 +191,15 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             eo = uint32_t(t + es < lastE ? t + es : lastE) * SZ;
             so = 0;
         }
-        ru = buffer_load_rawn<T, E>(rs_u, fo_u + eo, so);
-        rd = buffer_load_rawn<T, E>(rs_d, fo_d + eo, so);
-        if (zp) rz = buffer_load_rawn<T, E>(rs_z, fo_z + eo, so);
+        e.u = buffer_load_rawn<T, E>(rs_u, fo_u + eo, so);
+        e.d = buffer_load_rawn<T, E>(rs_d, fo_d + eo, so);
+        e.z = {};
+        if (zp) e.z = buffer_load_rawn<T, E>(rs_z, fo_z + eo, so);
     };
-    RawVec<T, 8> rbc[HR][2];
-    auto load_bc = [&](int64_t t0) {
+    struct BCs {
+        RawVec<T, 8> v[HR][2];
+    };
+    auto load_bc = [&](int64_t t0, BCs &r) {
         const bool whole = t0 + kT <= L;   // uniform
 #pragma unroll
         for (int i = 0; i < HR; ++i) {
@@ -199,15 +208,15 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
                 // whole tile: t0 (uniform) + a lane constant; else the row's clamped position
                 const int64_t t = t0 + 16 * bc_half[i] + 8 * h2;
                 const T *src = whole ? bcp[i] + t0 + 8 * h2 : bcp[i] - 16 * bc_half[i] + (t < last8 ? t : last8);
-                rbc[i][h2] = {};
-                if (bc_on[i]) rbc[i][h2] = load_raw<T, 8>(src);
+                r.v[i][h2] = {};
+                if (bc_on[i]) r.v[i][h2] = load_raw<T, 8>(src);
             }
         }
     };
     // Tile rows [step][B states | C states] as float32; states past dstate are 0 (their loads are
     // skipped). Steps past L of the last tile are 0 as well, although their dt' = 0 makes B and C
     // of those steps reach no state and no stored output.
-    auto stage_bc = [&](int64_t t0) {
+    auto stage_bc = [&](int64_t t0, const BCs &r) {
         const bool whole = t0 + kT <= L;   // uniform
 #pragma unroll
         for (int i = 0; i < HR; ++i) {
@@ -215,7 +224,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
                 float v[8];
-                unpack_raw<T, 8>(rbc[i][h2], v);
+                unpack_raw<T, 8>(r.v[i][h2], v);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int64_t t = first + 8 * h2 + e;
@@ -224,20 +233,26 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             }
         }
     };
-    load_elems(0);
-    load_bc(0);
-    stage_bc(0);
+    Elems e0, e1;
+    BCs b0, b1;
+    load_elems(0, e0);
+    if (D == 2) load_elems(kT, e1);
+    load_bc(0, b0);
+    stage_bc(0, b0);
+    if (D == 2) load_bc(kT, b1);
 
-    for (int64_t t0 = 0; t0 < L; t0 += kT) {
+    // Tile t0: its elements in ec, its B/C (already staged) in bc, the next tile's B/C in bn (the
+    // same entry as bc when D = 1: loaded at the top of the tile, staged at its end).
+    auto tile = [&](const int64_t t0, Elems &ec, BCs &bc, const BCs &bn) __attribute__((always_inline)) {
         const int64_t t1 = t0 + kT;
         const bool ev = t0 + es < L;       // this lane's E elements exist (L is a multiple of E)
         float uu[E], dd[E], zz[E];
-        unpack_raw<T, E>(ru, uu);
-        unpack_raw<T, E>(rd, dd);
-        unpack_raw<T, E>(rz, zz);
-        // Prefetch the next tile (clamped addresses: always in bounds).
-        load_elems(t1);
-        load_bc(t1);
+        unpack_raw<T, E>(ec.u, uu);
+        unpack_raw<T, E>(ec.d, dd);
+        unpack_raw<T, E>(ec.z, zz);
+        // Prefetch D tiles ahead into the entries just consumed (clamped addresses: in bounds).
+        load_elems(t0 + D * kT, ec);
+        load_bc(t0 + D * kT, bc);
 
         // Prologue: dt' and dt' u of (channel, steps es .. es + E - 1).
         float dtp[E], dup[E];
@@ -308,7 +323,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
 #pragma unroll
         for (int t = 0; t < kT; t += 4)
             *reinterpret_cast<float4 *>(&sY[(cw * LPR + k) * kPad + t]) = make_float4(yp[t], yp[t + 1], yp[t + 2], yp[t + 3]);
-        if (t1 < L) stage_bc(t1);
+        if (t1 < L) stage_bc(t1, bn);
         __syncthreads();
 
         // Epilogue: y of (channel, steps es .. es + E - 1) = the LPR partials, added in lane order.
@@ -352,6 +367,14 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             }
         }
         __syncthreads();                   // sY reads done before the next prologue overwrites sX
+    };
+    if constexpr (D == 2) {
+        for (int64_t t0 = 0; t0 < L; t0 += 2 * kT) {
+            tile(t0, e0, b0, b1);
+            if (t0 + kT < L) tile(t0 + kT, e1, b1, b0);
+        }
+    } else {
+        for (int64_t t0 = 0; t0 < L; t0 += kT) tile(t0, e0, b0, b0);
     }
     if (active && p.last_state) {
         float *ls = p.last_state + (b * p.dim + d) * N;
