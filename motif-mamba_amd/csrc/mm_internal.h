@@ -32,6 +32,10 @@ template <typename T>
 int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream);
 int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg);
 
+// SIMDs of the current device (4 per CU; cached per device), 1024 when it cannot be queried
+// (mm_scan_tiled.hip).
+int64_t device_simds();
+
 // Forward scan with the low-rank P/Q coupling (mm_scan_pq.hip): the tiled kernel when the request
 // fits it, else the lane-per-row kernel. pq_tiled_lanes_per_row() is the tiled kernel's lanes per
 // (batch, channel) row for `p`, 0 when `p` takes the lane-per-row kernel.

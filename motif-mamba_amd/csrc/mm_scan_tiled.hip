@@ -1461,7 +1461,7 @@ static bool k2s_segments_ok(const mm_scan_fwd_params &p) {
 
 #ifdef MM_TILED_COMMON
 // SIMDs of the current device (4 per CU), or 1024 (the MI355X's) when it cannot be queried.
-static int64_t device_simds() {
+int64_t device_simds() {
     static std::atomic<int64_t> cache[64] = {};   // per device; every thread computes the same value
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1024;
