@@ -483,13 +483,6 @@ scan_fwd_pq_rowlane(const mm_scan_fwd_params p, const int64_t ratio) {
 // ------------------------------------------------------------------------------------------------
 struct TiledShape { int S, LPR; };
 
-// dstate 17..64: waves wanted before fewer states per lane (more lanes per channel) are preferred,
-// two per SIMD.
-int64_t min_waves() {
-    const char *e = getenv("MM_PQ_MIN_WAVES");
-    return e ? atoll(e) : 2048;
-}
-
 // The tiled kernel loads u, delta and z with 32-bit byte offsets from the first of a wave's channel
 // rows (up to 16): every offset of those rows must fit.
 static bool offsets_ok(const mm_scan_fwd_params &p) {
@@ -516,20 +509,18 @@ TiledShape tiled_shape(const mm_scan_fwd_params &p) {
     else { cands[nc++] = {4, 16}; }
     for (int i = 0; i < nc; ++i)
         if (cands[i].LPR == want) return cands[i];
-    if (p.dstate <= 16) {
-        // Measured (fp16, L 2048, 2,048-5,120 channels, batch 1-8, on 1,024 SIMDs): 8 lanes of 2
-        // states per channel are the fastest up to 2.5 of their waves per SIMD (0.21 ms at up to
-        // one, 0.30 ms at two, 0.40 ms at 2.5 against 0.45 ms with 4 lanes); past that the 4-lane
-        // layout's half as many waves win (0.45 against 0.55 ms at 3). 16 lanes of one state add a
-        // butterfly stage to every reduction: they win only while their waves fit one per SIMD
-        // (0.207 against 0.213 ms at 4,096 channels x batch 1; 0.58 against 0.30 ms at batch 4).
-        const int64_t simds = device_simds();
-        if (waves(16) <= simds) return cands[2];
-        return 2 * waves(8) <= 5 * simds ? cands[1] : cands[0];
-    }
-    for (int i = 0; i < nc; ++i)
-        if (waves(cands[i].LPR) >= min_waves()) return cands[i];
-    return cands[nc - 1];
+    // Measured (fp16, rank 2, L 2048, 2,048-5,120 channels, batch 1-8, on 1,024 SIMDs). 16 lanes per
+    // channel add a butterfly stage to every reduction: they win only while their waves fit one per
+    // SIMD (dstate 16: 0.207 against 0.213 ms with 8 lanes; dstate 32: 0.244 against 0.31 ms with
+    // 8 lanes of 4 states), and lose beyond (dstate 16: 0.58 against 0.30 ms at two waves of 8 lanes
+    // per SIMD; dstate 32: 0.60 against 0.47 ms at 1.5). At dstate 16, 8 lanes of 2 states stay the
+    // fastest up to 2.5 of their waves per SIMD (0.30 ms at two, 0.40 ms at 2.5 against 0.45 ms with
+    // 4 lanes); past that the 4-lane layout's half as many waves win (0.45 against 0.55 ms at 3).
+    const int64_t simds = device_simds();
+    if (nc == 1) return cands[0];
+    if (waves(16) <= simds) return cands[nc - 1];
+    if (nc == 2) return cands[0];
+    return 2 * waves(8) <= 5 * simds ? cands[1] : cands[0];
 }
 
 template <typename T, int S, int LPR, int R>
