@@ -37,11 +37,9 @@ int64_t segment_workspace_bytes(const mm_scan_fwd_params &p, int64_t n_seg);
 int64_t device_simds();
 
 // Forward scan with the low-rank P/Q coupling (mm_scan_pq.hip): the tiled kernel when the request
-// fits it, else the lane-per-row kernel. pq_tiled_lanes_per_row() is the tiled kernel's lanes per
-// (batch, channel) row for `p`, 0 when `p` takes the lane-per-row kernel.
+// fits it, else the lane-per-row kernel.
 template <typename T>
 int launch_pq(const mm_scan_fwd_params &p, hipStream_t stream);
-int64_t pq_tiled_lanes_per_row(const mm_scan_fwd_params &p);
 
 // Backward (mm_scan_bwd.hip): clears the accumulated gradients and launches the backward kernels
 // on `stream`; bwd_workspace_bytes() is the scratch it uses best, bwd_workspace_min_bytes() the

@@ -550,8 +550,6 @@ int launch_rowlane(const mm_scan_fwd_params &p, hipStream_t s) {
 
 }  // namespace pq
 
-int64_t pq_tiled_lanes_per_row(const mm_scan_fwd_params &p) { return pq::tiled_shape(p).LPR; }
-
 template <typename T>
 int launch_pq(const mm_scan_fwd_params &p, hipStream_t s) {
     const pq::TiledShape sh = pq::tiled_shape(p);
