@@ -272,6 +272,29 @@ def test_pq_bench_shape_sampled_rows():
     _close(got_last, torch.from_numpy(r["last_state"]).float(), torch.float16, "bench last")
 
 
+@pytest.mark.parametrize("batch,dim,N", [(6, 4096, 16), (1, 2048, 16), (3, 4096, 32)])
+def test_pq_automatic_layout_every_row(batch, dim, N):
+    """The host's own choice of lanes per channel (no MM_PQ_LPR) at sizes where, on a device of
+    1,024 SIMDs, it picks 4 lanes (6 x 4096, dstate 16: more than 2.5 waves of 8 lanes per SIMD),
+    16 lanes (1 x 2048: one wave of 16 lanes per SIMD) and 8 lanes of 4 states (3 x 4096, dstate
+    32): every row's gated output and last state against the float64 restatement."""
+    import dataclasses
+    from motif_mamba_amd import selective_scan_fn
+    from motif_mamba_amd.workloads import PQ_CONFIGS, pq_inputs
+    c = dataclasses.replace(PQ_CONFIGS["pq_1p4b"], batch=batch, dim=dim, seqlen=64, dstate=N, seed=400 + batch)
+    _say(f"pq automatic layout {batch} x {dim} dstate {N}")
+    with _lpr(None):
+        os.environ.pop("MM_PQ_LPR", None)
+        inputs = pq_inputs(c, device="cuda")
+        out, last = selective_scan_fn(**inputs)
+        torch.cuda.synchronize()
+    cpu = {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in inputs.items()}
+    r = cscan.scan_rows(cpu["u"], cpu["delta"], cpu["A"], cpu["B"], cpu["C"], cpu["D"], cpu["z"],
+                        cpu["delta_bias"], True, P=cpu["P"], Q=cpu["Q"])
+    _close(out.cpu().reshape(batch * dim, -1), torch.from_numpy(r["out_z"]), torch.float16, "out")
+    _close(last.cpu().reshape(batch * dim, -1), torch.from_numpy(r["last_state"]), torch.float16, "last")
+
+
 # ---------------------------------------------------------------------------------------------
 # Boundary: the C ABI with P/Q, argument errors.
 # ---------------------------------------------------------------------------------------------
