@@ -241,6 +241,42 @@ def bench_pq_train(name, steps, warmup, torch):
             "elements_per_s": elems / (s_ms * 1e-3)}
 
 
+def bench_pq_layouts(steps, warmup, torch):
+    """The P/Q forward at the Motif layer's settings (rank 2, per-channel P/Q, fp16, L 2048) over
+    channel counts and batch sizes, with each tiled layout forced through MM_PQ_LPR (lanes per
+    channel: 4, 8, 16) and with the host's own choice ("auto"): the measurement behind that
+    choice. Milliseconds per call."""
+    import dataclasses
+    import os
+    from motif_mamba_amd import selective_scan_fn
+    from motif_mamba_amd.workloads import PQ_CONFIGS, pq_inputs
+    base = PQ_CONFIGS["pq_1p4b"]
+    grid = [(16, dim, (4, 8, 16)) for dim in (2048, 3072, 4096, 5120)] + [(32, dim, (8, 16)) for dim in (2048, 4096)]
+    rows = []
+    old = os.environ.get("MM_PQ_LPR")
+    try:
+        for n, dim, lprs in grid:
+            for batch in (1, 2, 3, 4, 6, 8):
+                x = pq_inputs(dataclasses.replace(base, batch=batch, dim=dim, dstate=n), device="cuda")
+                row = {"dstate": n, "dim": dim, "batch": batch}
+                for lpr in (*lprs, None):
+                    if lpr:
+                        os.environ["MM_PQ_LPR"] = str(lpr)
+                    else:
+                        os.environ.pop("MM_PQ_LPR", None)
+                    row[f"lpr{lpr}" if lpr else "auto"] = _time_loop(lambda i: selective_scan_fn(**x), steps, warmup, torch)
+                del x
+                torch.cuda.empty_cache()
+                _log(f"pq layouts {row}")
+                rows.append(row)
+    finally:
+        if old is None:
+            os.environ.pop("MM_PQ_LPR", None)
+        else:
+            os.environ["MM_PQ_LPR"] = old
+    return {"rank": base.rank, "per_dim": base.per_dim, "dtype": base.dtype, "seqlen": base.seqlen, "rows": rows}
+
+
 def bench_train(cfg_name, steps, warmup, torch):
     """Forward in training mode (pre-gate out and chunk states saved, ssi.py:47-61, plus the 16-step
     tile states SelectiveScanFn keeps) and the backward (selective_scan_cuda.bwd equivalent, reading
@@ -549,7 +585,7 @@ def main():
                     help="also run three 1 GiB device-to-device copies: the reference that scales the "
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
-                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, pq_1p4b_train, "
+                    help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, pq_1p4b_train, pq_layouts, "
                          "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_update_b<batch>, inner_2p8b) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
@@ -574,6 +610,8 @@ def main():
             res = {"cfg2": head, **per_cfg}
         elif name.startswith("cfg4_b"):
             res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
+        elif name == "pq_layouts":
+            res = bench_pq_layouts(args.steps, 2, torch)
         elif name.startswith("pq_") and name.endswith("_train"):
             res = bench_pq_train(name[: -len("_train")], args.steps, args.warmup, torch)
         elif name.startswith("pq_"):
