@@ -126,6 +126,29 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             Qr[j][s] = use ? p.Q[d * p.Q_d_stride + j * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
         }
     }
+    // With 16 lanes of one state per channel (dstate <= 16, chosen when their waves fit one per
+    // SIMD, where each step's dependent chain sets the time) and rank <= 2, the coupling carries
+    // gq = Q h_{t-1} over all states of the channel from step to step (h = 0 before the first
+    // step) and forms the next one as Q hb + K q with K = Q P over the lane's states (R x R): the
+    // chain from gq to the next gq is then q, R fmas and the butterfly instead of q, the P fmas,
+    // the S-term dot product and the butterfly, for R^2 + R S more VALU per step. Measured at one
+    // wave per SIMD: -8 % at one state per lane, +4 % at two (the extra VALU outweigh the shorter
+    // chain); +10 % at two waves per SIMD with 8 lanes, where issue sets the time. 16-bit inputs
+    // only: float32 callers keep the direct Q h, whose rounding the long-sequence float32 checks
+    // pin; 16-bit outputs round far above the float32 rounding difference of the two forms.
+    constexpr bool XK = LPR == 16 && S == 1 && R <= 2 && !std::is_same<T, float>::value;
+    float Kr[R][R], gq[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        gq[r] = 0.f;
+#pragma unroll
+        for (int r2 = 0; r2 < R; ++r2) {
+            float acc = Qr[r][0] * Pr[0][r2];
+#pragma unroll
+            for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], Pr[s][r2], acc);
+            Kr[r][r2] = acc;
+        }
+    }
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
     const bool softplus = p.delta_softplus != 0;
@@ -298,22 +321,52 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float q[R];
+                float q[R], y = 0.f;
+                if constexpr (XK) {
+                    // h_t = hb + P q with hb = a h_{t-1} + dt' u B and q = dt' gq; the next step's
+                    // lane partial of Q h_t as X + K q, where X = Q hb needs only h_{t-1} (off the
+                    // serial chain) and K = Q P over the lane's states.
+                    float hb[S], X[R];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float acc = Qr[r][0] * h[0];
+                    for (int s = 0; s < S; ++s) hb[s] = __builtin_fmaf(av[j][s], h[s], bu[j][s]);
 #pragma unroll
-                    for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
-                    q[r] = group_sum<LPR>(acc) * dts[j];
-                }
-                float y = 0.f;
+                    for (int r = 0; r < R; ++r) {
+                        X[r] = Qr[r][0] * hb[0];
 #pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    float w = bu[j][s];
+                        for (int s = 1; s < S; ++s) X[r] = __builtin_fmaf(Qr[r][s], hb[s], X[r]);
+                        q[r] = gq[r] * dts[j];
+                    }
 #pragma unroll
-                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                    h[s] = __builtin_fmaf(av[j][s], h[s], w);
-                    y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
+                    for (int r = 0; r < R; ++r) {
+                        float acc = X[r];
+#pragma unroll
+                        for (int r2 = 0; r2 < R; ++r2) acc = __builtin_fmaf(Kr[r][r2], q[r2], acc);
+                        gq[r] = group_sum<LPR>(acc);
+                    }
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        float w = hb[s];
+#pragma unroll
+                        for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                        h[s] = w;
+                        y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float acc = Qr[r][0] * h[0];
+#pragma unroll
+                        for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
+                        q[r] = group_sum<LPR>(acc) * dts[j];
+                    }
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        float w = bu[j][s];
+#pragma unroll
+                        for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                        h[s] = __builtin_fmaf(av[j][s], h[s], w);
+                        y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
+                    }
                 }
                 yp[4 * s4 + j] = y;
             }
