@@ -564,7 +564,7 @@ TiledShape tiled_shape(const mm_scan_fwd_params &p) {
         if (cands[i].LPR == want) return cands[i];
     // Measured (fp16, rank 2, L 2048, 2,048-5,120 channels, batch 1-8, on 1,024 SIMDs). 16 lanes per
     // channel add a butterfly stage to every reduction: they win only while their waves fit one per
-    // SIMD (dstate 16: 0.207 against 0.213 ms with 8 lanes; dstate 32: 0.244 against 0.31 ms with
+    // SIMD (dstate 16: 0.191 against 0.214 ms with 8 lanes; dstate 32: 0.244 against 0.31 ms with
     // 8 lanes of 4 states), and lose beyond (dstate 16: 0.58 against 0.30 ms at two waves of 8 lanes
     // per SIMD; dstate 32: 0.60 against 0.47 ms at 1.5). At dstate 16, 8 lanes of 2 states stay the
     // fastest up to 2.5 of their waves per SIMD (0.30 ms at two, 0.40 ms at 2.5 against 0.45 ms with
