@@ -16,7 +16,9 @@
 //       whose A, P, Q, B and C are zero, which stay zero). Per step each lane forms its partial
 //       Q h over its S states, a DPP butterfly inside the LPR lanes sums the partials (every lane
 //       ends with the same bits), and the lane updates its S states with P (dt' q) + dt' u B.
-//       The lane's rows of P and Q live in registers for the whole sequence.
+//       The lane's rows of P and Q live in registers for the whole sequence. (16-bit inputs with
+//       16 lanes of one state and rank <= 2 carry the butterfly's total from step to step and form
+//       the next partial as Q (a h + dt' u B) + (Q P) q, which shortens the dependent chain.)
 //       * B and C of the (batch, group) are staged per 32-step tile in LDS as float32, [step][state],
 //         and each step reads the lane's S states as one vector.
 //       * dt' = softplus(delta + bias) and dt' u are computed once per (channel, step): each lane
