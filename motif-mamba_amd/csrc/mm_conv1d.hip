@@ -262,64 +262,108 @@ conv1d_bwd_kernel(const mm_conv1d_bwd_params p) {
     float dw[W], db = 0.f;
 #pragma unroll
     for (int k = 0; k < W; ++k) dw[k] = 0.f;
-    for (int64_t b = 0; b < p.batch; ++b) {
-        const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
-        const T *gr = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
-        T *dxr = reinterpret_cast<T *>(p.dx) + b * p.dx_batch_stride + d * p.dx_d_stride;
-        for (int64_t tile = 0; tile < n_tiles; ++tile) {
-            const int64_t t0 = tile * kTile + int64_t(threadIdx.x) * (kChunk * NC);
-            if (t0 >= L) continue;   // lanes past the row's end (last tile only)
-            // xs: chunk before, the NC chunks, chunk after; gs: dout of the NC chunks and the chunk after.
-            constexpr int NX = kChunk * (NC + 2), NG = kChunk * (NC + 1);
-            float xs[NX], gs[NG];
-            auto ld = [&](const T *row, int64_t t, float *dst) {   // 8 elements at t (zeros outside [0, L))
-                if (VEC && t >= 0 && t + kChunk <= L) {
-                    load8(row + t, dst);
-                } else {
+    // xs: chunk before, the NC chunks, chunk after; gs: dout of the NC chunks and the chunk after.
+    constexpr int NX = kChunk * (NC + 2), NG = kChunk * (NC + 1);
+    // One tile of a row: dy at positions t0 .. t0 + 8 (NC + 1) - 1 (0 past L), dx of the NC chunks,
+    // and the lane's dweight / dbias terms.
+    auto tile_math = [&](T *dxr, const int64_t t0, const float *xs, const float *gs) {
+        float dy[NG];
 #pragma unroll
-                    for (int i = 0; i < kChunk; ++i) dst[i] = (t + i >= 0 && t + i < L) ? to_f32(row[t + i]) : 0.f;
-                }
-            };
+        for (int i = 0; i < NG; ++i) {
+            float y = bias;
 #pragma unroll
-            for (int c = 0; c < NC + 2; ++c) ld(xr, t0 + (c - 1) * kChunk, xs + c * kChunk);
+            for (int k = 0; k < W; ++k) y = __builtin_fmaf(w[k], xs[kChunk + i - (W - 1) + k], y);
+            float g = gs[i];
+            if (p.silu) {
+                const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * kLog2e));
+                g *= sg * (1.f + y * (1.f - sg));
+            }
+            dy[i] = (t0 + i < L) ? g : 0.f;
+        }
 #pragma unroll
-            for (int c = 0; c < NC + 1; ++c) ld(gr, t0 + c * kChunk, gs + c * kChunk);
-            // dy at positions t0 .. t0 + 8 (NC + 1) - 1 (0 past L).
-            float dy[NG];
+        for (int c = 0; c < NC; ++c) {
+            float o[kChunk];
 #pragma unroll
-            for (int i = 0; i < NG; ++i) {
-                float y = bias;
+            for (int i = 0; i < kChunk; ++i) {
+                const int s = c * kChunk + i;
+                float acc = 0.f;
 #pragma unroll
-                for (int k = 0; k < W; ++k) y = __builtin_fmaf(w[k], xs[kChunk + i - (W - 1) + k], y);
-                float g = gs[i];
-                if (p.silu) {
-                    const float sg = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-y * kLog2e));
-                    g *= sg * (1.f + y * (1.f - sg));
-                }
-                dy[i] = (t0 + i < L) ? g : 0.f;
+                for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], dy[s + W - 1 - k], acc);
+                o[i] = acc;
+                db += dy[s];
+#pragma unroll
+                for (int k = 0; k < W; ++k) dw[k] = __builtin_fmaf(dy[s], xs[kChunk + s - (W - 1) + k], dw[k]);
+            }
+            const int64_t tc = t0 + c * kChunk;
+            if (VEC && tc + kChunk <= L) {
+                store8(dxr + tc, o);
+            } else {
+#pragma unroll
+                for (int i = 0; i < kChunk; ++i)
+                    if (tc + i < L) dxr[tc + i] = from_f32<T>(o[i]);
+            }
+        }
+    };
+    if constexpr (VEC) {
+        // Rows in 16-byte vectors (L % 8 == 0, aligned rows): a chunk is wholly inside [0, L) or
+        // wholly outside. The walk over (batch row, tile) pairs loads the next pair's raw vectors
+        // before the current pair's arithmetic, so that their latency overlaps it.
+        struct Raw {
+            Vec8<T> x[NC + 2], g[NC + 1];
+        };
+        const int64_t n_it = p.batch * n_tiles;
+        auto lane_t0 = [&](int64_t it) { return (it % n_tiles) * kTile + int64_t(threadIdx.x) * (kChunk * NC); };
+        auto load_raw = [&](int64_t it, Raw &r) {
+            const int64_t b = it / n_tiles, t0 = lane_t0(it);
+            const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
+            const T *gr = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
+#pragma unroll
+            for (int c = 0; c < NC + 2; ++c) {
+                const int64_t t = t0 + (c - 1) * kChunk;
+                r.x[c] = {};
+                if (t >= 0 && t < L) r.x[c] = *reinterpret_cast<const Vec8<T> *>(xr + t);
             }
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                float o[kChunk];
+            for (int c = 0; c < NC + 1; ++c) {
+                const int64_t t = t0 + c * kChunk;
+                r.g[c] = {};
+                if (t < L) r.g[c] = *reinterpret_cast<const Vec8<T> *>(gr + t);
+            }
+        };
+        Raw cur, nxt;
+        if (n_it > 0) load_raw(0, cur);
+        for (int64_t it = 0; it < n_it; ++it) {
+            if (it + 1 < n_it) load_raw(it + 1, nxt);
+            const int64_t t0 = lane_t0(it);
+            if (t0 < L) {   // lanes past the row's end (last tile only) have nothing to do
+                float xs[NX], gs[NG];
 #pragma unroll
-                for (int i = 0; i < kChunk; ++i) {
-                    const int s = c * kChunk + i;
-                    float acc = 0.f;
+                for (int c = 0; c < NC + 2; ++c) unpack8(cur.x[c], xs + c * kChunk);
 #pragma unroll
-                    for (int k = 0; k < W; ++k) acc = __builtin_fmaf(w[k], dy[s + W - 1 - k], acc);
-                    o[i] = acc;
-                    db += dy[s];
+                for (int c = 0; c < NC + 1; ++c) unpack8(cur.g[c], gs + c * kChunk);
+                T *dxr = reinterpret_cast<T *>(p.dx) + (it / n_tiles) * p.dx_batch_stride + d * p.dx_d_stride;
+                tile_math(dxr, t0, xs, gs);
+            }
+            cur = nxt;
+        }
+    } else {
+        for (int64_t b = 0; b < p.batch; ++b) {
+            const T *xr = reinterpret_cast<const T *>(p.x) + b * p.x_batch_stride + d * p.x_d_stride;
+            const T *gr = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
+            T *dxr = reinterpret_cast<T *>(p.dx) + b * p.dx_batch_stride + d * p.dx_d_stride;
+            for (int64_t tile = 0; tile < n_tiles; ++tile) {
+                const int64_t t0 = tile * kTile + int64_t(threadIdx.x) * (kChunk * NC);
+                if (t0 >= L) continue;   // lanes past the row's end (last tile only)
+                float xs[NX], gs[NG];
+                auto ld = [&](const T *row, int64_t t, float *dst) {   // 8 elements at t (zeros outside [0, L))
 #pragma unroll
-                    for (int k = 0; k < W; ++k) dw[k] = __builtin_fmaf(dy[s], xs[kChunk + s - (W - 1) + k], dw[k]);
-                }
-                const int64_t tc = t0 + c * kChunk;
-                if (VEC && tc + kChunk <= L) {
-                    store8(dxr + tc, o);
-                } else {
+                    for (int i = 0; i < kChunk; ++i) dst[i] = (t + i >= 0 && t + i < L) ? to_f32(row[t + i]) : 0.f;
+                };
 #pragma unroll
-                    for (int i = 0; i < kChunk; ++i)
-                        if (tc + i < L) dxr[tc + i] = from_f32<T>(o[i]);
-                }
+                for (int c = 0; c < NC + 2; ++c) ld(xr, t0 + (c - 1) * kChunk, xs + c * kChunk);
+#pragma unroll
+                for (int c = 0; c < NC + 1; ++c) ld(gr, t0 + c * kChunk, gs + c * kChunk);
+                tile_math(dxr, t0, xs, gs);
             }
         }
     }
