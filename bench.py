@@ -338,6 +338,28 @@ def bench_conv(cfg_name, steps, warmup, torch):
             "GB_s": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_conv_bwd(cfg_name, steps, warmup, torch):
+    """causal_conv1d's backward (width 4, bias, SiLU: dx, dweight, dbias, as MambaInnerFn's
+    backward calls it) on the conv that feeds a scan configuration: HBM throughput of x and dout
+    read and dx written once."""
+    from motif_mamba_amd.causal_conv1d import causal_conv1d_bwd
+    from motif_mamba_amd.workloads import SCAN_CONFIGS
+    c = SCAN_CONFIGS[cfg_name]
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[c.dtype]
+    g = torch.Generator(device="cuda").manual_seed(13)
+    x = torch.randn(c.batch, c.dim, c.seqlen, device="cuda", generator=g).to(dt)
+    dout = torch.randn(c.batch, c.dim, c.seqlen, device="cuda", generator=g).to(dt)
+    w = (torch.randn(c.dim, 4, device="cuda", generator=g) * 0.5).to(dt)
+    b = (torch.randn(c.dim, device="cuda", generator=g) * 0.1).to(dt)
+    dx = torch.empty_like(x)
+    ms = _time_loop(lambda i: causal_conv1d_bwd(x, w, b, dout, dx, True), steps, warmup, torch)
+    nbytes = 3 * x.numel() * x.element_size() + 2 * (w.numel() + b.numel()) * w.element_size()
+    del x, dout, dx
+    torch.cuda.empty_cache()
+    return {"shape": [c.batch, c.dim, c.seqlen], "width": 4, "dtype": c.dtype, "us": ms * 1e3,
+            "GB_s": nbytes / (ms * 1e-3) / 1e9, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
 def bench_conv_update(batch, steps, warmup, torch, dim=5120):
     """causal_conv1d_update of one decode token (state (batch, dim, 4) bf16, width 4, SiLU)."""
     from motif_mamba_amd import causal_conv1d_update
@@ -586,7 +608,7 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
                     help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, pq_1p4b_train, pq_layouts, "
-                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_update_b<batch>, inner_2p8b) "
+                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_bwd_cfg1, conv_bwd_cfg2, conv_update_b<batch>, inner_2p8b) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -622,6 +644,8 @@ def main():
             res = bench_train(name[: -len("_train")], args.steps, args.warmup, torch)
         elif name.startswith("conv_update_b"):
             res = bench_conv_update(int(name[len("conv_update_b"):]), max(args.steps, 100), args.warmup, torch)
+        elif name.startswith("conv_bwd_"):
+            res = bench_conv_bwd(name[len("conv_bwd_"):], args.steps, args.warmup, torch)
         elif name.startswith("conv_"):
             res = bench_conv(name[len("conv_"):], args.steps, args.warmup, torch)
         else:
@@ -661,6 +685,9 @@ def main():
         for name in ("cfg1", "cfg2"):
             _log(f"causal_conv1d forward ({name} shape)")
             extra[f"conv_{name}"] = bench_conv(name, max(10, args.steps), 3, torch)
+        for name in ("cfg1", "cfg2"):
+            _log(f"causal_conv1d backward ({name} shape)")
+            extra[f"conv_bwd_{name}"] = bench_conv_bwd(name, max(10, args.steps), 3, torch)
         for b in (64, 256):
             _log(f"causal_conv1d decode update batch {b}")
             extra[f"conv_update_b{b}"] = bench_conv_update(b, 200, 10, torch)
