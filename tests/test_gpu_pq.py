@@ -252,6 +252,26 @@ def test_pq_long_sequence_fp32_vs_f64():
         assert bool((err <= bound).all()), f"{what}: row max error {err.max().item():.3g} beyond {bound.min().item():.3g}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pq_long_sequence_16bit_one_wave_layout(dtype):
+    """8192 steps with 16-bit inputs on 64 channels: the layout of 16 lanes of one state, whose
+    coupling carries Q h from step to step (Q hb + (Q P) q) instead of forming it from h. The
+    16-bit output element by element at the 16-bit tolerance; the float32 last state row by row in
+    the max norm at the float32 tolerance, the bound the direct form meets in the float32 case
+    above, so a drift of the carried form over the sequence would show there."""
+    _say(f"pq {dtype} L=8192 one-wave layout vs float64")
+    case = _pq_case(420, batch=1, dim=64, L=8192, N=16, R=2, dtype=dtype)
+    out, last = _gpu(case)
+    r = cscan.scan_rows(case["u"], case["delta"], case["A"], case["B"], case["C"], case["D"], case["z"],
+                        case["delta_bias"], True, P=case["P"], Q=case["Q"])
+    _close(out.cpu(), torch.from_numpy(r["out_z"]).reshape(out.shape), dtype, "out")
+    rtol, atol = fixtures.tolerances(torch.float32)
+    exact = torch.from_numpy(r["last_state"]).reshape(last.shape)
+    err = (last.double().cpu() - exact).abs().amax(dim=-1)
+    bound = atol + rtol * exact.abs().amax(dim=-1)
+    assert bool((err <= bound).all()), f"last: row max error {err.max().item():.3g} beyond {bound.min().item():.3g}"
+
+
 def test_pq_bench_shape_sampled_rows():
     """The PQ benchmark shape (Mamba-1.4B layer, rank 2, per-channel P/Q, fp16): sampled rows
     against the float64 restatement."""
