@@ -1010,45 +1010,39 @@ struct K2SData {                       // one lane's global data for pair iterat
     RawVec<T, 2> u0, d0, z0, u1, d1, z1;   // u, delta, z: 2 steps of tiles 0 and 1 of pair i + 1
 };
 
-template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT, bool YO, int SEG = 0>
-__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
-scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) {
+// LDS of one k2s group: dt' and dt'u of four tiles, and two buffers of the 8 row partials of y
+// ([row][channel][16 steps]); every row of 16 floats holds four 4-float blocks permuted by swz16.
+struct K2SLds {
+    float dt[4][kCh * kT1];
+    float du[4][kCh * kT1];
+    float y[2][8 * kCh * kT1];
+};
+
+// One 16-channel group of batch row b on 128 lanes (tid 0..127, two waves): the body of scan_fwd_k2s,
+// also run twice per workgroup by scan_fwd_mix. Every lane of the workgroup calls __syncthreads()
+// the same number of times (once per 16-step tile, the same tile count for both groups).
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT, bool YO, int SEG>
+__device__ __forceinline__ void k2s_group(const mm_scan_fwd_params &p, const int64_t ratio, const SegArgs &sg,
+                                          const int tid, const int64_t b, const int64_t d0, const int seg,
+                                          K2SLds &lds) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
     static_assert(SEG != 1 || !YO, "the first segment pass computes the states alone");
     static_assert(SEG != 2 || YO, "the second segment pass writes the outputs");
     constexpr int E = 2, LPS = 8, NR = 8;
-    __shared__ __align__(16) float sDt0[kCh * kT1], sDt1[kCh * kT1], sDt2[kCh * kT1], sDt3[kCh * kT1];
-    __shared__ __align__(16) float sDu0[kCh * kT1], sDu1[kCh * kT1], sDu2[kCh * kT1], sDu3[kCh * kT1];
-    // Row partials of y [row][channel][16 steps], 4-float blocks permuted by swz16(channel).
-    __shared__ __align__(16) float sY0[NR * kCh * kT1], sY1[NR * kCh * kT1];
-    auto DT = [&](auto I) -> float * {
-        constexpr int i = decltype(I)::value & 3;
-        if constexpr (i == 0) return sDt0; else if constexpr (i == 1) return sDt1;
-        else if constexpr (i == 2) return sDt2; else return sDt3;
-    };
-    auto DU = [&](auto I) -> float * {
-        constexpr int i = decltype(I)::value & 3;
-        if constexpr (i == 0) return sDu0; else if constexpr (i == 1) return sDu1;
-        else if constexpr (i == 2) return sDu2; else return sDu3;
-    };
-    auto YB = [&](auto I) -> float * {
-        if constexpr ((decltype(I)::value & 1) == 0) return sY0; else return sY1;
-    };
+    auto DT = [&](auto I) -> float * { return lds.dt[decltype(I)::value & 3]; };
+    auto DU = [&](auto I) -> float * { return lds.du[decltype(I)::value & 3]; };
+    auto YB = [&](auto I) -> float * { return lds.y[decltype(I)::value & 1]; };
 
-    const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int r = tid >> 4;                // row (states 2r, 2r+1) of this lane in the scan
     const int c = lane & 15;               // channel of this lane in the scan
     const int ce = tid >> 3;               // channel of this lane's elements
     const int es = E * (tid & 7);          // first step (within a tile) of its two elements
     const int swc = swz16(c), swe = swz16(ce);   // LDS block permutations of the two channels
-    const int64_t b = blockIdx.y;
-    const int64_t d0 = int64_t(blockIdx.x) * kCh;
     const int64_t g = d0 / ratio;
     const int64_t L = p.seqlen;
     const int32_t n_pairs = int32_t(L / (2 * kT1));   // L is a multiple of 32 here
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
-    const int seg = SEG ? int(blockIdx.z) : 0;
     const int32_t pb = SEG ? int32_t(seg * sg.pairs) : 0;                                 // first pair
     const int32_t pe = SEG ? (pb + int32_t(sg.pairs) < n_pairs ? pb + int32_t(sg.pairs) : n_pairs) : n_pairs;
     const int64_t srow = (b * p.dim + d0 + c) * int64_t(sg.n_seg) + seg;                 // segment slot
@@ -1303,8 +1297,287 @@ scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) 
     }
 }
 
+template <typename T, int PF, bool SOFTPLUS, bool CHUNKS, bool HAS_Z, bool HAS_OUT, bool YO, int SEG = 0>
+__global__ void __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(3, 8)))
+scan_fwd_k2s(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg) {
+    __shared__ __align__(16) K2SLds lds;
+    k2s_group<T, PF, SOFTPLUS, CHUNKS, HAS_Z, HAS_OUT, YO, SEG>(p, ratio, sg, threadIdx.x, blockIdx.y,
+                                                                int64_t(blockIdx.x) * kCh, SEG ? int(blockIdx.z) : 0, lds);
+}
+
 using K2SKernel = void (*)(const mm_scan_fwd_params, const int64_t, const SegArgs);
 constexpr SegArgs kWholeRows{0, 1, nullptr, nullptr, nullptr};
+
+// ---------------------------------------------------------------------------------------------
+// k1s: one state per lane. A 16-channel group of batch row b on 256 lanes (four waves), lane
+// 16 r + c holding state r of channel c, in k2s's interval structure: per 16-step tile j each lane
+// prepares one element of tile j + 2 (channel r, step c), scans tile j (16 state updates) and
+// finishes one element of tile j - 1, adding the 16 row partials of y in row order. Per state
+// update it issues what k2s issues (exp2 and its argument, B dt'u and C h by DPP row broadcast, the
+// state FMA) with the element work and the row partials spread over twice the lanes. scan_fwd_mix
+// runs it beside k2s groups so that every SIMD of the device carries the same number of states.
+// ---------------------------------------------------------------------------------------------
+struct K1SLds {
+    float dt[4][kCh * kT1];
+    float du[4][kCh * kT1];
+    float y[2][16 * kCh * kT1];
+};
+
+template <typename T>
+struct K1SData {                       // one lane's global data for pair iteration i
+    RawVec<T, 2> b, c;                 // B, C of the lane's state: steps 2c and 2c + 1 of pair i
+    uint32_t u0, d0, z0, u1, d1, z1;   // u, delta, z: one element of tiles 0 and 1 of pair i + 1 (raw bits)
+};
+
+// One element of T through a buffer resource, as raw bits (16-bit types zero-extended).
+template <typename T>
+__device__ __forceinline__ uint32_t buffer_load_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (sizeof(T) == 4)
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    else
+        return uint32_t(__builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+}
+template <typename T>
+__device__ __forceinline__ float elem_f32(uint32_t w) {
+    if constexpr (std::is_same_v<T, float>) return __uint_as_float(w);
+    else if constexpr (std::is_same_v<T, bf16_t>) return __uint_as_float(w << 16);
+    else return float(__builtin_bit_cast(_Float16, uint16_t(w)));
+}
+// One float stored as T (bf16 round-to-nearest-even, as buffer_store_vec converts).
+template <typename T>
+__device__ __forceinline__ void buffer_store_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float x) {
+    if constexpr (std::is_same_v<T, float>)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 0);
+    else if constexpr (std::is_same_v<T, bf16_t>)
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)(pack_bf16x2(x, 0.f) & 0xffffu), r, voff, soff, 0);
+    else
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (_Float16)x), r, voff, soff, 0);
+}
+
+template <typename T, int PF, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT>
+__device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int64_t ratio, const int tid,
+                                          const int64_t b, const int64_t d0, K1SLds &lds) {
+    static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
+    constexpr int NR = 16;
+    auto DT = [&](auto I) -> float * { return lds.dt[decltype(I)::value & 3]; };
+    auto DU = [&](auto I) -> float * { return lds.du[decltype(I)::value & 3]; };
+    auto YB = [&](auto I) -> float * { return lds.y[decltype(I)::value & 1]; };
+
+    const int r = tid >> 4;                // state of this lane in the scan; channel of its element
+    const int c = tid & 15;                // channel of this lane in the scan; step of its element
+    const int ce = r, es = c;
+    const int swc = swz16(c), swe = swz16(ce);
+    const int64_t g = d0 / ratio;
+    const int64_t L = p.seqlen;
+    const int32_t n_pairs = int32_t(L / (2 * kT1));   // L is a multiple of 32 here
+
+    const int64_t de = d0 + ce;
+    const T *ub = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d0 * p.u_d_stride;
+    const T *db = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d0 * p.delta_d_stride;
+    const T *zb = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d0 * p.z_d_stride : nullptr;
+    T *ob = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d0 * p.out_d_stride : nullptr;
+    T *ozb = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d0 * p.out_z_d_stride : nullptr;
+    const T *Bb = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
+    const T *Cb = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
+
+    const float At = p.A[(d0 + c) * p.A_d_stride + int64_t(r) * p.A_dstate_stride] * kLog2e;
+    float h = 0.f;
+    const float Dv = p.D ? p.D[de] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
+
+    // Buffer resources of the group's rows (the host checks that every byte offset of the group is
+    // below 2^32) and this lane's byte offsets from them; tile and pair offsets are scalar.
+    constexpr uint32_t SZ = sizeof(T);
+    const uint32_t fo_u = uint32_t(ce * p.u_d_stride + es) * SZ, fo_d = uint32_t(ce * p.delta_d_stride + es) * SZ;
+    const uint32_t fo_z = uint32_t(ce * p.z_d_stride + es) * SZ;
+    const uint32_t fo_b = uint32_t(r * p.B_dstate_stride + 2 * c) * SZ, fo_c = uint32_t(r * p.C_dstate_stride + 2 * c) * SZ;
+    const uint32_t fo_o = uint32_t(ce * p.out_d_stride + es) * SZ, fo_oz = uint32_t(ce * p.out_z_d_stride + es) * SZ;
+    const __amdgpu_buffer_rsrc_t rs_u = buffer_rsrc(ub), rs_d = buffer_rsrc(db), rs_z = buffer_rsrc(zb);
+    const __amdgpu_buffer_rsrc_t rs_b = buffer_rsrc(Bb), rs_c = buffer_rsrc(Cb);
+    const __amdgpu_buffer_rsrc_t rs_o = buffer_rsrc(ob), rs_oz = buffer_rsrc(ozb);
+    // Pair and tile indices past the end are clamped to the last ones (their data is never used).
+    auto pair_off = [&](int32_t i) { return uint32_t(i < n_pairs ? i : n_pairs - 1) * uint32_t(2 * kT1 * SZ); };
+    auto tile_off = [&](int32_t t) { return uint32_t(t < 2 * n_pairs ? t : 2 * n_pairs - 1) * uint32_t(kT1 * SZ); };
+    auto load_tile = [&](int32_t t, uint32_t &u, uint32_t &dl, uint32_t &z) {
+        const uint32_t sof = tile_off(t);
+        u = buffer_load_elem<T>(rs_u, fo_u, sof);
+        dl = buffer_load_elem<T>(rs_d, fo_d, sof);
+        z = HAS_Z ? buffer_load_elem<T>(rs_z, fo_z, sof) : 0u;
+    };
+    auto load_data = [&](int32_t i, K1SData<T> &dst) {
+        const uint32_t sof = pair_off(i);
+        dst.b = buffer_load_raw<T, 2>(rs_b, fo_b, sof);
+        dst.c = buffer_load_raw<T, 2>(rs_c, fo_c, sof);
+        load_tile(2 * i + 2, dst.u0, dst.d0, dst.z0);
+        load_tile(2 * i + 3, dst.u1, dst.d1, dst.z1);
+    };
+
+    // u (unpacked) and z of the tiles between their prologue and their epilogue: tile t in slot t % 4.
+    float ru[4];
+    uint32_t rz[4];
+    auto prologue = [&](auto Slot, uint32_t u, uint32_t dl, uint32_t z) {
+        constexpr int sl = decltype(Slot)::value & 3;
+        const float uu = elem_f32<T>(u);
+        const float x = elem_f32<T>(dl) + bias;
+        const float dtp = SOFTPLUS ? softplus_fast(x) : x;
+        const int pos = ce * kT1 + (((es >> 2) ^ swe) << 2) + (es & 3);
+        DT(Slot)[pos] = dtp;
+        DU(Slot)[pos] = dtp * uu;
+        ru[sl] = uu;
+        rz[sl] = z;
+    };
+    // Epilogue of tile t: the 16 row partials added in row order, D u, the silu(z) gate, one store.
+    // The first interval runs it on the unused buffers and stores to tile 0, which the same lane
+    // overwrites with tile 0's outputs one interval later (as k2s does).
+    auto epilogue = [&](auto Slot, const float *yb, int32_t t) {
+        constexpr int sl = decltype(Slot)::value & 3;
+        const int ecol = (((es >> 2) ^ swe) << 2) + (es & 3);
+        float a = yb[ce * kT1 + ecol];
+#pragma unroll
+        for (int rr = 1; rr < NR; ++rr) a += yb[(rr * kCh + ce) * kT1 + ecol];
+        float o = __builtin_fmaf(Dv, ru[sl], a);
+        const uint32_t sof = uint32_t(t) * uint32_t(kT1 * SZ);
+        if constexpr (HAS_OUT) buffer_store_elem<T>(rs_o, fo_o, sof, o);
+        if constexpr (HAS_Z) {
+            o *= silu_fast(elem_f32<T>(rz[sl]));
+            buffer_store_elem<T>(rs_oz, fo_oz, sof, o);
+        }
+    };
+
+    // Scan of one tile (pair half H): B/C of the lane's state at step s of the pair sit in lane s / 2
+    // of its row, register s % 2; dt' / dt'u are read one 4-step group ahead.
+    float bv[2], cv[2];
+    float4 pre_dt, pre_du;
+    auto scan_tile = [&](auto Hc, const float *dt, const float *du, float *yb, const float *dtn, const float *dun) {
+        constexpr int H = decltype(Hc)::value;
+        float4 dtq = pre_dt, duq = pre_du;
+        static_for<0, kT1 / 4>([&](auto S4) {
+            constexpr int s4 = decltype(S4)::value;
+            float4 ndt, ndu;
+            if constexpr (s4 + 1 < kT1 / 4) {
+                ndt = *reinterpret_cast<const float4 *>(&dt[c * kT1 + (((s4 + 1) ^ swc) << 2)]);
+                ndu = *reinterpret_cast<const float4 *>(&du[c * kT1 + (((s4 + 1) ^ swc) << 2)]);
+            } else {
+                ndt = *reinterpret_cast<const float4 *>(&dtn[c * kT1 + (swc << 2)]);
+                ndu = *reinterpret_cast<const float4 *>(&dun[c * kT1 + (swc << 2)]);
+            }
+            const float dts[4] = {dtq.x, dtq.y, dtq.z, dtq.w};
+            const float dus[4] = {duq.x, duq.y, duq.z, duq.w};
+            float av[4], bbv[4], pv[4];
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                av[j] = __builtin_amdgcn_exp2f(dts[j] * At);
+                bbv[j] = row_bcast<s / 2>(bv[s % 2]) * dus[j];
+            });
+            static_for<0, 4>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                constexpr int s = kT1 * H + 4 * s4 + j;
+                h = __builtin_fmaf(av[j], h, bbv[j]);
+                pv[j] = row_bcast<s / 2>(cv[s % 2]) * h;
+            });
+            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
+                make_float4(pv[0], pv[1], pv[2], pv[3]);
+            dtq = ndt;
+            duq = ndu;
+        });
+        pre_dt = dtq;
+        pre_du = duq;
+    };
+
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    K1SData<T> ring[PF];
+    {
+        uint32_t u0, dl0, z0, u1, dl1, z1;
+        load_tile(0, u0, dl0, z0);
+        load_tile(1, u1, dl1, z1);
+#pragma unroll
+        for (int s = 0; s < PF; ++s) load_data(s, ring[s]);
+        prologue(I0{}, u0, dl0, z0);
+        prologue(I1{}, u1, dl1, z1);
+    }
+    __syncthreads();
+    pre_dt = *reinterpret_cast<const float4 *>(&DT(I0{})[c * kT1 + (swc << 2)]);
+    pre_du = *reinterpret_cast<const float4 *>(&DU(I0{})[c * kT1 + (swc << 2)]);
+
+    for (int32_t i0 = 0; i0 < n_pairs; i0 += PF) {
+        static_for<0, PF>([&](auto Sc) {
+            constexpr int S = decltype(Sc)::value;
+            constexpr int P = S & 1;
+            using T2P = std::integral_constant<int, 2 * P>;
+            using T2P1 = std::integral_constant<int, 2 * P + 1>;
+            using T2P2 = std::integral_constant<int, 2 * P + 2>;
+            using T2P3 = std::integral_constant<int, 2 * P + 3>;
+            const int32_t i = i0 + S;
+            if (i < n_pairs) {
+                unpack_raw<T, 2>(ring[S].b, bv);
+                unpack_raw<T, 2>(ring[S].c, cv);
+                const K1SData<T> nxt = ring[S];
+                load_data(i + PF, ring[S]);
+                // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
+                scan_tile(I0{}, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
+                prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
+                epilogue(T2P3{}, YB(I1{}), i > 0 ? 2 * i - 1 : 0);
+                __syncthreads();
+                // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
+                scan_tile(I1{}, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
+                prologue(T2P3{}, nxt.u1, nxt.d1, nxt.z1);
+                epilogue(T2P{}, YB(I0{}), 2 * i);
+                __syncthreads();
+            }
+        });
+    }
+    // The last tile, 2 n_pairs - 1 (slot 1 or 3).
+    if (((n_pairs - 1) & 1) == 0) epilogue(I1{}, YB(I1{}), 2 * n_pairs - 1);
+    else epilogue(std::integral_constant<int, 3>{}, YB(I1{}), 2 * n_pairs - 1);
+    if (p.last_state) p.last_state[(b * p.dim + d0 + c) * 16 + r] = h;
+}
+
+// scan_fwd_mix: blocks [0, n_double) run two k2s groups each (waves 0-1 and 2-3), the blocks after
+// them one k1s group each; every block has four waves. The grid is sized so that each compute unit
+// holds n_double / CUs two-group blocks and one one-group block at once (the hardware places a
+// block's four waves on the four SIMDs of a CU and deals the blocks out round-robin), which puts
+// the same number of (channel, state) rows on every SIMD: at 5 groups per CU, 2 x 2 + 1 x 1 states
+// per lane; at 3 groups per CU, 1 x 2 + 1 x 1. Groups are numbered batch-major; group g always takes
+// the same path for a given shape and device, so results do not depend on scheduling.
+union MixLds {
+    K2SLds k2[2];
+    K1SLds k1;
+};
+
+template <typename T, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
+scan_fwd_mix(const mm_scan_fwd_params p, const int64_t ratio, const int32_t n_double) {
+    __shared__ __align__(16) MixLds lds;
+    const int64_t gpb = p.dim / kCh;   // 16-channel groups per batch row
+    if (int32_t(blockIdx.x) < n_double) {
+        // Waves 0-1 take the first group, waves 2-3 the second: uniform per wave, made scalar so
+        // that the group's buffer resources stay in SGPRs.
+        const int half = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 7));
+        const int64_t grp = 2 * int64_t(blockIdx.x) + half;
+        k2s_group<T, 2, SOFTPLUS, false, HAS_Z, HAS_OUT, true, 0>(p, ratio, kWholeRows, threadIdx.x & 127, grp / gpb,
+                                                                  (grp % gpb) * kCh, 0, lds.k2[half]);
+    } else {
+        const int64_t grp = 2 * int64_t(n_double) + (int64_t(blockIdx.x) - n_double);
+        k1s_group<T, 2, SOFTPLUS, HAS_Z, HAS_OUT>(p, ratio, threadIdx.x, grp / gpb, (grp % gpb) * kCh, lds.k1);
+    }
+}
+
+template <typename T, bool HAS_Z, bool HAS_OUT>
+int launch_mix_io(const mm_scan_fwd_params &p, hipStream_t stream, int32_t n_double, int32_t n_single) {
+    const int64_t ratio = p.dim / p.n_groups;
+    auto *kern = p.delta_softplus ? scan_fwd_mix<T, true, HAS_Z, HAS_OUT> : scan_fwd_mix<T, false, HAS_Z, HAS_OUT>;
+    hipLaunchKernelGGL(kern, dim3(unsigned(n_double + n_single)), dim3(256), 0, stream, p, ratio, n_double);
+    return launch_status("scan_fwd_mix");
+}
+
+template <typename T>
+int launch_mix(const mm_scan_fwd_params &p, hipStream_t stream, int32_t n_double, int32_t n_single) {
+    if (p.z) return p.out ? launch_mix_io<T, true, true>(p, stream, n_double, n_single)
+                          : launch_mix_io<T, true, false>(p, stream, n_double, n_single);
+    return launch_mix_io<T, false, true>(p, stream, n_double, n_single);
+}
 
 // fp32 rows: only the instances without chunk states (the training variants' chunk and tile state
 // stores take them past 168 VGPRs, where they spill); the caller routes chunk states elsewhere.
@@ -1451,12 +1724,23 @@ static bool pipe_offsets_ok(const mm_scan_fwd_params &p) {
     return span < (int64_t(1) << 31);
 }
 
-// Whether a segmented request runs on k2s: every 32-step pair whole, and neither a request that
-// writes both out and out_z nor fp32 with chunk states (the pipelined kernel's segments serve those;
-// MM_SCAN_KERNEL=k2 selects them always).
+// k2s, k1s and k2i address a 16-channel group with 32-bit BYTE offsets from a per-group buffer base
+// (lane offset + tile or pair offset): every byte they touch must lie below 2^32 from the base. For
+// 16-bit inputs pipe_offsets_ok implies it; fp32 rows whose channel stride puts the group's span
+// at or above 2^30 elements go to the pipelined kernel, which uses element offsets.
+static bool k2s_bytes_ok(const mm_scan_fwd_params &p) {
+    const int64_t span = p.seqlen + 15 * std::max({p.u_d_stride, p.delta_d_stride, p.z_d_stride, p.out_d_stride,
+                                                   p.out_z_d_stride, p.B_dstate_stride, p.C_dstate_stride});
+    const int64_t size = p.itype == MM_FLOAT32 ? 4 : 2;
+    return span * size < (int64_t(1) << 32);
+}
+
+// Whether a segmented request runs on k2s: every 32-step pair whole, byte offsets in range, and
+// neither a request that writes both out and out_z nor fp32 with chunk states (the pipelined
+// kernel's segments serve those; MM_SCAN_KERNEL=k2 selects them always).
 static bool k2s_segments_ok(const mm_scan_fwd_params &p) {
     return p.seqlen % (2 * tiled::kT1) == 0 && tiled_variant() != 20 && !(p.z && p.out) &&
-           !(p.itype == MM_FLOAT32 && p.chunk_states);
+           !(p.itype == MM_FLOAT32 && p.chunk_states) && k2s_bytes_ok(p);
 }
 
 #ifdef MM_TILED_COMMON
@@ -1510,19 +1794,48 @@ bool tile_states_ok(const mm_scan_fwd_params &p) {
 }
 #endif  // MM_TILED_COMMON
 
-// The two-states-per-lane kernels for 16-bit inputs: k2s (symmetric element work) when L is a
-// multiple of 32, else k2i (MM_SCAN_KERNEL=k2i selects k2i always, for comparison).
+// Balanced launch of one-pass inference requests (scan_fwd_mix): when the 16-channel groups give an
+// odd number q in {3, 5} per compute unit, k2s alone would put 3 waves on half the SIMDs and 2 on
+// the others (q = 5) or 2 and 1 (q = 3). The mixed grid runs (q - 1) / 2 two-group blocks and one
+// one-group (k1s) block per CU instead, the same states on every SIMD. MM_SCAN_MIX=0 turns it off
+// (for comparison).
+static bool mix_plan(const mm_scan_fwd_params &p, int32_t &n_double, int32_t &n_single) {
+    static const bool off = [] {
+        const char *e = getenv("MM_SCAN_MIX");
+        return e && !strcmp(e, "0");
+    }();
+    if (off || p.chunk_states || p.tile_states) return false;
+    const int64_t groups = p.batch * (p.dim / tiled::kCh);
+    const int64_t cus = device_simds() / 4;
+    if (cus <= 0 || groups % cus != 0) return false;
+    const int64_t q = groups / cus;
+    if (q != 3 && q != 5) return false;
+    n_double = int32_t((q / 2) * cus);
+    n_single = int32_t(cus);
+    return true;
+}
+
+// The two-states-per-lane kernels: k2s (symmetric element work, or the balanced mixed grid) when L
+// is a multiple of 32 and the byte offsets fit, else k2i for 16-bit inputs (MM_SCAN_KERNEL=k2i
+// selects k2i always, for comparison) and the pipelined kernel for fp32.
 template <typename T>
 static int launch_k2x(const mm_scan_fwd_params &p, hipStream_t stream) {
     static const bool nofull = getenv("MM_SCAN_NOFULL") != nullptr;
-    const bool whole_pairs = p.seqlen % (2 * tiled::kT1) == 0 && !nofull;
+    const bool whole_pairs = p.seqlen % (2 * tiled::kT1) == 0 && !nofull && k2s_bytes_ok(p);
+    int32_t n_double = 0, n_single = 0;
     if constexpr (sizeof(T) == 4) {
         // fp32: k2s for the inference requests it compiles for (no chunk or tile states), the
         // pipelined kernel for the rest.
-        if (whole_pairs && !p.chunk_states && !p.tile_states) return tiled::launch_k2s<T, 2>(p, stream);
+        if (whole_pairs && !p.chunk_states && !p.tile_states) {
+            if (mix_plan(p, n_double, n_single)) return tiled::launch_mix<T>(p, stream, n_double, n_single);
+            return tiled::launch_k2s<T, 2>(p, stream);
+        }
         return launch_pipe_pf<T, 2>(p, stream);
     } else {
-        if (tiled_variant() != 31 && whole_pairs) return tiled::launch_k2s<T, 2>(p, stream);
+        if (tiled_variant() != 31 && whole_pairs) {
+            if (mix_plan(p, n_double, n_single)) return tiled::launch_mix<T>(p, stream, n_double, n_single);
+            return tiled::launch_k2s<T, 2>(p, stream);
+        }
         return tiled::launch_k2i<T, 2>(p, stream);
     }
 }
@@ -1574,7 +1887,7 @@ int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream) {
         const char *e = getenv("MM_STATES_KERNEL");
         return e && !strcmp(e, "pipe");
     }();
-    if (!pipe && p.seqlen % (2 * tiled::kT1) == 0) return tiled::launch_k2s_states<T>(p, stream);
+    if (!pipe && p.seqlen % (2 * tiled::kT1) == 0 && k2s_bytes_ok(p)) return tiled::launch_k2s_states<T>(p, stream);
     return tiled::launch_fwd_states<T>(p, stream);
 }
 template int launch_states_only<MM_TILED_TYPE>(const mm_scan_fwd_params &, hipStream_t);

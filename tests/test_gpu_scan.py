@@ -409,3 +409,95 @@ def test_segmented_c_abi_with_and_without_workspace():
         res.append((out_z.cpu(), last.cpu()))
     for (o, l), what in zip(res, ("with workspace", "without workspace")):
         _seg_rows(o, l, case, what)
+
+
+# ---------------------------------------------------------------------------------------------
+# The balanced mixed grid (scan_fwd_mix): 3 or 5 sixteen-channel groups per compute unit.
+# ---------------------------------------------------------------------------------------------
+def _cus():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def _rows_vs_f64(inputs, out, last, what):
+    rtol, atol = fixtures.tolerances(inputs["u"].dtype)
+    y64, last64 = cscan.scan_all_rows(**inputs)
+    np.testing.assert_allclose(out.double().numpy(), y64, rtol=rtol, atol=atol, err_msg=f"{what} out")
+    if last is not None:
+        np.testing.assert_allclose(last.double().numpy(), last64, rtol=rtol, atol=atol,
+                                   err_msg=f"{what} last_state")
+
+
+@pytest.mark.parametrize("q", [3, 5])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+def test_balanced_grid_every_row(q, dtype):
+    """Shapes whose 16-channel groups number 3 or 5 per compute unit run the mixed grid: two-state
+    (k2s) groups in the first blocks, one-state (k1s) groups in the last ones. Every row -- both
+    paths and the group where one hands over to the other -- against the float64 restatement. With
+    batch 2 the one-state groups sit in the second batch row; L = 96 is an odd number of 32-step
+    pairs."""
+    cus = _cus()
+    batch, dim = 2, q * cus * 16 // 2
+    _say(f"balanced grid q={q} {dtype} batch {batch} dim {dim} L 96 (CUs {cus})")
+    case = _case(70 + q, batch, dim, 96, 16, dtype)
+    out, last = _run(case)
+    _rows_vs_f64(case, out, last, f"q={q} {dtype}")
+
+
+@pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False, with_bias=False), dict(softplus=False),
+                                   dict(bkind="4d", G=4)], ids=["no_z", "no_D_bias", "no_softplus", "G4"])
+def test_balanced_grid_optional_inputs(flags):
+    cus = _cus()
+    dim = 3 * cus * 16
+    _say(f"balanced grid optional inputs {flags} batch 1 dim {dim} L 64")
+    case = _case(75, 1, dim, 64, 16, torch.bfloat16, **flags)
+    out, last = _run(case)
+    _rows_vs_f64(case, out, last, f"balanced grid {flags}")
+
+
+def test_balanced_grid_out_and_out_z_c_abi():
+    """The pre-gate out and out_z written together (no chunk states) through the C ABI on the mixed
+    grid, plus two identical calls giving the same bits."""
+    lib = capi.load()
+    cus = _cus()
+    dim = 5 * cus * 16
+    _say(f"balanced grid out + out_z via C ABI, batch 1 dim {dim} L 64")
+    case = _case(76, 1, dim, 64, 16, torch.bfloat16)
+    g = _to(case, DEV)
+    res = []
+    for _ in range(2):
+        out = torch.empty_like(g["u"])
+        out_z = torch.empty_like(g["u"])
+        last = torch.empty(1, dim, 16, device=DEV)
+        p = capi.scan_fwd_params(g["u"], g["delta"], g["A"], g["B"].unsqueeze(1), g["C"].unsqueeze(1), g["D"],
+                                 g["z"], g["delta_bias"], True, out=out, out_z=out_z, last_state=last)
+        rc = lib.mm_scan_fwd(ctypes.byref(p), capi.stream_handle())
+        assert rc == 0, lib.mm_last_error()
+        torch.cuda.synchronize()
+        res.append((out.cpu(), out_z.cpu(), last.cpu()))
+    assert all(torch.equal(a, b) for a, b in zip(res[0], res[1]))
+    _rows_vs_f64(case, res[0][1], res[0][2], "out_z")
+    no_z = dict(case, z=None)
+    _rows_vs_f64(no_z, res[0][0], None, "pre-gate out")
+
+
+@pytest.mark.parametrize("L", [64, 2048])
+def test_fp32_group_span_above_4_gib(L):
+    """An fp32 u whose channel stride puts the 16-channel group's span above 2^32 bytes (but below
+    2^31 elements): the kernels that address a group with 32-bit byte offsets (k2s, k1s) would wrap
+    and read other rows, so the request must go to the element-offset kernels (L 64: one pass;
+    L 2048: sequence segments). Checked against the oracle."""
+    from motif_mamba_amd import selective_scan_fn
+    S = (1 << 26) + (1 << 24)                # 15 * S * 4 bytes > 2^32, 15 * S + L < 2^31
+    _say(f"fp32 u channel stride {S} (5.4 GB view), L {L}")
+    case = _case(80, 1, 16, L, 16, torch.float32)
+    base = torch.zeros(16 * S, device=DEV)
+    u = base.as_strided((1, 16, L), (16 * S, S, 1))
+    u.copy_(case["u"].to(DEV))
+    g = _to(case, DEV)
+    g["u"] = u
+    out, last = selective_scan_fn(**g, return_last_state=True)
+    torch.cuda.synchronize()
+    del base, u
+    exp, exp_last = selective_scan_ref(**case, return_last_state=True)
+    _close(out.cpu(), exp, torch.float32, "out_z")
+    _close(last.cpu(), exp_last, torch.float32, "last_state")
