@@ -300,10 +300,14 @@ int64_t mm_scan_fwd_tile_states_size(const mm_scan_fwd_params *params);
  * serving loops, harnesses that forbid hipMalloc. No counterpart in the reference. Same results
  * as mm_scan_fwd with a workspace of mm_scan_fwd_workspace_size() bytes; params->workspace and
  * workspace_bytes are ignored: the sequence-segment scratch is a static device array of
- * MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES per GPU (every request the segment heuristic selects needs
- * less than 2.5 MiB); a request needing more is refused with MM_ERR_INVALID_ARGUMENT. The call
- * allocates and frees nothing. All calls on one GPU share that GPU's scratch: calls that overlap
- * in time on one GPU (other streams, other threads) race and must be serialised by the caller. */
+ * MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES per GPU. The segment heuristic asks for at most about 3,456
+ * bytes per SIMD of the device (batch * dim * segments * 72 bytes with segments ~ 5 * SIMDs * 8 /
+ * (batch * dim)): up to ~3.4 MiB on the 1,024-SIMD MI355X (for instance, needs
+ * 2,949,120 bytes). A request that needs more than the static buffer (a device with more SIMDs, or
+ * MM_SCAN_SEGMENTS forcing more segments) runs the single-pass kernels, with the results of
+ * mm_scan_fwd given no workspace. The call allocates and frees nothing. All calls on one GPU share
+ * that GPU's scratch: calls that overlap in time on one GPU (other streams, other threads) race and
+ * must be serialised by the caller. */
 int mm_scan_fwd_noalloc(const mm_scan_fwd_params *params, void *stream);
 
 /* Backward scan. Replaces selective_scan_cuda.bwd (selective_scan.cpp:415-612, pybind :628-637). */

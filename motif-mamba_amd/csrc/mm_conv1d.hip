@@ -399,7 +399,7 @@ int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
     };
     const bool vec = p.seqlen % kChunk == 0 && row_ok(p.x, p.x_batch_stride, p.x_d_stride) &&
                      row_ok(p.dout, p.dout_batch_stride, p.dout_d_stride) && row_ok(p.dx, p.dx_batch_stride, p.dx_d_stride);
-    const dim3 grid(unsigned(p.dim));   // one workgroup per channel (dim < 2^31, checked on entry)
+    const dim3 grid(unsigned(p.dim));   // one workgroup per channel (dim < 2^24, checked on entry)
     if (vec)
         hipLaunchKernelGGL((conv1d_bwd_kernel<T, W, true, NC>), grid, dim3(kThreads), 0, s, p);
     else
@@ -535,8 +535,10 @@ int mm_causal_conv1d_bwd(const mm_conv1d_bwd_params *params, void *stream) {
     if (p.batch < 0 || p.dim < 0 || p.seqlen < 0) return invalid("mm_causal_conv1d_bwd: negative size");
     if (p.width < 1 || p.width > MM_CONV1D_MAX_WIDTH)
         return invalid("mm_causal_conv1d_bwd: width must be in [1, 8]");
-    if (p.dim > 0x7fffffff)   // one workgroup per channel on a one-dimensional grid
-        return mm::set_error(MM_ERR_UNSUPPORTED, "mm_causal_conv1d_bwd: dim must be < 2^31");
+    // One workgroup of kThreads lanes per channel on a one-dimensional grid: gridDim.x * blockDim.x
+    // (the grid's lane count) must stay below 2^32.
+    if (p.dim >= (int64_t(1) << 32) / mm::conv::kThreads)
+        return mm::set_error(MM_ERR_UNSUPPORTED, "mm_causal_conv1d_bwd: dim must be < 2^24");
     if (p.dim == 0) return MM_OK;
     if (!p.weight || !p.dweight || (p.bias && !p.dbias))
         return invalid("mm_causal_conv1d_bwd: weight and dweight (and dbias with bias) are required");

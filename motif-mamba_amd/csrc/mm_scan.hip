@@ -839,12 +839,9 @@ int mm_scan_fwd_noalloc(const mm_scan_fwd_params *params, void *stream) {
     mm_scan_fwd_params p = *params;
     p.workspace = nullptr;
     p.workspace_bytes = 0;
+    // A segment plan larger than the static buffer: the single-pass kernels (workspace left NULL).
     const int64_t need = mm_scan_fwd_workspace_size(params);
-    if (need > int64_t(MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES))
-        return fail(MM_ERR_INVALID_ARGUMENT,
-                    "mm_scan_fwd_noalloc: the request needs %lld bytes of scratch, more than the %d-byte static "
-                    "buffer; use mm_scan_fwd with a workspace", (long long)need, MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES);
-    if (need > 0) {
+    if (need > 0 && need <= int64_t(MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES)) {
         rc = noalloc_scratch(&p.workspace);
         if (rc != MM_OK) return rc;
         p.workspace_bytes = MM_SCAN_FWD_NOALLOC_SCRATCH_BYTES;

@@ -1768,7 +1768,7 @@ int64_t device_simds() {
 // (6, 8) cost most, and from ~5 waves per SIMD on the time is flat. MM_SCAN_SEGMENTS=n sets the count
 // (for measurements).
 int64_t segment_count(const mm_scan_fwd_params &p) {
-    if (!tiled_shape_ok(p) || !pipe_offsets_ok(p) || p.tile_states) return 1;
+    if (!tiled_shape_ok(p) || !fwd_vector_ok(&p) || !pipe_offsets_ok(p) || p.tile_states) return 1;
     const int64_t waves = 2 * p.batch * (p.dim / tiled::kCh);
     const int64_t n_pairs = (p.seqlen + 2 * tiled::kT1 - 1) / (2 * tiled::kT1);
     int64_t n_seg;
@@ -1800,16 +1800,24 @@ bool tile_states_ok(const mm_scan_fwd_params &p) {
 // one-group (k1s) block per CU instead, the same states on every SIMD. MM_SCAN_MIX=0 turns it off
 // (for comparison).
 static bool mix_plan(const mm_scan_fwd_params &p, int32_t &n_double, int32_t &n_single) {
-    static const bool off = [] {
+    static const int mode = [] {   // 0: off, 1: default, 2: one-state groups only (q = 3)
         const char *e = getenv("MM_SCAN_MIX");
-        return e && !strcmp(e, "0");
+        if (!e) return 1;
+        if (!strcmp(e, "0")) return 0;
+        if (!strcmp(e, "k1")) return 2;
+        return 1;
     }();
-    if (off || p.chunk_states || p.tile_states) return false;
+    if (mode == 0 || p.chunk_states || p.tile_states) return false;
     const int64_t groups = p.batch * (p.dim / tiled::kCh);
     const int64_t cus = device_simds() / 4;
     if (cus <= 0 || groups % cus != 0) return false;
     const int64_t q = groups / cus;
     if (q != 3 && q != 5) return false;
+    if (mode == 2 && q == 3) {
+        n_double = 0;
+        n_single = int32_t(3 * cus);
+        return true;
+    }
     n_double = int32_t((q / 2) * cus);
     n_single = int32_t(cus);
     return true;

@@ -188,6 +188,9 @@ def test_workspace_size_query():
     bad.dstate = 0
     assert lib.mm_scan_fwd_workspace_size(ctypes.byref(bad)) == 0                      # invalid request
     assert lib.mm_scan_fwd_workspace_size(None) == 0
+    odd = params(1, 2560, 65536, itype=0)
+    odd.u = 4098                         # rows not 16-byte aligned: the row-per-lane kernel, no segments
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(odd)) == 0
 
 
 def test_tile_states_size_query():
@@ -302,7 +305,10 @@ def test_conv1d_rejects_invalid_params():
     assert "required" in lib.mm_last_error().decode()
     r.x, r.width = 0x1000, 0
     assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_ERR_INVALID_ARGUMENT
-    r.width, r.dim = 4, 0                # nothing to write: returns before any launch
+    r.width, r.dim = 4, 1 << 24          # one 256-lane workgroup per channel: the grid's lanes reach 2^32
+    assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_ERR_UNSUPPORTED
+    assert "2^24" in lib.mm_last_error().decode()
+    r.dim = 0                            # nothing to write: returns before any launch
     assert lib.mm_causal_conv1d_bwd(ctypes.byref(r), None) == capi.MM_OK
 
 

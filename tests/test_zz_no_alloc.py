@@ -42,12 +42,14 @@ def _run(entry, lib, inp, workspace=None):
 
 
 # (batch, dim, L, dtype, groups): few (batch, 16-channel) groups and long sequences, so that the
-# dstate-16 forward cuts the sequence into segments; the second of each pair is smaller.
+# dstate-16 forward cuts the sequence into segments; the second of each pair is smaller. The third
+# pair is BASELINE config 3 (G = 4), whose 16-segment plan needs 2,949,120 bytes of scratch.
 PAIRS = [((1, 256, 8192, torch.bfloat16, 1), (1, 128, 4096, torch.bfloat16, 1)),
-         ((1, 160, 16384, torch.float32, 2), (2, 32, 2048, torch.float32, 1))]
+         ((1, 160, 16384, torch.float32, 2), (2, 32, 2048, torch.float32, 1)),
+         ((1, 2560, 65536, torch.float32, 4), (1, 1280, 65536, torch.float32, 1))]
 
 
-@pytest.mark.parametrize("pair", PAIRS, ids=["bf16", "fp32"])
+@pytest.mark.parametrize("pair", PAIRS, ids=["bf16", "fp32", "cfg3"])
 def test_noalloc_matches_workspace_entry(pair):
     lib = capi.load()
     for i, (batch, dim, L, dtype, G) in enumerate(pair):
@@ -73,4 +75,20 @@ def test_noalloc_without_scratch():
     assert lib.mm_scan_fwd_workspace_size(ctypes.byref(p)) == 0
     exp_z, exp_last, _ = _run(lib.mm_scan_fwd, lib, inp)
     torch.cuda.synchronize()
+    assert torch.equal(got_z, exp_z) and torch.equal(got_last, exp_last)
+
+
+def test_noalloc_plan_larger_than_scratch(monkeypatch):
+    """A segment plan that needs more than the static scratch (forced here with MM_SCAN_SEGMENTS,
+    which the library reads on every call) runs the single-pass kernels: the outputs equal those of
+    mm_scan_fwd given no workspace."""
+    lib = capi.load()
+    monkeypatch.setenv("MM_SCAN_SEGMENTS", "64")
+    _say("mm_scan_fwd_noalloc with a forced 64-segment plan: batch 1 dim 1024 L 65536 fp32")
+    inp = _inputs(50, 1, 1024, 65536, torch.float32)
+    got_z, got_last, p = _run(lib.mm_scan_fwd_noalloc, lib, inp)
+    assert lib.mm_scan_fwd_workspace_size(ctypes.byref(p)) > 4 << 20
+    exp_z, exp_last, _ = _run(lib.mm_scan_fwd, lib, inp)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got_z.float()).all() and torch.isfinite(got_last).all()
     assert torch.equal(got_z, exp_z) and torch.equal(got_last, exp_last)
