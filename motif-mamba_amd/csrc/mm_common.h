@@ -37,6 +37,20 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// exp2(dt * A2 + kExpBiasOffset) for a decay argument dt * (A log2 e) <= 0, as one FMA and one
+// v_exp_f32. Measured on gfx950 over 2^24 arguments, v_exp_f32 returns the correctly rounded 2^x
+// for ~95 % of them and is 1 ulp low for most of the rest: for |x| < 1e-3 (decays just below 1,
+// the states with the longest memory) its mean relative error is -7e-9 per call, -3.4e-9 for
+// |x| > 0.2. A recurrence multiplies that bias over its memory: in the coupled P/Q scan, 8,192
+// float32 steps drift 3.1e-4 from float64 where a correctly rounded exp2 drifts 2.4e-5 (a float32
+// emulation of the kernel's operation order). The offset 1e-8 (2^1e-8 = 1 + 6.9e-9) removes the
+// mean bias of the long-memory decays (the same emulation: 2.0e-5); for |x| >= 0.25 it is below
+// half an ulp of x and vanishes, and exp2(1e-8) is 1 (a zero step stays the identity).
+constexpr float kExpBiasOffset = 1.0e-8f;
+__device__ __forceinline__ float decay_exp2(float dt, float A2) {
+    return __builtin_amdgcn_exp2f(__builtin_fmaf(dt, A2, kExpBiasOffset));
+}
+
 // softplus with torch's threshold: x > 20 ? x : log1p(exp(x)).
 __device__ __forceinline__ float softplus_f32(float x) {
     return x > 20.f ? x : log1pf(expf(x));

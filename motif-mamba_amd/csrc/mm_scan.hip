@@ -127,7 +127,7 @@ scan_fwd_rowlane(const mm_scan_fwd_params p, const int64_t ratio, const int32_t 
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 if (VEC || t < nt) {
-                    const float a = fast_exp2(dtp[t] * an);
+                    const float a = decay_exp2(dtp[t], an);
                     hn = __builtin_fmaf(a, hn, du[t] * bb[t]);
                     y[t] = __builtin_fmaf(hn, cc[t], y[t]);
                 }
@@ -215,7 +215,7 @@ state_update_kernel(const mm_state_update_params p, const int64_t ratio) {
     for (int k = 0; k < SPL; ++k) {
         const int n = part * SPL + k;
         if (n < N) {
-            const float a = fast_exp2(dt * p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e);
+            const float a = decay_exp2(dt, p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e);
             float s = to_f32(sp[n * p.state_dstate_stride]);
             s = __builtin_fmaf(s, a, dtx * to_f32(Bp[n * p.B_dstate_stride]));
             if (active) sp[n * p.state_dstate_stride] = from_f32<S>(s);
@@ -349,10 +349,10 @@ state_update_vec16(const mm_state_update_params p, const uint32_t ratio, const u
         float4 s;
         if constexpr (std::is_same_v<S, float>) s = r[u].s;
         else s = unpack4<S>(r[u].sw);
-        s.x = __builtin_fmaf(s.x, fast_exp2(dl * a4.x), dtx * b4.x);
-        s.y = __builtin_fmaf(s.y, fast_exp2(dl * a4.y), dtx * b4.y);
-        s.z = __builtin_fmaf(s.z, fast_exp2(dl * a4.z), dtx * b4.z);
-        s.w = __builtin_fmaf(s.w, fast_exp2(dl * a4.w), dtx * b4.w);
+        s.x = __builtin_fmaf(s.x, decay_exp2(dl, a4.x), dtx * b4.x);
+        s.y = __builtin_fmaf(s.y, decay_exp2(dl, a4.y), dtx * b4.y);
+        s.z = __builtin_fmaf(s.z, decay_exp2(dl, a4.z), dtx * b4.z);
+        s.w = __builtin_fmaf(s.w, decay_exp2(dl, a4.w), dtx * b4.w);
         const bool live = dr < dim && b < uint32_t(p.batch);
         if (live) {
             S *sp = state + int64_t(b) * p.state_batch_stride + int64_t(dr) * p.state_d_stride + 4 * part;
@@ -451,10 +451,10 @@ state_update_vec16x(const mm_state_update_params p, const uint32_t ratio, const 
         float4 st;
         if constexpr (std::is_same_v<S, float>) st = sv[u];
         else st = unpack4<S>(sw[u]);
-        st.x = __builtin_fmaf(st.x, fast_exp2(dl * a4.x), dtx * b4.x);
-        st.y = __builtin_fmaf(st.y, fast_exp2(dl * a4.y), dtx * b4.y);
-        st.z = __builtin_fmaf(st.z, fast_exp2(dl * a4.z), dtx * b4.z);
-        st.w = __builtin_fmaf(st.w, fast_exp2(dl * a4.w), dtx * b4.w);
+        st.x = __builtin_fmaf(st.x, decay_exp2(dl, a4.x), dtx * b4.x);
+        st.y = __builtin_fmaf(st.y, decay_exp2(dl, a4.y), dtx * b4.y);
+        st.z = __builtin_fmaf(st.z, decay_exp2(dl, a4.z), dtx * b4.z);
+        st.w = __builtin_fmaf(st.w, decay_exp2(dl, a4.w), dtx * b4.w);
         if (dr < dim && b < batch) {
             S *sp = state + int64_t(b) * p.state_batch_stride + int64_t(dr) * p.state_d_stride + 4 * part;
             if constexpr (std::is_same_v<S, float>) *reinterpret_cast<float4 *>(sp) = st;

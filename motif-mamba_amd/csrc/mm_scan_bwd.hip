@@ -131,7 +131,7 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
         if (t % kBT == 0 && on) ck[(t / kBT) * N + n] = h;
         float raw;
         const float dt = dt_at(t, raw);
-        h = __builtin_fmaf(fast_exp2(dt * A2), h, dt * to_f32(up[t]) * b_at(t));
+        h = __builtin_fmaf(decay_exp2(dt, A2), h, dt * to_f32(up[t]) * b_at(t));
     }
     __syncthreads();  // orders this lane's checkpoint stores before its reloads (same lane, global memory)
 
@@ -150,7 +150,7 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
                 const int64_t t = t0 + s;
                 dts[s] = dt_at(t, raw);
                 us[s] = to_f32(up[t]);
-                as[s] = fast_exp2(dts[s] * A2);
+                as[s] = decay_exp2(dts[s], A2);
                 hh = __builtin_fmaf(as[s], hh, dts[s] * us[s] * b_at(t));
                 hs[s] = hh;
             }
@@ -435,8 +435,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 const float2 cv = *reinterpret_cast<const float2 *>(&sBC[0][t * kBCS + 16 + n0]);
                 gh0 = __builtin_fmaf(an0, gh0, x.w * cv.x);
                 gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
-                an0 = __builtin_amdgcn_exp2f(x.x * A20);
-                an1 = __builtin_amdgcn_exp2f(x.x * A21);
+                an0 = decay_exp2(x.x, A20);
+                an1 = decay_exp2(x.x, A21);
                 pa0 *= an0;
                 pa1 *= an1;
             }
@@ -461,8 +461,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
         for (int t = 0; t < kFT; ++t) {
             const float4 x = sX[buf][c * kXS + t];
             const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * kBCS + n0]);
-            h0 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A20), h0, x.y * bv.x);
-            h1 = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A21), h1, x.y * bv.y);
+            h0 = __builtin_fmaf(decay_exp2(x.x, A20), h0, x.y * bv.x);
+            h1 = __builtin_fmaf(decay_exp2(x.x, A21), h1, x.y * bv.y);
         }
         if (kBufs == 1) __syncthreads();   // reads done before the next commit rewrites the buffer
     }
@@ -503,8 +503,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             for (int t = 0; t < kFT; ++t) {
                 const float4 x = sX[buf][c * kXS + t];
                 const float2 bv = *reinterpret_cast<const float2 *>(&sBC[buf][t * kBCS + n0]);
-                as0[t] = __builtin_amdgcn_exp2f(x.x * A20);
-                as1[t] = __builtin_amdgcn_exp2f(x.x * A21);
+                as0[t] = decay_exp2(x.x, A20);
+                as1[t] = decay_exp2(x.x, A21);
                 x0 = __builtin_fmaf(as0[t], x0, x.y * bv.x);
                 x1 = __builtin_fmaf(as1[t], x1, x.y * bv.y);
                 hs0[t] = x0;

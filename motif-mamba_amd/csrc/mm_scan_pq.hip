@@ -317,7 +317,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
                 lds_read_vec<S>(&sBC[t * BCS + NP + k * S], cv[j]);
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    av[j][s] = __builtin_amdgcn_exp2f(dts[j] * A2[s]);
+                    av[j][s] = decay_exp2(dts[j], A2[s]);
                     bu[j][s] = dus[j] * bv[s];
                 }
             }
@@ -509,7 +509,7 @@ scan_fwd_pq_rowlane(const mm_scan_fwd_params p, const int64_t ratio) {
 #pragma unroll
             for (int j = 0; j < kMaxRank; ++j)
                 if (j < rank) w = __builtin_fmaf(Pd[n * p.P_dstate_stride + j * p.P_r_stride], q[j], w);
-            const float a = __builtin_amdgcn_exp2f(dt * (Ad[n * p.A_dstate_stride] * kLog2e));
+            const float a = decay_exp2(dt, Ad[n * p.A_dstate_stride] * kLog2e);
             const float hn = __builtin_fmaf(a, sH[n * kRowBlock + lane], w);
             sH[n * kRowBlock + lane] = hn;
             y = __builtin_fmaf(hn, cn, y);

@@ -242,7 +242,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                     float w = x.y * sBC[t * kBCS + k * S + s];
 #pragma unroll
                     for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                    h[s] = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A2[s]), h[s], w);
+                    h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
                 }
             }
             __syncthreads();
@@ -295,7 +295,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                     float w = x.y * sBC[t * kBCS + k * S + s];
 #pragma unroll
                     for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                    h[s] = __builtin_fmaf(__builtin_amdgcn_exp2f(x.x * A2[s]), h[s], w);
+                    h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
                     sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
                 }
             }
@@ -330,7 +330,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
             float pdd = 0.f, pgb = 0.f;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const float a = __builtin_amdgcn_exp2f(x.x * A2[s]);
+                const float a = decay_exp2(x.x, A2[s]);
                 const float ah = a * hp[s];
                 float pq = 0.f, qs = 0.f;
 #pragma unroll

@@ -186,7 +186,7 @@ scan_fwd_tiled16(const mm_scan_fwd_params p, const int64_t ratio) {
                 static_for<0, K>([&](auto KK) {
                     constexpr int k = decltype(KK)::value;
                     constexpr int src = k * LPS + t / SPL;
-                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    av[j][k] = decay_exp2(dts[j], At[k]);
                     bbv[j][k] = row_bcast<src>(bv[t % SPL]) * dus[j];
                 });
             });
@@ -478,7 +478,7 @@ scan_fwd_pipe(const mm_scan_fwd_params p, const int64_t ratio, const SegArgs sg)
                 static_for<0, K>([&](auto KK) {
                     constexpr int k = decltype(KK)::value;
                     constexpr int src = k * LPS + s / E;
-                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    av[j][k] = decay_exp2(dts[j], At[k]);
                     bbv[j][k] = mul_row_bcast<src>(bv[s % E], dus[j]);
                 });
             });
@@ -864,7 +864,7 @@ scan_fwd_k2i(const mm_scan_fwd_params p, const int64_t ratio) {
                 if (CHUNKS) cum_dt += dts[j];
                 static_for<0, 2>([&](auto KK) {
                     constexpr int k = decltype(KK)::value;
-                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    av[j][k] = decay_exp2(dts[j], At[k]);
                     bbv[j][k] = row_bcast<k * LPS + s / E>(bv[s % E]) * dus[j];
                 });
             });
@@ -1177,7 +1177,7 @@ __device__ __forceinline__ void k2s_group(const mm_scan_fwd_params &p, const int
                 if (CHUNKS || SEG == 1) cum_dt += dts[j];
                 static_for<0, 2>([&](auto KK) {
                     constexpr int k = decltype(KK)::value;
-                    av[j][k] = __builtin_amdgcn_exp2f(dts[j] * At[k]);
+                    av[j][k] = decay_exp2(dts[j], At[k]);
                     bbv[j][k] = row_bcast<k * LPS + s / 4>(bv[s % 4]) * dus[j];
                 });
             });
@@ -1467,7 +1467,7 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
             static_for<0, 4>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 constexpr int s = kT1 * H + 4 * s4 + j;
-                av[j] = __builtin_amdgcn_exp2f(dts[j] * At);
+                av[j] = decay_exp2(dts[j], At);
                 bbv[j] = row_bcast<s / 2>(bv[s % 2]) * dus[j];
             });
             static_for<0, 4>([&](auto J) {

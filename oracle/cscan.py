@@ -141,12 +141,15 @@ def scan_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus
     return {"out": out, "out_z": outz, "last_state": last, "h_chunks": hch}
 
 
-def scan_all_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False, batches=None):
+def scan_all_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_softplus=False, batches=None,
+                  P=None, Q=None):
     """Float64 scan of every (batch, dim) row of a variable-B/C selective scan, for full-size
     checks: the rows of one (batch, group) share their B/C slice, so each (batch, group) is one
     call with a B/C row stride of 0 (no per-row copies of B/C). B/C are (batch, N, L) or
-    (batch, G, N, L). Returns float64 numpy arrays out_z (or out, without z) of shape
-    (len(batches), dim, L) and last_state (len(batches), dim, N) for ``batches`` (all by default).
+    (batch, G, N, L). With P and Q (shared (N, R) / (R, N) or per channel (dim, N, R) / (dim, R, N))
+    the low-rank coupled scan is evaluated. Returns float64 numpy arrays out_z (or out, without z)
+    of shape (len(batches), dim, L) and last_state (len(batches), dim, N) for ``batches`` (all by
+    default).
     """
     batch, dim, L = u.shape
     N = A.shape[1]
@@ -172,11 +175,22 @@ def scan_all_rows(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_soft
             out = np.zeros((gsz, L))
             outz = np.zeros((gsz, L)) if zr is not None else None
             lst = np.zeros((gsz, N))
-            _load().mm_oracle_scan_rows_f64(gsz, L, N, _p(ur), _p(dr), _p(zr), _p(np.ascontiguousarray(Ad[sl])),
-                                            _p(Bg), 0, L, 1, _p(Cg), 0, L, 1,
-                                            _p(np.ascontiguousarray(Dd[sl]) if Dd is not None else None),
-                                            _p(np.ascontiguousarray(bd[sl]) if bd is not None else None),
-                                            int(bool(delta_softplus)), _p(out), _p(outz), _p(lst), 0, None)
+            Dg = np.ascontiguousarray(Dd[sl]) if Dd is not None else None
+            bg = np.ascontiguousarray(bd[sl]) if bd is not None else None
+            if P is not None:
+                K = P.shape[-1]
+                if P.dim() == 2:
+                    Ps, pR, Qs, qR = f64(P), 0, f64(Q), 0
+                else:
+                    Ps, pR, Qs, qR = f64(P[sl]), N * K, f64(Q[sl]), K * N
+                _load().mm_oracle_scan_pq_rows_f64(gsz, L, N, K, _p(ur), _p(dr), _p(zr),
+                                                   _p(np.ascontiguousarray(Ad[sl])), _p(Bg), 0, L, 1,
+                                                   _p(Cg), 0, L, 1, _p(Ps), pR, _p(Qs), qR, _p(Dg), _p(bg),
+                                                   int(bool(delta_softplus)), _p(out), _p(outz), _p(lst), 0, None)
+            else:
+                _load().mm_oracle_scan_rows_f64(gsz, L, N, _p(ur), _p(dr), _p(zr), _p(np.ascontiguousarray(Ad[sl])),
+                                                _p(Bg), 0, L, 1, _p(Cg), 0, L, 1, _p(Dg), _p(bg),
+                                                int(bool(delta_softplus)), _p(out), _p(outz), _p(lst), 0, None)
             ys[i, sl] = outz if outz is not None else out
             last[i, sl] = lst
     return ys, last

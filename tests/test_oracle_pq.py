@@ -90,6 +90,18 @@ def test_pq_oracle_c_f64_matches_brute():
         np.testing.assert_allclose(r["last_state"].reshape(b, d, -1), np.array(ref_last), rtol=1e-10, atol=1e-12)
 
 
+def test_pq_all_rows_wrapper_matches_brute():
+    """cscan.scan_all_rows with P/Q (one call per (batch, group), B/C shared with a row stride of 0,
+    per-channel P/Q sliced by group) against the transition-matrix brute force."""
+    for per_dim, seed in ((False, 145), (True, 146)):
+        case = _pq_case(seed, dim=6, per_dim=per_dim, bkind="4d", ckind="4d", G=3)
+        ref_out, ref_outz, ref_last = _brute(case, "4d", "4d")
+        y, last = cscan.scan_all_rows(case["u"], case["delta"], case["A"], case["B"], case["C"], case["D"],
+                                      case["z"], case["delta_bias"], True, P=case["P"], Q=case["Q"])
+        np.testing.assert_allclose(y, np.array(ref_outz), rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(last, np.array(ref_last), rtol=1e-10, atol=1e-12)
+
+
 def test_pq_zero_coupling_is_the_diagonal_scan():
     case = _pq_case(150, dim=5, L=40, N=16, bkind="4d", ckind="4d", G=5)
     case["P"] = torch.zeros_like(case["P"])
