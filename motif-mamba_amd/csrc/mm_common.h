@@ -294,4 +294,17 @@ __device__ __forceinline__ void buffer_store_vec(__amdgpu_buffer_rsrc_t r, uint3
     }
 }
 
+// N floats stored as T through a buffer resource, in 16-byte pieces when they take more than 16.
+template <typename T, int N>
+__device__ __forceinline__ void buffer_store_vecn(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, const float *x) {
+    if constexpr (N * int(sizeof(T)) <= 16) {
+        buffer_store_vec<T, N>(r, voff, soff, x);
+    } else {
+        constexpr int H = 16 / int(sizeof(T));
+        static_assert(N % H == 0, "buffer_store_vecn splits into 16-byte pieces");
+#pragma unroll
+        for (int i = 0; i < N / H; ++i) buffer_store_vec<T, H>(r, voff + 16 * i, soff, x + H * i);
+    }
+}
+
 }  // namespace mm

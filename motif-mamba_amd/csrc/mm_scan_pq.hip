@@ -86,7 +86,11 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     constexpr int NP = S * LPR;            // padded states per channel
     constexpr int CPW = 64 / LPR;          // channels per wave
     constexpr int E = kT / LPR;            // prologue / epilogue steps per lane per tile
-    constexpr int BCS = 2 * NP + 4;        // sBC row stride (floats): NP B values, then NP C values
+    // sBC row stride (floats): NP B values, then NP C values. The staging writes, for one element
+    // position, lanes (state n = lane / 4, step block q = lane % 4) at q 8 BCS + n: with BCS = 2 NP + 2
+    // (S <= 2; the scan reads S-vectors of 8 bytes) 8 BCS = 16 mod 64, so the 64 lanes cover 64
+    // consecutive banks; S = 4 needs 16-byte aligned rows (2 NP + 4).
+    constexpr int BCS = S <= 2 ? 2 * NP + 2 : 2 * NP + 4;
     constexpr int HR = NP / 16;            // B/C half-rows (16 steps of one state) staged per lane
     static_assert(HR >= 1 && E >= 2 && E % 2 == 0 && 2 * CPW <= 64, "tile shape");
     __shared__ __align__(16) float sBC[kT * BCS];
@@ -109,8 +113,6 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     const int rank = int(p.pq_rank);
 
     const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
-    T *op = p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
-    T *ozp = p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
     const T *Bg = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
     const T *Cg = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
 
@@ -179,27 +181,40 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
         buffer_rsrc(p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + dw * p.z_d_stride : nullptr);
     const uint32_t fo_u = uint32_t(dl * p.u_d_stride) * SZ, fo_d = uint32_t(dl * p.delta_d_stride) * SZ;
     const uint32_t fo_z = uint32_t(dl * p.z_d_stride) * SZ;
+    // The outputs likewise (stores only from lanes of real channels, at existing steps).
+    const __amdgpu_buffer_rsrc_t rs_o =
+        buffer_rsrc(p.out ? reinterpret_cast<T *>(p.out) + b * p.out_batch_stride + dw * p.out_d_stride : nullptr);
+    const __amdgpu_buffer_rsrc_t rs_oz =
+        buffer_rsrc(p.out_z ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + dw * p.out_z_d_stride : nullptr);
+    const uint32_t fo_o = uint32_t(dl * p.out_d_stride + es) * SZ, fo_oz = uint32_t(dl * p.out_z_d_stride + es) * SZ;
 
-    // The B/C half-rows this lane stages: index hr = lane HR + i -> tensor hr / (2 NP) (0: B, 1: C),
-    // state (hr % 2NP) / 2, steps 16 (hr % 2) .. +15 of the tile.
-    const T *bcp[HR];
-    int bc_lds[HR], bc_half[HR];
-    bool bc_on[HR];
+    // B and C of the (batch, group) through buffer resources too. Per 32-step tile every lane stages
+    // NU = NP / 16 units of each tensor: unit u = lane + 64 i is the 8 steps 8 (u % 4) .. + 7 of
+    // state u / 4, one 8-element load from B and one from C (a 32-bit offset per lane, the tile
+    // start as a scalar offset). Units of padded states (u / 4 >= dstate) and, in a last partial
+    // tile, units past L (L is a multiple of 8: a unit is all in or all out) are zeroed once when
+    // loaded, so the staging below writes every unit unconditionally.
+    constexpr int NU = NP / 16;
+    const __amdgpu_buffer_rsrc_t rs_B = buffer_rsrc(Bg), rs_C = buffer_rsrc(Cg);
+    uint32_t fo_B[NU], fo_C[NU];
+    int u_lds[NU], u_q[NU];
+    bool u_on[NU];
 #pragma unroll
-    for (int i = 0; i < HR; ++i) {
-        const int hr = lane * HR + i;
-        const int tensor = hr / (2 * NP);
-        const int n = (hr % (2 * NP)) / 2;
-        bc_half[i] = hr % 2;
-        bc_on[i] = n < N;
+    for (int i = 0; i < NU; ++i) {
+        const int u = lane + 64 * i;
+        const int n = u / 4;
+        u_q[i] = u % 4;
+        u_on[i] = n < N;
         const int64_t nn = n < N ? n : 0;
-        bcp[i] = (tensor == 0 ? Bg + nn * p.B_dstate_stride : Cg + nn * p.C_dstate_stride) + 16 * bc_half[i];
-        bc_lds[i] = 16 * bc_half[i] * BCS + tensor * NP + n;
+        fo_B[i] = uint32_t(nn * p.B_dstate_stride) * SZ;
+        fo_C[i] = uint32_t(nn * p.C_dstate_stride) * SZ;
+        u_lds[i] = 8 * u_q[i] * BCS + n;
     }
+    const bool padded = N < NP;            // uniform
 
     // Loads at or past the end of a row are redirected into the row's last elements (always in
     // bounds: L is a multiple of 8); the steps they feed are padding with dt' = 0.
-    const int64_t lastE = L - E, last8 = L - 8;
+    const int64_t lastE = L - E;
     // Loads run D tiles ahead: rings of D entries (elements, B/C) whose registers stay fixed (the
     // tile loop is unrolled by D below; copying an entry whose loads are in flight would wait for
     // them). D = 2 where the second entry fits in registers (S <= 2); at S = 4 it would spill.
@@ -218,43 +233,47 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
         }
         e.u = buffer_load_rawn<T, E>(rs_u, fo_u + eo, so);
         e.d = buffer_load_rawn<T, E>(rs_d, fo_d + eo, so);
-        e.z = {};
         if (zp) e.z = buffer_load_rawn<T, E>(rs_z, fo_z + eo, so);
+        else e.z = {};
     };
     struct BCs {
-        RawVec<T, 8> v[HR][2];
+        RawVec<T, 8> b[NU], c[NU];
     };
     auto load_bc = [&](int64_t t0, BCs &r) {
-        const bool whole = t0 + kT <= L;   // uniform
+        if (t0 + kT <= L) {                // uniform: a whole tile
+            const uint32_t so = uint32_t(t0) * SZ;
 #pragma unroll
-        for (int i = 0; i < HR; ++i) {
+            for (int i = 0; i < NU; ++i) {
+                r.b[i] = buffer_load_rawn<T, 8>(rs_B, fo_B[i] + uint32_t(8 * u_q[i]) * SZ, so);
+                r.c[i] = buffer_load_rawn<T, 8>(rs_C, fo_C[i] + uint32_t(8 * u_q[i]) * SZ, so);
+            }
+        } else {                           // the last, partial tile
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                // whole tile: t0 (uniform) + a lane constant; else the row's clamped position
-                const int64_t t = t0 + 16 * bc_half[i] + 8 * h2;
-                const T *src = whole ? bcp[i] + t0 + 8 * h2 : bcp[i] - 16 * bc_half[i] + (t < last8 ? t : last8);
-                r.v[i][h2] = {};
-                if (bc_on[i]) r.v[i][h2] = load_raw<T, 8>(src);
+            for (int i = 0; i < NU; ++i) {
+                const int64_t st = t0 + 8 * u_q[i];
+                const uint32_t o = uint32_t(st < L ? st : L - 8) * SZ;
+                r.b[i] = buffer_load_rawn<T, 8>(rs_B, fo_B[i] + o, 0);
+                r.c[i] = buffer_load_rawn<T, 8>(rs_C, fo_C[i] + o, 0);
+                if (st >= L) r.b[i] = r.c[i] = {};
             }
         }
+        if (padded) {
+#pragma unroll
+            for (int i = 0; i < NU; ++i)
+                if (!u_on[i]) r.b[i] = r.c[i] = {};
+        }
     };
-    // Tile rows [step][B states | C states] as float32; states past dstate are 0 (their loads are
-    // skipped). Steps past L of the last tile are 0 as well, although their dt' = 0 makes B and C
-    // of those steps reach no state and no stored output.
-    auto stage_bc = [&](int64_t t0, const BCs &r) {
-        const bool whole = t0 + kT <= L;   // uniform
+    // Tile rows [step][B states | C states] as float32 (zeros for padded states and past L).
+    auto stage_bc = [&](const BCs &r) {
 #pragma unroll
-        for (int i = 0; i < HR; ++i) {
-            const int64_t first = t0 + 16 * bc_half[i];
+        for (int i = 0; i < NU; ++i) {
+            float vb[8], vc[8];
+            unpack_raw<T, 8>(r.b[i], vb);
+            unpack_raw<T, 8>(r.c[i], vc);
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                float v[8];
-                unpack_raw<T, 8>(r.v[i][h2], v);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int64_t t = first + 8 * h2 + e;
-                    sBC[bc_lds[i] + (8 * h2 + e) * BCS] = (whole || t < L) ? v[e] : 0.f;
-                }
+            for (int e = 0; e < 8; ++e) {
+                sBC[u_lds[i] + e * BCS] = vb[e];
+                sBC[u_lds[i] + e * BCS + NP] = vc[e];
             }
         }
     };
@@ -263,7 +282,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     load_elems(0, e0);
     if (D == 2) load_elems(kT, e1);
     load_bc(0, b0);
-    stage_bc(0, b0);
+    stage_bc(b0);
     if (D == 2) load_bc(kT, b1);
 
     // Tile t0: its elements in ec, its B/C (already staged) in bc, the next tile's B/C in bn (the
@@ -378,7 +397,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
 #pragma unroll
         for (int t = 0; t < kT; t += 4)
             *reinterpret_cast<float4 *>(&sY[(cw * LPR + k) * kPad + t]) = make_float4(yp[t], yp[t + 1], yp[t + 2], yp[t + 3]);
-        if (t1 < L) stage_bc(t1, bn);
+        if (t1 < L) stage_bc(bn);
         __syncthreads();
 
         // Epilogue: y of (channel, steps es .. es + E - 1) = the LPR partials, added in lane order.
@@ -399,11 +418,11 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             float o[E];
 #pragma unroll
             for (int i = 0; i < E; ++i) o[i] = p.D ? __builtin_fmaf(Dv, uu[i], y[i]) : y[i];
-            if (op) store_vec<T, E>(op + t0 + es, o);
+            if (p.out) buffer_store_vecn<T, E>(rs_o, fo_o, uint32_t(t0) * SZ, o);
             if (zp) {
 #pragma unroll
                 for (int i = 0; i < E; ++i) o[i] *= silu_fast(zz[i]);
-                store_vec<T, E>(ozp + t0 + es, o);
+                buffer_store_vecn<T, E>(rs_oz, fo_oz, uint32_t(t0) * SZ, o);
             }
         }
         if (active && p.chunk_states) {
@@ -538,12 +557,14 @@ scan_fwd_pq_rowlane(const mm_scan_fwd_params p, const int64_t ratio) {
 // ------------------------------------------------------------------------------------------------
 struct TiledShape { int S, LPR; };
 
-// The tiled kernel loads u, delta and z with 32-bit byte offsets from the first of a wave's channel
-// rows (up to 16): every offset of those rows must fit.
+// The tiled kernel addresses u, delta, z, out and out_z with 32-bit byte offsets from the first of a
+// wave's channel rows (up to 16), and B / C from the (batch, group) base: every offset must fit.
 static bool offsets_ok(const mm_scan_fwd_params &p) {
     const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
-    const int64_t ch = 15 * std::max({p.u_d_stride, p.delta_d_stride, p.z ? p.z_d_stride : int64_t(0)});
-    return (ch + p.seqlen) * eb < (int64_t(1) << 32);
+    const int64_t ch = 15 * std::max({p.u_d_stride, p.delta_d_stride, p.z ? p.z_d_stride : int64_t(0),
+                                      p.out ? p.out_d_stride : int64_t(0), p.out_z ? p.out_z_d_stride : int64_t(0)});
+    const int64_t bc = (p.dstate - 1) * std::max(p.B_dstate_stride, p.C_dstate_stride);
+    return (std::max(ch, bc) + p.seqlen) * eb < (int64_t(1) << 32);
 }
 
 // The (S, LPR) of the tiled kernel for this request, or {0, 0} when the request needs the general
