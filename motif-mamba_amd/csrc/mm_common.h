@@ -307,4 +307,53 @@ __device__ __forceinline__ void buffer_store_vecn(__amdgpu_buffer_rsrc_t r, uint
     }
 }
 
+// ---- Sums over the LPR consecutive lanes of a group (a channel's lanes) with DPP ----
+
+// x + x[lane permuted by CTRL] as one v_add_f32 with a DPP operand (the compiler inserts the DPP
+// read hazard wait states itself for the builtin).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false);
+    return x + __builtin_bit_cast(float, o);
+}
+
+// x of the lane CTRL pairs this lane with.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the LPR consecutive lanes of a group. Every step pairs two partial sums and adds them
+// in both lanes (a + b == b + a exactly), so all LPR lanes hold bit-identical totals.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(LPR == 4 || LPR == 8 || LPR == 16, "LPR");
+    x = dpp_add<0xB1>(x);                           // quad_perm [1,0,3,2]
+    x = dpp_add<0x4E>(x);                           // quad_perm [2,3,0,1]
+    if constexpr (LPR >= 8) x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of 8 lanes
+    if constexpr (LPR >= 16) x = dpp_add<0x140>(x); // row_mirror: the other half of the 16-lane row
+    return x;
+}
+
+// The DPP control that pairs each lane of a group of LPR lanes with one in the other half of the
+// group: quad_perm [3,2,1,0], row_half_mirror, row_mirror.
+template <int LPR>
+constexpr int kHalfSwap = LPR == 4 ? 0x1B : (LPR == 8 ? 0x141 : 0x140);
+
+// Two sums over the LPR lanes of a group at once. Lanes of the first half hold, as `keep`, their
+// partial of sum 0 and, as `send`, their partial of sum 1; lanes of the second half the other way
+// round. The first stage adds each lane's `keep` to the `send` of its partner in the other half, so
+// that each half then carries one sum and completes it over its LPR / 2 lanes with the symmetric
+// stages of group_sum (every lane of a half ends with bit-identical totals); the partner's total
+// is the other sum. log2(LPR) + 1 DPP operations for the pair instead of 2 log2(LPR).
+template <int LPR>
+__device__ __forceinline__ void pair_sum2(float keep, float send, float &mine, float &other) {
+    float x = keep + dpp_mov<kHalfSwap<LPR>>(send);
+    x = dpp_add<0xB1>(x);                           // quad_perm [1,0,3,2]
+    if constexpr (LPR >= 8) x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
+    if constexpr (LPR >= 16) x = dpp_add<0x141>(x); // row_half_mirror: the other quad of the half
+    mine = x;
+    other = dpp_mov<kHalfSwap<LPR>>(x);
+}
+
 }  // namespace mm

@@ -15,7 +15,9 @@
 //       consecutive lanes of a channel hold S states each (S * LPR >= dstate, padded with states
 //       whose A, P, Q, B and C are zero, which stay zero). Per step each lane forms its partial
 //       Q h over its S states, a DPP butterfly inside the LPR lanes sums the partials (every lane
-//       ends with the same bits), and the lane updates its S states with P (dt' q) + dt' u B.
+//       ends with the same bits; at rank 2 one butterfly serves both sums: each half of the lanes
+//       completes one of them and takes the other from its partner), and the lane updates its S
+//       states with P (dt' q) + dt' u B.
 //       The lane's rows of P and Q live in registers for the whole sequence. (16-bit inputs with
 //       16 lanes of one state and rank <= 2 carry the butterfly's total from step to step and form
 //       the next partial as Q (a h + dt' u B) + (Q P) q, which shortens the dependent chain.)
@@ -45,26 +47,6 @@ namespace pq {
 constexpr int kT = 32;      // sequence steps per tile
 constexpr int kPad = 36;    // LDS row stride (floats) of per-channel step rows: 16-B aligned, spreads banks
 constexpr int kMaxRank = 8; // selective_scan.cpp:359
-
-// x + x[lane permuted by CTRL] as one v_add_f32 with a DPP operand (the compiler inserts the DPP
-// read hazard wait states itself for the builtin).
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float x) {
-    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false);
-    return x + __builtin_bit_cast(float, o);
-}
-
-// Sum over the LPR consecutive lanes of a channel. Every step pairs two partial sums and adds them
-// in both lanes (a + b == b + a exactly), so all LPR lanes hold bit-identical totals.
-template <int LPR>
-__device__ __forceinline__ float group_sum(float x) {
-    static_assert(LPR == 4 || LPR == 8 || LPR == 16, "LPR");
-    x = dpp_add<0xB1>(x);                         // quad_perm [1,0,3,2]
-    x = dpp_add<0x4E>(x);                         // quad_perm [2,3,0,1]
-    if constexpr (LPR >= 8) x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of 8 lanes
-    if constexpr (LPR >= 16) x = dpp_add<0x140>(x); // row_mirror: the other half of the 16-lane row
-    return x;
-}
 
 // S consecutive floats of LDS (16-B, 8-B or 4-B aligned by construction).
 template <int S>
@@ -152,6 +134,18 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], Pr[s][r2], acc);
             Kr[r][r2] = acc;
         }
+    }
+    // Rank 2, direct form: the lane's rows of Q and P in the order pair_sum2 takes them (sum 0 kept
+    // by the first LPR / 2 lanes of a channel, sum 1 by the others).
+    constexpr bool PS2 = R == 2 && !XK;
+    const bool upper = k >= LPR / 2;
+    float Qk[S], Qs[S], Pm[S], Po[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        Qk[s] = Qr[upper ? 1 : 0][s];
+        Qs[s] = Qr[upper ? 0 : 1][s];
+        Pm[s] = Pr[s][upper ? 1 : 0];
+        Po[s] = Pr[s][upper ? 0 : 1];
     }
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
@@ -370,6 +364,23 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
 #pragma unroll
                         for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
                         h[s] = w;
+                        y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
+                    }
+                } else if constexpr (PS2) {
+                    float ak = Qk[0] * h[0], as = Qs[0] * h[0];
+#pragma unroll
+                    for (int s = 1; s < S; ++s) {
+                        ak = __builtin_fmaf(Qk[s], h[s], ak);
+                        as = __builtin_fmaf(Qs[s], h[s], as);
+                    }
+                    float qm, qo;
+                    pair_sum2<LPR>(ak, as, qm, qo);
+                    qm *= dts[j];
+                    qo *= dts[j];
+#pragma unroll
+                    for (int s = 0; s < S; ++s) {
+                        const float w = __builtin_fmaf(Po[s], qo, __builtin_fmaf(Pm[s], qm, bu[j][s]));
+                        h[s] = __builtin_fmaf(av[j][s], h[s], w);
                         y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
                     }
                 } else {

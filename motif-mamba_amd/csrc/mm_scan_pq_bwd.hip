@@ -47,24 +47,6 @@ constexpr int kBCS = 36;         // sBC row stride (floats): B 16 | C 16 | pad 4
 constexpr int kRow = 20;         // sRed row stride (floats): 16 channels + 4
 constexpr int kRed = 2 * kH * 16 * kRow;   // sRed floats: [tensor][step of the half][state][channel]
 
-// x + x[lane permuted by CTRL] as one v_add_f32 with a DPP operand.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float x) {
-    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false);
-    return x + __builtin_bit_cast(float, o);
-}
-
-// Sum over the LPR consecutive lanes of a channel; every lane ends with the same bits (each step
-// adds the same two partial sums in both lanes of a pair).
-template <int LPR>
-__device__ __forceinline__ float group_sum(float x) {
-    static_assert(LPR == 4 || LPR == 8, "LPR");
-    x = dpp_add<0xB1>(x);                           // quad_perm [1,0,3,2]
-    x = dpp_add<0x4E>(x);                           // quad_perm [2,3,0,1]
-    if constexpr (LPR >= 8) x = dpp_add<0x141>(x);  // row_half_mirror: the other quad of 8 lanes
-    return x;
-}
-
 template <typename T, int S, int R>
 __global__ void __launch_bounds__(16 * (16 / S)) __attribute__((amdgpu_waves_per_eu(2)))
 scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, float *const partB,
@@ -119,6 +101,29 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
             Qr[r][s] = use ? p.Q[d * p.Q_d_stride + r * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
         }
     }
+    // Rank 2: the lane's rows of Q and P in the order pair_sum2 takes them (sum 0 kept by the first
+    // LPR / 2 lanes of a channel, sum 1 by the others), for Q h and P^T lam. The forward's 8-lane
+    // layout forms Q h the same way, so pass 1 reproduces its tile states bit for bit.
+    constexpr bool PS2 = R == 2;
+    const bool upper = k >= LPR / 2;
+    float Qk[S], Qs[S], Pm[S], Po[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        Qk[s] = Qr[upper ? 1 : 0][s];
+        Qs[s] = Qr[upper ? 0 : 1][s];
+        Pm[s] = Pr[s][upper ? 1 : 0];
+        Po[s] = Pr[s][upper ? 0 : 1];
+    }
+    // Q h over the channel's states for both ranks: qm is sum `upper` (1 or 0), qo the other.
+    auto qh2 = [&](const float *h, float &qm, float &qo) {
+        float ak = Qk[0] * h[0], as = Qs[0] * h[0];
+#pragma unroll
+        for (int s = 1; s < S; ++s) {
+            ak = __builtin_fmaf(Qk[s], h[s], ak);
+            as = __builtin_fmaf(Qs[s], h[s], as);
+        }
+        pair_sum2<LPR>(ak, as, qm, qo);
+    };
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
     // Checkpoints [tile][batch][dim][16] (states past dstate stay 0).
@@ -229,20 +234,32 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll
             for (int t = 0; t < kT; ++t) {
                 const float4 x = sX[cw * kXS + t];
-                float q[R];
+                if constexpr (PS2) {
+                    float qm, qo;
+                    qh2(h, qm, qo);
+                    qm *= x.x;
+                    qo *= x.x;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float acc = Qr[r][0] * h[0];
+                    for (int s = 0; s < S; ++s) {
+                        const float w = __builtin_fmaf(Po[s], qo, __builtin_fmaf(Pm[s], qm, x.y * sBC[t * kBCS + k * S + s]));
+                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
+                    }
+                } else {
+                    float q[R];
 #pragma unroll
-                    for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
-                    q[r] = group_sum<LPR>(acc) * x.x;
-                }
+                    for (int r = 0; r < R; ++r) {
+                        float acc = Qr[r][0] * h[0];
 #pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    float w = x.y * sBC[t * kBCS + k * S + s];
+                        for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
+                        q[r] = group_sum<LPR>(acc) * x.x;
+                    }
 #pragma unroll
-                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                    h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
+                    for (int s = 0; s < S; ++s) {
+                        float w = x.y * sBC[t * kBCS + k * S + s];
+#pragma unroll
+                        for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
+                    }
                 }
             }
             __syncthreads();
@@ -279,24 +296,40 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll 2
             for (int t = 0; t < kT; ++t) {
                 const float4 x = sX[cw * kXS + t];
-                float q[R], qw = 0.f;
+                if constexpr (PS2) {
+                    float qm, qo;
+                    qh2(h, qm, qo);
+                    // (Q h_{t-1})_k for k < 2 (lanes 0 and 1 are in the first half: sum k is
+                    // qm for lane 0, qo for lane 1), read by the whole channel.
+                    if (k < 2) sQ[(t * 16 + cw) * R + k] = k == 0 ? qm : qo;
+                    qm *= x.x;
+                    qo *= x.x;
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float acc = Qr[r][0] * h[0];
+                    for (int s = 0; s < S; ++s) {
+                        const float w = __builtin_fmaf(Po[s], qo, __builtin_fmaf(Pm[s], qm, x.y * sBC[t * kBCS + k * S + s]));
+                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
+                        sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
+                    }
+                } else {
+                    float q[R], qw = 0.f;
 #pragma unroll
-                    for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
-                    q[r] = group_sum<LPR>(acc);
-                    if (k == r) qw = q[r];
-                    q[r] *= x.x;
-                }
-                if (k < R) sQ[(t * 16 + cw) * R + k] = qw;     // (Q h_{t-1})_k, read by the whole channel
+                    for (int r = 0; r < R; ++r) {
+                        float acc = Qr[r][0] * h[0];
 #pragma unroll
-                for (int s = 0; s < S; ++s) {
-                    float w = x.y * sBC[t * kBCS + k * S + s];
+                        for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
+                        q[r] = group_sum<LPR>(acc);
+                        if (k == r) qw = q[r];
+                        q[r] *= x.x;
+                    }
+                    if (k < R) sQ[(t * 16 + cw) * R + k] = qw;     // (Q h_{t-1})_k, read by the whole channel
 #pragma unroll
-                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                    h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
-                    sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
+                    for (int s = 0; s < S; ++s) {
+                        float w = x.y * sBC[t * kBCS + k * S + s];
+#pragma unroll
+                        for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
+                        sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
+                    }
                 }
             }
         }
@@ -318,14 +351,27 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                 lam[s] = __builtin_fmaf(Cv[s], x.w, carry[s]);
                 hp[s] = t > 0 ? sHS[((t - 1) * 16 + cw) * 16 + k * S + s] : hck[s];   // h_{t-1}
             }
+            // (P^T lam_t)_r; at rank 2 in the lane's own order: sv[0] is rank `upper`, sv[1] the
+            // other (dQ[0] / dQ[1] follow the same order and are put back at the end).
             float q[R], sv[R];
+            if constexpr (PS2) {
+                float am = Pm[0] * lam[0], ao = Po[0] * lam[0];
+#pragma unroll
+                for (int s = 1; s < S; ++s) {
+                    am = __builtin_fmaf(Pm[s], lam[s], am);
+                    ao = __builtin_fmaf(Po[s], lam[s], ao);
+                }
+                pair_sum2<LPR>(am, ao, sv[0], sv[1]);
+            }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                float as = Pr[0][r] * lam[0];
-#pragma unroll
-                for (int s = 1; s < S; ++s) as = __builtin_fmaf(Pr[s][r], lam[s], as);
                 q[r] = sQ[(t * 16 + cw) * R + r];   // (Q h_{t-1})_r
-                sv[r] = group_sum<LPR>(as);         // (P^T lam_t)_r
+                if constexpr (!PS2) {
+                    float as = Pr[0][r] * lam[0];
+#pragma unroll
+                    for (int s = 1; s < S; ++s) as = __builtin_fmaf(Pr[s][r], lam[s], as);
+                    sv[r] = group_sum<LPR>(as);
+                }
             }
             float pdd = 0.f, pgb = 0.f;
 #pragma unroll
@@ -336,7 +382,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     pq = __builtin_fmaf(Pr[s][r], q[r], pq);
-                    qs = __builtin_fmaf(Qr[r][s], sv[r], qs);
+                    qs = __builtin_fmaf(PS2 ? (r == 0 ? Qk[s] : Qs[s]) : Qr[r][s], sv[r], qs);
                 }
                 // dt' term: A a h_{t-1} + P q + u B
                 pdd = __builtin_fmaf(lam[s], __builtin_fmaf(An[s], ah, __builtin_fmaf(x.z, Bv[s], pq)), pdd);
@@ -396,6 +442,15 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                 dD_acc = __builtin_fmaf(e_g[i], e_u[i], dD_acc);
                 dbias_acc += ddl;
             }
+        }
+    }
+    if constexpr (PS2) {
+        // dQ[0] accumulated rank `upper`: back to rank order.
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const float a = dQ[0][s], c = dQ[1][s];
+            dQ[0][s] = upper ? c : a;
+            dQ[1][s] = upper ? a : c;
         }
     }
     const bool shared_pq = p.dP_d_stride == 0 && p.dQ_d_stride == 0;
