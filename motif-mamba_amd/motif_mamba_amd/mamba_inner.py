@@ -29,11 +29,16 @@ recomputes both in the backward; ``0`` keeps them, and with dstate 16 also the s
 states, so that the scan backward need not recompute them (``MM_TILE_STATES=0`` turns that off). Autocast: the projection weights are cast to
 the autocast dtype as the reference does (ssi.py:469-474).
 
-Not provided (raise, as for the other parts of this build): the backward when RMSNorm weights are
-given (the reference's backward does not differentiate through its RMSNorms, and at
-checkpoint_lvl=1 normalises the saved, already normalised B and C a second time, ssi.py:582-593,
-so its gradients are not those of its forward -- no reference caller passes these weights,
-mamba_simplemotif.py:272-285); complex A.
+RMSNorm weights (b_rms_weight, c_rms_weight, dt_rms_weight) as the reference: the forward
+normalises B and C over dstate (projected or given; a given B/C must then be (batch, 1, dstate,
+seqlen)) and delta over channels (ssi.py:515-529). The backward is the reference's, which is not the
+gradient of its forward (ssi.py:571-645): dB, dC and ddelta pass the norms unchanged (no norm
+backward; the norm weights get no gradient), and at checkpoint_lvl=1 the saved B and C, already
+normalised, are normalised a second time before the scan backward (ssi.py:582-593) while delta is
+recomputed and normalised once. No reference caller passes these weights
+(mamba_simplemotif.py:272-285).
+
+Not provided (raises, as in the other parts of this build): complex A.
 """
 from __future__ import annotations
 
@@ -76,6 +81,14 @@ def _delta(delta_proj_weight, x_dbl, delta_rank, batch, dt_rms_weight, eps):
     if dt_rms_weight is not None:
         delta = _rms(delta, dt_rms_weight, eps)
     return delta
+
+
+def _rms_bc(t, weight, eps, name):
+    """RMSNorm over dstate of a (batch, 1, dstate, seqlen) B or C (ssi.py:515-524 reshapes it to
+    ((b l), dstate), which needs that form)."""
+    if t.dim() != 4 or t.shape[1] != 1:
+        raise ValueError(f"{name} must have shape (batch, 1, dstate, seqlen) to be RMS-normalised")
+    return _rms(t[:, 0], weight, eps).unsqueeze(1)
 
 
 def _state_input(x_dbl, rows, bias, batch, rms_weight, eps):
@@ -128,13 +141,19 @@ class MambaInnerFn(torch.autograd.Function):
         if B is None:
             B = _state_input(x_dbl, slice(delta_rank, delta_rank + d_state), B_proj_bias, batch, b_rms_weight,
                              b_c_dt_rms_eps)
-        elif B.stride(-1) != 1:
-            B = B.contiguous()
+        else:
+            if B.stride(-1) != 1:
+                B = B.contiguous()
+            if b_rms_weight is not None:
+                B = _rms_bc(B, b_rms_weight, b_c_dt_rms_eps, "B")
         if C is None:
             C = _state_input(x_dbl, slice(x_dbl.shape[0] - d_state, None), C_proj_bias, batch, c_rms_weight,
                              b_c_dt_rms_eps)
-        elif C.stride(-1) != 1:
-            C = C.contiguous()
+        else:
+            if C.stride(-1) != 1:
+                C = C.contiguous()
+            if c_rms_weight is not None:
+                C = _rms_bc(C, c_rms_weight, b_c_dt_rms_eps, "C")
         if D is not None:
             D = D.contiguous()
         if not grad_enabled or not any(ctx.needs_input_grad):
@@ -152,7 +171,8 @@ class MambaInnerFn(torch.autograd.Function):
         ctx.delta_softplus = delta_softplus
         ctx.out_proj_bias_is_None = out_proj_bias is None
         ctx.checkpoint_lvl = checkpoint_lvl
-        ctx.has_rms = any(w is not None for w in (b_rms_weight, c_rms_weight, dt_rms_weight))
+        ctx.b_rms_weight = b_rms_weight
+        ctx.c_rms_weight = c_rms_weight
         ctx.dt_rms_weight = dt_rms_weight
         ctx.b_c_dt_rms_eps = b_c_dt_rms_eps
         if checkpoint_lvl >= 1:
@@ -165,20 +185,25 @@ class MambaInnerFn(torch.autograd.Function):
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, dout):
-        """Gradients of every tensor input (ssi.py:555-645); dout: (batch, seqlen, d_model)."""
-        if ctx.has_rms:
-            raise NotImplementedError(
-                "MambaInnerFn backward with b/c/dt RMSNorm weights is not part of the MI355X build "
-                "(the reference's backward does not differentiate through these norms)")
+        """Gradients of every tensor input as the reference returns them (ssi.py:555-645); dout:
+        (batch, seqlen, d_model). With RMSNorm weights these are the reference's, not the gradient of
+        the forward: the norms are passed unchanged and, at checkpoint_lvl=1, B and C normalised twice."""
         (xz, conv1d_weight, conv1d_bias, x_dbl, x_proj_weight, delta_proj_weight, out_proj_weight, conv1d_out,
          delta, A, B, C, D, delta_bias, scan_states, out, ck) = ctx.saved_tensors
         batch, L = xz.shape[0], xz.shape[-1]
         delta_rank = delta_proj_weight.shape[1]
         d_state = A.shape[-1]
         x, z = xz.chunk(2, dim=1)
+        eps = ctx.b_c_dt_rms_eps
         if ctx.checkpoint_lvl == 1:
             conv1d_out = _conv(x, conv1d_weight, conv1d_bias)
-            delta = _delta(delta_proj_weight, x_dbl, delta_rank, batch, None, ctx.b_c_dt_rms_eps)
+            delta = _delta(delta_proj_weight, x_dbl, delta_rank, batch, ctx.dt_rms_weight, eps)
+            # The saved B and C are the normalised ones; the reference normalises them again here
+            # (ssi.py:582-593), so its scan backward runs at RMSNorm(RMSNorm(.)).
+            if ctx.b_rms_weight is not None:
+                B = _rms_bc(B, ctx.b_rms_weight, eps, "B")
+            if ctx.c_rms_weight is not None:
+                C = _rms_bc(C, ctx.c_rms_weight, eps, "C")
         dout2 = dout.reshape(batch * L, dout.shape[-1])                   # (batch * L, d_model)
         dxz = torch.empty_like(xz)
         dx, dz = dxz.chunk(2, dim=1)

@@ -22,9 +22,12 @@ equivalent); with gradients required, the forward saves the reference's tensors 
 C, D, [z], delta_bias, x, [out]); without, it writes only what it returns.
 
 ``SelectiveScanPQFn.backward`` returns the exact gradients of the coupled recurrence (dP and dQ
-included), which is what the reference returns in its default gradient mode: its dense CUDA
-backward (z-less calls) and autograd through its torch loop (calls with z, and dP/dQ always) both
-differentiate the same function. The gfx950 kernel covers pq_rank 1..8, dstate <= 16, dim and
+included), which is what the reference returns in both of its gradient modes
+(``MOTIFMAMBA_PQ_GRAD_MODE``, ssi.py:157-158): its dense CUDA backward (z-less calls) and autograd
+through its torch loop (calls with z) differentiate the same function; "exact" takes dP/dQ of
+z-less calls from that autograd, any other value ("fused") from the dense kernel, the only backward
+its launcher runs with P/Q (selective_scan_bwd_kernel.cuh:928-932), which accumulates the same
+chain rule (:307, :334). The variable is therefore not read here. The gfx950 kernel covers pq_rank 1..8, dstate <= 16, dim and
 dim / n_groups multiples of 16 and seqlen a multiple of 8, with variable B and C; other P/Q
 shapes raise NotImplementedError in the backward.
 

@@ -33,7 +33,7 @@ import math
 import torch
 
 from .conv_ref import causal_conv1d_ref
-from .ssm_ref import selective_scan_ref
+from .ssm_ref import selective_scan_bwd_ref, selective_scan_ref
 
 
 def rms_norm_ref(x, weight, eps=1e-6, dim=-1, compute_dtype=torch.float32):
@@ -147,3 +147,97 @@ def mamba_inner_brute(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_
     opb = t(out_proj_bias)
     return [[[sum(OW[e][c] * out_z[b][c][l] for c in range(d)) + (opb[e] if opb else 0.0)
               for e in range(len(OW))] for l in range(L)] for b in range(batch)]
+
+
+def mamba_inner_bwd_ref(xz, conv1d_weight, conv1d_bias, x_proj_weight, delta_proj_weight, out_proj_weight,
+                        out_proj_bias, A, dout, B=None, C=None, D=None, delta_bias=None, B_proj_bias=None,
+                        C_proj_bias=None, delta_softplus=True, checkpoint_lvl=1, b_rms_weight=None,
+                        c_rms_weight=None, dt_rms_weight=None, b_c_dt_rms_eps=1e-6, compute_dtype=torch.float32):
+    """The gradients ``MambaInnerFn.backward`` returns (ssi.py:555-645), step by step, in
+    ``compute_dtype`` without intermediate rounding. Returns a dict keyed by the input names (xz,
+    conv1d_weight, ..., C_proj_bias; None where the reference returns None).
+
+    The steps: the forward's quantities (ssi.py:482-553); dout_y = out_proj_weight^T dout; the scan
+    backward (selective_scan_bwd_ref) at the point the reference evaluates it -- the forward's
+    delta, B and C, except that at checkpoint_lvl 1 the saved B and C, already RMS-normalised, are
+    normalised again (ssi.py:582-593); dz from the forward's pre-gate output (the kernel reads the
+    saved ``out``); dB, dC into the x_dbl rows and ddelta into the delta projection unchanged, i.e.
+    without a backward through the RMSNorms, whose weights get no gradient (ssi.py:598-645); then the
+    x_proj products and the conv1d backward. Without RMSNorm weights this is the gradient of
+    ``mamba_inner_ref`` at either checkpoint level (tests/test_oracle_inner.py checks that against
+    autograd)."""
+    cd = compute_dtype
+    f = lambda t: None if t is None else t.detach().to(cd)          # noqa: E731
+    xz, A, D, delta_bias, dout = f(xz), f(A), f(D), f(delta_bias), f(dout)
+    Wc, bc, Wx, Wd, Wo = f(conv1d_weight), f(conv1d_bias), f(x_proj_weight), f(delta_proj_weight), f(out_proj_weight)
+    batch, two_d, L = xz.shape
+    d_inner = two_d // 2
+    R, N = Wd.shape[1], A.shape[-1]
+    eps = b_c_dt_rms_eps
+    x, z = xz.chunk(2, dim=1)
+    x = x.clone().requires_grad_(True)
+    Wc = Wc.clone().requires_grad_(True)
+    if bc is not None:
+        bc = bc.clone().requires_grad_(True)
+    conv_out = causal_conv1d_ref(x, Wc.reshape(d_inner, -1), bc, activation="silu", compute_dtype=cd)
+    u = conv_out.detach()
+    x_dbl = u.transpose(1, 2).reshape(batch * L, d_inner) @ Wx.t()                   # (b l, R + 2N)
+    delta = (Wd @ x_dbl[:, :R].t()).reshape(d_inner, batch, L).permute(1, 0, 2)      # (b, d, l)
+
+    def bc_in(given, cols, bias):
+        if given is not None:
+            return f(given)
+        v = x_dbl[:, cols]
+        if bias is not None:
+            v = v + f(bias)
+        return v.reshape(batch, L, N).permute(0, 2, 1).unsqueeze(1)                   # (b, 1, N, l)
+
+    norm = lambda t, w, dim: rms_norm_ref(t, w, eps, dim=dim, compute_dtype=cd)     # noqa: E731
+    Bs = bc_in(B, slice(R, R + N), B_proj_bias)
+    Cs = bc_in(C, slice(x_dbl.shape[1] - N, None), C_proj_bias)
+    if b_rms_weight is not None:
+        Bs = norm(Bs, b_rms_weight, 2)
+    if c_rms_weight is not None:
+        Cs = norm(Cs, c_rms_weight, 2)
+    if dt_rms_weight is not None:
+        delta = norm(delta, dt_rms_weight, 1)
+    sq = lambda t: t[:, 0] if t.dim() == 4 else t                                    # noqa: E731
+    out = selective_scan_ref(u, delta, A, sq(Bs), sq(Cs), D, None, delta_bias, delta_softplus, compute_dtype=cd)
+    out_z = out * torch.nn.functional.silu(z)
+    # The point of the scan backward.
+    Bb, Cb = Bs, Cs
+    if checkpoint_lvl == 1:
+        if b_rms_weight is not None:
+            Bb = norm(Bb, b_rms_weight, 2)
+        if c_rms_weight is not None:
+            Cb = norm(Cb, c_rms_weight, 2)
+    dout2 = dout.reshape(batch * L, -1)                                               # (b l, e)
+    dout_y = (dout2 @ Wo).reshape(batch, L, d_inner).permute(0, 2, 1)                  # (b, d, l)
+    sg = torch.sigmoid(z)
+    g = dout_y * sg * z                                                               # the pre-gate cotangent
+    sb = selective_scan_bwd_ref(u, delta, A, sq(Bb), sq(Cb), g, D, None, delta_bias, delta_softplus, dtype=cd)
+    dz = dout_y * out * sg * (1 + z * (1 - sg))
+    res = {"out_proj_weight": dout2.t() @ out_z.permute(0, 2, 1).reshape(batch * L, d_inner),
+           "out_proj_bias": dout2.sum(dim=0) if out_proj_bias is not None else None,
+           "A": sb["dA"], "D": sb["dD"] if D is not None else None,
+           "delta_bias": sb["ddelta_bias"] if delta_bias is not None else None,
+           "B": None, "C": None, "B_proj_bias": None, "C_proj_bias": None}
+    dx_dbl = torch.zeros_like(x_dbl)
+    for name, given, cols, grad, bias in (("B", B, slice(R, R + N), sb["dB"], B_proj_bias),
+                                           ("C", C, slice(x_dbl.shape[1] - N, None), sb["dC"], C_proj_bias)):
+        if given is None:
+            gr = grad.permute(0, 2, 1).reshape(batch * L, N)                          # (b, N, l) -> (b l, N)
+            dx_dbl[:, cols] = gr
+            res[name + "_proj_bias"] = gr.sum(dim=0) if bias is not None else None
+        else:
+            res[name] = grad.reshape(given.shape)
+    dd = sb["ddelta"].permute(1, 0, 2).reshape(d_inner, batch * L)                    # (d, b l)
+    res["delta_proj_weight"] = dd @ x_dbl[:, :R]
+    dx_dbl[:, :R] = dd.t() @ Wd
+    res["x_proj_weight"] = dx_dbl.t() @ u.transpose(1, 2).reshape(batch * L, d_inner)
+    dconv = sb["du"] + (Wx.t() @ dx_dbl.t()).reshape(d_inner, batch, L).permute(1, 0, 2)
+    conv_out.backward(dconv)
+    res["xz"] = torch.cat([x.grad, dz], dim=1)
+    res["conv1d_weight"] = Wc.grad
+    res["conv1d_bias"] = bc.grad if bc is not None else None
+    return res

@@ -186,12 +186,16 @@ def test_given_B_C():
             _check(gg[k], v, torch.float32, f"d{k}")
 
 
-def test_rms_norm_forward_and_backward_refusal():
-    _say("mamba_inner rms weights")
+def _rms_weights(seed, d_state=16, d_inner=64):
+    g = torch.Generator().manual_seed(seed)
+    return dict(b_rms_weight=torch.rand(d_state, generator=g) + 0.5, c_rms_weight=torch.rand(d_state, generator=g) + 0.5,
+                dt_rms_weight=torch.rand(d_inner, generator=g) + 0.5)
+
+
+def test_rms_norm_forward():
+    _say("mamba_inner rms weights forward")
     c = _case(950, L=64, dtype=torch.bfloat16)
-    g = torch.Generator().manual_seed(951)
-    rw = dict(b_rms_weight=torch.rand(16, generator=g) + 0.5, c_rms_weight=torch.rand(16, generator=g) + 0.5,
-              dt_rms_weight=torch.rand(64, generator=g) + 0.5)
+    rw = _rms_weights(951)
     got, _ = _run(c, **{k: v.to(DEV) for k, v in rw.items()})
     want, _ = _oracle(c, **rw)
     _check(got, want, torch.bfloat16, "out")
@@ -199,8 +203,40 @@ def test_rms_norm_forward_and_backward_refusal():
         got1, _ = _run(c, **{only: rw[only].to(DEV)})
         want1, _ = _oracle(c, **{only: rw[only]})
         _check(got1, want1, torch.bfloat16, f"out {only}")
-    with pytest.raises(NotImplementedError):
-        _run(c, _dout(952, c), b_rms_weight=rw["b_rms_weight"].to(DEV))
+    # A given (batch, 1, dstate, seqlen) B and C are normalised too (ssi.py:515-524).
+    g = torch.Generator().manual_seed(953)
+    cg = dict(c, B=torch.randn(2, 1, 16, 64, generator=g).to(torch.bfloat16),
+              C=torch.randn(2, 1, 16, 64, generator=g).to(torch.bfloat16))
+    kw = {k: rw[k] for k in ("b_rms_weight", "c_rms_weight")}
+    got2, _ = _run(cg, **{k: v.to(DEV) for k, v in kw.items()})
+    want2, _ = _oracle(cg, **kw)
+    _check(got2, want2, torch.bfloat16, "out given B/C")
+    cc = dict(c, C=torch.randn(64, 16, generator=g))                  # a constant C cannot be normalised
+    with pytest.raises(ValueError, match="RMS"):
+        _run(cc, c_rms_weight=rw["c_rms_weight"].to(DEV))
+
+
+@pytest.mark.parametrize("lvl", [0, 1])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rms_norm_backward(lvl, dtype):
+    """The reference's backward with RMSNorm weights (ssi.py:571-645): the norms passed unchanged and,
+    at checkpoint_lvl 1, B and C normalised a second time -- against its step-by-step restatement
+    (oracle.inner_ref.mamba_inner_bwd_ref, pinned in tests/test_oracle_inner.py)."""
+    from oracle.inner_ref import mamba_inner_bwd_ref
+    _say(f"mamba_inner rms weights backward lvl {lvl} {dtype}")
+    c = _case(960 + lvl, L=64, dtype=dtype, bc_bias=True)
+    rw = _rms_weights(962)
+    dout = _dout(963, c)
+    _, gg = _run(c, dout, checkpoint_lvl=lvl, **{k: v.to(DEV) for k, v in rw.items()})
+    eg = mamba_inner_bwd_ref(*[c[k] for k in ARGS[:8]], dout, B=c["B"], C=c["C"], D=c["D"],
+                             delta_bias=c["delta_bias"], B_proj_bias=c["B_proj_bias"], C_proj_bias=c["C_proj_bias"],
+                             checkpoint_lvl=lvl, **rw)
+    for k in ARGS:
+        if eg[k] is None:
+            assert gg.get(k) is None, k
+            continue
+        assert gg[k].dtype == c[k].dtype, f"{k}: grad dtype {gg[k].dtype}"
+        _check(gg[k], eg[k], dtype, f"d{k}")
 
 
 def test_rms_norm_kernel_layouts():

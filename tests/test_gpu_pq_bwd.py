@@ -80,6 +80,19 @@ def _vs_exact(case, dout, dtype, what):
         _check(gr, exact["d" + n], dtype, f"{what} d{n}")
 
 
+@pytest.mark.parametrize("mode", ["exact", "fused"])
+def test_pq_bwd_grad_modes(mode, monkeypatch):
+    """MOTIFMAMBA_PQ_GRAD_MODE (ssi.py:157-158): for z-less calls the reference's "exact" mode takes
+    dP / dQ from autograd through its full-matrix path, any other value from its dense CUDA
+    backward, the only backward its launcher runs with P/Q (selective_scan_bwd_kernel.cuh:928-932),
+    which accumulates the exact chain rule (:307, :334). Both are the exact gradient: the kernel's
+    match the float64 adjoint under either value."""
+    _say(f"pq bwd MOTIFMAMBA_PQ_GRAD_MODE={mode}")
+    monkeypatch.setenv("MOTIFMAMBA_PQ_GRAD_MODE", mode)
+    case = _pq_case(830, batch=2, dim=32, L=64, N=16, R=2, dtype=torch.float32, with_z=False)
+    _vs_exact(case, _dout(831, (2, 32, 64), torch.float32), torch.float32, mode)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("per_dim", [True, False])
 def test_pq_bwd_dtypes(dtype, per_dim):

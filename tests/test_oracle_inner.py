@@ -9,7 +9,12 @@ MambaInnerFn.forward, selective_scan_interface.py:458-553, and mamba_inner_ref, 
 * RMSNorm known answers (a constant row maps to the weight; [3, 4] to [3, 4] / sqrt(12.5)) and scale
   invariance;
 * float64 gradcheck of the restatement's autograd gradients (the gradients the GPU backward is
-  compared with) against finite differences.
+  compared with) against finite differences;
+* the step-by-step restatement of MambaInnerFn.backward (mamba_inner_bwd_ref, the expected values
+  when RMSNorm weights are given): without the norms it equals autograd of mamba_inner_ref at both
+  checkpoint levels, projected and given B/C; with them at checkpoint_lvl 0 it equals autograd
+  through straight-through norms (the norm's value, an identity gradient); at checkpoint_lvl 1 with
+  unit weights and eps 0 (where normalising twice changes nothing) it equals checkpoint_lvl 0.
 
 CPU only.
 """
@@ -20,7 +25,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle.inner_ref import mamba_inner_brute, mamba_inner_ref, rms_norm_ref
+import oracle.inner_ref as inner_mod
+from oracle.inner_ref import mamba_inner_brute, mamba_inner_bwd_ref, mamba_inner_ref, rms_norm_ref
 
 
 def _params(seed, batch=2, d_inner=3, L=6, d_state=2, rank=2, d_model=2, W=4, dtype=torch.float64, biases=True):
@@ -100,3 +106,86 @@ def test_gradcheck():
         q = dict(zip(names, a))
         return _call(q)
     assert torch.autograd.gradcheck(f, args, eps=1e-6, atol=1e-6, rtol=1e-5)
+
+
+NAMES = ["xz", "conv1d_weight", "conv1d_bias", "x_proj_weight", "delta_proj_weight", "out_proj_weight",
+         "out_proj_bias", "A", "B", "C", "D", "delta_bias", "B_proj_bias", "C_proj_bias"]
+
+
+def _bwd_case(seed, given):
+    p = _params(seed, batch=2, d_inner=3, L=7, d_state=2, rank=2, d_model=2)
+    g = torch.Generator().manual_seed(seed + 1)
+    if given:
+        p["B"] = torch.randn(2, 1, 2, 7, generator=g, dtype=torch.float64)
+        p["C"] = torch.randn(3, 2, generator=g, dtype=torch.float64) if given == "mixed" else \
+            torch.randn(2, 1, 2, 7, generator=g, dtype=torch.float64)
+    else:
+        p["B_proj_bias"] = torch.randn(2, generator=g, dtype=torch.float64) * 0.1
+        p["C_proj_bias"] = torch.randn(2, generator=g, dtype=torch.float64) * 0.1
+    dout = torch.randn(2, 7, 2, generator=g, dtype=torch.float64)
+    return p, dout
+
+
+def _autograd(p, dout, **kw):
+    leaves = {k: (v.clone().requires_grad_(True) if torch.is_tensor(v) else v) for k, v in p.items()}
+    y = mamba_inner_ref(*[leaves.get(k) for k in NAMES], round_to=None, compute_dtype=torch.float64, **kw)
+    y.backward(dout)
+    return {k: v.grad for k, v in leaves.items() if torch.is_tensor(v)}
+
+
+def _restated(p, dout, **kw):
+    args = {k: p.get(k) for k in NAMES}
+    return mamba_inner_bwd_ref(*[args[k] for k in NAMES[:8]], dout, B=args["B"], C=args["C"], D=args["D"],
+                               delta_bias=args["delta_bias"], B_proj_bias=args["B_proj_bias"],
+                               C_proj_bias=args["C_proj_bias"], compute_dtype=torch.float64, **kw)
+
+
+def _same(got, want, names, rtol=1e-10, atol=1e-12):
+    for k in names:
+        assert got[k] is not None, k
+        torch.testing.assert_close(got[k], want[k], rtol=rtol, atol=atol, msg=lambda m: f"d{k}: {m}")
+
+
+@pytest.mark.parametrize("lvl", [0, 1])
+@pytest.mark.parametrize("given", [None, "variable", "mixed"])
+def test_bwd_restatement_is_the_gradient_without_norms(lvl, given):
+    p, dout = _bwd_case(41 + lvl, given)
+    want = _autograd(p, dout)
+    got = _restated(p, dout, checkpoint_lvl=lvl)
+    _same(got, want, [k for k in want])
+
+
+def test_bwd_restatement_with_norms_passes_them_unchanged(monkeypatch):
+    """checkpoint_lvl 0 (no second normalisation): the reference's gradients are those of the block
+    with each RMSNorm replaced by its value and an identity gradient."""
+    p, dout = _bwd_case(51, None)
+    g = torch.Generator().manual_seed(52)
+    rw = dict(b_rms_weight=torch.rand(2, generator=g, dtype=torch.float64) + 0.5,
+              c_rms_weight=torch.rand(2, generator=g, dtype=torch.float64) + 0.5,
+              dt_rms_weight=torch.rand(3, generator=g, dtype=torch.float64) + 0.5)
+    got = _restated(p, dout, checkpoint_lvl=0, **rw)
+    orig = inner_mod.rms_norm_ref
+
+    def straight_through(x, weight, eps=1e-6, dim=-1, compute_dtype=torch.float32):
+        y = orig(x.detach(), weight.detach(), eps, dim, compute_dtype)
+        return x + (y - x).detach()
+    monkeypatch.setattr(inner_mod, "rms_norm_ref", straight_through)
+    want = _autograd(p, dout, **rw)
+    _same(got, want, [k for k in want])
+
+
+def test_bwd_restatement_second_normalisation():
+    """checkpoint_lvl 1 normalises the saved, normalised B and C again: with unit weights and eps 0
+    that changes nothing (x / rms(x) has rms 1), so the gradients equal checkpoint_lvl 0's; with
+    other weights they differ (the reference's behaviour, reproduced)."""
+    p, dout = _bwd_case(61, None)
+    unit = dict(b_rms_weight=torch.ones(2, dtype=torch.float64), c_rms_weight=torch.ones(2, dtype=torch.float64),
+                b_c_dt_rms_eps=0.0)
+    g0 = _restated(p, dout, checkpoint_lvl=0, **unit)
+    g1 = _restated(p, dout, checkpoint_lvl=1, **unit)
+    _same(g1, g0, [k for k in g0 if g0[k] is not None], rtol=1e-9, atol=1e-11)
+    w = dict(b_rms_weight=torch.tensor([0.5, 2.0], dtype=torch.float64),
+             c_rms_weight=torch.tensor([1.5, 0.7], dtype=torch.float64))
+    g0 = _restated(p, dout, checkpoint_lvl=0, **w)
+    g1 = _restated(p, dout, checkpoint_lvl=1, **w)
+    assert (g1["A"] - g0["A"]).abs().max() > 1e-6 * g0["A"].abs().max()
