@@ -529,10 +529,13 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 sRed[red_at(0, n0 + 1, s, c)] = gh1 * x.y;
                 sRed[red_at(1, n0, s, c)] = x.w * hs0[t];       // dC contributions
                 sRed[red_at(1, n0 + 1, s, c)] = x.w * hs1[t];
+                // sum_n gh (u B + A a h_{t-1}) = u sum_n gh B + sum_n A (gh a h_{t-1}); the products
+                // gh a h_{t-1} also give dA.
+                const float w0 = gh0 * ah0, w1 = gh1 * ah1;
                 pu[s] = __builtin_fmaf(gh1, bv.y, gh0 * bv.x);
-                pd[s] = __builtin_fmaf(gh1, __builtin_fmaf(A1, ah1, x.z * bv.y), gh0 * __builtin_fmaf(A0, ah0, x.z * bv.x));
-                dA_t0 = __builtin_fmaf(gh0 * x.x, ah0, dA_t0);
-                dA_t1 = __builtin_fmaf(gh1 * x.x, ah1, dA_t1);
+                pd[s] = __builtin_fmaf(x.z, pu[s], __builtin_fmaf(A1, w1, A0 * w0));
+                dA_t0 = __builtin_fmaf(x.x, w0, dA_t0);
+                dA_t1 = __builtin_fmaf(x.x, w1, dA_t1);
                 an0 = as0[t];
                 an1 = as1[t];
             }
