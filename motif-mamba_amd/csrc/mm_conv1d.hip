@@ -390,9 +390,17 @@ conv1d_bwd_kernel(const mm_conv1d_bwd_params p) {
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 
-template <typename T, int W>
-int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
-    constexpr int NC = 2;
+// Chunks of 8 positions per lane and tile: 2 (4,096-step tiles) unless 1 (2,048-step tiles) leaves
+// fewer lanes past the end of the rows' last tiles (a 2,048-step row fills only half of a
+// 4,096-step tile).
+int bwd_chunks(int64_t L) {
+    auto idle = [&](int64_t tile) { return ((L + tile - 1) / tile) * tile - L; };
+    const int64_t t2 = int64_t(kThreads) * kChunk * 2;
+    return idle(t2 / 2) < idle(t2) ? 1 : 2;
+}
+
+template <typename T, int W, int NC>
+int launch_bwd_wn(const mm_conv1d_bwd_params &p, hipStream_t s) {
     const int64_t eb = int64_t(sizeof(T));
     auto row_ok = [&](const void *ptr, int64_t s0, int64_t s1) {
         return aligned16(ptr) && (s0 * eb) % 16 == 0 && (s1 * eb) % 16 == 0;
@@ -405,6 +413,11 @@ int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
     else
         hipLaunchKernelGGL((conv1d_bwd_kernel<T, W, false, NC>), grid, dim3(kThreads), 0, s, p);
     return launch_status("conv1d_bwd");
+}
+
+template <typename T, int W>
+int launch_bwd_w(const mm_conv1d_bwd_params &p, hipStream_t s) {
+    return bwd_chunks(p.seqlen) == 1 ? launch_bwd_wn<T, W, 1>(p, s) : launch_bwd_wn<T, W, 2>(p, s);
 }
 
 // dweight and dbias are written (not accumulated) by the one workgroup of each channel, also for

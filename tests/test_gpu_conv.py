@@ -195,7 +195,10 @@ def _ref_grads(x, w, b, dout, act):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("W", [2, 3, 4])
-@pytest.mark.parametrize("L", [1, 7, 64, 1000, 9000])   # 9000: three 4096-step tiles, the last partial
+# The kernel takes 2,048-step tiles (8 positions per lane) where they leave fewer idle lanes than
+# 4,096-step tiles (16 per lane): L 1 .. 1000 and 9000 (five tiles, the last partial) take the
+# former, 4000 (one partial tile either way) the latter.
+@pytest.mark.parametrize("L", [1, 7, 64, 1000, 4000, 9000])
 def test_conv_bwd(dtype, W, L):
     _say(f"conv bwd {dtype} W={W} L={L}")
     from causal_conv1d import causal_conv1d_fn
@@ -250,6 +253,28 @@ def test_conv_bwd_benchmark_shape_rows():
     assert torch.equal(dw, dw2) and torch.equal(db, db2) and torch.equal(dx, dx2)
     dx, dw, db = dx.cpu(), dw.cpu(), db.cpu()
     for sl in (slice(1000, 1032), slice(5112, 5120)):
+        ex, ew, eb = _ref_grads(x[:, sl], w[sl], b[sl], dout[:, sl], "silu")
+        _gcheck(dx[:, sl], ex, torch.bfloat16, "dx rows")
+        _gcheck(dw[sl], ew, torch.bfloat16, "dweight rows")
+        _gcheck(db[sl], eb, torch.bfloat16, "dbias rows")
+
+
+def test_conv_bwd_config1_shape_rows():
+    """Config-1 conv shape (batch 8, 1536 channels, L 2048, bf16: one 2,048-step tile per row): a
+    slice of channels against the oracle, and the same bits on a second call."""
+    _say("conv bwd config-1 shape")
+    from motif_mamba_amd.causal_conv1d import causal_conv1d_bwd
+    g = torch.Generator().manual_seed(830)
+    x = torch.randn(8, 1536, 2048, generator=g).to(torch.bfloat16)
+    w = (torch.randn(1536, 4, generator=g) * 0.5).to(torch.bfloat16)
+    b = (torch.randn(1536, generator=g) * 0.1).to(torch.bfloat16)
+    dout = torch.randn(8, 1536, 2048, generator=g).to(torch.bfloat16)
+    gx, gw, gb, gd = x.to(DEV), w.to(DEV), b.to(DEV), dout.to(DEV)
+    dx, dw, db = causal_conv1d_bwd(gx, gw, gb, gd, None, True)
+    dx2, dw2, db2 = causal_conv1d_bwd(gx, gw, gb, gd, None, True)
+    assert torch.equal(dw, dw2) and torch.equal(db, db2) and torch.equal(dx, dx2)
+    dx, dw, db = dx.cpu(), dw.cpu(), db.cpu()
+    for sl in (slice(0, 16), slice(1520, 1536)):
         ex, ew, eb = _ref_grads(x[:, sl], w[sl], b[sl], dout[:, sl], "silu")
         _gcheck(dx[:, sl], ex, torch.bfloat16, "dx rows")
         _gcheck(dw[sl], ew, torch.bfloat16, "dweight rows")
