@@ -335,25 +335,50 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-// The DPP control that pairs each lane of a group of LPR lanes with one in the other half of the
-// group: quad_perm [3,2,1,0], row_half_mirror, row_mirror.
-template <int LPR>
-constexpr int kHalfSwap = LPR == 4 ? 0x1B : (LPR == 8 ? 0x141 : 0x140);
+// R sums over the LPR lanes of a group at once (R a power of 2, 2 <= R <= LPR), the DPP stages of
+// group_sum run as a transposed reduction. The stages pair lanes by kLaneStage<LPR, 0>, <1>, ...
+// (row_mirror, row_half_mirror, quad_perm [2,3,0,1], [1,0,3,2] at 16 lanes; the last three at 8;
+// quad_perm [3,2,1,0], [1,0,3,2] at 4), outermost first. Lane k of the group holds its partials in
+// the order x[t] = partial of sum t ^ c_k, c_k = lane_rank_offset<LPR, R>(k): then at stage j < log2 R
+// each lane adds the upper half of its partner's live values to the lower half of its own (the
+// partner's upper half holds the sums this lane keeps), halving the live values with one DPP add
+// each; the remaining stages add the single live value symmetrically; and the other totals come back
+// by the transposed stages' patterns in reverse (x[t + 2^i] = x[t] of the stage-(log2 R - 1 - i)
+// partner). On return x[t] is the total of sum t ^ c_k, the same bits in every lane that holds that
+// sum. R - 1 + log2(LPR / R) DPP adds and R - 1 DPP moves (which the compiler folds into a
+// consuming multiply where it can), against R log2(LPR) adds for R separate butterflies. The lane
+// orders were derived and checked by simulating the stages on symbolic partials.
+template <int LPR, int J>
+constexpr int kLaneStage = LPR == 16 ? (J == 0 ? 0x140 : J == 1 ? 0x141 : J == 2 ? 0x4E : 0xB1)
+                         : LPR == 8  ? (J == 0 ? 0x141 : J == 1 ? 0x4E : 0xB1)
+                                     : (J == 0 ? 0x1B : 0xB1);
 
-// Two sums over the LPR lanes of a group at once. Lanes of the first half hold, as `keep`, their
-// partial of sum 0 and, as `send`, their partial of sum 1; lanes of the second half the other way
-// round. The first stage adds each lane's `keep` to the `send` of its partner in the other half, so
-// that each half then carries one sum and completes it over its LPR / 2 lanes with the symmetric
-// stages of group_sum (every lane of a half ends with bit-identical totals); the partner's total
-// is the other sum. log2(LPR) + 1 DPP operations for the pair instead of 2 log2(LPR).
-template <int LPR>
-__device__ __forceinline__ void pair_sum2(float keep, float send, float &mine, float &other) {
-    float x = keep + dpp_mov<kHalfSwap<LPR>>(send);
-    x = dpp_add<0xB1>(x);                           // quad_perm [1,0,3,2]
-    if constexpr (LPR >= 8) x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
-    if constexpr (LPR >= 16) x = dpp_add<0x141>(x); // row_half_mirror: the other quad of the half
-    mine = x;
-    other = dpp_mov<kHalfSwap<LPR>>(x);
+template <int LPR, int R>
+__device__ __forceinline__ int lane_rank_offset(int k) {
+    static_assert((LPR == 4 || LPR == 8 || LPR == 16) && (R == 2 || R == 4 || R == 8) && R <= LPR, "shape");
+    // c_k of lane k in bits 4k .. 4k + 3.
+    constexpr uint64_t tab = LPR == 4  ? (R == 2 ? 0x1100ull : 0x2310ull)
+                           : LPR == 8  ? (R == 2 ? 0x11110000ull : R == 4 ? 0x22331100ull : 0x45673210ull)
+                                       : (R == 2 ? 0x1111111100000000ull : R == 4 ? 0x2222333311110000ull
+                                                                                  : 0x4455776622331100ull);
+    return int((tab >> (4 * k)) & 15u);
+}
+
+template <int LPR, int R>
+__device__ __forceinline__ void lane_sums(float (&x)[R]) {
+    constexpr int M = R == 2 ? 1 : R == 4 ? 2 : 3;               // transposed stages
+    constexpr int NS = LPR == 4 ? 2 : LPR == 8 ? 3 : 4;          // all stages
+    static_for<0, M>([&](auto Jc) {
+        constexpr int j = decltype(Jc)::value, n = R >> j;
+#pragma unroll
+        for (int t = 0; t < n / 2; ++t) x[t] = x[t] + dpp_mov<kLaneStage<LPR, j>>(x[n / 2 + t]);
+    });
+    static_for<M, NS>([&](auto Jc) { x[0] = dpp_add<kLaneStage<LPR, decltype(Jc)::value>>(x[0]); });
+    static_for<0, M>([&](auto Ic) {
+        constexpr int i = decltype(Ic)::value, j = M - 1 - i, h = 1 << i;
+#pragma unroll
+        for (int t = 0; t < h; ++t) x[t + h] = dpp_mov<kLaneStage<LPR, j>>(x[t]);
+    });
 }
 
 }  // namespace mm

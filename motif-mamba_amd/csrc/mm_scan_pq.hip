@@ -15,9 +15,9 @@
 //       consecutive lanes of a channel hold S states each (S * LPR >= dstate, padded with states
 //       whose A, P, Q, B and C are zero, which stay zero). Per step each lane forms its partial
 //       Q h over its S states, a DPP butterfly inside the LPR lanes sums the partials (every lane
-//       ends with the same bits; at rank 2 one butterfly serves both sums: each half of the lanes
-//       completes one of them and takes the other from its partner), and the lane updates its S
-//       states with P (dt' q) + dt' u B.
+//       ends with the same bits; where the rank is at most LPR one transposed butterfly serves all
+//       R sums, lane_sums in mm_common.h), and the lane updates its S states with
+//       P (dt' q) + dt' u B.
 //       The lane's rows of P and Q live in registers for the whole sequence. (16-bit inputs with
 //       16 lanes of one state and rank <= 2 carry the butterfly's total from step to step and form
 //       the next partial as Q (a h + dt' u B) + (Q P) q, which shortens the dependent chain.)
@@ -98,6 +98,13 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     const T *Bg = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
     const T *Cg = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
 
+    // XK: see below. TS: the coupling's R sums over the channel's lanes are one transposed
+    // reduction (lane_sums, R <= LPR), which wants the lane's rows of Q and columns of P in its
+    // order: position t holds rank t ^ ro.
+    constexpr bool XK = LPR == 16 && S == 1 && R <= 2 && !std::is_same<T, float>::value;
+    constexpr bool TS = R <= LPR && !XK;
+    int ro = 0;
+    if constexpr (TS) ro = lane_rank_offset<LPR, R>(k);
     float A2[S], h[S], Pr[S][R], Qr[R][S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -106,10 +113,11 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
         A2[s] = on ? p.A[d * p.A_d_stride + n * p.A_dstate_stride] * kLog2e : 0.f;
         h[s] = 0.f;
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
+        for (int t = 0; t < R; ++t) {
+            const int j = t ^ ro;
             const bool use = on && j < rank;
-            Pr[s][j] = use ? p.P[d * p.P_d_stride + n * p.P_dstate_stride + j * p.P_r_stride] : 0.f;
-            Qr[j][s] = use ? p.Q[d * p.Q_d_stride + j * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
+            Pr[s][t] = use ? p.P[d * p.P_d_stride + n * p.P_dstate_stride + j * p.P_r_stride] : 0.f;
+            Qr[t][s] = use ? p.Q[d * p.Q_d_stride + j * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
         }
     }
     // With 16 lanes of one state per channel (dstate <= 16, chosen when their waves fit one per
@@ -122,7 +130,6 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     // chain); +10 % at two waves per SIMD with 8 lanes, where issue sets the time. 16-bit inputs
     // only: float32 callers keep the direct Q h, whose rounding the long-sequence float32 checks
     // pin; 16-bit outputs round far above the float32 rounding difference of the two forms.
-    constexpr bool XK = LPR == 16 && S == 1 && R <= 2 && !std::is_same<T, float>::value;
     float Kr[R][R], gq[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -134,18 +141,6 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
             for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], Pr[s][r2], acc);
             Kr[r][r2] = acc;
         }
-    }
-    // Rank 2, direct form: the lane's rows of Q and P in the order pair_sum2 takes them (sum 0 kept
-    // by the first LPR / 2 lanes of a channel, sum 1 by the others).
-    constexpr bool PS2 = R == 2 && !XK;
-    const bool upper = k >= LPR / 2;
-    float Qk[S], Qs[S], Pm[S], Po[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-        Qk[s] = Qr[upper ? 1 : 0][s];
-        Qs[s] = Qr[upper ? 0 : 1][s];
-        Pm[s] = Pr[s][upper ? 1 : 0];
-        Po[s] = Pr[s][upper ? 0 : 1];
     }
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
@@ -366,20 +361,21 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
                         h[s] = w;
                         y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
                     }
-                } else if constexpr (PS2) {
-                    float ak = Qk[0] * h[0], as = Qs[0] * h[0];
+                } else if constexpr (TS) {
 #pragma unroll
-                    for (int s = 1; s < S; ++s) {
-                        ak = __builtin_fmaf(Qk[s], h[s], ak);
-                        as = __builtin_fmaf(Qs[s], h[s], as);
+                    for (int t = 0; t < R; ++t) {
+                        q[t] = Qr[t][0] * h[0];
+#pragma unroll
+                        for (int s = 1; s < S; ++s) q[t] = __builtin_fmaf(Qr[t][s], h[s], q[t]);
                     }
-                    float qm, qo;
-                    pair_sum2<LPR>(ak, as, qm, qo);
-                    qm *= dts[j];
-                    qo *= dts[j];
+                    lane_sums<LPR, R>(q);
+#pragma unroll
+                    for (int t = 0; t < R; ++t) q[t] *= dts[j];
 #pragma unroll
                     for (int s = 0; s < S; ++s) {
-                        const float w = __builtin_fmaf(Po[s], qo, __builtin_fmaf(Pm[s], qm, bu[j][s]));
+                        float w = bu[j][s];
+#pragma unroll
+                        for (int t = 0; t < R; ++t) w = __builtin_fmaf(Pr[s][t], q[t], w);
                         h[s] = __builtin_fmaf(av[j][s], h[s], w);
                         y = s == 0 ? cv[j][0] * h[0] : __builtin_fmaf(cv[j][s], h[s], y);
                     }

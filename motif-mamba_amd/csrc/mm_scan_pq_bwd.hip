@@ -21,7 +21,8 @@
 // (batch, group) and dstate <= 16 states; the LPR = 16 / S consecutive lanes of a channel hold S
 // states each (S = 2: 8 lanes per channel, two waves per workgroup), and the sums over a channel's
 // states (Q h, P^T lam, and the per-step sums that give du and ddelta) are DPP butterflies inside
-// those lanes, which leave bit-identical totals in all of them. P and Q of the lane's states live
+// those lanes, which leave bit-identical totals in all of them (the R sums of Q h and of P^T lam
+// each as one transposed butterfly, lane_sums). P and Q of the lane's states live
 // in registers. The states at every 16-step tile start come from the forward (its tile_states) or,
 // without them, from a first pass that recomputes the forward into the caller's workspace. The
 // second pass walks the tiles in reverse: it recomputes each tile from its checkpoint into LDS (the
@@ -87,6 +88,13 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
     const T *Bg = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
     const T *Cg = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
 
+    // The R sums over a channel's states (Q h and P^T lam) are one transposed reduction over its 8
+    // lanes (lane_sums), which wants the lane's rows of Q and columns of P in its order: position t
+    // holds rank t ^ ro. Every rank-indexed quantity of the lane (q, P^T lam, dP, dQ) is kept in that
+    // order. The forward's 8-lane layout forms Q h the same way, so pass 1 reproduces its tile states
+    // bit for bit.
+    static_assert(R <= LPR, "one transposed reduction per sum set");
+    const int ro = lane_rank_offset<LPR, R>(k);
     float An[S], A2[S], Pr[S][R], Qr[R][S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -95,34 +103,22 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
         An[s] = on ? p.A[d * p.A_d_stride + n * p.A_dstate_stride] : 0.f;
         A2[s] = An[s] * kLog2e;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int t = 0; t < R; ++t) {
+            const int r = t ^ ro;
             const bool use = on && r < rank;
-            Pr[s][r] = use ? p.P[d * p.P_d_stride + n * p.P_dstate_stride + r * p.P_r_stride] : 0.f;
-            Qr[r][s] = use ? p.Q[d * p.Q_d_stride + r * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
+            Pr[s][t] = use ? p.P[d * p.P_d_stride + n * p.P_dstate_stride + r * p.P_r_stride] : 0.f;
+            Qr[t][s] = use ? p.Q[d * p.Q_d_stride + r * p.Q_r_stride + n * p.Q_dstate_stride] : 0.f;
         }
     }
-    // Rank 2: the lane's rows of Q and P in the order pair_sum2 takes them (sum 0 kept by the first
-    // LPR / 2 lanes of a channel, sum 1 by the others), for Q h and P^T lam. The forward's 8-lane
-    // layout forms Q h the same way, so pass 1 reproduces its tile states bit for bit.
-    constexpr bool PS2 = R == 2;
-    const bool upper = k >= LPR / 2;
-    float Qk[S], Qs[S], Pm[S], Po[S];
+    // Q h over the channel's states, rank t ^ ro in q[t].
+    auto qh = [&](const float *h, float (&q)[R]) {
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-        Qk[s] = Qr[upper ? 1 : 0][s];
-        Qs[s] = Qr[upper ? 0 : 1][s];
-        Pm[s] = Pr[s][upper ? 1 : 0];
-        Po[s] = Pr[s][upper ? 0 : 1];
-    }
-    // Q h over the channel's states for both ranks: qm is sum `upper` (1 or 0), qo the other.
-    auto qh2 = [&](const float *h, float &qm, float &qo) {
-        float ak = Qk[0] * h[0], as = Qs[0] * h[0];
+        for (int t = 0; t < R; ++t) {
+            q[t] = Qr[t][0] * h[0];
 #pragma unroll
-        for (int s = 1; s < S; ++s) {
-            ak = __builtin_fmaf(Qk[s], h[s], ak);
-            as = __builtin_fmaf(Qs[s], h[s], as);
+            for (int s = 1; s < S; ++s) q[t] = __builtin_fmaf(Qr[t][s], h[s], q[t]);
         }
-        pair_sum2<LPR>(ak, as, qm, qo);
+        lane_sums<LPR, R>(q);
     };
     const float Dv = p.D ? p.D[d] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
@@ -234,32 +230,16 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll
             for (int t = 0; t < kT; ++t) {
                 const float4 x = sX[cw * kXS + t];
-                if constexpr (PS2) {
-                    float qm, qo;
-                    qh2(h, qm, qo);
-                    qm *= x.x;
-                    qo *= x.x;
+                float q[R];
+                qh(h, q);
 #pragma unroll
-                    for (int s = 0; s < S; ++s) {
-                        const float w = __builtin_fmaf(Po[s], qo, __builtin_fmaf(Pm[s], qm, x.y * sBC[t * kBCS + k * S + s]));
-                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
-                    }
-                } else {
-                    float q[R];
+                for (int r = 0; r < R; ++r) q[r] *= x.x;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float acc = Qr[r][0] * h[0];
+                for (int s = 0; s < S; ++s) {
+                    float w = x.y * sBC[t * kBCS + k * S + s];
 #pragma unroll
-                        for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
-                        q[r] = group_sum<LPR>(acc) * x.x;
-                    }
-#pragma unroll
-                    for (int s = 0; s < S; ++s) {
-                        float w = x.y * sBC[t * kBCS + k * S + s];
-#pragma unroll
-                        for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
-                    }
+                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                    h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
                 }
             }
             __syncthreads();
@@ -296,40 +276,24 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll 2
             for (int t = 0; t < kT; ++t) {
                 const float4 x = sX[cw * kXS + t];
-                if constexpr (PS2) {
-                    float qm, qo;
-                    qh2(h, qm, qo);
-                    // (Q h_{t-1})_k for k < 2 (lanes 0 and 1 are in the first half: sum k is
-                    // qm for lane 0, qo for lane 1), read by the whole channel.
-                    if (k < 2) sQ[(t * 16 + cw) * R + k] = k == 0 ? qm : qo;
-                    qm *= x.x;
-                    qo *= x.x;
+                float q[R];
+                qh(h, q);
+                // Q h_{t-1} in rank order, read by the whole channel: lane 0 of the channel (rank
+                // offset 0) holds it in order.
+                if (k == 0) {
 #pragma unroll
-                    for (int s = 0; s < S; ++s) {
-                        const float w = __builtin_fmaf(Po[s], qo, __builtin_fmaf(Pm[s], qm, x.y * sBC[t * kBCS + k * S + s]));
-                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
-                        sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
-                    }
-                } else {
-                    float q[R], qw = 0.f;
+                    for (int r = 0; r < R; r += 2)
+                        *reinterpret_cast<float2 *>(&sQ[(t * 16 + cw) * R + r]) = make_float2(q[r], q[r + 1]);
+                }
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float acc = Qr[r][0] * h[0];
+                for (int r = 0; r < R; ++r) q[r] *= x.x;
 #pragma unroll
-                        for (int s = 1; s < S; ++s) acc = __builtin_fmaf(Qr[r][s], h[s], acc);
-                        q[r] = group_sum<LPR>(acc);
-                        if (k == r) qw = q[r];
-                        q[r] *= x.x;
-                    }
-                    if (k < R) sQ[(t * 16 + cw) * R + k] = qw;     // (Q h_{t-1})_k, read by the whole channel
+                for (int s = 0; s < S; ++s) {
+                    float w = x.y * sBC[t * kBCS + k * S + s];
 #pragma unroll
-                    for (int s = 0; s < S; ++s) {
-                        float w = x.y * sBC[t * kBCS + k * S + s];
-#pragma unroll
-                        for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
-                        h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
-                        sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
-                    }
+                    for (int r = 0; r < R; ++r) w = __builtin_fmaf(Pr[s][r], q[r], w);
+                    h[s] = __builtin_fmaf(decay_exp2(x.x, A2[s]), h[s], w);
+                    sHS[(t * 16 + cw) * 16 + k * S + s] = h[s];
                 }
             }
         }
@@ -351,28 +315,16 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
                 lam[s] = __builtin_fmaf(Cv[s], x.w, carry[s]);
                 hp[s] = t > 0 ? sHS[((t - 1) * 16 + cw) * 16 + k * S + s] : hck[s];   // h_{t-1}
             }
-            // (P^T lam_t)_r; at rank 2 in the lane's own order: sv[0] is rank `upper`, sv[1] the
-            // other (dQ[0] / dQ[1] follow the same order and are put back at the end).
+            // Q h_{t-1} and P^T lam_t, rank t ^ ro at position t (as Pr, Qr, dP and dQ).
             float q[R], sv[R];
-            if constexpr (PS2) {
-                float am = Pm[0] * lam[0], ao = Po[0] * lam[0];
-#pragma unroll
-                for (int s = 1; s < S; ++s) {
-                    am = __builtin_fmaf(Pm[s], lam[s], am);
-                    ao = __builtin_fmaf(Po[s], lam[s], ao);
-                }
-                pair_sum2<LPR>(am, ao, sv[0], sv[1]);
-            }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                q[r] = sQ[(t * 16 + cw) * R + r];   // (Q h_{t-1})_r
-                if constexpr (!PS2) {
-                    float as = Pr[0][r] * lam[0];
+                q[r] = sQ[(t * 16 + cw) * R + (r ^ ro)];
+                sv[r] = Pr[0][r] * lam[0];
 #pragma unroll
-                    for (int s = 1; s < S; ++s) as = __builtin_fmaf(Pr[s][r], lam[s], as);
-                    sv[r] = group_sum<LPR>(as);
-                }
+                for (int s = 1; s < S; ++s) sv[r] = __builtin_fmaf(Pr[s][r], lam[s], sv[r]);
             }
+            lane_sums<LPR, R>(sv);
             float pdd = 0.f, pgb = 0.f;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
@@ -382,7 +334,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     pq = __builtin_fmaf(Pr[s][r], q[r], pq);
-                    qs = __builtin_fmaf(PS2 ? (r == 0 ? Qk[s] : Qs[s]) : Qr[r][s], sv[r], qs);
+                    qs = __builtin_fmaf(Qr[r][s], sv[r], qs);
                 }
                 // dt' term: A a h_{t-1} + P q + u B
                 pdd = __builtin_fmaf(lam[s], __builtin_fmaf(An[s], ah, __builtin_fmaf(x.z, Bv[s], pq)), pdd);
@@ -444,15 +396,7 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
             }
         }
     }
-    if constexpr (PS2) {
-        // dQ[0] accumulated rank `upper`: back to rank order.
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const float a = dQ[0][s], c = dQ[1][s];
-            dQ[0][s] = upper ? c : a;
-            dQ[1][s] = upper ? a : c;
-        }
-    }
+    // dP[s][t] and dQ[t][s] hold rank t ^ ro.
     const bool shared_pq = p.dP_d_stride == 0 && p.dQ_d_stride == 0;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -461,10 +405,11 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
         atomicAdd(p.dA + d * p.dA_d_stride + n * p.dA_dstate_stride, dA[s]);
         if (shared_pq) continue;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int t = 0; t < R; ++t) {
+            const int r = t ^ ro;
             if (r >= rank) continue;
-            atomicAdd(p.dP + d * p.dP_d_stride + n * p.dP_dstate_stride + r * p.dP_r_stride, dP[s][r]);
-            atomicAdd(p.dQ + d * p.dQ_d_stride + r * p.dQ_r_stride + n * p.dQ_dstate_stride, dQ[r][s]);
+            atomicAdd(p.dP + d * p.dP_d_stride + n * p.dP_dstate_stride + r * p.dP_r_stride, dP[s][t]);
+            atomicAdd(p.dQ + d * p.dQ_d_stride + r * p.dQ_r_stride + n * p.dQ_dstate_stride, dQ[t][s]);
         }
     }
     if (p.dD) atomicAdd(p.dD + d, dD_acc);
@@ -477,9 +422,10 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 #pragma unroll
         for (int s = 0; s < S; ++s) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                sHS[((0 * 16 + k * S + s) * R + r) * 16 + cw] = dP[s][r];
-                sHS[((1 * 16 + k * S + s) * R + r) * 16 + cw] = dQ[r][s];
+            for (int t = 0; t < R; ++t) {
+                const int r = t ^ ro;
+                sHS[((0 * 16 + k * S + s) * R + r) * 16 + cw] = dP[s][t];
+                sHS[((1 * 16 + k * S + s) * R + r) * 16 + cw] = dQ[t][s];
             }
         }
         __syncthreads();
