@@ -1354,7 +1354,10 @@ __device__ __forceinline__ void buffer_store_elem(__amdgpu_buffer_rsrc_t r, uint
         __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (_Float16)x), r, voff, soff, 0);
 }
 
-template <typename T, int PF, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT>
+// CHUNKS: the training outputs as k2s writes them -- the chunk states (the product of the decays
+// since step 0 and the state, at every chunk end) and, on request, the state after every 16-step
+// tile for the backward.
+template <typename T, int PF, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT, bool CHUNKS = false>
 __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int64_t ratio, const int tid,
                                           const int64_t b, const int64_t d0, K1SLds &lds) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
@@ -1382,6 +1385,8 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
 
     const float At = p.A[(d0 + c) * p.A_d_stride + int64_t(r) * p.A_dstate_stride] * kLog2e;
     float h = 0.f;
+    float cum_dt = 0.f;                    // CHUNKS: sum of dt' since step 0
+    const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
     const float Dv = p.D ? p.D[de] : 0.f;
     const float bias = p.delta_bias ? p.delta_bias[de] : 0.f;
 
@@ -1448,7 +1453,8 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
     // of its row, register s % 2; dt' / dt'u are read one 4-step group ahead.
     float bv[2], cv[2];
     float4 pre_dt, pre_du;
-    auto scan_tile = [&](auto Hc, const float *dt, const float *du, float *yb, const float *dtn, const float *dun) {
+    auto scan_tile = [&](auto Hc, int64_t t0, const float *dt, const float *du, float *yb, const float *dtn,
+                         const float *dun) {
         constexpr int H = decltype(Hc)::value;
         float4 dtq = pre_dt, duq = pre_du;
         static_for<0, kT1 / 4>([&](auto S4) {
@@ -1467,6 +1473,7 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
             static_for<0, 4>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 constexpr int s = kT1 * H + 4 * s4 + j;
+                if constexpr (CHUNKS) cum_dt += dts[j];
                 av[j] = decay_exp2(dts[j], At);
                 bbv[j] = row_bcast<s / 2>(bv[s % 2]) * dus[j];
             });
@@ -1483,10 +1490,23 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
         });
         pre_dt = dtq;
         pre_du = duq;
+        if constexpr (CHUNKS) {
+            const int64_t tend = t0 + kT1;
+            if (p.chunk_states && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
+                const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
+                float *csp = p.chunk_states + ((b * p.dim + d0 + c) * n_chunks + ci) * 32 + 2 * r;
+                csp[0] = __builtin_amdgcn_exp2f(At * cum_dt);
+                csp[1] = h;
+            }
+            if (p.tile_states && tend < L)
+                p.tile_states[((t0 / kT1 + 1) * p.batch * p.dim + b * p.dim + d0 + c) * 16 + r] = h;
+        }
     };
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
+    if (CHUNKS && p.tile_states)           // the checkpoint before the first tile: zero
+        p.tile_states[(b * p.dim + d0 + c) * 16 + r] = 0.f;
     K1SData<T> ring[PF];
     {
         uint32_t u0, dl0, z0, u1, dl1, z1;
@@ -1511,17 +1531,18 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
             using T2P3 = std::integral_constant<int, 2 * P + 3>;
             const int32_t i = i0 + S;
             if (i < n_pairs) {
+                const int64_t t0 = int64_t(i) * (2 * kT1);
                 unpack_raw<T, 2>(ring[S].b, bv);
                 unpack_raw<T, 2>(ring[S].c, cv);
                 const K1SData<T> nxt = ring[S];
                 load_data(i + PF, ring[S]);
                 // Interval 2i: scan tile 2i, prepare tile 2i + 2, finish tile 2i - 1.
-                scan_tile(I0{}, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
+                scan_tile(I0{}, t0, DT(T2P{}), DU(T2P{}), YB(I0{}), DT(T2P1{}), DU(T2P1{}));
                 prologue(T2P2{}, nxt.u0, nxt.d0, nxt.z0);
                 epilogue(T2P3{}, YB(I1{}), i > 0 ? 2 * i - 1 : 0);
                 __syncthreads();
                 // Interval 2i + 1: scan tile 2i + 1, prepare tile 2i + 3, finish tile 2i.
-                scan_tile(I1{}, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
+                scan_tile(I1{}, t0 + kT1, DT(T2P1{}), DU(T2P1{}), YB(I1{}), DT(T2P2{}), DU(T2P2{}));
                 prologue(T2P3{}, nxt.u1, nxt.d1, nxt.z1);
                 epilogue(T2P{}, YB(I0{}), 2 * i);
                 __syncthreads();
@@ -1546,7 +1567,8 @@ union MixLds {
     K1SLds k1;
 };
 
-template <typename T, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT>
+// CHUNKS: the training form (chunk states and, on request, tile states), 16-bit inputs.
+template <typename T, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT, bool CHUNKS>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
 scan_fwd_mix(const mm_scan_fwd_params p, const int64_t ratio, const int32_t n_double) {
     __shared__ __align__(16) MixLds lds;
@@ -1556,18 +1578,28 @@ scan_fwd_mix(const mm_scan_fwd_params p, const int64_t ratio, const int32_t n_do
         // that the group's buffer resources stay in SGPRs.
         const int half = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 7));
         const int64_t grp = 2 * int64_t(blockIdx.x) + half;
-        k2s_group<T, 2, SOFTPLUS, false, HAS_Z, HAS_OUT, true, 0>(p, ratio, kWholeRows, threadIdx.x & 127, grp / gpb,
-                                                                  (grp % gpb) * kCh, 0, lds.k2[half]);
+        k2s_group<T, 2, SOFTPLUS, CHUNKS, HAS_Z, HAS_OUT, true, 0>(p, ratio, kWholeRows, threadIdx.x & 127, grp / gpb,
+                                                                   (grp % gpb) * kCh, 0, lds.k2[half]);
     } else {
         const int64_t grp = 2 * int64_t(n_double) + (int64_t(blockIdx.x) - n_double);
-        k1s_group<T, 2, SOFTPLUS, HAS_Z, HAS_OUT>(p, ratio, threadIdx.x, grp / gpb, (grp % gpb) * kCh, lds.k1);
+        k1s_group<T, 2, SOFTPLUS, HAS_Z, HAS_OUT, CHUNKS>(p, ratio, threadIdx.x, grp / gpb, (grp % gpb) * kCh, lds.k1);
     }
 }
 
 template <typename T, bool HAS_Z, bool HAS_OUT>
 int launch_mix_io(const mm_scan_fwd_params &p, hipStream_t stream, int32_t n_double, int32_t n_single) {
     const int64_t ratio = p.dim / p.n_groups;
-    auto *kern = p.delta_softplus ? scan_fwd_mix<T, true, HAS_Z, HAS_OUT> : scan_fwd_mix<T, false, HAS_Z, HAS_OUT>;
+    using K = void (*)(const mm_scan_fwd_params, const int64_t, const int32_t);
+    K kern;
+    if constexpr (sizeof(T) == 4) {
+        if (p.chunk_states || p.tile_states) return MM_ERR_UNSUPPORTED;   // no fp32 training instance
+        kern = p.delta_softplus ? scan_fwd_mix<T, true, HAS_Z, HAS_OUT, false> : scan_fwd_mix<T, false, HAS_Z, HAS_OUT, false>;
+    } else {
+        kern = p.chunk_states ? (p.delta_softplus ? scan_fwd_mix<T, true, HAS_Z, HAS_OUT, true>
+                                                  : scan_fwd_mix<T, false, HAS_Z, HAS_OUT, true>)
+                              : (p.delta_softplus ? scan_fwd_mix<T, true, HAS_Z, HAS_OUT, false>
+                                                  : scan_fwd_mix<T, false, HAS_Z, HAS_OUT, false>);
+    }
     hipLaunchKernelGGL(kern, dim3(unsigned(n_double + n_single)), dim3(256), 0, stream, p, ratio, n_double);
     return launch_status("scan_fwd_mix");
 }
@@ -1807,7 +1839,8 @@ static bool mix_plan(const mm_scan_fwd_params &p, int32_t &n_double, int32_t &n_
         if (!strcmp(e, "k1")) return 2;
         return 1;
     }();
-    if (mode == 0 || p.chunk_states || p.tile_states) return false;
+    // The training form (chunk and tile states) is built for 16-bit inputs only.
+    if (mode == 0 || ((p.chunk_states || p.tile_states) && p.itype == MM_FLOAT32)) return false;
     const int64_t groups = p.batch * (p.dim / tiled::kCh);
     const int64_t cus = device_simds() / 4;
     if (cus <= 0 || groups % cus != 0) return false;

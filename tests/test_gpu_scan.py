@@ -443,6 +443,43 @@ def test_balanced_grid_every_row(q, dtype):
     _rows_vs_f64(case, out, last, f"q={q} {dtype}")
 
 
+@pytest.mark.parametrize("q", [3, 5])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_balanced_grid_training_outputs(q, dtype):
+    """The training forward (pre-gate out, out_z, chunk states x and tile states) on the mixed grid,
+    16-bit inputs: out and out_z of every row against the float64 restatement; x's (prod a, h)
+    pairs and the tile states (the state before every 16-step tile) on rows of both group kinds and
+    of the groups where one hands over to the other. L = 2144: a whole 2048-step chunk and a
+    partial one."""
+    from motif_mamba_amd import _native
+    cus = _cus()
+    batch, dim, L = 2, q * cus * 16 // 2, 2144
+    _say(f"balanced grid training outputs q={q} {dtype} batch {batch} dim {dim} L {L}")
+    case = _case(90 + q, batch, dim, L, 16, dtype, bkind="4d", G=1)
+    g = _to(case, DEV)
+    out, x, out_z, ck = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"],
+                                          g["delta_bias"], None, None, None, True, tile_states=True)
+    torch.cuda.synchronize()
+    n_tiles = L // 16
+    assert x.shape == (batch, dim, 2, 32) and ck.shape == (n_tiles, batch, dim, 16)
+    _rows_vs_f64(case, out_z.cpu(), None, f"q={q} {dtype} out_z")
+    _rows_vs_f64(dict(case, z=None), out.cpu(), None, f"q={q} {dtype} pre-gate out")
+    pa = chunk_states_ref(case["delta"], case["A"], case["delta_bias"], True)
+    np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
+    first_k1 = 2 * (q // 2) * cus * 16     # first (batch-major) channel of the one-state groups
+    sel = [0, 1, 15, first_k1 - 16, first_k1 - 1, first_k1, first_k1 + 15, batch * dim - 1]
+    rows = [(i // dim, i % dim) for i in sel]
+    r2 = cscan.scan_rows(**case, rows=rows, chunk=2048)
+    r16 = cscan.scan_rows(**case, rows=rows, chunk=16)
+    xc, ckc = x.cpu(), ck.cpu()
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(xc[b, d, :, 1::2].double().numpy(), r2["h_chunks"][i], rtol=1e-3, atol=1e-3,
+                                   err_msg=f"x row {(b, d)}")
+        assert float(ckc[0, b, d].abs().max()) == 0.0
+        np.testing.assert_allclose(ckc[1:, b, d].double().numpy(), r16["h_chunks"][i][:n_tiles - 1], rtol=1e-3,
+                                   atol=1e-3, err_msg=f"tile states row {(b, d)}")
+
+
 @pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False, with_bias=False), dict(softplus=False),
                                    dict(bkind="4d", G=4)], ids=["no_z", "no_D_bias", "no_softplus", "G4"])
 def test_balanced_grid_optional_inputs(flags):
