@@ -98,7 +98,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     const T *Bg = reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride;
     const T *Cg = reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride;
 
-    // XK: see below. TS: the coupling's R sums over the channel's lanes are one transposed
+    // XK: the carried form described below. TS: the coupling's R sums over the channel's lanes are one transposed
     // reduction (lane_sums, R <= LPR), which wants the lane's rows of Q and columns of P in its
     // order: position t holds rank t ^ ro.
     constexpr bool XK = LPR == 16 && S == 1 && R <= 2 && !std::is_same<T, float>::value;
