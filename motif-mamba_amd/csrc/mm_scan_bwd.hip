@@ -14,9 +14,10 @@
 // caller's workspace, and the reverse pass recomputes each tile from its checkpoint (keeping the
 // tile's states and decays in registers) and walks it backwards.
 //
-//   scan_bwd_tiled16<T>   dstate 16, variable B/C (the Mamba shape): 16 channels x 16 states per
-//       128-lane workgroup, sums over states and over the block's channels through LDS, dB/dC
-//       as per-block partials reduced by scan_bwd_reduce_bc (no atomics on them).
+//   scan_bwd_tiled16<T, CARRY, CH>   dstate 16, variable B/C (the Mamba shape): CH channels (16
+//       or 32) x 16 states per workgroup of 8 CH lanes, sums over states and over the block's
+//       channels through LDS, dB/dC as per-block partials reduced by scan_bwd_reduce_bc (no
+//       atomics on them).
 //   scan_bwd_general<T>   any shape: a 256-lane workgroup holds 256/NP rows, one lane per state
 //       (NP = next power of two >= dstate); sums over states go through LDS, sums over rows
 //       (dB, dC, dA, dD, ddelta_bias) are float32 device atomics.
@@ -223,13 +224,13 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
 
 
 // ------------------------------------------------------------------------------------------------
-// dstate-16 backward: a 128-lane workgroup owns 16 channels x 16 states of one (batch, group) --
-// lane (slot rs = lane / 16, channel c = lane % 16) holds states 2 rs and 2 rs + 1 of channel c.
+// dstate-16 backward: a workgroup of 8 CH lanes owns CH channels x 16 states of one (batch, group)
+// -- lane (slot rs = lane / CH, channel c = lane % CH) holds states 2 rs and 2 rs + 1 of channel c.
 // Per 16-step tile: the lane owning steps 2 rs, 2 rs + 1 of channel c computes dt', dt'u, u and
 // g = dout silu(z) (and writes dz) into LDS; B and C of the tile are staged in LDS as float32; the
 // tile is recomputed from its checkpoint with states and decays kept in registers, then walked
 // backwards in two halves of 8 steps. Per half, the dB/dC contributions (per state, step and
-// channel) go to LDS and are summed over the 16 channels, the sums written as this channel block's
+// channel) go to LDS and are summed over the CH channels, the sums written as this channel block's
 // partials (reduced over blocks by scan_bwd_reduce_bc, in a fixed order); the per-slot partial sums
 // over states of gh B and of the delta' derivative go to LDS and the owner of each step adds the 8
 // slots in order and finishes du and ddelta.
@@ -243,17 +244,20 @@ constexpr int kBufs = 1;         // sX / sBC buffers (one: 4 workgroups fit a CU
 // one 32-lane staging store touches on disjoint banks; the 8-byte reads stay aligned.
 constexpr int kBCS = 34;
 
-// sRed address of (tensor, state n, step t of the half, channel c): a block of 8 rows of 16
-// channels per (tensor, state), rows 20 floats apart so that 8 consecutive steps of one state (the
-// reduction reads, 16 bytes per lane) fall in distinct banks; blocks 168 floats apart (8 mod 16
-// banks) so that the 4 state pairs of a wave (the per-step writes) split over both bank halves.
-constexpr int kRedRow = 20;
-constexpr int kRedBlock = 168;
+// sRed address of (tensor, state n, step t of the half, channel c) for CH channels per workgroup:
+// a block of 8 rows of CH channels per (tensor, state). Rows are CH + 4 floats apart (CH = 16: 20),
+// so that the 8 consecutive steps of one state that 8 lanes read as 16-byte pieces in the reduction
+// fall in distinct 16-byte bank groups; blocks are an odd multiple of 8 such groups apart (CH = 16:
+// 168 floats, 8 mod 16 banks), which puts the next state's 8 steps in the other groups.
+template <int CH> constexpr int kRedRow = CH + 4;
+template <int CH> constexpr int kRedBlock = CH == 16 ? 168 : 288;
+template <int CH>
 __device__ __forceinline__ int red_at(int tensor, int n, int t, int c) {
-    return (tensor * 16 + n) * kRedBlock + t * kRedRow + c;
+    return (tensor * 16 + n) * kRedBlock<CH> + t * kRedRow<CH> + c;
 }
-constexpr int kRedFloats = 32 * kRedBlock;
-static_assert((kFH - 1) * kRedRow + 16 <= kRedBlock, "sRed rows overlap");
+template <int CH> constexpr int kRedFloats = 32 * kRedBlock<CH>;
+static_assert((kFH - 1) * kRedRow<16> + 16 <= kRedBlock<16>, "sRed rows overlap");
+static_assert((kFH - 1) * kRedRow<32> + 32 <= kRedBlock<32>, "sRed rows overlap");
 
 template <typename T>
 __device__ __forceinline__ void unpack2(const RawVec<T, 2> &r, float &a, float &b) {
@@ -275,50 +279,132 @@ struct FastWs {
     float *partC;
 };
 
-// Sequence segments. A launch covers the units (batch row, 16-channel block) unit0, unit0 + 1, ...
-// (unit = b * dim / 16 + d0 / 16), each as n_seg segments of seg_tiles tiles. With n_seg > 1 the
+// Sequence segments. A launch covers the units (batch row, CH-channel block) unit0, unit0 + 1, ...
+// (unit = b * dim / CH + d0 / CH), each as n_seg segments of seg_tiles tiles. With n_seg > 1 the
 // CARRY launch walks segments 1 .. n_seg-1 of each unit from a zero adjoint and stores, per channel
 // and state, (a_t0 gh_t0, prod of a over the segment): the adjoint the segment hands to the one
 // before it, and the factor that carries a later adjoint through it. The gradient launch then
 // starts each segment from the combination of those of the segments after it.
+//
+// The CARRY launch also reduces the dB/dC slab rows that the whole-row launch before it completed:
+// its workgroups past carry_blocks sum rows [0, red_rows) of both slabs over their n_blocks channel
+// blocks, memory-bound work beside the carries' latency-bound walks.
 struct BwdSeg {
     int64_t unit0;
     int64_t n_seg;
     int64_t seg_tiles;
-    float2 *carry;      // [unit - unit0][n_seg][16 channels][16 states]
+    float2 *carry;      // [unit - unit0][n_seg][CH channels][16 states]
+    int64_t carry_blocks, red_rows, n_blocks;
 };
+
+// dB or dC rows [row0, row1) (row = (b * n_groups + g) * 16 + n), by workgroup wg of n_wg, each of
+// NTH lanes: an element is four steps of a row, the sum of its n_blocks channel-block partials. The
+// blocks are split into K contiguous ranges summed by separate lanes (with K > 1 a short row range
+// still keeps enough loads in flight), each range in block order, and the range sums added in range
+// order through `scratch` (NTH float4, unused with K = 1). Each element is reduced by one call, whose
+// K the plan fixes, so the result is deterministic.
+constexpr int kRedChunks = 8;
+template <int NTH, int K>
+__device__ __forceinline__ void reduce_slab_rows(const mm_scan_bwd_params &p, const float *part, float *dst,
+                                                 int64_t bs, int64_t gs, int64_t ns, int64_t n_blocks, int64_t row0,
+                                                 int64_t row1, int64_t wg, int64_t n_wg, float4 *scratch) {
+    constexpr int E = NTH / K;   // elements per workgroup pass
+    const int tid = threadIdx.x, e = tid % E, k = tid / E;
+    const int64_t L4 = p.seqlen / 4;
+    const int64_t st = p.batch * p.n_groups * 16 * p.seqlen / 4;   // one block's slab, in float4
+    const int64_t b_lo = n_blocks * k / K, b_hi = n_blocks * (k + 1) / K;
+    const int64_t end = row1 * L4;
+    for (int64_t base = row0 * L4 + wg * E; base < end; base += n_wg * E) {   // uniform over the workgroup
+        const int64_t i = base + e;
+        const int64_t row = i / L4, t4 = i - row * L4;
+        // Slab rows past dstate (P/Q with dstate < 16) are not written.
+        const bool live = i < end && row % 16 < p.dstate;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (live) {
+            const float4 *src = reinterpret_cast<const float4 *>(part + row * p.seqlen) + t4;
+            int64_t blk = b_lo;
+            for (; blk + 8 <= b_hi; blk += 8) {   // eight loads in flight, added in block order
+                float4 v[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) v[q] = src[(blk + q) * st];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    acc.x += v[q].x; acc.y += v[q].y; acc.z += v[q].z; acc.w += v[q].w;
+                }
+            }
+            for (; blk < b_hi; ++blk) {
+                const float4 v = src[blk * st];
+                acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+            }
+        }
+        if constexpr (K > 1) {
+            scratch[k * E + e] = acc;
+            __syncthreads();
+        }
+        if (k == 0 && live) {
+#pragma unroll
+            for (int kk = 1; kk < K; ++kk) {
+                const float4 v = scratch[kk * E + e];
+                acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+            }
+            const int64_t n = row % 16, bg = row / 16;
+            const int64_t gg = bg % p.n_groups, bb = bg / p.n_groups;
+            float *o = dst + bb * bs + gg * gs + n * ns + 4 * t4;
+            o[0] = acc.x; o[1] = acc.y; o[2] = acc.z; o[3] = acc.w;
+        }
+        if constexpr (K > 1) __syncthreads();   // scratch reads done before the next pass rewrites it
+    }
+}
+
+// B/C staging of one tile: the first kStageLanes<CH> lanes each load kStageVals<CH> consecutive steps
+// of one state of B (first half of them) or C (second half): 2 x 16 states x 16 steps in all.
+template <int CH> constexpr int kStageLanes = 8 * CH < 256 ? 8 * CH : 256;
+template <int CH> constexpr int kStageVals = 512 / kStageLanes<CH>;
 
 // Global data of one tile for one lane, loaded a tile ahead of its use.
-template <typename T>
+template <typename T, int CH>
 struct TileRaw {
-    RawVec<T, 2> d, u, go, z, o;   // this lane's two steps of one channel
-    RawVec<T, 2> bc0, bc1;         // four B or C values of one state
-    float2 hc;                     // checkpoint of the lane's two states (pass 2)
+    RawVec<T, 2> d, u, go, z, o;             // this lane's two steps of one channel
+    RawVec<T, 2> bc[kStageVals<CH> / 2];     // B or C values of one state (staging lanes)
+    float2 hc;                               // checkpoint of the lane's two states (pass 2)
 };
 
-template <typename T, bool CARRY>
-__global__ void __launch_bounds__(128)
+// CH channels (16 or 32) x 16 states per workgroup of 8 CH lanes.
+template <typename T, bool CARRY, int CH>
+__global__ void __launch_bounds__(8 * CH)
 scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws, const BwdSeg sg) {
-    __shared__ __align__(16) float4 sX[kBufs][16 * kXS];    // [buf][c][t]: (dt', dt'u, u, g)
-    __shared__ __align__(16) float sBC[kBufs][kFT * kBCS];   // [buf][t][B 16 | C 16 | pad]
-    __shared__ __align__(16) float sRed[kRedFloats];         // red_at(tensor, n, t, c)
-    __shared__ __align__(16) float sPart[8 * 2 * 16 * kPS];  // [slot][gh B | ddt][c][t]
+    constexpr int NT = 8 * CH;
+    constexpr int SL = kStageLanes<CH>, SV = kStageVals<CH>;
+    __shared__ __align__(16) float4 sX[kBufs][CH * kXS];       // [buf][c][t]: (dt', dt'u, u, g)
+    __shared__ __align__(16) float sBC[kBufs][kFT * kBCS];      // [buf][t][B 16 | C 16 | pad]
+    __shared__ __align__(16) float sRed[kRedFloats<CH>];        // red_at<CH>(tensor, n, t, c)
+    __shared__ __align__(16) float sPart[8 * 2 * CH * kPS];     // [slot][gh B | ddt][c][t]
 
     const int tid = threadIdx.x;
-    const int rs = tid >> 4;               // state slot: states 2 rs, 2 rs + 1; prologue steps 2 rs, 2 rs + 1
-    const int c = tid & 15;                // channel within the block
+    if constexpr (CARRY) {
+        if (int64_t(blockIdx.x) >= sg.carry_blocks) {   // a slab-reduction workgroup: one lane per element
+            const int64_t wg = int64_t(blockIdx.x) - sg.carry_blocks, n_wg = int64_t(gridDim.x) - sg.carry_blocks;
+            reduce_slab_rows<NT, 1>(p, ws.partB, p.dB, p.dB_batch_stride, p.dB_group_stride, p.dB_dstate_stride,
+                                    sg.n_blocks, 0, sg.red_rows, wg, n_wg, nullptr);
+            reduce_slab_rows<NT, 1>(p, ws.partC, p.dC, p.dC_batch_stride, p.dC_group_stride, p.dC_dstate_stride,
+                                    sg.n_blocks, 0, sg.red_rows, wg, n_wg, nullptr);
+            return;
+        }
+    }
+    const int rs = tid / CH;               // state slot: states 2 rs, 2 rs + 1; prologue steps 2 rs, 2 rs + 1
+    const int c = tid % CH;                // channel within the block
     const int n0 = 2 * rs;
     const int pswz = (c >> 2) & 3;         // sPart step-pair permutation of this channel
     // The CARRY launch walks segments 1 .. n_seg-1 (segment 0 hands nothing on).
     const int64_t nsw = CARRY ? sg.n_seg - 1 : sg.n_seg;
     const int64_t uo = int64_t(blockIdx.x) / nsw;
     const int64_t seg = int64_t(blockIdx.x) - uo * nsw + (CARRY ? 1 : 0);
-    const int64_t per_b = p.dim / 16;
+    const int64_t per_b = p.dim / CH;
     const int64_t b = (sg.unit0 + uo) / per_b;
-    const int64_t d0 = (sg.unit0 + uo - b * per_b) * 16;
+    const int64_t d0 = (sg.unit0 + uo - b * per_b) * CH;
     const int64_t d = d0 + c;
     const int64_t g = d0 / ratio;
-    const int64_t blk = (d0 - g * ratio) / 16;
+    const int64_t blk = (d0 - g * ratio) / CH;
     const int64_t L = p.seqlen;
     const int64_t n_tiles = (L + kFT - 1) / kFT;
     const int64_t j_lo = seg * sg.seg_tiles;
@@ -333,8 +419,10 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     T *ddp = reinterpret_cast<T *>(p.ddelta) + b * p.ddelta_batch_stride + d * p.ddelta_d_stride;
     T *dzp = p.z ? reinterpret_cast<T *>(p.dz) + b * p.dz_batch_stride + d * p.dz_d_stride : nullptr;
     T *ozp = (p.z && p.out_z) ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
-    // B/C staging: lane -> tensor tid / 64, state (tid / 4) % 16, steps 4 (tid % 4) .. +3 of the tile.
-    const int st_tensor = tid >> 6, st_n = (tid >> 2) & 15, st_q = tid & 3;
+    // B/C staging (lanes tid < SL): lane -> tensor tid / (SL / 2), state, steps SV q .. SV q + SV - 1.
+    const bool stager = tid < SL;
+    const int st_li = tid % (SL / 2);
+    const int st_tensor = (tid / (SL / 2)) & 1, st_n = st_li / (16 / SV), st_q = st_li % (16 / SV);
     const T *stp = st_tensor == 0
         ? reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + st_n * p.B_dstate_stride
         : reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + st_n * p.C_dstate_stride;
@@ -350,7 +438,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     // Loads of tile j (clamped into the row: always in bounds). Steps past L are padding, made
     // inert in commit(): dt' = g = 0 and B = C = 0 leave every state and gradient unchanged.
     auto load = [&](int64_t j, bool full) {
-        TileRaw<T> r;
+        TileRaw<T, CH> r;
         const int64_t jj = j < 0 ? 0 : (j >= n_tiles ? n_tiles - 1 : j);
         const int64_t te = jj * kFT + 2 * rs;
         const int64_t tl = te < L ? te : L - 2;
@@ -366,13 +454,13 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 r.o = load_raw<T, 2>(outp + tl);
             }
         }
-        const int64_t ts0 = jj * kFT + 4 * st_q;
-        const int64_t ts = ts0 < L ? ts0 : L - 4;
-        r.bc0 = {};
-        r.bc1 = {};
-        if (full || st_tensor == 0) {
-            r.bc0 = load_raw<T, 2>(stp + ts);
-            r.bc1 = load_raw<T, 2>(stp + ts + 2);
+        const int64_t ts0 = jj * kFT + SV * st_q;
+        const int64_t ts = ts0 < L ? ts0 : L - SV;
+#pragma unroll
+        for (int i = 0; i < SV / 2; ++i) r.bc[i] = {};
+        if (stager && (full || st_tensor == 0)) {
+#pragma unroll
+            for (int i = 0; i < SV / 2; ++i) r.bc[i] = load_raw<T, 2>(stp + ts + 2 * i);
         }
         r.hc = full ? *reinterpret_cast<const float2 *>(ckp + jj * ck_tile) : make_float2(0.f, 0.f);
         return r;
@@ -380,7 +468,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     // Tile j's per-step values into LDS buffer `buf`; the lane's own steps kept for the epilogue;
     // dz (and out_z) written.
     float e_raw[2], e_dt[2], e_u[2], e_g[2];
-    auto commit = [&](const TileRaw<T> &r, int64_t j, int buf, bool full) {
+    auto commit = [&](const TileRaw<T, CH> &r, int64_t j, int buf, bool full) {
         const int64_t te = j * kFT + 2 * rs;
         const bool ev = te < L;            // L is a multiple of 8: both steps exist or neither
         float dd[2], go[2] = {0.f, 0.f};
@@ -412,19 +500,21 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             e_g[i] = ev ? go[i] : 0.f;
             sX[buf][c * kXS + 2 * rs + i] = make_float4(e_dt[i], e_dt[i] * e_u[i], e_u[i], e_g[i]);
         }
-        const bool bv_ok = j * kFT + 4 * st_q < L;   // L is a multiple of 4: the four exist or none do
-        float v[4];
-        unpack2<T>(r.bc0, v[0], v[1]);
-        unpack2<T>(r.bc1, v[2], v[3]);
+        if (stager) {
+            const bool bv_ok = j * kFT + SV * st_q < L;   // L is a multiple of 8: all SV exist or none do
+            float v[SV];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sBC[buf][(4 * st_q + i) * kBCS + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
+            for (int i = 0; i < SV / 2; ++i) unpack2<T>(r.bc[i], v[2 * i], v[2 * i + 1]);
+#pragma unroll
+            for (int i = 0; i < SV; ++i) sBC[buf][(SV * st_q + i) * kBCS + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
+        }
     };
 
     if constexpr (CARRY) {
         // The segment's adjoint from a zero carry, gh_t = C_t g_t + a_{t+1} gh_{t+1}, and the
         // product of its decays. Steps past L (last segment only) have dt' = g = 0: a = 1, inert.
         float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f, pa0 = 1.f, pa1 = 1.f;
-        TileRaw<T> nx = load(j_hi - 1, true);
+        TileRaw<T, CH> nx = load(j_hi - 1, true);
         for (int64_t j = j_hi - 1; j >= j_lo; --j) {
             commit(nx, j, 0, true);
             nx = load(j - 1, true);
@@ -442,7 +532,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             }
             __syncthreads();   // reads done before the next commit rewrites the buffer
         }
-        float4 *cp = reinterpret_cast<float4 *>(sg.carry + ((uo * sg.n_seg + seg) * 16 + c) * 16 + n0);
+        float4 *cp = reinterpret_cast<float4 *>(sg.carry + ((uo * sg.n_seg + seg) * CH + c) * 16 + n0);
         *cp = make_float4(an0 * gh0, pa0, an1 * gh1, pa1);
         return;
     }
@@ -450,7 +540,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     // Pass 1: the states before every tile, into the checkpoint workspace (skipped when the
     // forward wrote them: ws.ck then points at its tile_states; segmented launches always have them).
     float h0 = 0.f, h1 = 0.f;
-    TileRaw<T> nxt = load(0, false);
+    TileRaw<T, CH> nxt = load(0, false);
     for (int64_t j = 0; j < (p.tile_states ? 0 : n_tiles); ++j) {
         const int buf = int(j % kBufs);
         *reinterpret_cast<float2 *>(ckp + j * ck_tile) = make_float2(h0, h1);
@@ -472,10 +562,10 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f;   // state adjoints, decays of the step after
     if (seg + 1 < sg.n_seg) {
         // The adjoint entering from the later segments: c_{S-1} = 0, c_{s-1} = e_s + P_s c_s.
-        const float4 *cp = reinterpret_cast<const float4 *>(sg.carry + ((uo * sg.n_seg) * 16 + c) * 16 + n0);
+        const float4 *cp = reinterpret_cast<const float4 *>(sg.carry + ((uo * sg.n_seg) * CH + c) * 16 + n0);
         float c0 = 0.f, c1 = 0.f;
         for (int64_t s2 = sg.n_seg - 1; s2 > seg; --s2) {
-            const float4 v = cp[s2 * 128];
+            const float4 v = cp[s2 * CH * 8];   // one segment: CH channels x 16 states x (e, P)
             c0 = __builtin_fmaf(v.y, c0, v.x);
             c1 = __builtin_fmaf(v.w, c1, v.z);
         }
@@ -488,8 +578,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     // Two tiles in flight: the loads of tile j - 2 are issued once tile j is committed. The two ring
     // entries keep their registers (the loop is unrolled by two below): a copy of an entry whose
     // loads are still in flight would wait for them.
-    TileRaw<T> ra = load(j_hi - 1, true), rb = load(j_hi - 2, true);
-    auto tile = [&](const int64_t j, TileRaw<T> &cur) {
+    TileRaw<T, CH> ra = load(j_hi - 1, true), rb = load(j_hi - 2, true);
+    auto tile = [&](const int64_t j, TileRaw<T, CH> &cur) {
         const int64_t t0 = j * kFT;
         const int buf = int(j % kBufs);
         const float2 hc = cur.hc;
@@ -525,10 +615,10 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 gh1 = __builtin_fmaf(an1, gh1, x.w * cv.y);
                 const float ah0 = __builtin_fmaf(-x.y, bv.x, hs0[t]);   // a_t h_{t-1}
                 const float ah1 = __builtin_fmaf(-x.y, bv.y, hs1[t]);
-                sRed[red_at(0, n0, s, c)] = gh0 * x.y;          // dB contributions
-                sRed[red_at(0, n0 + 1, s, c)] = gh1 * x.y;
-                sRed[red_at(1, n0, s, c)] = x.w * hs0[t];       // dC contributions
-                sRed[red_at(1, n0 + 1, s, c)] = x.w * hs1[t];
+                sRed[red_at<CH>(0, n0, s, c)] = gh0 * x.y;          // dB contributions
+                sRed[red_at<CH>(0, n0 + 1, s, c)] = gh1 * x.y;
+                sRed[red_at<CH>(1, n0, s, c)] = x.w * hs0[t];       // dC contributions
+                sRed[red_at<CH>(1, n0 + 1, s, c)] = x.w * hs1[t];
                 // sum_n gh (u B + A a h_{t-1}) = u sum_n gh B + sum_n A (gh a h_{t-1}); the products
                 // gh a h_{t-1} also give dA.
                 const float w0 = gh0 * ah0, w1 = gh1 * ah1;
@@ -542,30 +632,39 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             dA0 += dA_t0;
             dA1 += dA_t1;
             // sPart rows hold 4 step pairs; pair q of channel c sits at pair position q ^ pswz, so
-            // that the 16 channels one 64-bit LDS cycle serves hit 16 distinct bank pairs, for these
-            // stores and for the owners' reads below (8-float rows alone put 4 channels on each).
-            float2 *pp = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 0) * 16 + c) * kPS]);
-            float2 *pq = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 1) * 16 + c) * kPS]);
+            // that 16 consecutive channels (what one 64-bit LDS cycle serves) hit 16 distinct bank
+            // pairs, for these stores and for the owners' reads below (8-float rows alone put 4
+            // channels on each).
+            float2 *pp = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 0) * CH + c) * kPS]);
+            float2 *pq = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 1) * CH + c) * kPS]);
 #pragma unroll
             for (int q = 0; q < kFH / 2; ++q) {
                 pp[q ^ pswz] = make_float2(pu[2 * q], pu[2 * q + 1]);
                 pq[q ^ pswz] = make_float2(pd[2 * q], pd[2 * q + 1]);
             }
             __syncthreads();
-            // dB / dC of this half summed over the block's 16 channels: rows (tensor, state, step)
-            // tid and tid + 128, step fastest, so consecutive lanes read consecutive steps.
+            // dB / dC of this half summed over the block's CH channels: the 256 rows (tensor, state,
+            // step), step fastest, one per lane (two per lane with 128 lanes; lanes past 256 idle),
+            // so consecutive lanes read consecutive steps.
+            constexpr int kRowsPerLane = NT >= 256 ? 1 : 256 / NT;
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const int row = tid + 128 * k;
+            for (int k = 0; k < kRowsPerLane; ++k) {
+                const int row = tid + NT * k;
+                if (NT > 256 && row >= 256) break;
                 const int tz = row >> 7, tn = (row >> 3) & 15, tt = row & 7;
-                const float4 *rv = reinterpret_cast<const float4 *>(&sRed[red_at(tz, tn, tt, 0)]);
-                float q4[4];
+                const float4 *rv = reinterpret_cast<const float4 *>(&sRed[red_at<CH>(tz, tn, tt, 0)]);
+                float q4[CH / 4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {   // pairwise: short dependency chains, fixed order
+                for (int q = 0; q < CH / 4; ++q) {   // pairwise: short dependency chains, fixed order
                     const float4 v = rv[q];
                     q4[q] = (v.x + v.y) + (v.z + v.w);
                 }
-                const float acc = (q4[0] + q4[1]) + (q4[2] + q4[3]);
+#pragma unroll
+                for (int w = 1; w < CH / 4; w *= 2) {
+#pragma unroll
+                    for (int q = 0; q < CH / 4; q += 2 * w) q4[q] += q4[q + w];
+                }
+                const float acc = q4[0];
                 const int64_t ts = t0 + half * kFH + tt;
                 if (ts < L)
                     (tz == 0 ? ws.partB : ws.partC)[(((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * L + ts] = acc;
@@ -579,8 +678,8 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int pos = 2 * ((sl >> 1) ^ pswz);
-                    const float2 a = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 0) * 16 + c) * kPS + pos]);
-                    const float2 bq = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 1) * 16 + c) * kPS + pos]);
+                    const float2 a = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 0) * CH + c) * kPS + pos]);
+                    const float2 bq = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 1) * CH + c) * kPS + pos]);
                     su[0] += a.x; su[1] += a.y;
                     sd[0] += bq.x; sd[1] += bq.y;
                 }
@@ -611,40 +710,16 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     if (p.ddelta_bias) atomicAdd(p.ddelta_bias + d, dbias_acc);
 }
 
-// dB / dC = the sum of the channel blocks' partials, in block order (deterministic).
+// dB and dC rows [row0, all) = the sums of the channel blocks' partials, in a fixed order.
 __global__ void __launch_bounds__(256)
-scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *part, float *dst, int64_t bs, int64_t gs, int64_t ns,
-                   int64_t n_blocks) {
-    const int64_t L4 = p.seqlen / 4;
+scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *partB, const float *partC, int64_t n_blocks,
+                   int64_t row0) {
+    __shared__ float4 scratch[256];
     const int64_t rows = p.batch * p.n_groups * 16;
-    const int64_t total = rows * L4;
-    const int64_t slice = rows * p.seqlen;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-        const int64_t row = i / L4, t4 = i - row * L4;
-        if (row % 16 >= p.dstate) continue;   // slab rows past dstate (P/Q with dstate < 16) are not written
-        const float4 *src = reinterpret_cast<const float4 *>(part + row * p.seqlen) + t4;
-        const int64_t st = slice / 4;
-        float4 acc = src[0];
-        int64_t k = 1;
-        // Eight loads in flight per lane, added in block order (the sum stays deterministic).
-        for (; k + 8 <= n_blocks; k += 8) {
-            float4 v[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = src[(k + i) * st];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                acc.x += v[i].x; acc.y += v[i].y; acc.z += v[i].z; acc.w += v[i].w;
-            }
-        }
-        for (; k < n_blocks; ++k) {
-            const float4 v = src[k * st];
-            acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
-        }
-        const int64_t n = row % 16, bg = row / 16;
-        const int64_t gg = bg % p.n_groups, bb = bg / p.n_groups;
-        float *o = dst + bb * bs + gg * gs + n * ns + 4 * t4;
-        o[0] = acc.x; o[1] = acc.y; o[2] = acc.z; o[3] = acc.w;
-    }
+    reduce_slab_rows<256, kRedChunks>(p, partB, p.dB, p.dB_batch_stride, p.dB_group_stride, p.dB_dstate_stride,
+                                      n_blocks, row0, rows, blockIdx.x, gridDim.x, scratch);
+    reduce_slab_rows<256, kRedChunks>(p, partC, p.dC, p.dC_batch_stride, p.dC_group_stride, p.dC_dstate_stride,
+                                      n_blocks, row0, rows, blockIdx.x, gridDim.x, scratch);
 }
 
 template <typename T>
@@ -716,9 +791,10 @@ int64_t fast_part_floats(const mm_scan_bwd_params &p) {
     return (p.dim / 16) * p.batch * 16 * p.seqlen;   // blocks per group x groups = dim / 16
 }
 
-// Workgroups of scan_bwd_tiled16<T> that the current device runs at once (one round), or 0 when the
-// device cannot be queried. MM_BWD_SLOTS overrides it (tests exercise the segmented tail with it).
-template <typename T>
+// Workgroups of scan_bwd_tiled16<T, false, CH> that the current device runs at once (one round), or
+// 0 when the device cannot be queried. MM_BWD_SLOTS overrides it (tests exercise the segmented tail
+// with it).
+template <typename T, int CH>
 int64_t round_slots() {
     if (const char *e = std::getenv("MM_BWD_SLOTS")) {
         const long long v = std::atoll(e);
@@ -731,29 +807,58 @@ int64_t round_slots() {
     if (v == 0) {
         int cus = 0, per_cu = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, scan_bwd_tiled16<T, false>, 128, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, scan_bwd_tiled16<T, false, CH>, 8 * CH, 0) !=
+            hipSuccess)
             return 0;
         v = int64_t(cus) * per_cu;
         cache[dev].store(v, std::memory_order_relaxed);
     }
     return v;
 }
+template <typename T>
+int64_t round_slots_ch(int ch) {
+    return ch == 32 ? round_slots<T, 32>() : round_slots<T, 16>();
+}
+
+// Channels per workgroup. Every workgroup writes its own dB/dC partial slab (16 x L floats per
+// tensor and batch row), which the reduction reads back, so wider workgroups move fewer bytes: at
+// the Mamba-2.8B layer shape the 16-channel slabs (670 MB) exceed the 256 MB Infinity Cache. 32
+// channels are taken when the group's channels divide into 32-channel blocks and those fill at
+// least one whole round (two 32-channel workgroups share a CU where four 16-channel ones do, and
+// a partial round of them costs more); otherwise 16. MM_BWD_CH=16/32 forces a width the group
+// allows.
+template <typename T>
+int pick_ch(const mm_scan_bwd_params &p) {
+    const int64_t ratio = p.dim / p.n_groups;
+    if (const char *e = std::getenv("MM_BWD_CH")) {
+        const int v = std::atoi(e);
+        if ((v == 16 || v == 32) && ratio % v == 0) return v;
+    }
+    if (ratio % 32 == 0) {
+        const int64_t slots = round_slots_ch<T>(32);
+        if (slots > 0 && p.batch * (p.dim / 32) >= slots) return 32;
+    }
+    return 16;
+}
 
 // How the dstate-16 backward covers its units. The kernel is latency-bound, so a last round with
 // few workgroups per CU costs nearly as much as a full one. With the forward's tile states the
 // units of that last round (or all of them, when they fill at most half a round) are instead cut
 // along the sequence into n_seg segments, enough to fill a round, joined by a carry pass.
+// A unit is (batch row, block of ch channels).
 struct SegPlan {
     int64_t main_units, tail_units, n_seg, seg_tiles;
+    int ch;
 };
 template <typename T>
 SegPlan seg_plan(const mm_scan_bwd_params &p) {
-    const int64_t units = p.batch * (p.dim / 16);
+    const int ch = pick_ch<T>(p);
+    const int64_t units = p.batch * (p.dim / ch);
     const int64_t n_tiles = (p.seqlen + kFT - 1) / kFT;
-    const SegPlan whole{units, 0, 1, n_tiles};
+    const SegPlan whole{units, 0, 1, n_tiles, ch};
     const char *off = std::getenv("MM_BWD_SEGMENTS");
     if (!p.tile_states || (off && off[0] == '0')) return whole;
-    const int64_t slots = round_slots<T>();
+    const int64_t slots = round_slots_ch<T>(ch);
     if (slots <= 0 || units == 0) return whole;
     const int64_t tail = units % slots;
     if (tail == 0) return whole;
@@ -762,14 +867,14 @@ SegPlan seg_plan(const mm_scan_bwd_params &p) {
     const int64_t seg_tiles = (n_tiles + n_seg - 1) / n_seg;
     n_seg = (n_tiles + seg_tiles - 1) / seg_tiles;   // every segment holds at least one tile
     if (n_seg < 2) return whole;
-    return {units - tail, tail, n_seg, seg_tiles};
+    return {units - tail, tail, n_seg, seg_tiles, ch};
 }
 SegPlan seg_plan_for(const mm_scan_bwd_params &p) {
     if (p.itype == MM_FLOAT32) return seg_plan<float>(p);
     if (p.itype == MM_FLOAT16) return seg_plan<f16_t>(p);
     return seg_plan<bf16_t>(p);
 }
-int64_t carry_floats(const SegPlan &pl) { return pl.tail_units * pl.n_seg * 16 * 16 * 2; }
+int64_t carry_floats(const SegPlan &pl) { return pl.tail_units * pl.n_seg * pl.ch * 16 * 2; }
 
 // The forward parameter block of the states-only pass the backward runs when no tile states were
 // handed to it: the scan's inputs, no outputs, tile_states = the checkpoint region `ck`.
@@ -810,6 +915,52 @@ bool states_pass_ok(const mm_scan_bwd_params &p) {
     return seg_plan_for(q).tail_units > 0;
 }
 
+// dB and dC rows [row0, all): the n_blocks channel-block partials of each element summed in a fixed
+// order, one launch.
+int launch_reduce(const mm_scan_bwd_params &p, hipStream_t s, const float *partB, const float *partC,
+                  int64_t n_blocks, int64_t row0) {
+    const int64_t total = (p.batch * p.n_groups * 16 - row0) * (p.seqlen / 4);
+    if (total <= 0) return MM_OK;
+    constexpr int64_t per_wg = 256 / kRedChunks;   // elements per workgroup pass
+    const unsigned blocks = unsigned(std::min<int64_t>((total + per_wg - 1) / per_wg, 8192));
+    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partB, partC, n_blocks, row0);
+    return launch_status("scan_bwd_reduce_bc");
+}
+
+// The launches of the dstate-16 kernel with CH channels per workgroup: the whole rows of the full
+// rounds, then (segmented tail) the carries and every segment of the cut units. *red_rows returns
+// the dB/dC slab rows already reduced (by the carry launch): those of the (batch, group) pairs whose
+// units all ran in the whole-row launch.
+template <typename T, int CH>
+int launch_units(const mm_scan_bwd_params &p, hipStream_t s, int64_t ratio, const FastWs &fw, const SegPlan &pl,
+                 float *carry, int64_t *red_rows) {
+    int rc = MM_OK;
+    *red_rows = 0;
+    if (pl.main_units > 0) {
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH>), dim3(unsigned(pl.main_units)), dim3(8 * CH), 0, s, p,
+                           ratio, fw, BwdSeg{0, 1, (p.seqlen + kFT - 1) / kFT, nullptr, 0, 0, 0});
+        rc = launch_status("scan_bwd_tiled16");
+        if (rc != MM_OK) return rc;
+    }
+    if (pl.tail_units > 0) {
+        // Units run (batch, group)-major: the pairs below main_units / (blocks per group) are complete.
+        const int64_t rows = pl.main_units / (ratio / CH) * 16;
+        const int64_t carry_blocks = pl.tail_units * (pl.n_seg - 1);
+        const int64_t red_blocks = std::min<int64_t>((rows * (p.seqlen / 4) + 8 * CH - 1) / (8 * CH), 8192);
+        const BwdSeg sg{pl.main_units, pl.n_seg, pl.seg_tiles, reinterpret_cast<float2 *>(carry), carry_blocks, rows,
+                        ratio / CH};
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, true, CH>), dim3(unsigned(carry_blocks + red_blocks)), dim3(8 * CH),
+                           0, s, p, ratio, fw, sg);
+        rc = launch_status("scan_bwd_tiled16 (carries)");
+        if (rc != MM_OK) return rc;
+        *red_rows = rows;
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH>), dim3(unsigned(pl.tail_units * pl.n_seg)), dim3(8 * CH),
+                           0, s, p, ratio, fw, sg);
+        rc = launch_status("scan_bwd_tiled16 (segments)");
+    }
+    return rc;
+}
+
 template <typename T>
 int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
     float *ws = static_cast<float *>(p_in.workspace);
@@ -835,35 +986,12 @@ int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
     // A workspace without room for the segment carries (sized by bwd_workspace_min_bytes, or queried
     // under another round size: MM_BWD_SLOTS or another device) runs every unit as a whole row.
     if (pl.tail_units > 0 && p.workspace_bytes < need)
-        pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT};
-    int rc = MM_OK;
-    if (pl.main_units > 0) {
-        hipLaunchKernelGGL((scan_bwd_tiled16<T, false>), dim3(unsigned(pl.main_units)), dim3(128), 0, s, p, ratio,
-                           fw, BwdSeg{0, 1, (p.seqlen + kFT - 1) / kFT, nullptr});
-        rc = launch_status("scan_bwd_tiled16");
-        if (rc != MM_OK) return rc;
-    }
-    if (pl.tail_units > 0) {
-        const BwdSeg sg{pl.main_units, pl.n_seg, pl.seg_tiles,
-                        reinterpret_cast<float2 *>(partB + 2 * fast_part_floats(p))};
-        hipLaunchKernelGGL((scan_bwd_tiled16<T, true>), dim3(unsigned(pl.tail_units * (pl.n_seg - 1))), dim3(128), 0,
-                           s, p, ratio, fw, sg);
-        rc = launch_status("scan_bwd_tiled16 (carries)");
-        if (rc != MM_OK) return rc;
-        hipLaunchKernelGGL((scan_bwd_tiled16<T, false>), dim3(unsigned(pl.tail_units * pl.n_seg)), dim3(128), 0, s,
-                           p, ratio, fw, sg);
-        rc = launch_status("scan_bwd_tiled16 (segments)");
-        if (rc != MM_OK) return rc;
-    }
-    const int64_t total = p.batch * p.n_groups * 16 * (p.seqlen / 4);
-    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 8192));
-    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, fw.partB, p.dB, p.dB_batch_stride,
-                       p.dB_group_stride, p.dB_dstate_stride, ratio / 16);
-    rc = launch_status("scan_bwd_reduce_bc");
+        pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT, pl.ch};
+    int64_t red_rows = 0;
+    const int rc = pl.ch == 32 ? launch_units<T, 32>(p, s, ratio, fw, pl, partB + 2 * fast_part_floats(p), &red_rows)
+                               : launch_units<T, 16>(p, s, ratio, fw, pl, partB + 2 * fast_part_floats(p), &red_rows);
     if (rc != MM_OK) return rc;
-    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, fw.partC, p.dC, p.dC_batch_stride,
-                       p.dC_group_stride, p.dC_dstate_stride, ratio / 16);
-    return launch_status("scan_bwd_reduce_bc");
+    return launch_reduce(p, s, fw.partB, fw.partC, ratio / pl.ch, red_rows);
 }
 
 // The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
@@ -873,20 +1001,11 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
     float *ws = static_cast<float *>(p.workspace);
     float *ck = p.tile_states ? const_cast<float *>(p.tile_states) : ws;
     float *partB = p.tile_states ? ws : ws + fast_ck_floats(p), *partC = partB + fast_part_floats(p);
-    int rc = launch_pq_bwd<T>(p, s, ck, partB, partC);
+    const int rc = launch_pq_bwd<T>(p, s, ck, partB, partC);
     if (rc != MM_OK) return rc;
     // Slab rows past dstate are never written; the reduction reads only rows n < 16 of each slab
     // and writes rows n < dstate (dB / dC hold dstate rows).
-    const int64_t ratio = p.dim / p.n_groups;
-    const int64_t total = p.batch * p.n_groups * 16 * (p.seqlen / 4);
-    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 8192));
-    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partB, p.dB, p.dB_batch_stride,
-                       p.dB_group_stride, p.dB_dstate_stride, ratio / 16);
-    rc = launch_status("scan_bwd_reduce_bc");
-    if (rc != MM_OK) return rc;
-    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partC, p.dC, p.dC_batch_stride,
-                       p.dC_group_stride, p.dC_dstate_stride, ratio / 16);
-    return launch_status("scan_bwd_reduce_bc");
+    return launch_reduce(p, s, partB, partC, p.dim / p.n_groups / 16, 0);
 }
 
 }  // namespace bwd

@@ -368,6 +368,48 @@ def test_bwd_states_pass(dtype, slots, L, monkeypatch):
                                    msg=lambda m: f"{name}: {m}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ch,slots", [(32, 6)])
+def test_bwd_channel_widths(dtype, ch, slots, monkeypatch):
+    """The dstate-16 backward with 32- or 64-channel workgroups (MM_BWD_CH; one dB/dC partial slab
+    per block of ch channels) on 2 x 128 channels, L 1000 (a padded last tile): against the exact
+    gradients through autograd, and against the 16-channel kernel on the same inputs -- whole rows,
+    a segmented last round (MM_BWD_SLOTS: 8 units as 6 whole + 2 cut for ch 32, 4 units as 3 whole
+    + 1 cut for ch 64) and without tile states."""
+    _say(f"bwd channel width {ch} slots={slots} {dtype}")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(720 + ch, 2, 128, 1000, 16, dtype, bkind="4d", G=1)
+    dout = _dout(721, (2, 128, 1000), dtype)
+    monkeypatch.setenv("MM_BWD_CH", str(ch))
+    _vs_exact(case, dout, dtype, f"ch={ch}")
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+    out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    d = dout.to(DEV)
+    runs = {}
+    for width in (ch, 16):
+        monkeypatch.setenv("MM_BWD_CH", str(width))
+        monkeypatch.setenv("MM_BWD_SLOTS", str(slots))
+        monkeypatch.delenv("MM_BWD_SEGMENTS", raising=False)
+        runs[width, "seg"] = ext.bwd(*args, d, x, out, None, None, None, True, False, ck)
+        runs[width, "none"] = ext.bwd(*args, d, x, out, None, None, None, True, False)
+        monkeypatch.setenv("MM_BWD_SEGMENTS", "0")
+        runs[width, "whole"] = ext.bwd(*args, d, x, out, None, None, None, True, False, ck)
+    torch.cuda.synchronize()
+    rtol = 1e-5 if dtype == torch.float32 else 1e-2
+    names = ["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"]
+    for kind in ("seg", "none", "whole"):
+        for name, a, b in zip(names, runs[ch, kind], runs[16, kind]):
+            scale = max(1.0, b.abs().max().item())
+            torch.testing.assert_close(a.float(), b.float(), rtol=rtol, atol=rtol * 0.1 * scale,
+                                       msg=lambda m: f"{kind} {name}: {m}")
+    # Whole rows at both widths walk the same steps in the same order: du, ddelta and dz agree bit
+    # for bit (only the dB/dC block sums and the atomics are grouped differently).
+    for i in (0, 1, 7):
+        assert torch.equal(runs[ch, "whole"][i], runs[16, "whole"][i]), names[i]
+
+
 def test_training_step_graph_replay_matches_eager():
     """The training forward (with tile states) and the backward captured in one HIP graph: the
     workspace and outputs come from the graph's memory pool and the clears are fill kernels, so
