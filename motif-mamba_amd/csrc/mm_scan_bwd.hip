@@ -293,7 +293,8 @@ struct BwdSeg {
     int64_t unit0;
     int64_t n_seg;
     int64_t seg_tiles;
-    float2 *carry;      // [unit - unit0][n_seg][CH channels][16 states]
+    float2 *carry;      // [unit - unit0][n_seg * csplit][CH channels][16 states]
+    int64_t csplit;     // carry pieces per segment
     int64_t carry_blocks, red_rows, n_blocks;
 };
 
@@ -395,10 +396,11 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const int c = tid % CH;                // channel within the block
     const int n0 = 2 * rs;
     const int pswz = (c >> 2) & 3;         // sPart step-pair permutation of this channel
-    // The CARRY launch walks segments 1 .. n_seg-1 (segment 0 hands nothing on).
-    const int64_t nsw = CARRY ? sg.n_seg - 1 : sg.n_seg;
+    // The CARRY launch walks segments 1 .. n_seg-1 (segment 0 hands nothing on), each as csplit
+    // pieces: piece cs is part cs % csplit of segment cs / csplit.
+    const int64_t nsw = CARRY ? (sg.n_seg - 1) * sg.csplit : sg.n_seg;
     const int64_t uo = int64_t(blockIdx.x) / nsw;
-    const int64_t seg = int64_t(blockIdx.x) - uo * nsw + (CARRY ? 1 : 0);
+    const int64_t seg = int64_t(blockIdx.x) - uo * nsw + (CARRY ? sg.csplit : 0);   // CARRY: the piece cs
     const int64_t per_b = p.dim / CH;
     const int64_t b = (sg.unit0 + uo) / per_b;
     const int64_t d0 = (sg.unit0 + uo - b * per_b) * CH;
@@ -407,8 +409,15 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const int64_t blk = (d0 - g * ratio) / CH;
     const int64_t L = p.seqlen;
     const int64_t n_tiles = (L + kFT - 1) / kFT;
-    const int64_t j_lo = seg * sg.seg_tiles;
-    const int64_t j_hi = j_lo + sg.seg_tiles < n_tiles ? j_lo + sg.seg_tiles : n_tiles;
+    int64_t j_lo = seg * sg.seg_tiles;
+    int64_t j_hi = j_lo + sg.seg_tiles < n_tiles ? j_lo + sg.seg_tiles : n_tiles;
+    if constexpr (CARRY) {   // the tiles of piece seg (empty when the segment is short)
+        const int64_t s_lo = (seg / sg.csplit) * sg.seg_tiles;
+        const int64_t s_hi = s_lo + sg.seg_tiles < n_tiles ? s_lo + sg.seg_tiles : n_tiles;
+        const int64_t piece = (sg.seg_tiles + sg.csplit - 1) / sg.csplit;
+        j_lo = std::min(s_lo + (seg % sg.csplit) * piece, s_hi);
+        j_hi = std::min(j_lo + piece, s_hi);
+    }
 
     const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
     const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
@@ -532,7 +541,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             }
             __syncthreads();   // reads done before the next commit rewrites the buffer
         }
-        float4 *cp = reinterpret_cast<float4 *>(sg.carry + ((uo * sg.n_seg + seg) * CH + c) * 16 + n0);
+        float4 *cp = reinterpret_cast<float4 *>(sg.carry + ((uo * sg.n_seg * sg.csplit + seg) * CH + c) * 16 + n0);
         *cp = make_float4(an0 * gh0, pa0, an1 * gh1, pa1);
         return;
     }
@@ -562,9 +571,12 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     float gh0 = 0.f, gh1 = 0.f, an0 = 0.f, an1 = 0.f;   // state adjoints, decays of the step after
     if (seg + 1 < sg.n_seg) {
         // The adjoint entering from the later segments: c_{S-1} = 0, c_{s-1} = e_s + P_s c_s.
-        const float4 *cp = reinterpret_cast<const float4 *>(sg.carry + ((uo * sg.n_seg) * CH + c) * 16 + n0);
+        // Pieces compose like segments (c entering a piece = e + P c leaving it), so the carry is
+        // the same chain over the pieces of the later segments.
+        const float4 *cp =
+            reinterpret_cast<const float4 *>(sg.carry + ((uo * sg.n_seg * sg.csplit) * CH + c) * 16 + n0);
         float c0 = 0.f, c1 = 0.f;
-        for (int64_t s2 = sg.n_seg - 1; s2 > seg; --s2) {
+        for (int64_t s2 = sg.n_seg * sg.csplit - 1; s2 >= (seg + 1) * sg.csplit; --s2) {
             const float4 v = cp[s2 * CH * 8];   // one segment: CH channels x 16 states x (e, P)
             c0 = __builtin_fmaf(v.y, c0, v.x);
             c1 = __builtin_fmaf(v.w, c1, v.z);
@@ -710,12 +722,11 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     if (p.ddelta_bias) atomicAdd(p.ddelta_bias + d, dbias_acc);
 }
 
-// dB and dC rows [row0, all) = the sums of the channel blocks' partials, in a fixed order.
+// dB and dC rows [row0, rows) = the sums of the channel blocks' partials, in a fixed order.
 __global__ void __launch_bounds__(256)
 scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *partB, const float *partC, int64_t n_blocks,
-                   int64_t row0) {
+                   int64_t row0, int64_t rows) {
     __shared__ float4 scratch[256];
-    const int64_t rows = p.batch * p.n_groups * 16;
     reduce_slab_rows<256, kRedChunks>(p, partB, p.dB, p.dB_batch_stride, p.dB_group_stride, p.dB_dstate_stride,
                                       n_blocks, row0, rows, blockIdx.x, gridDim.x, scratch);
     reduce_slab_rows<256, kRedChunks>(p, partC, p.dC, p.dC_batch_stride, p.dC_group_stride, p.dC_dstate_stride,
@@ -849,13 +860,14 @@ int pick_ch(const mm_scan_bwd_params &p) {
 struct SegPlan {
     int64_t main_units, tail_units, n_seg, seg_tiles;
     int ch;
+    int64_t csplit;   // carry pieces per segment (more, shorter carry walks)
 };
 template <typename T>
 SegPlan seg_plan(const mm_scan_bwd_params &p) {
     const int ch = pick_ch<T>(p);
     const int64_t units = p.batch * (p.dim / ch);
     const int64_t n_tiles = (p.seqlen + kFT - 1) / kFT;
-    const SegPlan whole{units, 0, 1, n_tiles, ch};
+    const SegPlan whole{units, 0, 1, n_tiles, ch, 1};
     const char *off = std::getenv("MM_BWD_SEGMENTS");
     if (!p.tile_states || (off && off[0] == '0')) return whole;
     const int64_t slots = round_slots_ch<T>(ch);
@@ -867,14 +879,22 @@ SegPlan seg_plan(const mm_scan_bwd_params &p) {
     const int64_t seg_tiles = (n_tiles + n_seg - 1) / n_seg;
     n_seg = (n_tiles + seg_tiles - 1) / seg_tiles;   // every segment holds at least one tile
     if (n_seg < 2) return whole;
-    return {units - tail, tail, n_seg, seg_tiles, ch};
+    // Two carry pieces per segment halve the carry launch's walk (config 2: 1.535 -> 1.505 ms; three
+    // or four pieces, more workgroups than one round holds, measured 1.53 and 1.52).
+    // MM_BWD_CARRY_SPLIT=n sets the count (tests cover uneven and empty pieces with it).
+    int64_t csplit = seg_tiles >= 8 ? 2 : 1;
+    if (const char *e = std::getenv("MM_BWD_CARRY_SPLIT")) {
+        const long long v = std::atoll(e);
+        if (v >= 1 && v <= 8) csplit = v;
+    }
+    return {units - tail, tail, n_seg, seg_tiles, ch, csplit};
 }
 SegPlan seg_plan_for(const mm_scan_bwd_params &p) {
     if (p.itype == MM_FLOAT32) return seg_plan<float>(p);
     if (p.itype == MM_FLOAT16) return seg_plan<f16_t>(p);
     return seg_plan<bf16_t>(p);
 }
-int64_t carry_floats(const SegPlan &pl) { return pl.tail_units * pl.n_seg * pl.ch * 16 * 2; }
+int64_t carry_floats(const SegPlan &pl) { return pl.tail_units * pl.n_seg * pl.csplit * pl.ch * 16 * 2; }
 
 // The forward parameter block of the states-only pass the backward runs when no tile states were
 // handed to it: the scan's inputs, no outputs, tile_states = the checkpoint region `ck`.
@@ -915,15 +935,15 @@ bool states_pass_ok(const mm_scan_bwd_params &p) {
     return seg_plan_for(q).tail_units > 0;
 }
 
-// dB and dC rows [row0, all): the n_blocks channel-block partials of each element summed in a fixed
-// order, one launch.
+// dB and dC rows [row0, row1): the n_blocks channel-block partials of each element summed in a
+// fixed order, one launch.
 int launch_reduce(const mm_scan_bwd_params &p, hipStream_t s, const float *partB, const float *partC,
-                  int64_t n_blocks, int64_t row0) {
-    const int64_t total = (p.batch * p.n_groups * 16 - row0) * (p.seqlen / 4);
+                  int64_t n_blocks, int64_t row0, int64_t row1) {
+    const int64_t total = (row1 - row0) * (p.seqlen / 4);
     if (total <= 0) return MM_OK;
     constexpr int64_t per_wg = 256 / kRedChunks;   // elements per workgroup pass
     const unsigned blocks = unsigned(std::min<int64_t>((total + per_wg - 1) / per_wg, 8192));
-    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partB, partC, n_blocks, row0);
+    hipLaunchKernelGGL(scan_bwd_reduce_bc, dim3(blocks), dim3(256), 0, s, p, partB, partC, n_blocks, row0, row1);
     return launch_status("scan_bwd_reduce_bc");
 }
 
@@ -938,17 +958,18 @@ int launch_units(const mm_scan_bwd_params &p, hipStream_t s, int64_t ratio, cons
     *red_rows = 0;
     if (pl.main_units > 0) {
         hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH>), dim3(unsigned(pl.main_units)), dim3(8 * CH), 0, s, p,
-                           ratio, fw, BwdSeg{0, 1, (p.seqlen + kFT - 1) / kFT, nullptr, 0, 0, 0});
+                           ratio, fw, BwdSeg{0, 1, (p.seqlen + kFT - 1) / kFT, nullptr, 1, 0, 0, 0});
         rc = launch_status("scan_bwd_tiled16");
         if (rc != MM_OK) return rc;
     }
     if (pl.tail_units > 0) {
         // Units run (batch, group)-major: the pairs below main_units / (blocks per group) are complete.
+        // (Measured at config 2: this beats a separate reduction launch before or after the carries.)
         const int64_t rows = pl.main_units / (ratio / CH) * 16;
-        const int64_t carry_blocks = pl.tail_units * (pl.n_seg - 1);
+        const int64_t carry_blocks = pl.tail_units * (pl.n_seg - 1) * pl.csplit;
         const int64_t red_blocks = std::min<int64_t>((rows * (p.seqlen / 4) + 8 * CH - 1) / (8 * CH), 8192);
-        const BwdSeg sg{pl.main_units, pl.n_seg, pl.seg_tiles, reinterpret_cast<float2 *>(carry), carry_blocks, rows,
-                        ratio / CH};
+        const BwdSeg sg{pl.main_units, pl.n_seg, pl.seg_tiles, reinterpret_cast<float2 *>(carry), pl.csplit,
+                        carry_blocks, rows, ratio / CH};
         hipLaunchKernelGGL((scan_bwd_tiled16<T, true, CH>), dim3(unsigned(carry_blocks + red_blocks)), dim3(8 * CH),
                            0, s, p, ratio, fw, sg);
         rc = launch_status("scan_bwd_tiled16 (carries)");
@@ -986,12 +1007,12 @@ int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
     // A workspace without room for the segment carries (sized by bwd_workspace_min_bytes, or queried
     // under another round size: MM_BWD_SLOTS or another device) runs every unit as a whole row.
     if (pl.tail_units > 0 && p.workspace_bytes < need)
-        pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT, pl.ch};
+        pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT, pl.ch, 1};
     int64_t red_rows = 0;
     const int rc = pl.ch == 32 ? launch_units<T, 32>(p, s, ratio, fw, pl, partB + 2 * fast_part_floats(p), &red_rows)
                                : launch_units<T, 16>(p, s, ratio, fw, pl, partB + 2 * fast_part_floats(p), &red_rows);
     if (rc != MM_OK) return rc;
-    return launch_reduce(p, s, fw.partB, fw.partC, ratio / pl.ch, red_rows);
+    return launch_reduce(p, s, fw.partB, fw.partC, ratio / pl.ch, red_rows, p.batch * p.n_groups * 16);
 }
 
 // The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
@@ -1005,7 +1026,7 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
     if (rc != MM_OK) return rc;
     // Slab rows past dstate are never written; the reduction reads only rows n < 16 of each slab
     // and writes rows n < dstate (dB / dC hold dstate rows).
-    return launch_reduce(p, s, partB, partC, p.dim / p.n_groups / 16, 0);
+    return launch_reduce(p, s, partB, partC, p.dim / p.n_groups / 16, 0, p.batch * p.n_groups * 16);
 }
 
 }  // namespace bwd

@@ -295,10 +295,13 @@ def test_bwd_tile_states(dtype, monkeypatch):
     a = ext.bwd(*args, dout, x, out, None, None, None, True, False, ck)
     b = ext.bwd(*args, dout, x, out, None, None, None, True, False)
     torch.cuda.synchronize()
-    atomic = {2, 5, 6}                 # dA, dD, ddelta_bias: float32 atomic sums
+    # dA, dD, ddelta_bias: float32 atomic sums of 8 lane partials per channel and batch row, added in
+    # whatever order the lanes arrive: a few roundings of the partials' size apart between runs.
+    atomic = {2, 5, 6}
     for i, (ta, tb) in enumerate(zip(a, b)):
-        tol = 1e-6 if i in atomic else 0.0
-        torch.testing.assert_close(ta, tb, rtol=tol, atol=tol)
+        tol = 1e-5 if i in atomic else 0.0
+        scale = max(1.0, tb.abs().max().item()) if i in atomic else 0.0
+        torch.testing.assert_close(ta, tb, rtol=tol, atol=tol * scale)
     # A request the dstate-16 kernels do not take (dstate 8): no tile states, and training still runs.
     c8 = _case(692, 1, 16, 64, 8, dtype)
     g8 = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in c8.items()}
@@ -366,6 +369,33 @@ def test_bwd_states_pass(dtype, slots, L, monkeypatch):
         rtol = 1e-5 if dtype == torch.float32 else 1e-2
         torch.testing.assert_close(a.float(), b.float(), rtol=rtol, atol=rtol * 0.1 * scale,
                                    msg=lambda m: f"{name}: {m}")
+
+
+@pytest.mark.parametrize("split,slots,L", [(3, 7, 256), (3, 6, 1000), (1, 6, 1000)])
+def test_bwd_carry_pieces(split, slots, L, monkeypatch):
+    """The carry launch walks each segment as MM_BWD_CARRY_SPLIT pieces, which compose like
+    segments: 4-tile segments in 3 pieces of 2 tiles (the last one empty), 21-tile segments in
+    pieces of 7, and one piece per segment. The gradients match the exact ones and the unsegmented
+    backward."""
+    _say(f"bwd carry pieces split={split} slots={slots} L={L}")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    dtype = torch.float32
+    case = _case(730 + slots, 2, 64, L, 16, dtype, bkind="4d", G=2)
+    dout = _dout(731, (2, 64, L), dtype)
+    monkeypatch.setenv("MM_BWD_SLOTS", str(slots))
+    monkeypatch.setenv("MM_BWD_CARRY_SPLIT", str(split))
+    _vs_exact(case, dout, dtype, f"carry pieces {split}")
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+    out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    seg = ext.bwd(*args, dout.to(DEV), x, out, None, None, None, True, False, ck)
+    monkeypatch.setenv("MM_BWD_SEGMENTS", "0")
+    whole = ext.bwd(*args, dout.to(DEV), x, out, None, None, None, True, False, ck)
+    torch.cuda.synchronize()
+    for name, a, b in zip(["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"], seg, whole):
+        scale = max(1.0, b.abs().max().item())
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6 * scale, msg=lambda m: f"{name}: {m}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
