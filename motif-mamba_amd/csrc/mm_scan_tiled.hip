@@ -1356,8 +1356,9 @@ __device__ __forceinline__ void buffer_store_elem(__amdgpu_buffer_rsrc_t r, uint
 
 // CHUNKS: the training outputs as k2s writes them -- the chunk states (the product of the decays
 // since step 0 and the state, at every chunk end) and, on request, the state after every 16-step
-// tile for the backward.
-template <typename T, int PF, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT, bool CHUNKS = false>
+// tile for the backward. YO false: the states alone (no C, y or outputs), the tile states written,
+// as k2s's states-only form.
+template <typename T, int PF, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT, bool CHUNKS = false, bool YO = true>
 __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int64_t ratio, const int tid,
                                           const int64_t b, const int64_t d0, K1SLds &lds) {
     static_assert(PF % 2 == 0, "the pair loop is unrolled by PF and needs a static parity");
@@ -1412,7 +1413,8 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
     auto load_data = [&](int32_t i, K1SData<T> &dst) {
         const uint32_t sof = pair_off(i);
         dst.b = buffer_load_raw<T, 2>(rs_b, fo_b, sof);
-        dst.c = buffer_load_raw<T, 2>(rs_c, fo_c, sof);
+        if constexpr (YO) dst.c = buffer_load_raw<T, 2>(rs_c, fo_c, sof);
+        else dst.c = {};
         load_tile(2 * i + 2, dst.u0, dst.d0, dst.z0);
         load_tile(2 * i + 3, dst.u1, dst.d1, dst.z1);
     };
@@ -1435,6 +1437,7 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
     // The first interval runs it on the unused buffers and stores to tile 0, which the same lane
     // overwrites with tile 0's outputs one interval later (as k2s does).
     auto epilogue = [&](auto Slot, const float *yb, int32_t t) {
+        if constexpr (!YO) return;
         constexpr int sl = decltype(Slot)::value & 3;
         const int ecol = (((es >> 2) ^ swe) << 2) + (es & 3);
         float a = yb[ce * kT1 + ecol];
@@ -1481,18 +1484,19 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
                 constexpr int j = decltype(J)::value;
                 constexpr int s = kT1 * H + 4 * s4 + j;
                 h = __builtin_fmaf(av[j], h, bbv[j]);
-                pv[j] = row_bcast<s / 2>(cv[s % 2]) * h;
+                if constexpr (YO) pv[j] = row_bcast<s / 2>(cv[s % 2]) * h;
             });
-            *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
-                make_float4(pv[0], pv[1], pv[2], pv[3]);
+            if constexpr (YO)
+                *reinterpret_cast<float4 *>(&yb[(r * kCh + c) * kT1 + ((s4 ^ swc) << 2)]) =
+                    make_float4(pv[0], pv[1], pv[2], pv[3]);
             dtq = ndt;
             duq = ndu;
         });
         pre_dt = dtq;
         pre_du = duq;
-        if constexpr (CHUNKS) {
+        if constexpr (CHUNKS || !YO) {
             const int64_t tend = t0 + kT1;
-            if (p.chunk_states && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
+            if (CHUNKS && p.chunk_states && (tend % MM_SCAN_CHUNK == 0 || tend == L)) {
                 const int64_t ci = (tend - 1) / MM_SCAN_CHUNK;
                 float *csp = p.chunk_states + ((b * p.dim + d0 + c) * n_chunks + ci) * 32 + 2 * r;
                 csp[0] = __builtin_amdgcn_exp2f(At * cum_dt);
@@ -1505,7 +1509,7 @@ __device__ __forceinline__ void k1s_group(const mm_scan_fwd_params &p, const int
 
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    if (CHUNKS && p.tile_states)           // the checkpoint before the first tile: zero
+    if ((CHUNKS || !YO) && p.tile_states)  // the checkpoint before the first tile: zero
         p.tile_states[(b * p.dim + d0 + c) * 16 + r] = 0.f;
     K1SData<T> ring[PF];
     {
@@ -1567,8 +1571,9 @@ union MixLds {
     K1SLds k1;
 };
 
-// CHUNKS: the training form (chunk states and, on request, tile states), 16-bit inputs.
-template <typename T, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT, bool CHUNKS>
+// CHUNKS: the training form (chunk states and, on request, tile states), 16-bit inputs. YO false:
+// the states alone (the backward's checkpoints), 16-bit inputs.
+template <typename T, bool SOFTPLUS, bool HAS_Z, bool HAS_OUT, bool CHUNKS, bool YO = true>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 8)))
 scan_fwd_mix(const mm_scan_fwd_params p, const int64_t ratio, const int32_t n_double) {
     __shared__ __align__(16) MixLds lds;
@@ -1578,11 +1583,12 @@ scan_fwd_mix(const mm_scan_fwd_params p, const int64_t ratio, const int32_t n_do
         // that the group's buffer resources stay in SGPRs.
         const int half = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 7));
         const int64_t grp = 2 * int64_t(blockIdx.x) + half;
-        k2s_group<T, 2, SOFTPLUS, CHUNKS, HAS_Z, HAS_OUT, true, 0>(p, ratio, kWholeRows, threadIdx.x & 127, grp / gpb,
-                                                                   (grp % gpb) * kCh, 0, lds.k2[half]);
+        k2s_group<T, 2, SOFTPLUS, CHUNKS, HAS_Z, HAS_OUT, YO, 0>(p, ratio, kWholeRows, threadIdx.x & 127, grp / gpb,
+                                                                 (grp % gpb) * kCh, 0, lds.k2[half]);
     } else {
         const int64_t grp = 2 * int64_t(n_double) + (int64_t(blockIdx.x) - n_double);
-        k1s_group<T, 2, SOFTPLUS, HAS_Z, HAS_OUT, CHUNKS>(p, ratio, threadIdx.x, grp / gpb, (grp % gpb) * kCh, lds.k1);
+        k1s_group<T, 2, SOFTPLUS, HAS_Z, HAS_OUT, CHUNKS, YO>(p, ratio, threadIdx.x, grp / gpb, (grp % gpb) * kCh,
+                                                              lds.k1);
     }
 }
 
@@ -1638,10 +1644,19 @@ int launch_k2s(const mm_scan_fwd_params &p, hipStream_t stream) {
     return launch_k2s_io<T, PF, false, true>(p, stream);   // without z the pre-gate out is the output
 }
 
-// The states alone (L a multiple of 32): p.tile_states, and p.last_state when given.
+// The states alone (L a multiple of 32): p.tile_states, and p.last_state when given; on the
+// balanced mixed grid when the caller found a plan for it (n_double + n_single > 0, 16-bit inputs).
 template <typename T>
-int launch_k2s_states(const mm_scan_fwd_params &p, hipStream_t stream) {
+int launch_k2s_states(const mm_scan_fwd_params &p, hipStream_t stream, int32_t n_double, int32_t n_single) {
     const int64_t ratio = p.dim / p.n_groups;
+    if constexpr (sizeof(T) == 2) {
+        if (n_double + n_single > 0) {
+            auto *kern = p.delta_softplus ? scan_fwd_mix<T, true, false, false, false, false>
+                                          : scan_fwd_mix<T, false, false, false, false, false>;
+            hipLaunchKernelGGL(kern, dim3(unsigned(n_double + n_single)), dim3(256), 0, stream, p, ratio, n_double);
+            return launch_status("scan_fwd_mix_states");
+        }
+    }
     dim3 grid(unsigned(p.dim / kCh), unsigned(p.batch));
     auto *kern = p.delta_softplus ? scan_fwd_k2s<T, 2, true, false, false, false, false>
                                   : scan_fwd_k2s<T, 2, false, false, false, false, false>;
@@ -1928,7 +1943,11 @@ int launch_states_only(const mm_scan_fwd_params &p, hipStream_t stream) {
         const char *e = getenv("MM_STATES_KERNEL");
         return e && !strcmp(e, "pipe");
     }();
-    if (!pipe && p.seqlen % (2 * tiled::kT1) == 0 && k2s_bytes_ok(p)) return tiled::launch_k2s_states<T>(p, stream);
+    if (!pipe && p.seqlen % (2 * tiled::kT1) == 0 && k2s_bytes_ok(p)) {
+        int32_t n_double = 0, n_single = 0;
+        if (!mix_plan(p, n_double, n_single)) n_double = n_single = 0;
+        return tiled::launch_k2s_states<T>(p, stream, n_double, n_single);
+    }
     return tiled::launch_fwd_states<T>(p, stream);
 }
 template int launch_states_only<MM_TILED_TYPE>(const mm_scan_fwd_params &, hipStream_t);

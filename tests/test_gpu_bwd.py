@@ -371,6 +371,54 @@ def test_bwd_states_pass(dtype, slots, L, monkeypatch):
                                    msg=lambda m: f"{name}: {m}")
 
 
+@pytest.mark.parametrize("q,dtype", [(3, torch.bfloat16), (5, torch.bfloat16), (5, torch.float16)])
+def test_bwd_states_pass_balanced_grid(q, dtype):
+    """Shapes with 3 or 5 sixteen-channel groups per compute unit run the backward's states pass on
+    the balanced mixed grid (two-state and one-state groups, states only). Its checkpoints are the
+    training forward's (same grid, same state arithmetic), so the backward recomputing them equals
+    the one handed the forward's tile states bit for bit, up to the float32 atomic sums (dA, dD,
+    ddelta_bias); du, ddelta and dz of rows of both group kinds match the exact gradients."""
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    batch, dim, L = 2, q * cus * 16 // 2, 256
+    _say(f"bwd states pass on the mixed grid q={q} {dtype} batch {batch} dim {dim} L {L}")
+    case = _case(740 + q, batch, dim, L, 16, dtype, bkind="4d", G=1)
+    dout = _dout(741, (batch, dim, L), dtype)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+    out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    d = dout.to(DEV)
+    recomputed = ext.bwd(*args, d, x, out, None, None, None, True, False)
+    saved = ext.bwd(*args, d, x, out, None, None, None, True, False, ck)
+    torch.cuda.synchronize()
+    names = ["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"]
+    for i, (a, b) in enumerate(zip(recomputed, saved)):
+        if names[i] in ("dA", "dD", "ddelta_bias"):
+            scale = max(1.0, b.abs().max().item())
+            torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5 * scale, msg=lambda m: f"{names[i]}: {m}")
+        else:
+            assert torch.equal(a, b), names[i]
+    # Exact du / ddelta / dz of channels in the two-state groups, at the hand-over and in the
+    # one-state groups (each channel's row needs only its own inputs and the shared B, C).
+    first_k1 = 2 * (q // 2) * cus * 16            # first batch-major channel of the one-state groups
+    flat = [0, 17, first_k1 - 1, first_k1, first_k1 + 31, batch * dim - 1]
+    for bb in range(batch):
+        chans = sorted({i % dim for i in flat if i // dim == bb})
+        if not chans:
+            continue
+        sub = {k: v for k, v in case.items()}
+        for k in ("u", "delta", "z"):
+            sub[k] = case[k][bb:bb + 1, chans]
+        for k in ("B", "C"):
+            sub[k] = case[k][bb:bb + 1]
+        for k in ("A", "D", "delta_bias"):
+            sub[k] = case[k][chans]
+        exact = selective_scan_bwd_ref(**sub, dout=dout[bb:bb + 1, chans], dtype=torch.float64)
+        for name, idx in (("du", 0), ("ddelta", 1), ("dz", 7)):
+            _check(recomputed[idx][bb:bb + 1, chans], exact[name], dtype, f"states pass q={q} b{bb} {name}")
+
+
 @pytest.mark.parametrize("split,slots,L", [(3, 7, 256), (3, 6, 1000), (1, 6, 1000)])
 def test_bwd_carry_pieces(split, slots, L, monkeypatch):
     """The carry launch walks each segment as MM_BWD_CARRY_SPLIT pieces, which compose like
