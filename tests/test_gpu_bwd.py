@@ -446,18 +446,20 @@ def test_bwd_carry_pieces(split, slots, L, monkeypatch):
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6 * scale, msg=lambda m: f"{name}: {m}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype,G", [(torch.float32, 1), (torch.bfloat16, 1), (torch.float16, 2),
+                                     (torch.bfloat16, 2)])
 @pytest.mark.parametrize("ch,slots", [(32, 6)])
-def test_bwd_channel_widths(dtype, ch, slots, monkeypatch):
-    """The dstate-16 backward with 32- or 64-channel workgroups (MM_BWD_CH; one dB/dC partial slab
-    per block of ch channels) on 2 x 128 channels, L 1000 (a padded last tile): against the exact
-    gradients through autograd, and against the 16-channel kernel on the same inputs -- whole rows,
-    a segmented last round (MM_BWD_SLOTS: 8 units as 6 whole + 2 cut for ch 32, 4 units as 3 whole
-    + 1 cut for ch 64) and without tile states."""
-    _say(f"bwd channel width {ch} slots={slots} {dtype}")
+def test_bwd_channel_widths(dtype, G, ch, slots, monkeypatch):
+    """The dstate-16 backward with 32-channel workgroups (MM_BWD_CH; one dB/dC partial slab per
+    block of ch channels) on 2 x 128 channels, L 1000 (a padded last tile), one group or two (two
+    blocks per group): against the exact gradients through autograd, and against the 16-channel
+    kernel on the same inputs -- whole rows, a segmented last round (MM_BWD_SLOTS: 8 units as 6
+    whole + 2 cut, whose carry launch also reduces the slab rows of the 3 complete (batch, group)
+    pairs) and without tile states."""
+    _say(f"bwd channel width {ch} slots={slots} {dtype} G={G}")
     from motif_mamba_amd import _native
     ext = _native.ext()
-    case = _case(720 + ch, 2, 128, 1000, 16, dtype, bkind="4d", G=1)
+    case = _case(720 + ch + G, 2, 128, 1000, 16, dtype, bkind="4d", G=G)
     dout = _dout(721, (2, 128, 1000), dtype)
     monkeypatch.setenv("MM_BWD_CH", str(ch))
     _vs_exact(case, dout, dtype, f"ch={ch}")
