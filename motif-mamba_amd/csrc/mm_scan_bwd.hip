@@ -577,7 +577,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             reinterpret_cast<const float4 *>(sg.carry + ((uo * sg.n_seg * sg.csplit) * CH + c) * 16 + n0);
         float c0 = 0.f, c1 = 0.f;
         for (int64_t s2 = sg.n_seg * sg.csplit - 1; s2 >= (seg + 1) * sg.csplit; --s2) {
-            const float4 v = cp[s2 * CH * 8];   // one segment: CH channels x 16 states x (e, P)
+            const float4 v = cp[s2 * CH * 8];   // one piece: CH channels x 16 states x (e, P)
             c0 = __builtin_fmaf(v.y, c0, v.x);
             c1 = __builtin_fmaf(v.w, c1, v.z);
         }
