@@ -305,14 +305,16 @@ struct BwdSeg {
 // order through `scratch` (NTH float4, unused with K = 1). Each element is reduced by one call, whose
 // K the plan fixes, so the result is deterministic.
 constexpr int kRedChunks = 8;
+// The row stride (floats) of the partial slabs: L rounded up to whole float4s.
+__host__ __device__ __forceinline__ int64_t slab_row(int64_t L) { return (L + 3) & ~int64_t(3); }
 template <int NTH, int K>
 __device__ __forceinline__ void reduce_slab_rows(const mm_scan_bwd_params &p, const float *part, float *dst,
                                                  int64_t bs, int64_t gs, int64_t ns, int64_t n_blocks, int64_t row0,
                                                  int64_t row1, int64_t wg, int64_t n_wg, float4 *scratch) {
     constexpr int E = NTH / K;   // elements per workgroup pass
     const int tid = threadIdx.x, e = tid % E, k = tid / E;
-    const int64_t L4 = p.seqlen / 4;
-    const int64_t st = p.batch * p.n_groups * 16 * p.seqlen / 4;   // one block's slab, in float4
+    const int64_t Lp = slab_row(p.seqlen), L4 = Lp / 4;
+    const int64_t st = p.batch * p.n_groups * 16 * L4;   // one block's slab, in float4
     const int64_t b_lo = n_blocks * k / K, b_hi = n_blocks * (k + 1) / K;
     const int64_t end = row1 * L4;
     for (int64_t base = row0 * L4 + wg * E; base < end; base += n_wg * E) {   // uniform over the workgroup
@@ -322,7 +324,7 @@ __device__ __forceinline__ void reduce_slab_rows(const mm_scan_bwd_params &p, co
         const bool live = i < end && row % 16 < p.dstate;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         if (live) {
-            const float4 *src = reinterpret_cast<const float4 *>(part + row * p.seqlen) + t4;
+            const float4 *src = reinterpret_cast<const float4 *>(part + row * Lp) + t4;
             int64_t blk = b_lo;
             for (; blk + 8 <= b_hi; blk += 8) {   // eight loads in flight, added in block order
                 float4 v[8];
@@ -351,7 +353,10 @@ __device__ __forceinline__ void reduce_slab_rows(const mm_scan_bwd_params &p, co
             const int64_t n = row % 16, bg = row / 16;
             const int64_t gg = bg % p.n_groups, bb = bg / p.n_groups;
             float *o = dst + bb * bs + gg * gs + n * ns + 4 * t4;
-            o[0] = acc.x; o[1] = acc.y; o[2] = acc.z; o[3] = acc.w;
+            const float a4[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)   // the row's last float4 may reach past L (L % 4 = 2)
+                if (4 * t4 + q < p.seqlen) o[q] = a4[q];
         }
         if constexpr (K > 1) __syncthreads();   // scratch reads done before the next pass rewrites it
     }
@@ -408,6 +413,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     const int64_t g = d0 / ratio;
     const int64_t blk = (d0 - g * ratio) / CH;
     const int64_t L = p.seqlen;
+    const int64_t Lp = slab_row(L);
     const int64_t n_tiles = (L + kFT - 1) / kFT;
     int64_t j_lo = seg * sg.seg_tiles;
     int64_t j_hi = j_lo + sg.seg_tiles < n_tiles ? j_lo + sg.seg_tiles : n_tiles;
@@ -464,12 +470,14 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             }
         }
         const int64_t ts0 = jj * kFT + SV * st_q;
-        const int64_t ts = ts0 < L ? ts0 : L - SV;
 #pragma unroll
         for (int i = 0; i < SV / 2; ++i) r.bc[i] = {};
         if (stager && (full || st_tensor == 0)) {
 #pragma unroll
-            for (int i = 0; i < SV / 2; ++i) r.bc[i] = load_raw<T, 2>(stp + ts + 2 * i);
+            for (int i = 0; i < SV / 2; ++i) {   // each step pair clamped into the row on its own
+                const int64_t ts = ts0 + 2 * i < L ? ts0 + 2 * i : L - 2;
+                r.bc[i] = load_raw<T, 2>(stp + ts);
+            }
         }
         r.hc = full ? *reinterpret_cast<const float2 *>(ckp + jj * ck_tile) : make_float2(0.f, 0.f);
         return r;
@@ -479,7 +487,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     float e_raw[2], e_dt[2], e_u[2], e_g[2];
     auto commit = [&](const TileRaw<T, CH> &r, int64_t j, int buf, bool full) {
         const int64_t te = j * kFT + 2 * rs;
-        const bool ev = te < L;            // L is a multiple of 8: both steps exist or neither
+        const bool ev = te < L;            // L is even: both steps exist or neither
         float dd[2], go[2] = {0.f, 0.f};
         unpack2<T>(r.d, dd[0], dd[1]);
         unpack2<T>(r.u, e_u[0], e_u[1]);
@@ -510,12 +518,14 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             sX[buf][c * kXS + 2 * rs + i] = make_float4(e_dt[i], e_dt[i] * e_u[i], e_u[i], e_g[i]);
         }
         if (stager) {
-            const bool bv_ok = j * kFT + SV * st_q < L;   // L is a multiple of 8: all SV exist or none do
             float v[SV];
 #pragma unroll
             for (int i = 0; i < SV / 2; ++i) unpack2<T>(r.bc[i], v[2 * i], v[2 * i + 1]);
 #pragma unroll
-            for (int i = 0; i < SV; ++i) sBC[buf][(SV * st_q + i) * kBCS + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
+            for (int i = 0; i < SV; ++i) {   // L is even: a step pair exists whole or not at all
+                const bool bv_ok = j * kFT + SV * st_q + (i & ~1) < L;
+                sBC[buf][(SV * st_q + i) * kBCS + st_tensor * 16 + st_n] = bv_ok ? v[i] : 0.f;
+            }
         }
     };
 
@@ -679,7 +689,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 const float acc = q4[0];
                 const int64_t ts = t0 + half * kFH + tt;
                 if (ts < L)
-                    (tz == 0 ? ws.partB : ws.partC)[(((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * L + ts] = acc;
+                    (tz == 0 ? ws.partB : ws.partC)[(((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * Lp + ts] = acc;
             }
             // du / ddelta of the steps this lane owns, if they are in this half: the 8 slots' partial
             // sums over states, added in slot order.
@@ -772,11 +782,11 @@ struct Fills {
     }
 };
 
-// The dstate-16 kernel's requirements: variable B/C, 16-channel blocks inside one group, L a
-// multiple of 8, two-element-aligned activation rows and four-element-aligned B/C rows.
+// The dstate-16 kernel's requirements: variable B/C, 16-channel blocks inside one group, L even,
+// two-element-aligned activation and B/C rows (each lane moves step pairs).
 bool fast_ok(const mm_scan_bwd_params &p) {
     if (p.P || p.dstate != 16 || !p.is_variable_B || !p.is_variable_C) return false;
-    if (p.dim % 16 != 0 || (p.dim / p.n_groups) % 16 != 0 || p.seqlen < 8 || p.seqlen % 8 != 0) return false;
+    if (p.dim % 16 != 0 || (p.dim / p.n_groups) % 16 != 0 || p.seqlen < 2 || p.seqlen % 2 != 0) return false;
     // One 128-lane workgroup per unit in a 1-D grid: gridDim.x * blockDim.x must stay below 2^32.
     if (p.batch * (p.dim / 16) >= (int64_t(1) << 25)) return false;
     const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
@@ -799,7 +809,7 @@ int64_t fast_ck_floats(const mm_scan_bwd_params &p) {
     return ((p.seqlen + kFT - 1) / kFT) * p.batch * p.dim * 16;
 }
 int64_t fast_part_floats(const mm_scan_bwd_params &p) {
-    return (p.dim / 16) * p.batch * 16 * p.seqlen;   // blocks per group x groups = dim / 16
+    return (p.dim / 16) * p.batch * 16 * slab_row(p.seqlen);   // blocks per group x groups = dim / 16
 }
 
 // Workgroups of scan_bwd_tiled16<T, false, CH> that the current device runs at once (one round), or
@@ -939,7 +949,7 @@ bool states_pass_ok(const mm_scan_bwd_params &p) {
 // fixed order, one launch.
 int launch_reduce(const mm_scan_bwd_params &p, hipStream_t s, const float *partB, const float *partC,
                   int64_t n_blocks, int64_t row0, int64_t row1) {
-    const int64_t total = (row1 - row0) * (p.seqlen / 4);
+    const int64_t total = (row1 - row0) * (slab_row(p.seqlen) / 4);
     if (total <= 0) return MM_OK;
     constexpr int64_t per_wg = 256 / kRedChunks;   // elements per workgroup pass
     const unsigned blocks = unsigned(std::min<int64_t>((total + per_wg - 1) / per_wg, 8192));
@@ -967,7 +977,7 @@ int launch_units(const mm_scan_bwd_params &p, hipStream_t s, int64_t ratio, cons
         // (Measured at config 2: this beats a separate reduction launch before or after the carries.)
         const int64_t rows = pl.main_units / (ratio / CH) * 16;
         const int64_t carry_blocks = pl.tail_units * (pl.n_seg - 1) * pl.csplit;
-        const int64_t red_blocks = std::min<int64_t>((rows * (p.seqlen / 4) + 8 * CH - 1) / (8 * CH), 8192);
+        const int64_t red_blocks = std::min<int64_t>((rows * (slab_row(p.seqlen) / 4) + 8 * CH - 1) / (8 * CH), 8192);
         const BwdSeg sg{pl.main_units, pl.n_seg, pl.seg_tiles, reinterpret_cast<float2 *>(carry), pl.csplit,
                         carry_blocks, rows, ratio / CH};
         hipLaunchKernelGGL((scan_bwd_tiled16<T, true, CH>), dim3(unsigned(carry_blocks + red_blocks)), dim3(8 * CH),

@@ -419,6 +419,24 @@ def test_bwd_states_pass_balanced_grid(q, dtype):
             _check(recomputed[idx][bb:bb + 1, chans], exact[name], dtype, f"states pass q={q} b{bb} {name}")
 
 
+@pytest.mark.parametrize("L", [2, 6, 18, 1002, 2054])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_bwd_even_lengths(L, dtype, monkeypatch):
+    """Even lengths that are not multiples of 8 or 4 run the dstate-16 kernel (the last tile holds
+    2 to 14 valid steps; the dB/dC slab rows are padded to whole float4s and the reduction stores
+    only steps below L): against the exact gradients, whole rows and (MM_BWD_SLOTS) with a segmented
+    last round, 16- and 32-channel workgroups."""
+    _say(f"bwd even length L={L} {dtype}")
+    case = _case(750 + L, 2, 64, L, 16, dtype, bkind="4d", G=1)
+    dout = _dout(751, (2, 64, L), dtype)
+    _vs_exact(case, dout, dtype, f"L{L}")
+    monkeypatch.setenv("MM_BWD_SLOTS", "6")
+    _vs_exact(case, dout, dtype, f"L{L} segmented")
+    monkeypatch.setenv("MM_BWD_CH", "32")
+    monkeypatch.setenv("MM_BWD_SLOTS", "3")
+    _vs_exact(case, dout, dtype, f"L{L} 32 channels")
+
+
 @pytest.mark.parametrize("split,slots,L", [(3, 7, 256), (3, 6, 1000), (1, 6, 1000)])
 def test_bwd_carry_pieces(split, slots, L, monkeypatch):
     """The carry launch walks each segment as MM_BWD_CARRY_SPLIT pieces, which compose like
