@@ -16,6 +16,7 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
+#include <cstdlib>
 #include <vector>
 
 #include "mm_conv1d.h"
@@ -294,6 +295,27 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
     FwdSetup s = setup_fwd(u, delta, A, B, C, D_, z_, delta_bias_, delta_softplus);
     mm_scan_fwd_params &p = s.p;
     const std::vector<at::Tensor> pq = attach_pq(p, u, P_, Q_, gamma_);
+    // A length that is not a multiple of 8 keeps a request off the fast kernels (their lanes move
+    // vectors of 2 to 8 steps) and on the general one, ~14x slower at the Mamba-2.8B layer shape.
+    // Such requests run on copies padded in front to a multiple of 32 steps with u, delta, z, B and
+    // C zero: from the zero initial state a step with u = 0 leaves the state exactly zero, whatever
+    // its decay (and, with P/Q, whatever the coupling), so the real steps run the recurrence of the
+    // unpadded request; the outputs are the padded call's last L steps, the last state its own.
+    // MM_SCAN_PAD=0 turns this off (read per call: the tests run the general kernels with it).
+    const char *pad_env = std::getenv("MM_SCAN_PAD");
+    const bool pad_off = pad_env && pad_env[0] == '0';
+    const bool fast_shape = p.is_variable_B && p.is_variable_C && p.dim % 16 == 0 &&
+                            (p.dim / p.n_groups) % 16 == 0 && (p.P ? p.dstate <= 64 : p.dstate == 16);
+    if (!pad_off && fast_shape && p.seqlen % 8 != 0) {
+        const int64_t L = p.seqlen, pad = (L + 31) / 32 * 32 - L;
+        auto front = [&](const at::Tensor &t) { return at::constant_pad_nd(t, {pad, 0}, 0); };
+        const c10::optional<at::Tensor> zp = z_.has_value() ? c10::optional<at::Tensor>(front(z_.value()))
+                                                            : c10::optional<at::Tensor>();
+        std::vector<at::Tensor> res = fwd_infer(front(u), front(delta), A, front(B), front(C), D_, zp, delta_bias_,
+                                                delta_softplus, return_last_state, P_, Q_, gamma_);
+        res[0] = res[0].narrow(-1, pad, L).contiguous();
+        return res;
+    }
     at::Tensor main;
     if (z_.has_value()) {
         main = z_.value().is_non_overlapping_and_dense() ? torch::empty_like(z_.value()) : torch::empty_like(delta);

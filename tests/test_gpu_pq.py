@@ -164,8 +164,12 @@ def test_pq_general_large_dstate(N):
     _vs_oracle(case, torch.float32, f"N{N}")
 
 
-def test_pq_general_odd_length_and_strided_rows():
-    _say("pq general odd L and strided u")
+@pytest.mark.parametrize("pad", ["0", "1"], ids=["general", "padded"])
+def test_pq_general_odd_length_and_strided_rows(pad, monkeypatch):
+    """Odd L with misaligned u rows: the lane-per-row P/Q kernel (MM_SCAN_PAD=0), or the fast
+    kernel on the binding's front-padded copies."""
+    _say(f"pq odd L and strided u, padding {pad}")
+    monkeypatch.setenv("MM_SCAN_PAD", pad)
     from motif_mamba_amd import selective_scan_fn
     case = _pq_case(380, batch=2, dim=16, L=37, N=16, R=2, dtype=torch.bfloat16)
     g = _to(case, DEV)
@@ -177,6 +181,15 @@ def test_pq_general_odd_length_and_strided_rows():
     ref, ref_last = selective_scan_pq_ref(**case, return_last_state=True)
     _close(out.cpu(), ref, torch.bfloat16, "odd L out")
     _close(last.cpu(), ref_last, torch.bfloat16, "odd L last")
+
+
+@pytest.mark.parametrize("L,R", [(1001, 2), (2047, 4)])
+def test_pq_padded_length(L, R):
+    """P/Q inference at lengths that are not multiples of 8: the fast kernel on front-padded copies
+    (zero u keeps the coupled state at zero through the padding) against the float64 restatement."""
+    _say(f"pq padded length L={L} R={R}")
+    case = _pq_case(390 + R, batch=2, dim=64, L=L, N=16, R=R, dtype=torch.bfloat16, bkind="4d", G=2)
+    _vs_oracle(case, torch.bfloat16, f"padded L={L}")
 
 
 def test_pq_rank_zero_is_the_diagonal_scan():

@@ -113,6 +113,36 @@ def test_random_shapes(shape, dtype):
     _close(last, exp_last, dtype, "last_state")
 
 
+@pytest.mark.parametrize("shape", [s for s in SHAPES if s[2] % 8 != 0],
+                         ids=[f"b{s[0]}d{s[1]}L{s[2]}N{s[3]}{s[4]}G{s[5]}" for s in SHAPES if s[2] % 8 != 0])
+def test_random_shapes_general_kernels(shape, monkeypatch):
+    """The shapes with L % 8 != 0 again with the front padding off (MM_SCAN_PAD=0), so that the
+    general kernels that serve them then stay covered."""
+    monkeypatch.setenv("MM_SCAN_PAD", "0")
+    batch, dim, L, N, bkind, G = shape
+    _say(f"random shape {shape} bf16, padding off")
+    case = _case(7, batch, dim, L, N, torch.bfloat16, bkind, G)
+    exp, exp_last = selective_scan_ref(**case, return_last_state=True)
+    out, last = _run(case)
+    _close(out, exp, torch.bfloat16, "out_z")
+    _close(last, exp_last, torch.bfloat16, "last_state")
+
+
+@pytest.mark.parametrize("L", [7, 1001, 2047])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("with_z", [True, False], ids=["z", "noz"])
+def test_padded_lengths_every_row(L, dtype, with_z):
+    """Inference requests whose length is not a multiple of 8 run the fast kernels on copies padded
+    in front to a multiple of 32 steps with zero u (the binding's fwd_infer): every row's output and
+    last state against the float64 restatement, G = 2."""
+    batch, dim = 2, 256
+    _say(f"padded length L={L} {dtype} z={with_z}")
+    case = _case(110 + L, batch, dim, L, 16, dtype, bkind="4d", G=2, with_z=with_z)
+    out, last = _run(case)
+    assert out.shape == (batch, dim, L) and out.is_contiguous() and last.shape == (batch, dim, 16)
+    _rows_vs_f64(case, out, last, f"padded L={L}")
+
+
 @pytest.mark.parametrize("flags", [dict(with_D=False), dict(with_z=False), dict(with_bias=False),
                                    dict(softplus=False), dict(with_D=False, with_z=False, with_bias=False,
                                                               softplus=False)],
