@@ -28,8 +28,9 @@ through its torch loop (calls with z) differentiate the same function; "exact" t
 z-less calls from that autograd, any other value ("fused") from the dense kernel, the only backward
 its launcher runs with P/Q (selective_scan_bwd_kernel.cuh:928-932), which accumulates the same
 chain rule (:307, :334). The variable is therefore not read here. The gfx950 kernel covers pq_rank 1..8, dstate <= 16, dim and
-dim / n_groups multiples of 16 and seqlen a multiple of 8, with variable B and C; other P/Q
-shapes raise NotImplementedError in the backward.
+dim / n_groups multiples of 16 and seqlen a multiple of 8, with variable B and C; training requests
+of other lengths are padded in front with zero-u steps (_train_pad), other P/Q shapes raise
+NotImplementedError in the backward.
 
 Differences (all raise instead of computing something else): complex A, and the P/Q backward
 outside the shapes above, are not part of this build.
@@ -49,6 +50,36 @@ def _save_tile_states():
     MM_TILE_STATES=0 trades the B * dim * L float32 of saved activations for the backward's recompute
     of the scan)."""
     return os.environ.get("MM_TILE_STATES", "1") != "0"
+
+
+def _train_pad(u, A, B, C, pq):
+    """Steps to put in front of a training request whose length is not a multiple of 8, so that
+    the forward and backward run the fast kernels (the diagonal ones take dstate 16, the P/Q
+    backward dstate <= 16; with other lengths the diagonal scan would run the general kernels, ~14x
+    and ~100x slower, and the P/Q backward would refuse the call). The padded steps carry zero u,
+    delta, z, B and C, and dout is zero over them: from the zero initial state a zero-u step leaves
+    every state exactly zero, so the real steps run the unpadded recurrence, and the padded steps
+    add nothing to dA, dD, ddelta_bias, dP or dQ (each of their terms holds u, h or Q h of a padded
+    step). 0 when no padding applies, or with MM_SCAN_PAD=0 (which also turns off the binding's
+    padding of inference requests)."""
+    L = u.shape[-1]
+    if L % 8 == 0 or B.dim() != 4 or C.dim() != 4 or os.environ.get("MM_SCAN_PAD", "1") == "0":
+        return 0
+    n = A.shape[1]
+    if (n > 16) if pq else (n != 16):
+        return 0
+    dim, groups = u.shape[1], B.shape[1]
+    if dim % 16 or (dim // groups) % 16:
+        return 0
+    return (-L) % 32
+
+
+def _pad_front(t, pad):
+    return t if t is None or pad == 0 else torch.nn.functional.pad(t, (pad, 0))
+
+
+def _unpad(t, pad):
+    return t if t is None or pad == 0 else t[..., pad:]
 
 
 class SelectiveScanFn(torch.autograd.Function):
@@ -88,6 +119,8 @@ class SelectiveScanFn(torch.autograd.Function):
         # the states before every 16-step tile (None where the kernels do not write them), which
         # spare the backward its recompute of the scan.
         want_ck = A.shape[1] == 16 and _save_tile_states()
+        pad = ctx.pad = _train_pad(u, A, B, C, pq=False)
+        u, delta, z, B, C = (_pad_front(t, pad) for t in (u, delta, z, B, C))
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, None, None, None, delta_softplus,
                                   tile_states=want_ck)
         ck = rest.pop() if want_ck else None
@@ -96,9 +129,10 @@ class SelectiveScanFn(torch.autograd.Function):
         last_state = x[:, :, -1, 1::2]
         if not ctx.has_z:
             ctx.save_for_backward(u, delta, A, B, C, D, delta_bias, x, ck)
+            out = _unpad(out, pad).contiguous() if pad else out
             return out if not return_last_state else (out, last_state)
         ctx.save_for_backward(u, delta, A, B, C, D, z, delta_bias, x, out, ck)
-        out_z = rest[0]
+        out_z = _unpad(rest[0], pad).contiguous() if pad else rest[0]
         return out_z if not return_last_state else (out_z, last_state)
 
     @staticmethod
@@ -112,10 +146,13 @@ class SelectiveScanFn(torch.autograd.Function):
             u, delta, A, B, C, D, z, delta_bias, x, out, ck = ctx.saved_tensors
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
+        pad = ctx.pad
+        dout = _pad_front(dout, pad)
         du, ddelta, dA, dB, dC, dD, ddelta_bias, *rest = ext().bwd(
             u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, dout=dout, x=x, out=out, dz=None,
             delta_softplus=ctx.delta_softplus, recompute_out_z=False, tile_states=ck)
         dz = rest[0] if ctx.has_z else None
+        du, ddelta, dz, dB, dC = (_unpad(t, pad) for t in (du, ddelta, dz, dB, dC))
         dB = dB.squeeze(1) if getattr(ctx, "squeeze_B", False) else dB
         dC = dC.squeeze(1) if getattr(ctx, "squeeze_C", False) else dC
         return (du, ddelta, dA, dB, dC,
@@ -165,6 +202,8 @@ class SelectiveScanPQFn(torch.autograd.Function):
         # dstate <= 16 the forward also writes the states before every 16-step tile (B * dim * L
         # float32, about one float32 copy of u), which spare the backward a recompute of the scan.
         want_ck = A.shape[1] <= 16 and P.shape[-1] > 0 and _save_tile_states()
+        pad = ctx.pad = _train_pad(u, A, B, C, pq=True)
+        u, delta, z, B, C = (_pad_front(t, pad) for t in (u, delta, z, B, C))
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus,
                                   tile_states=want_ck)
         ck = rest.pop() if want_ck else None
@@ -174,6 +213,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
                               out if ctx.has_z else None, ck)
         last_state = x[:, :, -1, 1::2]
         result = rest[0] if ctx.has_z else out
+        result = _unpad(result, pad).contiguous() if pad else result
         return result if not return_last_state else (result, last_state)
 
     @staticmethod
@@ -185,6 +225,8 @@ class SelectiveScanPQFn(torch.autograd.Function):
         u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, x, out, ck = ctx.saved_tensors
         if dout.stride(-1) != 1:
             dout = dout.contiguous()
+        pad = ctx.pad
+        dout = _pad_front(dout, pad)
         dP = torch.zeros(P.shape, dtype=torch.float32, device=P.device)
         dQ = torch.zeros(Q.shape, dtype=torch.float32, device=Q.device)
         du, ddelta, dA, dB, dC, dD, ddelta_bias, *rest = ext().bwd(
@@ -192,6 +234,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
             x=x, out=out, dz=None, dP_out=dP, dQ_out=dQ, delta_softplus=ctx.delta_softplus,
             recompute_out_z=False, tile_states=ck)
         dz = rest[0] if ctx.has_z else None
+        du, ddelta, dz, dB, dC = (_unpad(t, pad) for t in (du, ddelta, dz, dB, dC))
         dB = dB.squeeze(1) if getattr(ctx, "squeeze_B", False) else dB
         dC = dC.squeeze(1) if getattr(ctx, "squeeze_C", False) else dC
         return (du, ddelta, dA, dB, dC,

@@ -99,9 +99,12 @@ def test_bwd_options(flags):
     _vs_exact(case, _dout(611, (2, 32, 100), torch.float32), torch.float32, str(flags))
 
 
+@pytest.mark.parametrize("pad", ["1", "0"], ids=["padded", "general"])
 @pytest.mark.parametrize("L", [1, 7, 2049, 4100, 2056, 4096])
-def test_bwd_lengths(L):
-    _say(f"bwd L={L}")
+def test_bwd_lengths(L, pad, monkeypatch):
+    """Odd lengths run padded (the fast kernels) or, with MM_SCAN_PAD=0, on the general kernels."""
+    monkeypatch.setenv("MM_SCAN_PAD", pad)
+    _say(f"bwd L={L} padding {pad}")
     case = _case(620 + L, 1, 16, L, 16, torch.float32)
     _vs_exact(case, _dout(621, (1, 16, L), torch.float32), torch.float32, f"L{L}")
 
@@ -417,6 +420,31 @@ def test_bwd_states_pass_balanced_grid(q, dtype):
         exact = selective_scan_bwd_ref(**sub, dout=dout[bb:bb + 1, chans], dtype=torch.float64)
         for name, idx in (("du", 0), ("ddelta", 1), ("dz", 7)):
             _check(recomputed[idx][bb:bb + 1, chans], exact[name], dtype, f"states pass q={q} b{bb} {name}")
+
+
+@pytest.mark.parametrize("L,dtype", [(13, torch.float32), (1001, torch.bfloat16), (2047, torch.float32)])
+def test_bwd_padded_lengths(L, dtype):
+    """Training at lengths that are not multiples of 8: selective_scan_fn pads the request in front
+    with zero-u steps (forward and backward on the padded copies, gradients of the real steps
+    returned); the output, last state and every gradient against the exact ones."""
+    _say(f"bwd padded length L={L} {dtype}")
+    from motif_mamba_amd import selective_scan_fn
+    case = _case(760 + L, 2, 64, L, 16, dtype, bkind="4d", G=2)
+    dout = _dout(761, (2, 64, L), dtype)
+    g = {k: (v.to(DEV).requires_grad_(True) if torch.is_tensor(v) else v) for k, v in case.items()}
+    out, last = selective_scan_fn(**g, return_last_state=True)
+    assert out.shape == (2, 64, L) and out.is_contiguous()
+    ref, ref_last = selective_scan_ref(**case, return_last_state=True)
+    rtol, atol = _tol(dtype)
+    torch.testing.assert_close(out.detach().cpu().float(), ref.float(), rtol=rtol, atol=atol)
+    torch.testing.assert_close(last.cpu(), ref_last.float(), rtol=rtol, atol=atol)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    exact = selective_scan_bwd_ref(**case, dout=dout, dtype=torch.float64)
+    for n in NAMES:
+        gr = g[n].grad
+        assert gr.shape == case[n].shape, (n, gr.shape)
+        _check(gr, exact[GRAD[n]], dtype, f"padded L{L} {GRAD[n]}")
 
 
 @pytest.mark.parametrize("L", [2, 6, 18, 1002, 2054])

@@ -246,7 +246,16 @@ def test_pq_bwd_c_abi_direct():
     assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_INVALID_ARGUMENT
 
 
-@pytest.mark.parametrize("what", ["dstate32", "L12", "constB"])
+@pytest.mark.parametrize("L", [12, 1001])
+def test_pq_bwd_padded_lengths(L):
+    """Lengths that are not multiples of 8: the training forward and the backward run on copies
+    padded in front with zero-u steps, which add nothing to any gradient; against the exact ones."""
+    _say(f"pq bwd padded length L={L}")
+    case = _pq_case(795 + L, batch=2, dim=32, L=L, N=16, R=2, dtype=torch.float32, bkind="4d", G=2)
+    _vs_exact(case, _dout(796, (2, 32, L), torch.float32), torch.float32, f"padded L{L}")
+
+
+@pytest.mark.parametrize("what", ["dstate32", "constB"])
 def test_pq_bwd_unsupported_shapes_raise(what):
     """Shapes outside the kernel raise NotImplementedError in the backward; the forward runs."""
     _say(f"pq bwd unsupported {what}")
@@ -254,8 +263,6 @@ def test_pq_bwd_unsupported_shapes_raise(what):
     kw = dict(batch=1, dim=16, L=32, N=16, R=2, dtype=torch.float32)
     if what == "dstate32":
         kw["N"] = 32
-    elif what == "L12":
-        kw["L"] = 12
     case = _pq_case(790, **kw)
     if what == "constB":
         case["B"] = torch.randn(16, 16)
