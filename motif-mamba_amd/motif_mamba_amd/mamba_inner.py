@@ -46,7 +46,7 @@ import torch
 import torch.nn.functional as F
 
 from ._native import ext
-from .selective_scan import _save_tile_states
+from .selective_scan import _pad_front, _save_tile_states, _train_pad, _unpad
 
 
 def _cm_empty(batch, ch, L, like, dtype=None):
@@ -165,9 +165,14 @@ class MambaInnerFn(torch.autograd.Function):
         # checkpoint_lvl 0 keeps activations rather than recomputing them: the scan's 16-step tile
         # states too (None where the kernels do not write them), which spare the backward a recompute.
         want_ck = checkpoint_lvl == 0 and A.shape[-1] == 16 and _save_tile_states()
-        out, scan_states, out_z, *ck = ext().fwd(conv1d_out, delta, A, B, C, D, z, delta_bias, None, None, None,
-                                                 delta_softplus, tile_states=want_ck)
+        # A length that is not a multiple of 8: the scan runs on copies padded in front with zero-u
+        # steps, forward and backward (as selective_scan_fn pads), and its outputs are cut back.
+        pad = ctx.scan_pad = _train_pad(conv1d_out, A, B, C, pq=False)
+        out, scan_states, out_z, *ck = ext().fwd(*(_pad_front(t, pad) for t in (conv1d_out, delta)), A,
+                                                 *(_pad_front(t, pad) for t in (B, C)), D, _pad_front(z, pad),
+                                                 delta_bias, None, None, None, delta_softplus, tile_states=want_ck)
         ck = ck[0] if want_ck else None
+        out_z = _unpad(out_z, pad)
         ctx.delta_softplus = delta_softplus
         ctx.out_proj_bias_is_None = out_proj_bias is None
         ctx.checkpoint_lvl = checkpoint_lvl
@@ -208,9 +213,20 @@ class MambaInnerFn(torch.autograd.Function):
         dxz = torch.empty_like(xz)
         dx, dz = dxz.chunk(2, dim=1)
         dout_y = _cm_view(out_proj_weight.t() @ dout2.t(), batch)          # (batch, d_inner, L), channel-major
-        du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, out_z = ext().bwd(
-            conv1d_out, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, dout=dout_y, x=scan_states, out=out,
-            dz=dz, delta_softplus=ctx.delta_softplus, recompute_out_z=True, tile_states=ck)
+        pad = ctx.scan_pad
+        if pad:
+            # The forward's padded scan (dout zero over the padding): dz comes back padded and is
+            # copied into dxz; du, ddelta, dB, dC and out_z are cut back to the real steps.
+            du, ddelta, dA, dB, dC, dD, ddelta_bias, dz_p, out_z = ext().bwd(
+                *(_pad_front(t, pad) for t in (conv1d_out, delta)), A, *(_pad_front(t, pad) for t in (B, C)),
+                D=D, z=_pad_front(z, pad), delta_bias=delta_bias, dout=_pad_front(dout_y, pad), x=scan_states,
+                out=out, dz=None, delta_softplus=ctx.delta_softplus, recompute_out_z=True, tile_states=ck)
+            dz.copy_(_unpad(dz_p, pad))
+            du, ddelta, dB, dC, out_z = (_unpad(t, pad) for t in (du, ddelta, dB, dC, out_z))
+        else:
+            du, ddelta, dA, dB, dC, dD, ddelta_bias, dz, out_z = ext().bwd(
+                conv1d_out, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, dout=dout_y, x=scan_states, out=out,
+                dz=dz, delta_softplus=ctx.delta_softplus, recompute_out_z=True, tile_states=ck)
         dout_proj_weight = dout2.t() @ _cm_flat(out_z).t()                 # (d_model, d_inner)
         dout_proj_bias = dout2.sum(dim=0) if not ctx.out_proj_bias_is_None else None
         # Rows of x_dbl that feed nothing (B or C given by the caller) get a zero gradient; the

@@ -129,11 +129,16 @@ def test_backward(dtype, ckpt, bc_bias):
         _check(gg[k], v, dtype, f"d{k}")
 
 
-def test_backward_without_biases_ragged_length():
-    _say("mamba_inner bwd no biases L=37")
+@pytest.mark.parametrize("pad", ["1", "0"], ids=["padded", "general"])
+@pytest.mark.parametrize("ckpt", [0, 1])
+def test_backward_without_biases_ragged_length(pad, ckpt, monkeypatch):
+    """L = 37: the scan runs on copies padded in front with zero-u steps (forward and backward), or,
+    with MM_SCAN_PAD=0, on the general kernels."""
+    monkeypatch.setenv("MM_SCAN_PAD", pad)
+    _say(f"mamba_inner bwd no biases L=37 padding {pad} checkpoint_lvl={ckpt}")
     c = _case(920, L=37, biases=False)
     dout = _dout(921, c)
-    got, gg = _run(c, dout)
+    got, gg = _run(c, dout, checkpoint_lvl=ckpt)
     want, eg = _oracle(c, dout)
     _check(got, want, torch.float32, "out")
     for k, v in eg.items():
