@@ -41,6 +41,15 @@ int64_t device_simds();
 template <typename T>
 int launch_pq(const mm_scan_fwd_params &p, hipStream_t stream);
 
+// The diagonal scan on the P/Q kernels with a zero rank-1 coupling (mm_scan_pq.hip), for diagonal
+// requests the dstate-16 kernels do not take: diag_via_pq_fwd / diag_via_pq_bwd tell whether a
+// request goes that way (inference forwards with dstate != 16 up to 64; backwards with dstate < 16),
+// attach_zero_pair fills a copy of its parameters with the zero pair (and the gradient sink).
+bool diag_via_pq_fwd(const mm_scan_fwd_params &p);
+int attach_zero_pair(mm_scan_fwd_params &q);
+bool diag_via_pq_bwd(const mm_scan_bwd_params &p);
+int attach_zero_pair(mm_scan_bwd_params &q);
+
 // Backward (mm_scan_bwd.hip): clears the accumulated gradients and launches the backward kernels
 // on `stream`; bwd_workspace_bytes() is the scratch it uses best, bwd_workspace_min_bytes() the
 // least it accepts (with tile states: without the segment carries, every unit then a whole row).

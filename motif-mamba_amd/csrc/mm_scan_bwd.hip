@@ -1042,6 +1042,8 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
+    if (diag_via_pq_bwd(p))   // the P/Q backward with the zero pair (no tile states at dstate < 16)
+        return ((p.tile_states ? 0 : bwd::fast_ck_floats(p)) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p) && p.tile_states)
         return (2 * bwd::fast_part_floats(p) + bwd::carry_floats(bwd::seg_plan_for(p))) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p) && bwd::states_pass_ok(p)) {
@@ -1059,13 +1061,17 @@ int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
 }
 
 int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p) {
+    if (diag_via_pq_bwd(p)) return bwd_workspace_bytes(p);
     if (!p.P && bwd::fast_ok(p) && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     return bwd_workspace_bytes(p);
 }
 
 template <typename T>
-int launch_bwd(const mm_scan_bwd_params &p, hipStream_t s) {
+int launch_bwd(const mm_scan_bwd_params &p_in, hipStream_t s) {
+    // Diagonal requests with dstate < 16 run the P/Q backward with a zero rank-1 pair.
+    mm_scan_bwd_params p = p_in;
+    if (diag_via_pq_bwd(p_in) && attach_zero_pair(p) != MM_OK) p = p_in;
     // The accumulated gradients start from zero on the launch stream (the dstate-16 kernel writes
     // dB and dC whole and only accumulates dA, dD and ddelta_bias).
     const bool fast = bwd::fast_ok(p) && p.seqlen > 0;

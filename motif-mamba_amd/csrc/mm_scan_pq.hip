@@ -35,6 +35,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include <type_traits>
 
@@ -649,5 +650,88 @@ int launch_pq(const mm_scan_fwd_params &p, hipStream_t s) {
 template int launch_pq<float>(const mm_scan_fwd_params &, hipStream_t);
 template int launch_pq<f16_t>(const mm_scan_fwd_params &, hipStream_t);
 template int launch_pq<bf16_t>(const mm_scan_fwd_params &, hipStream_t);
+
+// ------------------------------------------------------------------------------------------------
+// The diagonal scan through the P/Q kernels. A zero rank-1 pair shared by every channel (P = Q = 0)
+// leaves the coupled recurrence exactly the diagonal one: q = Q h = 0 and every coupling term is
+// fma(0, q, w) = w. Diagonal requests the dstate-16 kernels do not take (dstate below 16, or 17 to
+// 64, variable B and C) run several times faster this way than on the general kernels. The pair and
+// the sink for its dP / dQ (written by the backward's atomics, never read) are static device arrays;
+// their addresses are looked up once per device.
+namespace {
+__device__ __align__(16) float pq_zero_pair[64];   // zero-initialised, never written
+__device__ __align__(16) float pq_grad_sink[64];   // receives the zero pair's gradients
+
+constexpr int kMaxDev = 64;
+std::atomic<float *> g_zero_ptr[kMaxDev], g_sink_ptr[kMaxDev];
+
+int zero_pair_pointers(float **zero, float **sink) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return MM_ERR_UNSUPPORTED;
+    float *z = g_zero_ptr[dev].load(std::memory_order_acquire);
+    float *k = g_sink_ptr[dev].load(std::memory_order_acquire);
+    if (z == nullptr || k == nullptr) {
+        void *a = nullptr, *b = nullptr;
+        if (hipGetSymbolAddress(&a, HIP_SYMBOL(pq_zero_pair)) != hipSuccess || a == nullptr) return MM_ERR_UNSUPPORTED;
+        if (hipGetSymbolAddress(&b, HIP_SYMBOL(pq_grad_sink)) != hipSuccess || b == nullptr) return MM_ERR_UNSUPPORTED;
+        z = static_cast<float *>(a);
+        k = static_cast<float *>(b);
+        g_zero_ptr[dev].store(z, std::memory_order_release);
+        g_sink_ptr[dev].store(k, std::memory_order_release);
+    }
+    *zero = z;
+    *sink = k;
+    return MM_OK;
+}
+
+// MM_DIAG_VIA_PQ=0 keeps such requests on the general kernels (read per call, for the tests).
+bool diag_pq_enabled() {
+    const char *e = getenv("MM_DIAG_VIA_PQ");
+    return !(e && e[0] == '0');
+}
+}  // namespace
+
+bool diag_via_pq_fwd(const mm_scan_fwd_params &p) {
+    // Inference only: the P/Q kernels write chunk states as (1, h), the diagonal form is (prod a, h).
+    if (p.P || p.dstate == 16 || p.dstate > 64 || p.chunk_states || p.tile_states || !diag_pq_enabled())
+        return false;
+    return pq::tiled_shape(p).LPR != 0;
+}
+
+int attach_zero_pair(mm_scan_fwd_params &q) {
+    float *zero = nullptr, *sink = nullptr;
+    const int rc = zero_pair_pointers(&zero, &sink);
+    if (rc != MM_OK) return rc;
+    q.P = zero;
+    q.Q = zero;
+    q.gamma = nullptr;
+    q.pq_rank = 1;
+    q.P_d_stride = 0; q.P_dstate_stride = 1; q.P_r_stride = 0;
+    q.Q_d_stride = 0; q.Q_r_stride = 0; q.Q_dstate_stride = 1;
+    return MM_OK;
+}
+
+bool diag_via_pq_bwd(const mm_scan_bwd_params &p) {
+    if (p.P || p.dstate >= 16 || !diag_pq_enabled()) return false;
+    mm_scan_bwd_params q = p;
+    q.pq_rank = 1;
+    return pq_bwd_ok(q);
+}
+
+int attach_zero_pair(mm_scan_bwd_params &q) {
+    float *zero = nullptr, *sink = nullptr;
+    const int rc = zero_pair_pointers(&zero, &sink);
+    if (rc != MM_OK) return rc;
+    q.P = zero;
+    q.Q = zero;
+    q.pq_rank = 1;
+    q.P_d_stride = 0; q.P_dstate_stride = 1; q.P_r_stride = 0;
+    q.Q_d_stride = 0; q.Q_r_stride = 0; q.Q_dstate_stride = 1;
+    q.dP = sink;
+    q.dQ = sink;
+    q.dP_d_stride = 0; q.dP_dstate_stride = 1; q.dP_r_stride = 0;
+    q.dQ_d_stride = 0; q.dQ_r_stride = 0; q.dQ_dstate_stride = 1;
+    return MM_OK;
+}
 
 }  // namespace mm

@@ -90,6 +90,17 @@ def test_bwd_shapes(dtype, N):
     _vs_exact(case, _dout(601, (2, 32, 136), dtype), dtype, f"N{N}")
 
 
+@pytest.mark.parametrize("N", [1, 4, 8, 12])
+@pytest.mark.parametrize("via_pq", ["1", "0"], ids=["zero-pair", "general"])
+def test_bwd_small_dstate(N, via_pq, monkeypatch):
+    """Diagonal backward at dstate < 16 (variable B/C): the P/Q backward with a zero rank-1 pair,
+    or (MM_DIAG_VIA_PQ=0) the general kernel; against the exact gradients."""
+    monkeypatch.setenv("MM_DIAG_VIA_PQ", via_pq)
+    _say(f"bwd dstate {N} via_pq={via_pq}")
+    case = _case(770 + N, 2, 64, 264, N, torch.float32, bkind="4d", G=2)
+    _vs_exact(case, _dout(771, (2, 64, 264), torch.float32), torch.float32, f"N{N} via_pq={via_pq}")
+
+
 @pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False), dict(with_bias=False),
                                    dict(softplus=False), dict(bkind="4d", G=2), dict(bkind="4d", G=4),
                                    dict(bkind="const")])

@@ -128,6 +128,20 @@ def test_random_shapes_general_kernels(shape, monkeypatch):
     _close(last, exp_last, torch.bfloat16, "last_state")
 
 
+@pytest.mark.parametrize("N", [4, 8, 12, 24, 32, 64])
+@pytest.mark.parametrize("via_pq", ["1", "0"], ids=["zero-pair", "general"])
+def test_other_dstate_every_row(N, via_pq, monkeypatch):
+    """Diagonal inference at dstate != 16 (variable B/C): the P/Q kernels with a zero rank-1 pair,
+    which leaves the recurrence exactly diagonal, or (MM_DIAG_VIA_PQ=0) the general kernel; every
+    row's output and last state against the float64 restatement, G = 2, L = 256."""
+    monkeypatch.setenv("MM_DIAG_VIA_PQ", via_pq)
+    batch, dim, L = 2, 128, 256
+    _say(f"dstate {N} via_pq={via_pq}")
+    case = _case(130 + N, batch, dim, L, N, torch.bfloat16, bkind="4d", G=2)
+    out, last = _run(case)
+    _rows_vs_f64(case, out, last, f"dstate {N}")
+
+
 @pytest.mark.parametrize("L", [7, 1001, 2047])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 @pytest.mark.parametrize("with_z", [True, False], ids=["z", "noz"])
