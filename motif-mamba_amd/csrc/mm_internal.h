@@ -39,7 +39,7 @@ int64_t device_simds();
 // Forward scan with the low-rank P/Q coupling (mm_scan_pq.hip): the tiled kernel when the request
 // fits it, else the lane-per-row kernel.
 template <typename T>
-int launch_pq(const mm_scan_fwd_params &p, hipStream_t stream);
+int launch_pq(const mm_scan_fwd_params &p, hipStream_t stream, bool diag_x = false);
 
 // The diagonal scan on the P/Q kernels with a zero rank-1 coupling (mm_scan_pq.hip), for diagonal
 // requests the dstate-16 kernels do not take: diag_via_pq_fwd / diag_via_pq_bwd tell whether a

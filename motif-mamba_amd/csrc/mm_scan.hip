@@ -604,7 +604,7 @@ int dispatch_fwd(const mm_scan_fwd_params &p, hipStream_t s) {
     if (p.P) return mm::launch_pq<T>(p, s);
     if (mm::diag_via_pq_fwd(p)) {
         mm_scan_fwd_params q = p;
-        if (mm::attach_zero_pair(q) == MM_OK) return mm::launch_pq<T>(q, s);
+        if (mm::attach_zero_pair(q) == MM_OK) return mm::launch_pq<T>(q, s, true);
     }
     int rc = mm::try_launch_tiled<T>(p, s);
     if (rc != MM_ERR_UNSUPPORTED || p.tile_states) return rc;   // the general kernel writes no tile states

@@ -63,7 +63,9 @@ __device__ __forceinline__ void lds_read_vec(const float *src, float *o) {
     }
 }
 
-template <typename T, int S, int LPR, int R>
+// DX: the chunk states in the diagonal scan's form, (prod of the decays since step 0, h), for the
+// diagonal requests run with a zero P/Q pair; otherwise (1, h), the P/Q form.
+template <typename T, int S, int LPR, int R, bool DX = false>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t blocks_per_group) {
     constexpr int NP = S * LPR;            // padded states per channel
@@ -148,6 +150,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
     const bool softplus = p.delta_softplus != 0;
     const int es = E * k;                  // first step (within a tile) of this lane's elements
     const int64_t n_chunks = (L + MM_SCAN_CHUNK - 1) / MM_SCAN_CHUNK;
+    float cum_dt = 0.f;                    // DX: running sum of dt' (prod a = exp2(A log2e cum_dt))
     // Checkpoints for the backward: the S states of this lane before every 16-step tile.
     const int64_t ck_tile = p.batch * p.dim * 16;
     float *const ckp = (p.tile_states && active) ? p.tile_states + (b * p.dim + d) * 16 + k * S : nullptr;
@@ -324,6 +327,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
                 float bv[S];
                 lds_read_vec<S>(&sBC[t * BCS + k * S], bv);
                 lds_read_vec<S>(&sBC[t * BCS + NP + k * S], cv[j]);
+                if constexpr (DX) cum_dt += dts[j];   // steps past L have dt' = 0
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
                     av[j][s] = decay_exp2(dts[j], A2[s]);
@@ -442,7 +446,7 @@ scan_fwd_pq_tiled(const mm_scan_fwd_params p, const int64_t ratio, const int32_t
                 for (int s = 0; s < S; ++s) {
                     const int n = k * S + s;
                     if (n < N) {
-                        cs[2 * n] = 1.f;
+                        cs[2 * n] = DX ? __builtin_amdgcn_exp2f(A2[s] * cum_dt) : 1.f;
                         cs[2 * n + 1] = h[s];
                     }
                 }
@@ -607,18 +611,20 @@ TiledShape tiled_shape(const mm_scan_fwd_params &p) {
     return 2 * waves(8) <= 5 * simds ? cands[1] : cands[0];
 }
 
-template <typename T, int S, int LPR, int R>
+template <typename T, int S, int LPR, int R, bool DX = false>
 int launch_tiled_sr(const mm_scan_fwd_params &p, hipStream_t s) {
     constexpr int CPW = 64 / LPR;
     const int64_t ratio = p.dim / p.n_groups;
     const int64_t bpg = (ratio + CPW - 1) / CPW;
     dim3 grid(unsigned(bpg * p.n_groups), unsigned(p.batch));
-    hipLaunchKernelGGL((scan_fwd_pq_tiled<T, S, LPR, R>), grid, dim3(64), 0, s, p, ratio, int32_t(bpg));
+    hipLaunchKernelGGL((scan_fwd_pq_tiled<T, S, LPR, R, DX>), grid, dim3(64), 0, s, p, ratio, int32_t(bpg));
     return launch_status("scan_fwd_pq_tiled");
 }
 
+// diag_x: the zero-pair diagonal route, which has rank 1 and wants the diagonal chunk states.
 template <typename T, int S, int LPR>
-int launch_tiled_s(const mm_scan_fwd_params &p, hipStream_t s) {
+int launch_tiled_s(const mm_scan_fwd_params &p, hipStream_t s, bool diag_x) {
+    if (diag_x) return launch_tiled_sr<T, S, LPR, 2, true>(p, s);
     if (p.pq_rank <= 2) return launch_tiled_sr<T, S, LPR, 2>(p, s);
     if (p.pq_rank <= 4) return launch_tiled_sr<T, S, LPR, 4>(p, s);
     return launch_tiled_sr<T, S, LPR, 8>(p, s);
@@ -635,21 +641,22 @@ int launch_rowlane(const mm_scan_fwd_params &p, hipStream_t s) {
 }  // namespace pq
 
 template <typename T>
-int launch_pq(const mm_scan_fwd_params &p, hipStream_t s) {
+int launch_pq(const mm_scan_fwd_params &p, hipStream_t s, bool diag_x) {
     const pq::TiledShape sh = pq::tiled_shape(p);
-    if (sh.LPR == 4) return pq::launch_tiled_s<T, 4, 4>(p, s);
-    if (sh.LPR == 8) return sh.S == 4 ? pq::launch_tiled_s<T, 4, 8>(p, s) : pq::launch_tiled_s<T, 2, 8>(p, s);
+    if (sh.LPR == 4) return pq::launch_tiled_s<T, 4, 4>(p, s, diag_x);
+    if (sh.LPR == 8)
+        return sh.S == 4 ? pq::launch_tiled_s<T, 4, 8>(p, s, diag_x) : pq::launch_tiled_s<T, 2, 8>(p, s, diag_x);
     if (sh.LPR == 16) {
-        if (sh.S == 4) return pq::launch_tiled_s<T, 4, 16>(p, s);
-        if (sh.S == 2) return pq::launch_tiled_s<T, 2, 16>(p, s);
-        return pq::launch_tiled_s<T, 1, 16>(p, s);
+        if (sh.S == 4) return pq::launch_tiled_s<T, 4, 16>(p, s, diag_x);
+        if (sh.S == 2) return pq::launch_tiled_s<T, 2, 16>(p, s, diag_x);
+        return pq::launch_tiled_s<T, 1, 16>(p, s, diag_x);
     }
-    return pq::launch_rowlane<T>(p, s);
+    return pq::launch_rowlane<T>(p, s);   // not reached with diag_x (diag_via_pq_fwd requires a tiled shape)
 }
 
-template int launch_pq<float>(const mm_scan_fwd_params &, hipStream_t);
-template int launch_pq<f16_t>(const mm_scan_fwd_params &, hipStream_t);
-template int launch_pq<bf16_t>(const mm_scan_fwd_params &, hipStream_t);
+template int launch_pq<float>(const mm_scan_fwd_params &, hipStream_t, bool);
+template int launch_pq<f16_t>(const mm_scan_fwd_params &, hipStream_t, bool);
+template int launch_pq<bf16_t>(const mm_scan_fwd_params &, hipStream_t, bool);
 
 // ------------------------------------------------------------------------------------------------
 // The diagonal scan through the P/Q kernels. A zero rank-1 pair shared by every channel (P = Q = 0)
@@ -692,9 +699,9 @@ bool diag_pq_enabled() {
 }  // namespace
 
 bool diag_via_pq_fwd(const mm_scan_fwd_params &p) {
-    // Inference only: the P/Q kernels write chunk states as (1, h), the diagonal form is (prod a, h).
-    if (p.P || p.dstate == 16 || p.dstate > 64 || p.chunk_states || p.tile_states || !diag_pq_enabled())
-        return false;
+    // The tiled P/Q kernel then writes the chunk states in the diagonal form (DX); no tile states
+    // (the diagonal forward writes them at dstate 16 only).
+    if (p.P || p.dstate == 16 || p.dstate > 64 || p.tile_states || !diag_pq_enabled()) return false;
     return pq::tiled_shape(p).LPR != 0;
 }
 

@@ -305,7 +305,7 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
     const char *pad_env = std::getenv("MM_SCAN_PAD");
     const bool pad_off = pad_env && pad_env[0] == '0';
     const bool fast_shape = p.is_variable_B && p.is_variable_C && p.dim % 16 == 0 &&
-                            (p.dim / p.n_groups) % 16 == 0 && (p.P ? p.dstate <= 64 : p.dstate == 16);
+                            (p.dim / p.n_groups) % 16 == 0 && p.dstate <= 64;   // diagonal or P/Q
     if (!pad_off && fast_shape && p.seqlen % 8 != 0) {
         const int64_t L = p.seqlen, pad = (L + 31) / 32 * 32 - L;
         auto front = [&](const at::Tensor &t) { return at::constant_pad_nd(t, {pad, 0}, 0); };

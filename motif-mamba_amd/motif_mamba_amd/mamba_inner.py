@@ -167,7 +167,7 @@ class MambaInnerFn(torch.autograd.Function):
         want_ck = checkpoint_lvl == 0 and A.shape[-1] == 16 and _save_tile_states()
         # A length that is not a multiple of 8: the scan runs on copies padded in front with zero-u
         # steps, forward and backward (as selective_scan_fn pads), and its outputs are cut back.
-        pad = ctx.scan_pad = _train_pad(conv1d_out, A, B, C, pq=False)
+        pad = ctx.scan_pad = _train_pad(conv1d_out, A, B, C)
         out, scan_states, out_z, *ck = ext().fwd(*(_pad_front(t, pad) for t in (conv1d_out, delta)), A,
                                                  *(_pad_front(t, pad) for t in (B, C)), D, _pad_front(z, pad),
                                                  delta_bias, None, None, None, delta_softplus, tile_states=want_ck)

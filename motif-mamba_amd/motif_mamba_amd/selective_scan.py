@@ -52,21 +52,21 @@ def _save_tile_states():
     return os.environ.get("MM_TILE_STATES", "1") != "0"
 
 
-def _train_pad(u, A, B, C, pq):
+def _train_pad(u, A, B, C):
     """Steps to put in front of a training request whose length is not a multiple of 8, so that
-    the forward and backward run the fast kernels (the diagonal ones take dstate 16, the P/Q
-    backward dstate <= 16; with other lengths the diagonal scan would run the general kernels, ~14x
-    and ~100x slower, and the P/Q backward would refuse the call). The padded steps carry zero u,
-    delta, z, B and C, and dout is zero over them: from the zero initial state a zero-u step leaves
-    every state exactly zero, so the real steps run the unpadded recurrence, and the padded steps
-    add nothing to dA, dD, ddelta_bias, dP or dQ (each of their terms holds u, h or Q h of a padded
-    step). 0 when no padding applies, or with MM_SCAN_PAD=0 (which also turns off the binding's
-    padding of inference requests)."""
+    the forward and backward run the fast kernels (the diagonal ones at dstate 16, the P/Q ones at
+    dstate <= 16, which also run the diagonal scan at other dstate values with a zero coupling;
+    with other lengths the diagonal scan would run the general kernels, ~14x and ~100x slower, and
+    the P/Q backward would refuse the call). The padded steps carry zero u, delta, z, B and C, and
+    dout is zero over them: from the zero initial state a zero-u step leaves every state exactly
+    zero, so the real steps run the unpadded recurrence, and the padded steps add nothing to dA,
+    dD, ddelta_bias, dP or dQ (each of their terms holds u, h or Q h of a padded step). 0 when no
+    padding applies, or with MM_SCAN_PAD=0 (which also turns off the binding's padding of
+    inference requests)."""
     L = u.shape[-1]
     if L % 8 == 0 or B.dim() != 4 or C.dim() != 4 or os.environ.get("MM_SCAN_PAD", "1") == "0":
         return 0
-    n = A.shape[1]
-    if (n > 16) if pq else (n != 16):
+    if A.shape[1] > 16:
         return 0
     dim, groups = u.shape[1], B.shape[1]
     if dim % 16 or (dim // groups) % 16:
@@ -119,7 +119,7 @@ class SelectiveScanFn(torch.autograd.Function):
         # the states before every 16-step tile (None where the kernels do not write them), which
         # spare the backward its recompute of the scan.
         want_ck = A.shape[1] == 16 and _save_tile_states()
-        pad = ctx.pad = _train_pad(u, A, B, C, pq=False)
+        pad = ctx.pad = _train_pad(u, A, B, C)
         u, delta, z, B, C = (_pad_front(t, pad) for t in (u, delta, z, B, C))
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, None, None, None, delta_softplus,
                                   tile_states=want_ck)
@@ -202,7 +202,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
         # dstate <= 16 the forward also writes the states before every 16-step tile (B * dim * L
         # float32, about one float32 copy of u), which spare the backward a recompute of the scan.
         want_ck = A.shape[1] <= 16 and P.shape[-1] > 0 and _save_tile_states()
-        pad = ctx.pad = _train_pad(u, A, B, C, pq=True)
+        pad = ctx.pad = _train_pad(u, A, B, C)
         u, delta, z, B, C = (_pad_front(t, pad) for t in (u, delta, z, B, C))
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, P, Q, gamma, delta_softplus,
                                   tile_states=want_ck)

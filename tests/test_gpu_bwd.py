@@ -433,14 +433,16 @@ def test_bwd_states_pass_balanced_grid(q, dtype):
             _check(recomputed[idx][bb:bb + 1, chans], exact[name], dtype, f"states pass q={q} b{bb} {name}")
 
 
-@pytest.mark.parametrize("L,dtype", [(13, torch.float32), (1001, torch.bfloat16), (2047, torch.float32)])
-def test_bwd_padded_lengths(L, dtype):
+@pytest.mark.parametrize("L,dtype,N", [(13, torch.float32, 16), (1001, torch.bfloat16, 16), (2047, torch.float32, 16),
+                                       (13, torch.float32, 8), (1001, torch.bfloat16, 4)])
+def test_bwd_padded_lengths(L, dtype, N):
     """Training at lengths that are not multiples of 8: selective_scan_fn pads the request in front
     with zero-u steps (forward and backward on the padded copies, gradients of the real steps
-    returned); the output, last state and every gradient against the exact ones."""
-    _say(f"bwd padded length L={L} {dtype}")
+    returned); the output, last state and every gradient against the exact ones. dstate 16 runs
+    the diagonal kernels, dstate 8 and 4 the P/Q ones with a zero pair."""
+    _say(f"bwd padded length L={L} {dtype} dstate {N}")
     from motif_mamba_amd import selective_scan_fn
-    case = _case(760 + L, 2, 64, L, 16, dtype, bkind="4d", G=2)
+    case = _case(760 + L + N, 2, 64, L, N, dtype, bkind="4d", G=2)
     dout = _dout(761, (2, 64, L), dtype)
     g = {k: (v.to(DEV).requires_grad_(True) if torch.is_tensor(v) else v) for k, v in case.items()}
     out, last = selective_scan_fn(**g, return_last_state=True)

@@ -142,6 +142,44 @@ def test_other_dstate_every_row(N, via_pq, monkeypatch):
     _rows_vs_f64(case, out, last, f"dstate {N}")
 
 
+@pytest.mark.parametrize("N,L", [(8, 4104), (32, 4096), (4, 2056)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("via_pq", ["1", "0"], ids=["zero-pair", "general"])
+def test_other_dstate_reference_fwd_chunk_states(N, L, dtype, via_pq, monkeypatch):
+    """The training forward (ext.fwd with chunk states) at dstate != 16: on the P/Q kernels with a
+    zero pair, which then write x in the diagonal form, (prod a, h) per 2048-step chunk, or
+    (MM_DIAG_VIA_PQ=0) on the general kernel. Whole and partial last chunks; the prod-a half
+    against the closed form exp(A * sum delta'), the h half and the outputs of sampled rows against
+    the float64 restatement (16-bit outputs element by element; float32 ones row by row in the max
+    norm, as the long float32 P/Q check does: over thousands of steps, where a row's output cancels
+    towards zero, no float32 evaluation meets the element-wise bound)."""
+    monkeypatch.setenv("MM_DIAG_VIA_PQ", via_pq)
+    _say(f"reference-format fwd dstate {N} L={L} {dtype} via_pq={via_pq}")
+    from motif_mamba_amd import _native
+    case = _case(140 + N, 2, 64, L, N, dtype, bkind="4d", G=2)
+    g = _to(case, DEV)
+    out, x, out_z = _native.ext().fwd(g["u"], g["delta"], g["A"], g["B"], g["C"], D=g["D"], z=g["z"],
+                                      delta_bias=g["delta_bias"], delta_softplus=True)
+    torch.cuda.synchronize()
+    assert x.shape == (2, 64, (L + 2047) // 2048, 2 * N) and x.dtype == torch.float32
+    rows = [(b, d) for b in (0, 1) for d in range(b, 64, 11)]
+    r = cscan.scan_rows(**case, rows=rows, chunk=2048)    # out: pre-gate, out_z: gated
+    rtol, atol = fixtures.tolerances(dtype)
+    for got, exact, what in ((out, r["out"], "out"), (out_z, r["out_z"], "out_z")):
+        got = torch.stack([got[b, d] for b, d in rows]).cpu().double()
+        exact = torch.from_numpy(exact)
+        if dtype == torch.float32:
+            err = (got - exact).abs().amax(dim=-1)
+            bound = atol + rtol * exact.abs().amax(dim=-1)
+            assert bool((err <= bound).all()), f"{what}: row max error {err.max().item():.3g}"
+        else:
+            torch.testing.assert_close(got, exact, rtol=rtol, atol=atol, msg=lambda m: f"{what}: {m}")
+    for i, (b, d) in enumerate(rows):
+        np.testing.assert_allclose(x[b, d, :, 1::2].cpu().double().numpy(), r["h_chunks"][i], rtol=1e-3, atol=1e-3)
+    pa = chunk_states_ref(case["delta"], case["A"], case["delta_bias"], True)
+    np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
+
+
 @pytest.mark.parametrize("L", [7, 1001, 2047])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 @pytest.mark.parametrize("with_z", [True, False], ids=["z", "noz"])
