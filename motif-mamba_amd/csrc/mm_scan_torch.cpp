@@ -286,6 +286,9 @@ std::vector<at::Tensor> fwd(const at::Tensor &u, const at::Tensor &delta, const 
     return result;
 }
 
+// Shortest lengths (not multiples of 8) that fwd_infer pads for the fast kernels.
+constexpr int64_t kMinPaddedDiag = 14, kMinPaddedPQ = 5;
+
 std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, const at::Tensor &A,
                                   const at::Tensor &B, const at::Tensor &C, const c10::optional<at::Tensor> &D_,
                                   const c10::optional<at::Tensor> &z_,
@@ -302,11 +305,17 @@ std::vector<at::Tensor> fwd_infer(const at::Tensor &u, const at::Tensor &delta, 
     // its decay (and, with P/Q, whatever the coupling), so the real steps run the recurrence of the
     // unpadded request; the outputs are the padded call's last L steps, the last state its own.
     // MM_SCAN_PAD=0 turns this off (read per call: the tests run the general kernels with it).
+    // Short requests stay on the general kernels: the padded call's five pad copies, allocations
+    // and output copy cost ~50 us of host time, more than the general kernels take for a few
+    // steps (measured, bf16, batch 1 and 64: the diagonal general kernel is as fast up to L 13 at
+    // 5,120 channels, the P/Q one up to L 4 at 2,048; the Motif decode step calls the P/Q scan
+    // with L 1: 17 us against 58 us padded).
     const char *pad_env = std::getenv("MM_SCAN_PAD");
     const bool pad_off = pad_env && pad_env[0] == '0';
     const bool fast_shape = p.is_variable_B && p.is_variable_C && p.dim % 16 == 0 &&
                             (p.dim / p.n_groups) % 16 == 0 && p.dstate <= 64;   // diagonal or P/Q
-    if (!pad_off && fast_shape && p.seqlen % 8 != 0) {
+    const int64_t min_padded = p.P ? kMinPaddedPQ : kMinPaddedDiag;
+    if (!pad_off && fast_shape && p.seqlen % 8 != 0 && p.seqlen >= min_padded) {
         const int64_t L = p.seqlen, pad = (L + 31) / 32 * 32 - L;
         auto front = [&](const at::Tensor &t) { return at::constant_pad_nd(t, {pad, 0}, 0); };
         const c10::optional<at::Tensor> zp = z_.has_value() ? c10::optional<at::Tensor>(front(z_.value()))

@@ -183,10 +183,11 @@ def test_pq_general_odd_length_and_strided_rows(pad, monkeypatch):
     _close(last.cpu(), ref_last, torch.bfloat16, "odd L last")
 
 
-@pytest.mark.parametrize("L,R", [(1001, 2), (2047, 4)])
+@pytest.mark.parametrize("L,R", [(1, 2), (4, 2), (5, 2), (1001, 2), (2047, 4)])
 def test_pq_padded_length(L, R):
-    """P/Q inference at lengths that are not multiples of 8: the fast kernel on front-padded copies
-    (zero u keeps the coupled state at zero through the padding) against the float64 restatement."""
+    """P/Q inference at lengths that are not multiples of 8: from 5 steps on the fast kernel on
+    front-padded copies (zero u keeps the coupled state at zero through the padding), below the
+    lane-per-row kernel (L 1 is the Motif decode step's call); against selective_scan_pq_ref."""
     _say(f"pq padded length L={L} R={R}")
     case = _pq_case(390 + R, batch=2, dim=64, L=L, N=16, R=R, dtype=torch.bfloat16, bkind="4d", G=2)
     _vs_oracle(case, torch.bfloat16, f"padded L={L}")

@@ -180,13 +180,14 @@ def test_other_dstate_reference_fwd_chunk_states(N, L, dtype, via_pq, monkeypatc
     np.testing.assert_allclose(x[..., 0::2].cpu().double().numpy(), pa.numpy(), rtol=1e-3, atol=1e-30)
 
 
-@pytest.mark.parametrize("L", [7, 1001, 2047])
+@pytest.mark.parametrize("L", [7, 13, 14, 1001, 2047])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 @pytest.mark.parametrize("with_z", [True, False], ids=["z", "noz"])
 def test_padded_lengths_every_row(L, dtype, with_z):
     """Inference requests whose length is not a multiple of 8 run the fast kernels on copies padded
-    in front to a multiple of 32 steps with zero u (the binding's fwd_infer): every row's output and
-    last state against the float64 restatement, G = 2."""
+    in front to a multiple of 32 steps with zero u (the binding's fwd_infer) from 14 steps on, the
+    general kernel below (L 7, 13): every row's output and last state against the float64
+    restatement, G = 2."""
     batch, dim = 2, 256
     _say(f"padded length L={L} {dtype} z={with_z}")
     case = _case(110 + L, batch, dim, L, 16, dtype, bkind="4d", G=2, with_z=with_z)
