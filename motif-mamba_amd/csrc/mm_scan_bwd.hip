@@ -256,6 +256,24 @@ __device__ __forceinline__ int red_at(int tensor, int n, int t, int c) {
     return (tensor * 16 + n) * kRedBlock<CH> + t * kRedRow<CH> + c;
 }
 template <int CH> constexpr int kRedFloats = 32 * kRedBlock<CH>;
+
+// The per-slot state sums: the two slots a wave holds per channel (lanes l and l + 32 of the wave,
+// slots rs and rs ^ kPairBit) are added before the LDS exchange, with one v_permlane32_swap per
+// step: the lower lane ends with the pair's gh B sum, the upper lane with its ddt sum. Each lane
+// then stores one value per step instead of two, and the owners add 4 pair sums instead of 8
+// slot sums.
+#ifndef MM_BWD_PAIR_SUMS
+#define MM_BWD_PAIR_SUMS 1
+#endif
+constexpr bool kPairSums = MM_BWD_PAIR_SUMS != 0;
+template <int CH> constexpr int kPairBit = 32 / CH;             // slot bit that lane bit 5 carries
+template <int CH> constexpr int kPartSlots = kPairSums ? 4 : 8;  // sPart rows per tensor and channel
+
+// Lower half of the wave: pu + the upper lane's pu; upper half: the lower lane's pd + pd.
+__device__ __forceinline__ float pair_sum(float pu, float pd) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(pu), __float_as_uint(pd), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 static_assert((kFH - 1) * kRedRow<16> + 16 <= kRedBlock<16>, "sRed rows overlap");
 static_assert((kFH - 1) * kRedRow<32> + 32 <= kRedBlock<32>, "sRed rows overlap");
 
@@ -384,7 +402,7 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
     __shared__ __align__(16) float4 sX[kBufs][CH * kXS];       // [buf][c][t]: (dt', dt'u, u, g)
     __shared__ __align__(16) float sBC[kBufs][kFT * kBCS];      // [buf][t][B 16 | C 16 | pad]
     __shared__ __align__(16) float sRed[kRedFloats<CH>];        // red_at<CH>(tensor, n, t, c)
-    __shared__ __align__(16) float sPart[8 * 2 * CH * kPS];     // [slot][gh B | ddt][c][t]
+    __shared__ __align__(16) float sPart[kPartSlots<CH> * 2 * CH * kPS];   // [slot (pair)][gh B | ddt][c][t]
 
     const int tid = threadIdx.x;
     if constexpr (CARRY) {
@@ -657,12 +675,24 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             // that 16 consecutive channels (what one 64-bit LDS cycle serves) hit 16 distinct bank
             // pairs, for these stores and for the owners' reads below (8-float rows alone put 4
             // channels on each).
-            float2 *pp = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 0) * CH + c) * kPS]);
-            float2 *pq = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 1) * CH + c) * kPS]);
+            if constexpr (kPairSums) {
+                // Pair index of the slot pair (rs, rs ^ kPairBit), 0 .. 3; the lower lane writes the
+                // gh B row, the upper lane the ddt row.
+                constexpr int PB = kPairBit<CH>;
+                const int pi = (rs & (PB - 1)) | ((rs >> 1) & ~(PB - 1));
+                const int tz = (rs & PB) ? 1 : 0;
+                float2 *pw = reinterpret_cast<float2 *>(&sPart[((pi * 2 + tz) * CH + c) * kPS]);
 #pragma unroll
-            for (int q = 0; q < kFH / 2; ++q) {
-                pp[q ^ pswz] = make_float2(pu[2 * q], pu[2 * q + 1]);
-                pq[q ^ pswz] = make_float2(pd[2 * q], pd[2 * q + 1]);
+                for (int q = 0; q < kFH / 2; ++q)
+                    pw[q ^ pswz] = make_float2(pair_sum(pu[2 * q], pd[2 * q]), pair_sum(pu[2 * q + 1], pd[2 * q + 1]));
+            } else {
+                float2 *pp = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 0) * CH + c) * kPS]);
+                float2 *pq = reinterpret_cast<float2 *>(&sPart[((rs * 2 + 1) * CH + c) * kPS]);
+#pragma unroll
+                for (int q = 0; q < kFH / 2; ++q) {
+                    pp[q ^ pswz] = make_float2(pu[2 * q], pu[2 * q + 1]);
+                    pq[q ^ pswz] = make_float2(pd[2 * q], pd[2 * q + 1]);
+                }
             }
             __syncthreads();
             // dB / dC of this half summed over the block's CH channels: the 256 rows (tensor, state,
@@ -691,14 +721,14 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                 if (ts < L)
                     (tz == 0 ? ws.partB : ws.partC)[(((blk * p.batch + b) * p.n_groups + g) * 16 + tn) * Lp + ts] = acc;
             }
-            // du / ddelta of the steps this lane owns, if they are in this half: the 8 slots' partial
-            // sums over states, added in slot order.
+            // du / ddelta of the steps this lane owns, if they are in this half: the partial sums
+            // over states of the 4 slot pairs (or 8 slots), added in order.
             if ((rs >> 2) == half) {
                 const int sl = 2 * (rs & 3);               // first owned step within the half
                 const int64_t te = t0 + 2 * rs;
                 float su[2] = {0.f, 0.f}, sd[2] = {0.f, 0.f};
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
+                for (int k = 0; k < kPartSlots<CH>; ++k) {
                     const int pos = 2 * ((sl >> 1) ^ pswz);
                     const float2 a = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 0) * CH + c) * kPS + pos]);
                     const float2 bq = *reinterpret_cast<const float2 *>(&sPart[((k * 2 + 1) * CH + c) * kPS + pos]);

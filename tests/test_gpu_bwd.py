@@ -543,10 +543,11 @@ def test_bwd_channel_widths(dtype, G, ch, slots, monkeypatch):
             scale = max(1.0, b.abs().max().item())
             torch.testing.assert_close(a.float(), b.float(), rtol=rtol, atol=rtol * 0.1 * scale,
                                        msg=lambda m: f"{kind} {name}: {m}")
-    # Whole rows at both widths walk the same steps in the same order: du, ddelta and dz agree bit
-    # for bit (only the dB/dC block sums and the atomics are grouped differently).
-    for i in (0, 1, 7):
-        assert torch.equal(runs[ch, "whole"][i], runs[16, "whole"][i]), names[i]
+    # Whole rows at both widths walk the same steps in the same order: dz agrees bit for bit. du and
+    # ddelta differ only in the order of their sums over states (a wave pre-adds the two slots it
+    # holds per channel: slots rs and rs ^ 1 at 32 channels, rs and rs ^ 2 at 16), within the
+    # bound above; the dB/dC block sums and the atomics are grouped differently too.
+    assert torch.equal(runs[ch, "whole"][7], runs[16, "whole"][7]), names[7]
 
 
 def test_training_step_graph_replay_matches_eager():
