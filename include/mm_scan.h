@@ -137,9 +137,10 @@ typedef struct mm_scan_fwd_params {
      * tile, float32 [ceil(seqlen / 16)][batch][dim][16], states past dstate written as 0 --
      * B * dim * seqlen * 4 bytes, about one float32 copy of u. Passed to mm_scan_bwd as
      * `tile_states`, they spare it the recompute of the whole forward. Written with P/Q and
-     * dstate <= 16, and without P/Q by the dstate-16 kernels together with chunk_states (the
-     * training forward; mm_scan_fwd_tile_states_size() is non-zero exactly when this request can
-     * write them). NULL: not written. */
+     * dstate <= 16, and without P/Q together with chunk_states (the training forward) by the
+     * dstate-16 kernels or, below dstate 16, the P/Q kernels run with a zero coupling
+     * (mm_scan_fwd_tile_states_size() is non-zero exactly when this request can write them).
+     * NULL: not written. */
     float *tile_states;
 } mm_scan_fwd_params;
 

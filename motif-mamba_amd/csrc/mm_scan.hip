@@ -570,10 +570,11 @@ int validate_fwd(const mm_scan_fwd_params *p) {
     if (p->tile_states && !p->P && !p->chunk_states)
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_fwd: without P/Q, tile_states are written with chunk_states "
                                              "(the training forward)");
-    if (p->tile_states && !p->P && !mm::tile_states_ok(*p))
+    if (p->tile_states && !p->P && !mm::tile_states_ok(*p) && !mm::diag_via_pq_fwd(*p))
         return fail(MM_ERR_UNSUPPORTED, "mm_scan_fwd: without P/Q, tile_states are written by the dstate-16 kernels "
-                                        "(variable B/C, dim and dim / n_groups multiples of 16, L a multiple of 8, "
-                                        "aligned rows); mm_scan_fwd_tile_states_size tells");
+                                        "and, below dstate 16, by the P/Q kernels with a zero coupling (variable "
+                                        "B/C, dim and dim / n_groups multiples of 16, L a multiple of 8, aligned "
+                                        "rows); mm_scan_fwd_tile_states_size tells");
     return MM_OK;
 }
 
@@ -826,7 +827,7 @@ int64_t mm_scan_fwd_tile_states_size(const mm_scan_fwd_params *params) {
         params->dstate > 16 || params->n_groups < 1 || (params->dim > 0 && params->dim % params->n_groups))
         return 0;
     const mm_scan_fwd_params &p = *params;
-    if (!p.P && (!p.chunk_states || !mm::tile_states_ok(p))) return 0;
+    if (!p.P && (!p.chunk_states || !(mm::tile_states_ok(p) || mm::diag_via_pq_fwd(p)))) return 0;
     return ((p.seqlen + 15) / 16) * p.batch * p.dim * 16 * int64_t(sizeof(float));
 }
 

@@ -1072,7 +1072,7 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
-    if (diag_via_pq_bwd(p))   // the P/Q backward with the zero pair (no tile states at dstate < 16)
+    if (diag_via_pq_bwd(p))   // the P/Q backward with the zero pair (its own checkpoints without tile states)
         return ((p.tile_states ? 0 : bwd::fast_ck_floats(p)) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p) && p.tile_states)
         return (2 * bwd::fast_part_floats(p) + bwd::carry_floats(bwd::seg_plan_for(p))) * int64_t(sizeof(float));

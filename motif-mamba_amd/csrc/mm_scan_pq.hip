@@ -699,9 +699,10 @@ bool diag_pq_enabled() {
 }  // namespace
 
 bool diag_via_pq_fwd(const mm_scan_fwd_params &p) {
-    // The tiled P/Q kernel then writes the chunk states in the diagonal form (DX); no tile states
-    // (the diagonal forward writes them at dstate 16 only).
-    if (p.P || p.dstate == 16 || p.dstate > 64 || p.tile_states || !diag_pq_enabled()) return false;
+    // The tiled P/Q kernel then writes the chunk states in the diagonal form (DX), and the tile
+    // states below dstate 16 (states past dstate stay 0), which the zero-pair backward reads.
+    if (p.P || p.dstate == 16 || p.dstate > 64 || (p.tile_states && p.dstate > 16) || !diag_pq_enabled())
+        return false;
     return pq::tiled_shape(p).LPR != 0;
 }
 

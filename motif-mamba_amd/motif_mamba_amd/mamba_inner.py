@@ -164,7 +164,7 @@ class MambaInnerFn(torch.autograd.Function):
             return y.view(batch, L, -1)
         # checkpoint_lvl 0 keeps activations rather than recomputing them: the scan's 16-step tile
         # states too (None where the kernels do not write them), which spare the backward a recompute.
-        want_ck = checkpoint_lvl == 0 and A.shape[-1] == 16 and _save_tile_states()
+        want_ck = checkpoint_lvl == 0 and A.shape[-1] <= 16 and _save_tile_states()
         # A length that is not a multiple of 8: the scan runs on copies padded in front with zero-u
         # steps, forward and backward (as selective_scan_fn pads), and its outputs are cut back.
         pad = ctx.scan_pad = _train_pad(conv1d_out, A, B, C)

@@ -115,10 +115,10 @@ class SelectiveScanFn(torch.autograd.Function):
             if return_last_state:
                 return res[0], res[1]
             return res[0]
-        # Training: the reference's outputs and saved tensors (ssi.py:47-61), plus, for dstate 16,
+        # Training: the reference's outputs and saved tensors (ssi.py:47-61), plus, for dstate <= 16,
         # the states before every 16-step tile (None where the kernels do not write them), which
         # spare the backward its recompute of the scan.
-        want_ck = A.shape[1] == 16 and _save_tile_states()
+        want_ck = A.shape[1] <= 16 and _save_tile_states()
         pad = ctx.pad = _train_pad(u, A, B, C)
         u, delta, z, B, C = (_pad_front(t, pad) for t in (u, delta, z, B, C))
         out, x, *rest = ext().fwd(u, delta, A, B, C, D, z, delta_bias, None, None, None, delta_softplus,

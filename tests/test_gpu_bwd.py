@@ -316,13 +316,52 @@ def test_bwd_tile_states(dtype, monkeypatch):
         tol = 1e-5 if i in atomic else 0.0
         scale = max(1.0, tb.abs().max().item()) if i in atomic else 0.0
         torch.testing.assert_close(ta, tb, rtol=tol, atol=tol * scale)
-    # A request the dstate-16 kernels do not take (dstate 8): no tile states, and training still runs.
+    # A request no fast kernel takes (dstate 8 with the zero-coupling route off): no tile states.
+    monkeypatch.setenv("MM_DIAG_VIA_PQ", "0")
     c8 = _case(692, 1, 16, 64, 8, dtype)
     g8 = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in c8.items()}
     B8, C8 = g8["B"].unsqueeze(1), g8["C"].unsqueeze(1)
     res = ext.fwd(g8["u"], g8["delta"], g8["A"], B8, C8, g8["D"], g8["z"], g8["delta_bias"], None, None, None, True,
                   tile_states=True)
     assert res[-1] is None
+
+
+@pytest.mark.parametrize("N", [4, 8, 12])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_bwd_tile_states_small_dstate(N, dtype):
+    """Below dstate 16 the training forward runs on the P/Q kernels with a zero coupling and writes
+    the tile states too (ck[j] = the state after the first 16 j steps, states past dstate 0); the
+    zero-coupling backward reading them matches the one recomputing them to float32 rounding, and
+    both match the exact gradients."""
+    _say(f"bwd tile states dstate {N} {dtype}")
+    from motif_mamba_amd import _native
+    ext = _native.ext()
+    case = _case(693 + N, 2, 64, 200, N, dtype, bkind="4d", G=2)
+    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
+    args = (g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None)
+    out, x, out_z, ck = ext.fwd(*args, True, tile_states=True)
+    assert ck is not None and ck.shape == (13, 2, 64, 16)
+    ckc = ck.cpu()
+    assert float(ckc[0].abs().max()) == 0.0 and float(ckc[..., N:].abs().max()) == 0.0
+    for j in (1, 6, 12):
+        pre = {k: (v[..., : 16 * j] if k in ("u", "delta", "z", "B", "C") else v) for k, v in case.items()}
+        _, last = selective_scan_ref(**pre, return_last_state=True)
+        torch.testing.assert_close(ckc[j, ..., :N], last, rtol=1e-4 if dtype == torch.float32 else 1e-3,
+                                   atol=1e-5 if dtype == torch.float32 else 1e-4)
+    dout = _dout(694, (2, 64, 200), dtype)
+    a = ext.bwd(*args, dout.to(DEV), x, out, None, None, None, True, False, ck)
+    b = ext.bwd(*args, dout.to(DEV), x, out, None, None, None, True, False)
+    torch.cuda.synchronize()
+    names = ["du", "ddelta", "dA", "dB", "dC", "dD", "ddelta_bias", "dz"]
+    for name, ta, tb in zip(names, a, b):
+        scale = max(1.0, tb.abs().max().item())
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        torch.testing.assert_close(ta.float(), tb.float(), rtol=tol, atol=tol * 0.1 * scale,
+                                   msg=lambda m: f"{name}: {m}")
+    exact = selective_scan_bwd_ref(**case, dout=dout, dtype=torch.float64)
+    got = dict(zip(names, a))
+    for n in NAMES:
+        _check(got[GRAD[n]], exact[GRAD[n]], dtype, f"N{N} tile states {GRAD[n]}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
