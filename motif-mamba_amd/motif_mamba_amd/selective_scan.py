@@ -82,6 +82,32 @@ def _unpad(t, pad):
     return t if t is None or pad == 0 else t[..., pad:]
 
 
+def _infer(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state, P=None, Q=None, gamma=None):
+    """The inference forward (no gradient needed): the stride fix-ups of the autograd forwards
+    (ssi.py:24-36) and the binding's fwd_infer, which writes only what is returned."""
+    if u.stride(-1) != 1:
+        u = u.contiguous()
+    if delta.stride(-1) != 1:
+        delta = delta.contiguous()
+    if D is not None:
+        D = D.contiguous()
+    if B.stride(-1) != 1:
+        B = B.contiguous()
+    if C.stride(-1) != 1:
+        C = C.contiguous()
+    if z is not None and z.stride(-1) != 1:
+        z = z.contiguous()
+    if delta_bias is not None and delta_bias.stride(-1) != 1:
+        delta_bias = delta_bias.contiguous()
+    if B.dim() == 3:
+        B = B.unsqueeze(1)
+    if C.dim() == 3:
+        C = C.unsqueeze(1)
+    res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias, delta_softplus=delta_softplus,
+                          return_last_state=return_last_state, P=P, Q=Q, gamma=gamma)
+    return (res[0], res[1]) if return_last_state else res[0]
+
+
 class SelectiveScanFn(torch.autograd.Function):
 
     @staticmethod
@@ -110,11 +136,7 @@ class SelectiveScanFn(torch.autograd.Function):
             ctx.squeeze_C = True
         if not grad_enabled or not any(ctx.needs_input_grad[:8]):
             # Inference: only what is returned is written (no pre-gate out, no chunk states).
-            res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
-                                  delta_softplus=delta_softplus, return_last_state=return_last_state)
-            if return_last_state:
-                return res[0], res[1]
-            return res[0]
+            return _infer(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state)
         # Training: the reference's outputs and saved tensors (ssi.py:47-61), plus, for dstate <= 16,
         # the states before every 16-step tile (None where the kernels do not write them), which
         # spare the backward its recompute of the scan.
@@ -191,12 +213,7 @@ class SelectiveScanPQFn(torch.autograd.Function):
             C = rearrange(C, "b dstate l -> b 1 dstate l")
             ctx.squeeze_C = True
         if not grad_enabled or not (any(ctx.needs_input_grad[:8]) or any(ctx.needs_input_grad[10:12])):
-            res = ext().fwd_infer(u, delta, A, B, C, D=D, z=z, delta_bias=delta_bias,
-                                  delta_softplus=delta_softplus, return_last_state=return_last_state,
-                                  P=P, Q=Q, gamma=gamma)
-            if return_last_state:
-                return res[0], res[1]
-            return res[0]
+            return _infer(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state, P, Q, gamma)
         # Training: the forward's outputs plus what the backward reads (ssi.py:123-137 saves
         # u, delta, A, B, C, D, delta_bias, P, Q, gamma, x; out joins them when z is given). With
         # dstate <= 16 the forward also writes the states before every 16-step tile (B * dim * L
@@ -277,9 +294,17 @@ def selective_scan_fn(u, delta, A, B, C, D=None, z=None, delta_bias=None, delta_
     last_state has shape (batch, dim, dstate). Note that the gradient of the last state is
     not considered in the backward pass.
     """
-    if P is not None or Q is not None or gamma is not None:
+    pq = P is not None or Q is not None or gamma is not None
+    if pq:
         _check_pq(u, delta, A, B, C, P, Q)
+    # Without a gradient to take (grad mode off, or no input that requires one) the inference
+    # forward runs directly, without the autograd Function's own host cost (~5 us per call; the
+    # Motif decode step calls the P/Q scan once per layer and token, mamba_simplemotif.py:378-396).
+    grads = (u, delta, A, B, C, D, z, delta_bias) + ((P, Q) if pq else ())
+    if not torch.is_grad_enabled() or not any(t is not None and t.requires_grad for t in grads):
+        return _infer(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state,
+                      *((P, Q, gamma) if pq else ()))
+    if pq:
         return SelectiveScanPQFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus,
-                                       return_last_state, P, Q, gamma, torch.is_grad_enabled())
-    return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state,
-                                 torch.is_grad_enabled())
+                                       return_last_state, P, Q, gamma, True)
+    return SelectiveScanFn.apply(u, delta, A, B, C, D, z, delta_bias, delta_softplus, return_last_state, True)

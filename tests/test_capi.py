@@ -193,10 +193,11 @@ def test_workspace_size_query():
     assert lib.mm_scan_fwd_workspace_size(ctypes.byref(odd)) == 0
 
 
-def test_tile_states_size_query():
+def test_tile_states_size_query(monkeypatch):
     """mm_scan_fwd_tile_states_size (sizes, flags, strides and pointer alignment only; fake pointers
-    are never dereferenced): the training forward of the dstate-16 kernels and every P/Q request
-    with dstate <= 16 write them; other requests do not."""
+    are never dereferenced): the training forward of the dstate-16 kernels, the diagonal training
+    forward below dstate 16 (the P/Q kernels with a zero coupling) and every P/Q request with
+    dstate <= 16 write them; other requests do not."""
     lib = capi.load()
 
     def params(batch, dim, L, N=16, chunks=True, pq=False):
@@ -221,15 +222,20 @@ def test_tile_states_size_query():
     assert size(params(4, 5120, 4096)) == 256 * 4 * 5120 * 16 * 4           # config 2 training forward
     assert size(params(2, 64, 200)) == 13 * 2 * 64 * 16 * 4                 # ragged last tile
     assert size(params(4, 5120, 4096, chunks=False)) == 0                  # the inference forward
-    assert size(params(2, 64, 256, N=8)) == 0                              # not the dstate-16 kernels
+    assert size(params(2, 64, 256, N=8)) == 16 * 2 * 64 * 16 * 4           # zero-coupling P/Q kernels
+    monkeypatch.setenv("MM_DIAG_VIA_PQ", "0")
+    assert size(params(2, 64, 256, N=8)) == 0                              # that route off: none
+    monkeypatch.delenv("MM_DIAG_VIA_PQ")
     assert size(params(2, 64, 100)) == 0                                   # L % 8 != 0
     assert size(params(2, 64, 256, N=8, chunks=False, pq=True)) == 16 * 2 * 64 * 16 * 4   # P/Q
     assert size(params(2, 64, 256, N=32, pq=True)) == 0                    # P/Q, dstate > 16
     assert lib.mm_scan_fwd_tile_states_size(None) == 0
     # A diagonal request the kernels cannot serve is refused when tile states are asked for.
+    monkeypatch.setenv("MM_DIAG_VIA_PQ", "0")
     p = params(2, 64, 256, N=8)
     p.tile_states = 32768
     assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_ERR_UNSUPPORTED
+    monkeypatch.delenv("MM_DIAG_VIA_PQ")
     p = params(2, 64, 256, chunks=False)
     p.tile_states = 32768
     assert lib.mm_scan_fwd(ctypes.byref(p), None) == capi.MM_ERR_INVALID_ARGUMENT
