@@ -231,9 +231,10 @@ typedef struct mm_scan_bwd_params {
     int64_t dQ_d_stride, dQ_r_stride, dQ_dstate_stride;
 
     /* Optional (ABI version 8, 9 without P/Q): the `tile_states` mm_scan_fwd wrote for the same
-     * inputs; the P/Q backward and the dstate-16 backward then read their checkpoints there
-     * instead of recomputing them (and need a smaller workspace); the general backward ignores
-     * them. The contents are trusted: stale states give wrong gradients. */
+     * inputs; the P/Q backward (also serving diagonal requests below dstate 16 with a zero
+     * coupling) and the dstate-16 backward then read their checkpoints there instead of
+     * recomputing them (and need a smaller workspace); the general backward ignores them. The
+     * contents are trusted: stale states give wrong gradients. */
     const float *tile_states;
 } mm_scan_bwd_params;
 
