@@ -470,13 +470,16 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
 
     // Loads of tile j (clamped into the row: always in bounds). Steps past L are padding, made
     // inert in commit(): dt' = g = 0 and B = C = 0 leave every state and gradient unchanged.
+    // The carry walk (CARRY) reads only delta', g and C: it loads neither u, the pre-gate out, B
+    // nor the checkpoint (their registers stay zero).
     auto load = [&](int64_t j, bool full) {
         TileRaw<T, CH> r;
         const int64_t jj = j < 0 ? 0 : (j >= n_tiles ? n_tiles - 1 : j);
         const int64_t te = jj * kFT + 2 * rs;
         const int64_t tl = te < L ? te : L - 2;
         r.d = load_raw<T, 2>(dp + tl);
-        r.u = load_raw<T, 2>(up + tl);
+        r.u = {};
+        if constexpr (!CARRY) r.u = load_raw<T, 2>(up + tl);
         r.go = {};
         r.z = {};
         r.o = {};
@@ -484,20 +487,20 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
             r.go = load_raw<T, 2>(gop + tl);
             if (zp) {
                 r.z = load_raw<T, 2>(zp + tl);
-                r.o = load_raw<T, 2>(outp + tl);
+                if constexpr (!CARRY) r.o = load_raw<T, 2>(outp + tl);
             }
         }
         const int64_t ts0 = jj * kFT + SV * st_q;
 #pragma unroll
         for (int i = 0; i < SV / 2; ++i) r.bc[i] = {};
-        if (stager && (full || st_tensor == 0)) {
+        if (stager && (CARRY ? st_tensor == 1 : (full || st_tensor == 0))) {
 #pragma unroll
             for (int i = 0; i < SV / 2; ++i) {   // each step pair clamped into the row on its own
                 const int64_t ts = ts0 + 2 * i < L ? ts0 + 2 * i : L - 2;
                 r.bc[i] = load_raw<T, 2>(stp + ts);
             }
         }
-        r.hc = full ? *reinterpret_cast<const float2 *>(ckp + jj * ck_tile) : make_float2(0.f, 0.f);
+        r.hc = (full && !CARRY) ? *reinterpret_cast<const float2 *>(ckp + jj * ck_tile) : make_float2(0.f, 0.f);
         return r;
     };
     // Tile j's per-step values into LDS buffer `buf`; the lane's own steps kept for the epilogue;
