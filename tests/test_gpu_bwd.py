@@ -92,13 +92,15 @@ def test_bwd_shapes(dtype, N):
 
 @pytest.mark.parametrize("N", [1, 4, 8, 12])
 @pytest.mark.parametrize("via_pq", ["1", "0"], ids=["zero-pair", "general"])
-def test_bwd_small_dstate(N, via_pq, monkeypatch):
-    """Diagonal backward at dstate < 16 (variable B/C): the P/Q backward with a zero rank-1 pair,
-    or (MM_DIAG_VIA_PQ=0) the general kernel; against the exact gradients."""
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
+def test_bwd_small_dstate(N, via_pq, dtype, monkeypatch):
+    """Diagonal training at dstate < 16 (variable B/C): the forward and the backward on the P/Q
+    kernels with a zero rank-1 pair (the forward's tile states handed over), or (MM_DIAG_VIA_PQ=0)
+    on the general kernels; against the exact gradients, 3 dtypes."""
     monkeypatch.setenv("MM_DIAG_VIA_PQ", via_pq)
-    _say(f"bwd dstate {N} via_pq={via_pq}")
-    case = _case(770 + N, 2, 64, 264, N, torch.float32, bkind="4d", G=2)
-    _vs_exact(case, _dout(771, (2, 64, 264), torch.float32), torch.float32, f"N{N} via_pq={via_pq}")
+    _say(f"bwd dstate {N} via_pq={via_pq} {dtype}")
+    case = _case(770 + N, 2, 64, 264, N, dtype, bkind="4d", G=2)
+    _vs_exact(case, _dout(771, (2, 64, 264), dtype), dtype, f"N{N} via_pq={via_pq}")
 
 
 @pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False), dict(with_bias=False),

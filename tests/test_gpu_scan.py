@@ -143,7 +143,7 @@ def test_other_dstate_every_row(N, via_pq, monkeypatch):
 
 
 @pytest.mark.parametrize("N,L", [(8, 4104), (32, 4096), (4, 2056)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["fp32", "bf16", "fp16"])
 @pytest.mark.parametrize("via_pq", ["1", "0"], ids=["zero-pair", "general"])
 def test_other_dstate_reference_fwd_chunk_states(N, L, dtype, via_pq, monkeypatch):
     """The training forward (ext.fwd with chunk states) at dstate != 16: on the P/Q kernels with a
