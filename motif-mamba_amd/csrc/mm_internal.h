@@ -64,5 +64,10 @@ int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p);
 bool pq_bwd_ok(const mm_scan_bwd_params &p);
 template <typename T>
 int launch_pq_bwd(const mm_scan_bwd_params &p, hipStream_t stream, float *ck, float *partB, float *partC);
+// The P/Q backward for the other shapes (dstate up to 256, constant B or C, any length and channel
+// count): one lane per state, checkpoints `ck` of pq_general_ck_floats() floats, float32 atomics.
+template <typename T>
+int launch_pq_general(const mm_scan_bwd_params &p, hipStream_t stream, float *ck);
+int64_t pq_general_ck_floats(const mm_scan_bwd_params &p);
 
 }  // namespace mm

@@ -642,9 +642,6 @@ int validate_bwd(const mm_scan_bwd_params *p) {
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: dP and dQ are required when P and Q are given");
     if (p->P && (p->pq_rank < 1 || p->pq_rank > 8))
         return fail(MM_ERR_INVALID_ARGUMENT, "mm_scan_bwd: pq_rank must be in [1, 8] (got %lld)", (long long)p->pq_rank);
-    if (p->P && !mm::pq_bwd_ok(*p))
-        return fail(MM_ERR_UNSUPPORTED, "mm_scan_bwd: the P/Q backward covers variable B/C, dstate <= 16, "
-                                        "dim and dim / n_groups multiples of 16 and seqlen a multiple of 8");
 
     const int64_t need = mm::bwd_workspace_min_bytes(*p);
     if (p->seqlen > 0 && (!p->workspace || p->workspace_bytes < need || reinterpret_cast<uintptr_t>(p->workspace) % 16))

@@ -1061,6 +1061,7 @@ int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
 // The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
 template <typename T>
 int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
+    if (!pq_bwd_ok(p)) return launch_pq_general<T>(p, s, static_cast<float *>(p.workspace));
     // Checkpoints: the forward's tile_states when given, else the head of the workspace.
     float *ws = static_cast<float *>(p.workspace);
     float *ck = p.tile_states ? const_cast<float *>(p.tile_states) : ws;
@@ -1075,6 +1076,7 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 }  // namespace bwd
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
+    if (p.P && !pq_bwd_ok(p)) return pq_general_ck_floats(p) * int64_t(sizeof(float));   // its own checkpoints
     if (diag_via_pq_bwd(p))   // the P/Q backward with the zero pair (its own checkpoints without tile states)
         return ((p.tile_states ? 0 : bwd::fast_ck_floats(p)) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p) && p.tile_states)

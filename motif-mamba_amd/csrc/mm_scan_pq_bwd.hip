@@ -443,6 +443,298 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
     }
 }
 
+// ------------------------------------------------------------------------------------------------
+// scan_bwd_pq_general<T, NP, R>: the P/Q backward for the shapes scan_bwd_pq16 does not take --
+// dstate 17 .. 256 (the reference's dense kernel takes dstate <= 256, rank <= 8: the Motif module's
+// "small" and "base" presets use dstate 32 and 64, mamba_simplemotif.py:33-35), constant B or C,
+// lengths that are not multiples of 8 and channel counts that are not multiples of 16. One lane per
+// state: a 256-lane workgroup holds 256 / NP rows (batch, channel), NP the next power of two
+// >= max(dstate, 16). The two sums over a row's states that feed the recurrences -- q_t = Q h_{t-1}
+// in the forward recompute and P^T lam_t in the reverse walk -- are taken every step as xor
+// butterflies inside a wave (bit-identical totals in every lane), rows wider than a wave adding
+// their waves' totals through LDS; the sums that only give du and ddelta are per-lane partials in
+// LDS, added by one lane per step after each 16-step tile. Checkpoints every 16 steps in the
+// workspace ([tile][row][NP]). The variable dB/dC terms of a tile are summed over the workgroup's
+// rows of one (batch, group) in LDS before their float32 atomics (one per run of such rows, state
+// and step); dA, dP, dQ, dD and ddelta_bias are float32 atomics once per lane.
+constexpr int kGT = 256;   // lanes per workgroup
+constexpr int kGBT = 16;   // steps per checkpoint tile
+
+// Sum of v over the NP lanes of each row, in every lane. sx: (kGT / 64) * R floats of LDS, used
+// only when a row spans several waves (then every lane of the workgroup must call this).
+template <int NP, int R>
+__device__ __forceinline__ void row_allreduce(float (&v)[R], float *sx, int tid) {
+    constexpr int W = NP < 64 ? NP : 64;
+#pragma unroll
+    for (int off = 1; off < W; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] += __shfl_xor(v[r], off, 64);
+    }
+    if constexpr (NP > 64) {
+        constexpr int WPR = NP / 64;   // waves per row
+        const int wave = tid >> 6;
+        __syncthreads();               // the previous call's reads of sx are done
+        if ((tid & 63) == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) sx[wave * R + r] = v[r];
+        }
+        __syncthreads();
+        const int w0 = wave - wave % WPR;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float acc = sx[w0 * R + r];
+            for (int w = 1; w < WPR; ++w) acc += sx[(w0 + w) * R + r];
+            v[r] = acc;
+        }
+    }
+}
+
+template <typename T, int NP, int R>
+__global__ void __launch_bounds__(kGT)
+scan_bwd_pq_general(const mm_scan_bwd_params p, const int64_t ratio, float *const ck) {
+    constexpr int RPW = kGT / NP;                        // rows per workgroup
+    __shared__ float sDu[kGBT * kGT];                    // [step][lane]: lam B
+    __shared__ float sDdt[kGBT * kGT];                   // [step][lane]: the delta' derivative's term
+    __shared__ float sQ[RPW * kGBT * R];                 // [row][step][r]: q_t of the tile
+    __shared__ float sB[kGBT * kGT];                     // [step][lane]: dB terms of the tile
+    __shared__ float sC[kGBT * kGT];                     // [step][lane]: dC terms of the tile
+    __shared__ float sX[(NP > 64 ? kGT / 64 : 1) * R];   // waves' totals of the wider rows
+    const int tid = threadIdx.x;
+    const int slot = tid / NP;
+    const int n = tid % NP;
+    const int N = int(p.dstate);
+    const int rank = int(p.pq_rank);
+    const int64_t rows = p.batch * p.dim;
+    const int64_t r_ = int64_t(blockIdx.x) * RPW + slot;
+    const bool row_ok = r_ < rows;
+    const int64_t rr = row_ok ? r_ : rows - 1;           // clamped for loads; stores are predicated
+    const int64_t b = rr / p.dim;
+    const int64_t d = rr - b * p.dim;
+    const int64_t g = d / ratio;
+    const bool on = row_ok && n < N;
+    const int nn = n < N ? n : N - 1;
+    const int64_t L = p.seqlen;
+    const int64_t n_tiles = (L + kGBT - 1) / kGBT;
+
+    const T *up = reinterpret_cast<const T *>(p.u) + b * p.u_batch_stride + d * p.u_d_stride;
+    const T *dp = reinterpret_cast<const T *>(p.delta) + b * p.delta_batch_stride + d * p.delta_d_stride;
+    const T *zp = p.z ? reinterpret_cast<const T *>(p.z) + b * p.z_batch_stride + d * p.z_d_stride : nullptr;
+    const T *outp = p.z ? reinterpret_cast<const T *>(p.out) + b * p.out_batch_stride + d * p.out_d_stride : nullptr;
+    const T *gop = reinterpret_cast<const T *>(p.dout) + b * p.dout_batch_stride + d * p.dout_d_stride;
+    T *dup = reinterpret_cast<T *>(p.du) + b * p.du_batch_stride + d * p.du_d_stride;
+    T *ddp = reinterpret_cast<T *>(p.ddelta) + b * p.ddelta_batch_stride + d * p.ddelta_d_stride;
+    T *dzp = p.z ? reinterpret_cast<T *>(p.dz) + b * p.dz_batch_stride + d * p.dz_d_stride : nullptr;
+    T *ozp = (p.z && p.out_z) ? reinterpret_cast<T *>(p.out_z) + b * p.out_z_batch_stride + d * p.out_z_d_stride : nullptr;
+    const T *Bv = p.is_variable_B ? reinterpret_cast<const T *>(p.B) + b * p.B_batch_stride + g * p.B_group_stride + nn * p.B_dstate_stride : nullptr;
+    const T *Cv = p.is_variable_C ? reinterpret_cast<const T *>(p.C) + b * p.C_batch_stride + g * p.C_group_stride + nn * p.C_dstate_stride : nullptr;
+    const float Bc = p.is_variable_B ? 0.f : reinterpret_cast<const float *>(p.B)[d * p.B_d_stride + nn * p.B_dstate_stride];
+    const float Cc = p.is_variable_C ? 0.f : reinterpret_cast<const float *>(p.C)[d * p.C_d_stride + nn * p.C_dstate_stride];
+    // Lanes past dstate hold zero A, B, C, P and Q: their state and adjoint stay zero and they add
+    // nothing to any sum.
+    const float An = on ? p.A[d * p.A_d_stride + nn * p.A_dstate_stride] : 0.f;
+    const float A2 = An * kLog2e;
+    float Pn[R], Qn[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const bool use = on && r < rank;
+        Pn[r] = use ? p.P[d * p.P_d_stride + nn * p.P_dstate_stride + r * p.P_r_stride] : 0.f;
+        Qn[r] = use ? p.Q[d * p.Q_d_stride + r * p.Q_r_stride + nn * p.Q_dstate_stride] : 0.f;
+    }
+    const float Dv = p.D ? p.D[d] : 0.f;
+    const float bias = p.delta_bias ? p.delta_bias[d] : 0.f;
+    const int64_t ck_tile = rows * NP;
+    float *const ckr = ck + rr * NP + n;
+
+    auto dt_at = [&](int64_t t, float &raw) {
+        raw = to_f32(dp[t]) + bias;
+        return p.delta_softplus ? softplus_fast(raw) : raw;
+    };
+    auto b_at = [&](int64_t t) { return on ? (Bv ? to_f32(Bv[t]) : Bc) : 0.f; };
+    auto c_at = [&](int64_t t) { return on ? (Cv ? to_f32(Cv[t]) : Cc) : 0.f; };
+    // g_t = dout_t silu(z_t) (or dout_t); `writer` also writes dz_t (and out_z_t).
+    auto g_at = [&](int64_t t, bool writer) {
+        float go = to_f32(gop[t]);
+        if (zp) {
+            const float zz = to_f32(zp[t]);
+            const float sg = 1.f / (1.f + expf(-zz));
+            if (writer) {
+                const float o = to_f32(outp[t]);
+                dzp[t] = from_f32<T>(go * o * sg * (1.f + zz * (1.f - sg)));
+                if (ozp) ozp[t] = from_f32<T>(o * zz * sg);
+            }
+            go *= zz * sg;
+        }
+        return go;
+    };
+
+    // Pass 1: the states at every tile start.
+    float h = 0.f;
+    for (int64_t t = 0; t < L; ++t) {
+        if (t % kGBT == 0 && row_ok) ckr[(t / kGBT) * ck_tile] = h;
+        float raw;
+        const float dt = dt_at(t, raw);
+        float q[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) q[r] = Qn[r] * h;
+        row_allreduce<NP, R>(q, sX, tid);
+        float pq = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) pq = __builtin_fmaf(Pn[r], q[r], pq);
+        h = __builtin_fmaf(decay_exp2(dt, A2), h, dt * __builtin_fmaf(to_f32(up[t]), b_at(t), pq));
+    }
+    __syncthreads();
+
+    // Pass 2: tiles in reverse order. lam is the state adjoint, pl = P^T lam of the step after.
+    float lam = 0.f, a_next = 0.f, dt_next = 0.f, pl[R];
+    float dA_acc = 0.f, dBc = 0.f, dCc = 0.f, dD_acc = 0.f, dbias_acc = 0.f, dP_acc[R], dQ_acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) pl[r] = dP_acc[r] = dQ_acc[r] = 0.f;
+    for (int64_t j = n_tiles - 1; j >= 0; --j) {
+        const int64_t t0 = j * kGBT;
+        const int cnt = int(L - t0 < kGBT ? L - t0 : kGBT);   // the same in every lane
+        float hp[kGBT], hs[kGBT], as[kGBT], dts[kGBT], us[kGBT];
+        float hh = row_ok ? ckr[j * ck_tile] : 0.f;
+#pragma unroll
+        for (int s = 0; s < kGBT; ++s) {
+            if (s < cnt) {
+                const int64_t t = t0 + s;
+                float raw;
+                dts[s] = dt_at(t, raw);
+                us[s] = to_f32(up[t]);
+                as[s] = decay_exp2(dts[s], A2);
+                hp[s] = hh;
+                float q[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) q[r] = Qn[r] * hh;
+                row_allreduce<NP, R>(q, sX, tid);
+                float pq = 0.f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    pq = __builtin_fmaf(Pn[r], q[r], pq);
+                    if (n == r) sQ[(slot * kGBT + s) * R + r] = q[r];
+                }
+                hh = __builtin_fmaf(as[s], hh, dts[s] * __builtin_fmaf(us[s], b_at(t), pq));
+                hs[s] = hh;
+            }
+        }
+        __syncthreads();   // sQ of the tile
+        float dA_tile = 0.f, dB_tile = 0.f, dC_tile = 0.f;
+#pragma unroll
+        for (int s = kGBT - 1; s >= 0; --s) {
+            if (s < cnt) {
+                const int64_t t = t0 + s;
+                const float gt = g_at(t, row_ok && n == 0);
+                const float bn = b_at(t);
+                // lam_t = C_t g_t + a_{t+1} lam_{t+1} + dt'_{t+1} Q^T (P^T lam_{t+1})
+                float qpl = 0.f;
+#pragma unroll
+                for (int r = 0; r < R; ++r) qpl = __builtin_fmaf(Qn[r], pl[r], qpl);
+                lam = __builtin_fmaf(c_at(t), gt, __builtin_fmaf(a_next, lam, dt_next * qpl));
+#pragma unroll
+                for (int r = 0; r < R; ++r) pl[r] = Pn[r] * lam;
+                row_allreduce<NP, R>(pl, sX, tid);
+                float pq = 0.f;
+                const float ldt = lam * dts[s];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const float q = sQ[(slot * kGBT + s) * R + r];
+                    pq = __builtin_fmaf(Pn[r], q, pq);
+                    dP_acc[r] = __builtin_fmaf(ldt, q, dP_acc[r]);
+                    dQ_acc[r] = __builtin_fmaf(dts[s] * pl[r], hp[s], dQ_acc[r]);
+                }
+                const float ah = as[s] * hp[s];            // a_t h_{t-1}
+                const float dcv = gt * hs[s];
+                const float dbv = ldt * us[s];
+                sB[s * kGT + tid] = dbv;
+                sC[s * kGT + tid] = dcv;
+                dC_tile += dcv;
+                dB_tile += dbv;
+                dA_tile = __builtin_fmaf(ldt, ah, dA_tile);
+                sDu[s * kGT + tid] = lam * bn;
+                sDdt[s * kGT + tid] = lam * __builtin_fmaf(An, ah, __builtin_fmaf(us[s], bn, pq));
+                a_next = as[s];
+                dt_next = dts[s];
+            }
+        }
+        dA_acc += dA_tile;
+        dBc += dB_tile;
+        dCc += dC_tile;
+        __syncthreads();
+        // The variable dB / dC of the tile: per (step, state), the terms of consecutive rows of one
+        // (batch, group) added in row order, one atomic per such run.
+        if (p.is_variable_B || p.is_variable_C) {
+            const int64_t row0 = int64_t(blockIdx.x) * RPW;
+            for (int e = tid; e < kGBT * NP; e += kGT) {
+                const int se = e / NP, ne = e % NP;
+                if (se >= cnt || ne >= N) continue;
+                const int64_t t = t0 + se;
+                float accB = 0.f, accC = 0.f;
+                int64_t key = -1, kb = 0, kg = 0;
+                for (int sl = 0; sl < RPW; ++sl) {
+                    const int64_t rw = row0 + sl;
+                    if (rw >= rows) break;
+                    const int64_t bw = rw / p.dim, gw = (rw - bw * p.dim) / ratio;
+                    const int64_t kw = bw * p.n_groups + gw;
+                    if (kw != key) {
+                        if (key >= 0) {
+                            if (p.is_variable_B)
+                                atomicAdd(p.dB + kb * p.dB_batch_stride + kg * p.dB_group_stride + ne * p.dB_dstate_stride + t, accB);
+                            if (p.is_variable_C)
+                                atomicAdd(p.dC + kb * p.dC_batch_stride + kg * p.dC_group_stride + ne * p.dC_dstate_stride + t, accC);
+                        }
+                        key = kw; kb = bw; kg = gw; accB = 0.f; accC = 0.f;
+                    }
+                    accB += sB[se * kGT + sl * NP + ne];
+                    accC += sC[se * kGT + sl * NP + ne];
+                }
+                if (key >= 0) {
+                    if (p.is_variable_B)
+                        atomicAdd(p.dB + kb * p.dB_batch_stride + kg * p.dB_group_stride + ne * p.dB_dstate_stride + t, accB);
+                    if (p.is_variable_C)
+                        atomicAdd(p.dC + kb * p.dC_batch_stride + kg * p.dC_group_stride + ne * p.dC_dstate_stride + t, accC);
+                }
+            }
+        }
+        // Per step: the sums over the row's states; the lane of state s finishes step s (NP >= 16).
+        if (n < cnt && row_ok) {
+            const int s = n;
+            float su = 0.f, sd = 0.f;
+            for (int k = 0; k < N; ++k) {
+                su += sDu[s * kGT + slot * NP + k];
+                sd += sDdt[s * kGT + slot * NP + k];
+            }
+            const int64_t t = t0 + s;
+            float raw;
+            const float dt = dt_at(t, raw);
+            const float gt = g_at(t, false);
+            const float uu = to_f32(up[t]);
+            const float dd = (p.delta_softplus && raw <= 20.f) ? sd / (1.f + expf(-raw)) : sd;
+            dup[t] = from_f32<T>(__builtin_fmaf(Dv, gt, dt * su));
+            ddp[t] = from_f32<T>(dd);
+            dD_acc = __builtin_fmaf(gt, uu, dD_acc);
+            dbias_acc += dd;
+        }
+        __syncthreads();   // sDu, sDdt and sQ are rewritten by the next tile
+    }
+    if (on) {
+        atomicAdd(p.dA + d * p.dA_d_stride + n * p.dA_dstate_stride, dA_acc);
+        if (!p.is_variable_B) atomicAdd(p.dB + d * p.dB_d_stride + n * p.dB_dstate_stride, dBc);
+        if (!p.is_variable_C) atomicAdd(p.dC + d * p.dC_d_stride + n * p.dC_dstate_stride, dCc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < rank) {
+                atomicAdd(p.dP + d * p.dP_d_stride + n * p.dP_dstate_stride + r * p.dP_r_stride, dP_acc[r]);
+                atomicAdd(p.dQ + d * p.dQ_d_stride + r * p.dQ_r_stride + n * p.dQ_dstate_stride, dQ_acc[r]);
+            }
+        }
+    }
+    // dD and ddelta_bias: the per-lane sums of the steps each lane finished (lanes 0 .. 15).
+    if (row_ok && n < kGBT) {
+        if (p.dD) atomicAdd(p.dD + d, dD_acc);
+        if (p.ddelta_bias) atomicAdd(p.ddelta_bias + d, dbias_acc);
+    }
+}
+
 }  // namespace pqbwd
 
 // The P/Q backward's shape conditions: variable B/C, dstate <= 16, rank 1..8, 16-channel blocks
@@ -473,6 +765,47 @@ template <typename T>
 int launch_pq_bwd(const mm_scan_bwd_params &p, hipStream_t s, float *ck, float *partB, float *partC) {
     return launch_pq_bwd_s<T, 2>(p, s, ck, partB, partC);
 }
+
+int pq_general_np(const mm_scan_bwd_params &p) {
+    int np = 16;
+    while (np < p.dstate) np *= 2;
+    return np;
+}
+
+int64_t pq_general_ck_floats(const mm_scan_bwd_params &p) {
+    return ((p.seqlen + pqbwd::kGBT - 1) / pqbwd::kGBT) * p.batch * p.dim * pq_general_np(p);
+}
+
+template <typename T, int NP>
+static int launch_pq_general_np(const mm_scan_bwd_params &p, hipStream_t s, float *ck) {
+    const int64_t rows = p.batch * p.dim;
+    const int64_t blocks = (rows + pqbwd::kGT / NP - 1) / (pqbwd::kGT / NP);
+    if (blocks >= (int64_t(1) << 32) / pqbwd::kGT)   // gridDim.x * blockDim.x must stay below 2^32
+        return set_error(MM_ERR_UNSUPPORTED, "mm_scan_bwd: batch * dim too large for one launch of the P/Q backward");
+    const int64_t ratio = p.dim / p.n_groups;
+    if (p.pq_rank <= 2)
+        hipLaunchKernelGGL((pqbwd::scan_bwd_pq_general<T, NP, 2>), dim3(unsigned(blocks)), dim3(pqbwd::kGT), 0, s, p,
+                           ratio, ck);
+    else
+        hipLaunchKernelGGL((pqbwd::scan_bwd_pq_general<T, NP, 8>), dim3(unsigned(blocks)), dim3(pqbwd::kGT), 0, s, p,
+                           ratio, ck);
+    return launch_status("scan_bwd_pq_general");
+}
+
+template <typename T>
+int launch_pq_general(const mm_scan_bwd_params &p, hipStream_t s, float *ck) {
+    switch (pq_general_np(p)) {
+    case 16: return launch_pq_general_np<T, 16>(p, s, ck);
+    case 32: return launch_pq_general_np<T, 32>(p, s, ck);
+    case 64: return launch_pq_general_np<T, 64>(p, s, ck);
+    case 128: return launch_pq_general_np<T, 128>(p, s, ck);
+    default: return launch_pq_general_np<T, 256>(p, s, ck);
+    }
+}
+
+template int launch_pq_general<float>(const mm_scan_bwd_params &, hipStream_t, float *);
+template int launch_pq_general<f16_t>(const mm_scan_bwd_params &, hipStream_t, float *);
+template int launch_pq_general<bf16_t>(const mm_scan_bwd_params &, hipStream_t, float *);
 
 template int launch_pq_bwd<float>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
 template int launch_pq_bwd<f16_t>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);

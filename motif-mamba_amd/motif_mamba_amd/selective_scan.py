@@ -27,13 +27,13 @@ included), which is what the reference returns in both of its gradient modes
 through its torch loop (calls with z) differentiate the same function; "exact" takes dP/dQ of
 z-less calls from that autograd, any other value ("fused") from the dense kernel, the only backward
 its launcher runs with P/Q (selective_scan_bwd_kernel.cuh:928-932), which accumulates the same
-chain rule (:307, :334). The variable is therefore not read here. The gfx950 kernel covers pq_rank 1..8, dstate <= 16, dim and
-dim / n_groups multiples of 16 and seqlen a multiple of 8, with variable B and C; training requests
-of other lengths are padded in front with zero-u steps (_train_pad), other P/Q shapes raise
-NotImplementedError in the backward.
+chain rule (:307, :334). The variable is therefore not read here. The fast gfx950 backward covers
+pq_rank 1..8, dstate <= 16, dim and dim / n_groups multiples of 16 and seqlen a multiple of 8, with
+variable B and C; training requests of other lengths are padded in front with zero-u steps
+(_train_pad); the other shapes the reference takes (dstate <= 256, rank <= 8, constant B or C) run
+a general P/Q backward with one lane per state.
 
-Differences (all raise instead of computing something else): complex A, and the P/Q backward
-outside the shapes above, are not part of this build.
+Differences (all raise instead of computing something else): complex A is not part of this build.
 """
 from __future__ import annotations
 

@@ -234,15 +234,11 @@ def test_pq_bwd_c_abi_direct():
     for name, t in (("du", du), ("ddelta", ddelta), ("dz", dz), ("dA", dA), ("dB", dB.squeeze(1)),
                     ("dC", dC.squeeze(1)), ("dD", dD), ("ddelta_bias", dbias), ("dP", dP), ("dQ", dQ)):
         _check(t, exact[name], torch.float32, f"capi {name}")
-    # Refusals, nothing launched: a rank past the reference's limit of 8 (invalid), a length the
-    # kernel does not cover (unsupported), missing dP.
+    # Refusals, nothing launched: a rank past the reference's limit of 8, missing dP (invalid).
     p.pq_rank = 9
     assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_INVALID_ARGUMENT
     assert b"pq_rank" in lib.mm_last_error()
-    p.pq_rank, p.seqlen = 3, 92
-    assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_UNSUPPORTED
-    assert b"P/Q backward" in lib.mm_last_error()
-    p.seqlen, p.dP = 96, None
+    p.pq_rank, p.dP = 3, None
     assert lib.mm_scan_bwd(ctypes.byref(p), capi.stream_handle()) == capi.MM_ERR_INVALID_ARGUMENT
 
 
@@ -255,22 +251,31 @@ def test_pq_bwd_padded_lengths(L):
     _vs_exact(case, _dout(796, (2, 32, L), torch.float32), torch.float32, f"padded L{L}")
 
 
-@pytest.mark.parametrize("what", ["dstate32", "constB"])
-def test_pq_bwd_unsupported_shapes_raise(what):
-    """Shapes outside the kernel raise NotImplementedError in the backward; the forward runs."""
-    _say(f"pq bwd unsupported {what}")
-    from motif_mamba_amd import selective_scan_fn
-    kw = dict(batch=1, dim=16, L=32, N=16, R=2, dtype=torch.float32)
-    if what == "dstate32":
-        kw["N"] = 32
-    case = _pq_case(790, **kw)
+GENERAL_SHAPES = {
+    "dstate20": dict(N=20), "dstate32": dict(N=32), "dstate64": dict(N=64), "dstate32_rank5": dict(N=32, R=5),
+    "dstate130": dict(N=130, R=3, dim=8, G=1), "constB": dict(G=1), "constBC": dict(bkind="const"),
+    "dim24": dict(dim=24, G=1), "L100": dict(L=100), "shared_pq_dstate32": dict(N=32, per_dim=False),
+}
+
+
+@pytest.mark.parametrize("what", list(GENERAL_SHAPES))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_pq_bwd_general_shapes(what, dtype, monkeypatch):
+    """Shapes outside the 16-state kernel run the general P/Q backward (one lane per state, the sums
+    over states as wave butterflies, LDS across waves past 64 states): dstate 20, 32, 64 and 130
+    (the Motif module's "small" and "base" presets use 32 and 64, mamba_simplemotif.py:33-35; the
+    reference's dense kernel takes up to 256), rank 5, a P/Q pair shared by every channel, constant
+    B, constant B and C, 24 channels, L 100 with the training padding off; against the exact
+    gradients (dP and dQ included), with z."""
+    _say(f"pq bwd general {what} {dtype}")
+    kw = dict(batch=2, dim=32, L=64, N=16, R=2, dtype=dtype, bkind="4d", G=2)
+    kw.update(GENERAL_SHAPES[what])
+    if what == "L100":
+        monkeypatch.setenv("MM_SCAN_PAD", "0")
+    case = _pq_case(790 + len(what), **kw)
     if what == "constB":
-        case["B"] = torch.randn(16, 16)
-    g = {k: (v.to(DEV) if torch.is_tensor(v) else v) for k, v in case.items()}
-    g["u"].requires_grad_(True)
-    out = selective_scan_fn(**g)
-    with pytest.raises(NotImplementedError, match="P/Q backward"):
-        out.backward(torch.ones_like(out))
+        case["B"] = torch.randn(kw["dim"], kw["N"], generator=torch.Generator().manual_seed(791))
+    _vs_exact(case, _dout(792, (kw["batch"], kw["dim"], kw["L"]), dtype), dtype, what)
 
 
 def test_pq_fwd_tile_states_are_the_prefix_states():
