@@ -66,6 +66,8 @@ __global__ void __launch_bounds__(kGenThreads)
 scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_log2) {
     __shared__ float sDu[kBT * kGenThreads];   // [step][lane]: per-state partials of sum_n gh B
     __shared__ float sDdt[kBT * kGenThreads];  // [step][lane]: per-state partials of ddt
+    __shared__ float sB[kBT * kGenThreads];    // [step][lane]: variable dB terms of the tile
+    __shared__ float sC[kBT * kGenThreads];    // [step][lane]: variable dC terms of the tile
     const int NP = 1 << np_log2;
     const int tid = threadIdx.x;
     const int slot = tid >> np_log2;
@@ -168,10 +170,8 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
                 const float ah = hs[s] - dtu * bn;        // a_t h_{t-1}
                 const float dcv = gt * hs[s];
                 const float dbv = gh * dtu;
-                if (on) {
-                    if (dCv) atomicAdd(dCv + t, dcv);
-                    if (dBv) atomicAdd(dBv + t, dbv);
-                }
+                sB[s * kGenThreads + tid] = dbv;
+                sC[s * kGenThreads + tid] = dcv;
                 dC_tile += dcv;
                 dB_tile += dbv;
                 du_part = gh * bn;
@@ -186,6 +186,37 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
         dBc += dB_tile;
         dCc += dC_tile;
         __syncthreads();
+        // The variable dB / dC of the tile: per (step, state), the terms of consecutive rows of one
+        // (batch, group) added in row order, one float32 atomic per such run (instead of one per row).
+        if (dBv || dCv) {
+            const int rpb = kGenThreads >> np_log2;
+            const int64_t row0 = int64_t(blockIdx.x) * rpb;
+            for (int e = tid; e < kBT * NP; e += kGenThreads) {
+                const int se = e >> np_log2, ne = e & (NP - 1);
+                if (se >= cnt || ne >= N) continue;
+                const int64_t t = t0 + se;
+                float accB = 0.f, accC = 0.f;
+                int64_t key = -1, kb = 0, kg = 0;
+                auto flush = [&]() {
+                    if (key < 0) return;
+                    if (dBv) atomicAdd(p.dB + kb * p.dB_batch_stride + kg * p.dB_group_stride + ne * p.dB_dstate_stride + t, accB);
+                    if (dCv) atomicAdd(p.dC + kb * p.dC_batch_stride + kg * p.dC_group_stride + ne * p.dC_dstate_stride + t, accC);
+                };
+                for (int sl = 0; sl < rpb; ++sl) {
+                    const int64_t rw = row0 + sl;
+                    if (rw >= rows) break;
+                    const int64_t bw = rw / p.dim, gw = (rw - bw * p.dim) / ratio;
+                    const int64_t kw = bw * p.n_groups + gw;
+                    if (kw != key) {
+                        flush();
+                        key = kw; kb = bw; kg = gw; accB = 0.f; accC = 0.f;
+                    }
+                    accB += sB[se * kGenThreads + sl * NP + ne];
+                    accC += sC[se * kGenThreads + sl * NP + ne];
+                }
+                flush();
+            }
+        }
         // Per step: sums over the row's states; the lane of state s % NP finishes step s.
         float dD_tile = 0.f, dbias_tile = 0.f;
         for (int s = n; s < cnt; s += NP) {

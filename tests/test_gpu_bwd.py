@@ -182,10 +182,14 @@ def test_bwd_native_api_outputs():
     with pytest.raises(RuntimeError):   # x is required past one chunk, as in the reference
         ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"], None, None, None,
                 dout, None, out, None, None, None, True, False)
-    with pytest.raises(NotImplementedError):   # P/Q with 8 channels per group: outside the P/Q backward
-        ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"],
-                torch.zeros(16, 2, device=DEV), torch.zeros(2, 16, device=DEV), None,
-                dout, x, out, None, None, None, True, False)
+    # P/Q with 8 channels per group, outside the 16-state P/Q kernel: the general P/Q backward takes
+    # it (its gradients are checked in test_gpu_pq_bwd.py); a zero pair leaves the diagonal ones.
+    res = ext.bwd(g["u"], g["delta"], g["A"], g["B"], g["C"], g["D"], g["z"], g["delta_bias"],
+                  torch.zeros(16, 2, device=DEV), torch.zeros(2, 16, device=DEV), None,
+                  dout, x, out, None, None, None, True, False)
+    torch.cuda.synchronize()
+    for name, t in (("du", res[0]), ("ddelta", res[1]), ("dA", res[2])):
+        _check(t, exact[name], torch.bfloat16, f"native zero P/Q {name}")
 
 
 def test_bwd_c_abi_direct():
