@@ -255,6 +255,9 @@ GENERAL_SHAPES = {
     "dstate20": dict(N=20), "dstate32": dict(N=32), "dstate64": dict(N=64), "dstate32_rank5": dict(N=32, R=5),
     "dstate130": dict(N=130, R=3, dim=8, G=1), "constB": dict(G=1), "constBC": dict(bkind="const"),
     "dim24": dict(dim=24, G=1), "L100": dict(L=100), "shared_pq_dstate32": dict(N=32, per_dim=False),
+    # workgroups whose rows span two groups (12 channels per group, 16 rows per workgroup) and two
+    # batch rows (12 channels, 8 rows per workgroup): the dB/dC runs split there
+    "dim24_G2": dict(dim=24, G=2), "dstate32_dim12": dict(N=32, dim=12, G=1),
 }
 
 
@@ -265,8 +268,8 @@ def test_pq_bwd_general_shapes(what, dtype, monkeypatch):
     over states as wave butterflies, LDS across waves past 64 states): dstate 20, 32, 64 and 130
     (the Motif module's "small" and "base" presets use 32 and 64, mamba_simplemotif.py:33-35; the
     reference's dense kernel takes up to 256), rank 5, a P/Q pair shared by every channel, constant
-    B, constant B and C, 24 channels, L 100 with the training padding off; against the exact
-    gradients (dP and dQ included), with z."""
+    B, constant B and C, 24 and 12 channels (workgroups spanning two groups or two batch rows), L 100
+    with the training padding off; against the exact gradients (dP and dQ included), with z."""
     _say(f"pq bwd general {what} {dtype}")
     kw = dict(batch=2, dim=32, L=64, N=16, R=2, dtype=dtype, bkind="4d", G=2)
     kw.update(GENERAL_SHAPES[what])
