@@ -67,7 +67,17 @@ int launch_pq_bwd(const mm_scan_bwd_params &p, hipStream_t stream, float *ck, fl
 // The P/Q backward for the other shapes (dstate up to 256, constant B or C, any length and channel
 // count): one lane per state, checkpoints `ck` of pq_general_ck_floats() floats, float32 atomics.
 template <typename T>
-int launch_pq_general(const mm_scan_bwd_params &p, hipStream_t stream, float *ck);
+int launch_pq_general(const mm_scan_bwd_params &p, hipStream_t stream, float *ck, float *partB, float *partC);
 int64_t pq_general_ck_floats(const mm_scan_bwd_params &p);
+int pq_general_rows_per_block(const mm_scan_bwd_params &p);
+
+// The general backward kernels' dB/dC partial slabs (mm_scan_bwd.hip): when the rows a workgroup
+// holds (rpb) all belong to one (batch, group) -- channels per group a multiple of rpb -- and the
+// slabs stay under 4 GiB, each workgroup stores its sums over its rows into its own slab
+// [block][batch][group][dstate][seqlen] and gen_slab_reduce adds the blocks in order (no atomics);
+// gen_slab_floats() is 0 otherwise (the kernels then add with float32 atomics).
+int64_t gen_slab_floats(const mm_scan_bwd_params &p, int64_t rpb);
+int launch_gen_slab_reduce(const mm_scan_bwd_params &p, hipStream_t stream, const float *partB, const float *partC,
+                           int64_t rpb);
 
 }  // namespace mm

@@ -63,7 +63,8 @@ __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + expf
 
 template <typename T>
 __global__ void __launch_bounds__(kGenThreads)
-scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_log2) {
+scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_log2, float *const partB,
+                 float *const partC) {
     __shared__ float sDu[kBT * kGenThreads];   // [step][lane]: per-state partials of sum_n gh B
     __shared__ float sDdt[kBT * kGenThreads];  // [step][lane]: per-state partials of ddt
     __shared__ float sB[kBT * kGenThreads];    // [step][lane]: variable dB terms of the tile
@@ -187,8 +188,27 @@ scan_bwd_general(const mm_scan_bwd_params p, const int64_t ratio, const int np_l
         dCc += dC_tile;
         __syncthreads();
         // The variable dB / dC of the tile: per (step, state), the terms of consecutive rows of one
-        // (batch, group) added in row order, one float32 atomic per such run (instead of one per row).
-        if (dBv || dCv) {
+        // (batch, group) added in row order -- into this workgroup's slab when there is one (its
+        // rows are then all of one (batch, group)), else one float32 atomic per such run.
+        if (partB || partC) {
+            const int rpb = kGenThreads >> np_log2;
+            const int64_t row0 = int64_t(blockIdx.x) * rpb;
+            const int64_t b0 = row0 / p.dim, d0 = row0 - b0 * p.dim, g0 = d0 / ratio;
+            const int64_t blk = (d0 - g0 * ratio) / rpb;
+            float *const slabB = partB ? partB + ((blk * p.batch + b0) * p.n_groups + g0) * N * L : nullptr;
+            float *const slabC = partC ? partC + ((blk * p.batch + b0) * p.n_groups + g0) * N * L : nullptr;
+            for (int e = tid; e < kBT * NP; e += kGenThreads) {
+                const int se = e >> np_log2, ne = e & (NP - 1);
+                if (se >= cnt || ne >= N) continue;
+                float accB = 0.f, accC = 0.f;
+                for (int sl = 0; sl < rpb; ++sl) {
+                    accB += sB[se * kGenThreads + sl * NP + ne];
+                    accC += sC[se * kGenThreads + sl * NP + ne];
+                }
+                if (slabB) slabB[ne * L + t0 + se] = accB;
+                if (slabC) slabC[ne * L + t0 + se] = accC;
+            }
+        } else if (dBv || dCv) {
             const int rpb = kGenThreads >> np_log2;
             const int64_t row0 = int64_t(blockIdx.x) * rpb;
             for (int e = tid; e < kBT * NP; e += kGenThreads) {
@@ -807,6 +827,34 @@ scan_bwd_reduce_bc(const mm_scan_bwd_params p, const float *partB, const float *
                                       n_blocks, row0, rows, blockIdx.x, gridDim.x, scratch);
 }
 
+// dB / dC from the general kernels' slabs [block][batch][group][dstate][seqlen]: each element the
+// sum of its n_blocks partials in block order.
+__global__ void __launch_bounds__(256)
+gen_slab_reduce(const mm_scan_bwd_params p, const float *partB, const float *partC, int64_t n_blocks) {
+    const int64_t L = p.seqlen, N = p.dstate;
+    const int64_t total = p.batch * p.n_groups * N * L;
+    for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int64_t t = e % L, n = (e / L) % N, bg = e / (L * N);
+        const int64_t b = bg / p.n_groups, g = bg % p.n_groups;
+        if (partB) {
+            float acc = 0.f;
+            for (int64_t k = 0; k < n_blocks; ++k) acc += partB[k * total + e];
+            p.dB[b * p.dB_batch_stride + g * p.dB_group_stride + n * p.dB_dstate_stride + t] = acc;
+        }
+        if (partC) {
+            float acc = 0.f;
+            for (int64_t k = 0; k < n_blocks; ++k) acc += partC[k * total + e];
+            p.dC[b * p.dC_batch_stride + g * p.dC_group_stride + n * p.dC_dstate_stride + t] = acc;
+        }
+    }
+}
+
+int gen_rows_per_block(const mm_scan_bwd_params &p) {
+    int np_log2 = 0;
+    while ((1 << np_log2) < p.dstate) ++np_log2;
+    return kGenThreads >> np_log2;
+}
+
 template <typename T>
 int launch_general(const mm_scan_bwd_params &p, hipStream_t s) {
     int np_log2 = 0;
@@ -816,9 +864,18 @@ int launch_general(const mm_scan_bwd_params &p, hipStream_t s) {
     const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
     if (blocks >= (int64_t(1) << 32) / kGenThreads)   // gridDim.x * blockDim.x must stay below 2^32
         return set_error(MM_ERR_UNSUPPORTED, "mm_scan_bwd: batch * dim too large for one launch of the general kernel");
+    // Workspace: the checkpoints, then the dB / dC slabs when this shape has them.
+    const int64_t n_tiles = (p.seqlen + kBT - 1) / kBT;
+    float *const ws = static_cast<float *>(p.workspace);
+    const int64_t slab = gen_slab_floats(p, rows_per_block);
+    float *const partB = slab && p.is_variable_B ? ws + rows * n_tiles * p.dstate : nullptr;
+    float *const partC = slab && p.is_variable_C ? ws + rows * n_tiles * p.dstate + slab : nullptr;
     const dim3 grid(static_cast<unsigned>(blocks));
-    hipLaunchKernelGGL((scan_bwd_general<T>), grid, dim3(kGenThreads), 0, s, p, p.dim / p.n_groups, np_log2);
-    return launch_status("scan_bwd_general");
+    hipLaunchKernelGGL((scan_bwd_general<T>), grid, dim3(kGenThreads), 0, s, p, p.dim / p.n_groups, np_log2, partB,
+                       partC);
+    const int rc = launch_status("scan_bwd_general");
+    if (rc != MM_OK || !slab) return rc;
+    return launch_gen_slab_reduce(p, s, partB, partC, rows_per_block);
 }
 
 // Tensors to zero, collected and cleared by one launch of fill_zero_set.
@@ -1092,7 +1149,15 @@ int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
 // The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
 template <typename T>
 int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
-    if (!pq_bwd_ok(p)) return launch_pq_general<T>(p, s, static_cast<float *>(p.workspace));
+    if (!pq_bwd_ok(p)) {   // the general P/Q backward: checkpoints, then the dB / dC slabs if any
+        float *const ck = static_cast<float *>(p.workspace);
+        const int64_t rpb = pq_general_rows_per_block(p), slab = gen_slab_floats(p, rpb);
+        float *const partB = slab && p.is_variable_B ? ck + pq_general_ck_floats(p) : nullptr;
+        float *const partC = slab && p.is_variable_C ? ck + pq_general_ck_floats(p) + slab : nullptr;
+        const int rc = launch_pq_general<T>(p, s, ck, partB, partC);
+        if (rc != MM_OK || !slab) return rc;
+        return launch_gen_slab_reduce(p, s, partB, partC, rpb);
+    }
     // Checkpoints: the forward's tile_states when given, else the head of the workspace.
     float *ws = static_cast<float *>(p.workspace);
     float *ck = p.tile_states ? const_cast<float *>(p.tile_states) : ws;
@@ -1106,8 +1171,26 @@ int launch_pq(const mm_scan_bwd_params &p, hipStream_t s) {
 
 }  // namespace bwd
 
+int64_t gen_slab_floats(const mm_scan_bwd_params &p, int64_t rpb) {
+    if (!p.is_variable_B && !p.is_variable_C) return 0;
+    if (p.n_groups < 1 || p.dim % p.n_groups || (p.dim / p.n_groups) % rpb) return 0;
+    const int64_t floats = (p.dim / rpb) * p.batch * p.dstate * p.seqlen;
+    return 2 * floats * int64_t(sizeof(float)) <= (int64_t(1) << 32) ? floats : 0;
+}
+
+int launch_gen_slab_reduce(const mm_scan_bwd_params &p, hipStream_t s, const float *partB, const float *partC,
+                           int64_t rpb) {
+    const int64_t total = p.batch * p.n_groups * p.dstate * p.seqlen;
+    if (total <= 0) return MM_OK;
+    const unsigned blocks = unsigned(std::min<int64_t>((total + 255) / 256, 16384));
+    hipLaunchKernelGGL(bwd::gen_slab_reduce, dim3(blocks), dim3(256), 0, s, p, partB, partC,
+                       p.dim / p.n_groups / rpb);
+    return launch_status("gen_slab_reduce");
+}
+
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
-    if (p.P && !pq_bwd_ok(p)) return pq_general_ck_floats(p) * int64_t(sizeof(float));   // its own checkpoints
+    if (p.P && !pq_bwd_ok(p))   // the general P/Q backward: its own checkpoints and the slabs
+        return (pq_general_ck_floats(p) + 2 * gen_slab_floats(p, pq_general_rows_per_block(p))) * int64_t(sizeof(float));
     if (diag_via_pq_bwd(p))   // the P/Q backward with the zero pair (its own checkpoints without tile states)
         return ((p.tile_states ? 0 : bwd::fast_ck_floats(p)) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p) && p.tile_states)
@@ -1123,7 +1206,8 @@ int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
     if (p.P && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (p.P || bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     const int64_t n_tiles = (p.seqlen + bwd::kBT - 1) / bwd::kBT;
-    return p.batch * p.dim * n_tiles * p.dstate * int64_t(sizeof(float));
+    return (p.batch * p.dim * n_tiles * p.dstate + 2 * gen_slab_floats(p, bwd::gen_rows_per_block(p))) *
+           int64_t(sizeof(float));
 }
 
 int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p) {

@@ -491,7 +491,8 @@ __device__ __forceinline__ void row_allreduce(float (&v)[R], float *sx, int tid)
 
 template <typename T, int NP, int R>
 __global__ void __launch_bounds__(kGT)
-scan_bwd_pq_general(const mm_scan_bwd_params p, const int64_t ratio, float *const ck) {
+scan_bwd_pq_general(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, float *const partB,
+                    float *const partC) {
     constexpr int RPW = kGT / NP;                        // rows per workgroup
     __shared__ float sDu[kGBT * kGT];                    // [step][lane]: lam B
     __shared__ float sDdt[kGBT * kGT];                   // [step][lane]: the delta' derivative's term
@@ -661,8 +662,26 @@ scan_bwd_pq_general(const mm_scan_bwd_params p, const int64_t ratio, float *cons
         dCc += dC_tile;
         __syncthreads();
         // The variable dB / dC of the tile: per (step, state), the terms of consecutive rows of one
-        // (batch, group) added in row order, one atomic per such run.
-        if (p.is_variable_B || p.is_variable_C) {
+        // (batch, group) added in row order -- into this workgroup's slab when there is one (its
+        // rows are then all of one (batch, group)), else one atomic per such run.
+        if (partB || partC) {
+            const int64_t row0 = int64_t(blockIdx.x) * RPW;
+            const int64_t b0 = row0 / p.dim, d0 = row0 - b0 * p.dim, g0 = d0 / ratio;
+            const int64_t blk = (d0 - g0 * ratio) / RPW;
+            float *const slabB = partB ? partB + ((blk * p.batch + b0) * p.n_groups + g0) * N * L : nullptr;
+            float *const slabC = partC ? partC + ((blk * p.batch + b0) * p.n_groups + g0) * N * L : nullptr;
+            for (int e = tid; e < kGBT * NP; e += kGT) {
+                const int se = e / NP, ne = e % NP;
+                if (se >= cnt || ne >= N) continue;
+                float accB = 0.f, accC = 0.f;
+                for (int sl = 0; sl < RPW; ++sl) {
+                    accB += sB[se * kGT + sl * NP + ne];
+                    accC += sC[se * kGT + sl * NP + ne];
+                }
+                if (slabB) slabB[ne * L + t0 + se] = accB;
+                if (slabC) slabC[ne * L + t0 + se] = accC;
+            }
+        } else if (p.is_variable_B || p.is_variable_C) {
             const int64_t row0 = int64_t(blockIdx.x) * RPW;
             for (int e = tid; e < kGBT * NP; e += kGT) {
                 const int se = e / NP, ne = e % NP;
@@ -766,7 +785,7 @@ int launch_pq_bwd(const mm_scan_bwd_params &p, hipStream_t s, float *ck, float *
     return launch_pq_bwd_s<T, 2>(p, s, ck, partB, partC);
 }
 
-int pq_general_np(const mm_scan_bwd_params &p) {
+int pq_general_np(const mm_scan_bwd_params &p) {   // lanes per row of the general kernel
     int np = 16;
     while (np < p.dstate) np *= 2;
     return np;
@@ -776,8 +795,10 @@ int64_t pq_general_ck_floats(const mm_scan_bwd_params &p) {
     return ((p.seqlen + pqbwd::kGBT - 1) / pqbwd::kGBT) * p.batch * p.dim * pq_general_np(p);
 }
 
+int pq_general_rows_per_block(const mm_scan_bwd_params &p) { return pqbwd::kGT / pq_general_np(p); }
+
 template <typename T, int NP>
-static int launch_pq_general_np(const mm_scan_bwd_params &p, hipStream_t s, float *ck) {
+static int launch_pq_general_np(const mm_scan_bwd_params &p, hipStream_t s, float *ck, float *partB, float *partC) {
     const int64_t rows = p.batch * p.dim;
     const int64_t blocks = (rows + pqbwd::kGT / NP - 1) / (pqbwd::kGT / NP);
     if (blocks >= (int64_t(1) << 32) / pqbwd::kGT)   // gridDim.x * blockDim.x must stay below 2^32
@@ -785,27 +806,27 @@ static int launch_pq_general_np(const mm_scan_bwd_params &p, hipStream_t s, floa
     const int64_t ratio = p.dim / p.n_groups;
     if (p.pq_rank <= 2)
         hipLaunchKernelGGL((pqbwd::scan_bwd_pq_general<T, NP, 2>), dim3(unsigned(blocks)), dim3(pqbwd::kGT), 0, s, p,
-                           ratio, ck);
+                           ratio, ck, partB, partC);
     else
         hipLaunchKernelGGL((pqbwd::scan_bwd_pq_general<T, NP, 8>), dim3(unsigned(blocks)), dim3(pqbwd::kGT), 0, s, p,
-                           ratio, ck);
+                           ratio, ck, partB, partC);
     return launch_status("scan_bwd_pq_general");
 }
 
 template <typename T>
-int launch_pq_general(const mm_scan_bwd_params &p, hipStream_t s, float *ck) {
+int launch_pq_general(const mm_scan_bwd_params &p, hipStream_t s, float *ck, float *partB, float *partC) {
     switch (pq_general_np(p)) {
-    case 16: return launch_pq_general_np<T, 16>(p, s, ck);
-    case 32: return launch_pq_general_np<T, 32>(p, s, ck);
-    case 64: return launch_pq_general_np<T, 64>(p, s, ck);
-    case 128: return launch_pq_general_np<T, 128>(p, s, ck);
-    default: return launch_pq_general_np<T, 256>(p, s, ck);
+    case 16: return launch_pq_general_np<T, 16>(p, s, ck, partB, partC);
+    case 32: return launch_pq_general_np<T, 32>(p, s, ck, partB, partC);
+    case 64: return launch_pq_general_np<T, 64>(p, s, ck, partB, partC);
+    case 128: return launch_pq_general_np<T, 128>(p, s, ck, partB, partC);
+    default: return launch_pq_general_np<T, 256>(p, s, ck, partB, partC);
     }
 }
 
-template int launch_pq_general<float>(const mm_scan_bwd_params &, hipStream_t, float *);
-template int launch_pq_general<f16_t>(const mm_scan_bwd_params &, hipStream_t, float *);
-template int launch_pq_general<bf16_t>(const mm_scan_bwd_params &, hipStream_t, float *);
+template int launch_pq_general<float>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
+template int launch_pq_general<f16_t>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
+template int launch_pq_general<bf16_t>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
 
 template int launch_pq_bwd<float>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
 template int launch_pq_bwd<f16_t>(const mm_scan_bwd_params &, hipStream_t, float *, float *, float *);
