@@ -203,8 +203,9 @@ typedef struct mm_scan_bwd_params {
 
     /* Device scratch of mm_scan_bwd_workspace_size() bytes (16-byte aligned), owned by the caller:
      * the recomputed forward states at every 16-step tile start (and, for dstate 16 and for P/Q,
-     * the per-16-channel-block partial sums of dB and dC; for dstate 16 with tile_states, the
-     * adjoint carries of the sequence segments its last round of workgroups is cut into). Required.
+     * the per-16-channel-block partial sums of dB and dC -- per-workgroup partial sums for the
+     * general kernels of the other shapes; for dstate 16 with tile_states, the adjoint carries of
+     * the sequence segments its last round of workgroups is cut into). Required.
      * With tile_states at dstate 16, a workspace without room for the carries (sized for another
      * device or round size) is accepted too: the call then scans every row whole, without segments. */
     void *workspace;
