@@ -258,6 +258,9 @@ GENERAL_SHAPES = {
     # workgroups whose rows span two groups (12 channels per group, 16 rows per workgroup) and two
     # batch rows (12 channels, 8 rows per workgroup): the dB/dC runs split there
     "dim24_G2": dict(dim=24, G=2), "dstate32_dim12": dict(N=32, dim=12, G=1),
+    # lengths of one step and of one tile plus one; no z; no D, delta_bias or softplus
+    "dstate32_L1": dict(N=32, L=1), "dstate32_L17": dict(N=32, L=17), "dstate32_noz": dict(N=32, with_z=False),
+    "dstate32_bare": dict(N=32, with_D=False, with_bias=False, softplus=False),
 }
 
 
