@@ -450,9 +450,9 @@ scan_bwd_pq16(const mm_scan_bwd_params p, const int64_t ratio, float *const ck, 
 // lengths that are not multiples of 8 and channel counts that are not multiples of 16. One lane per
 // state: a 256-lane workgroup holds 256 / NP rows (batch, channel), NP the next power of two
 // >= max(dstate, 16). The two sums over a row's states that feed the recurrences -- q_t = Q h_{t-1}
-// in the forward recompute and P^T lam_t in the reverse walk -- are taken every step as xor
-// butterflies inside a wave (bit-identical totals in every lane), rows wider than a wave adding
-// their waves' totals through LDS; the sums that only give du and ddelta are per-lane partials in
+// in the forward recompute and P^T lam_t in the reverse walk -- are taken every step as butterflies
+// inside a wave (DPP and lane swaps; bit-identical totals in every lane), rows wider than a wave
+// adding their waves' totals through LDS; the sums that only give du and ddelta are per-lane partials in
 // LDS, added by one lane per step after each 16-step tile. Checkpoints every 16 steps in the
 // workspace ([tile][row][NP]). The variable dB/dC terms of a tile are summed over the workgroup's
 // rows of one (batch, group) in LDS before their float32 atomics (one per run of such rows, state
@@ -464,11 +464,21 @@ constexpr int kGBT = 16;   // steps per checkpoint tile
 // only when a row spans several waves (then every lane of the workgroup must call this).
 template <int NP, int R>
 __device__ __forceinline__ void row_allreduce(float (&v)[R], float *sx, int tid) {
-    constexpr int W = NP < 64 ? NP : 64;
+    // 16 lanes with DPP (group_sum), then the 16-lane rows of a wave pairwise with
+    // v_permlane16_swap and its halves with v_permlane32_swap: every stage adds two equal-valued
+    // pairs, so all lanes keep bit-identical totals.
 #pragma unroll
-    for (int off = 1; off < W; off <<= 1) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) v[r] += __shfl_xor(v[r], off, 64);
+    for (int r = 0; r < R; ++r) {
+        float x = group_sum<16>(v[r]);
+        if constexpr (NP >= 32) {
+            const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+            x = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+        }
+        if constexpr (NP >= 64) {
+            const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+            x = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+        }
+        v[r] = x;
     }
     if constexpr (NP > 64) {
         constexpr int WPR = NP / 64;   // waves per row
