@@ -346,6 +346,14 @@ struct FastWs {
     float *ck;      // [n_tiles][batch][dim][16]: states before each tile
     float *partB;   // [block][batch][group][16][L]: dB summed over one 16-channel block
     float *partC;
+    // State split (dstate a multiple of 16 above 16: one launch sequence per 16 states): the sums
+    // over states of gh B and of the delta' term, float32 [batch][dim][L], carried from part to
+    // part. part 0: no split; 1: the first part (stores its sums); 2: a middle part (adds its
+    // own); 3: the last part (adds the carried sums to its own and finishes du, ddelta, dD and
+    // ddelta_bias, which the other parts leave alone).
+    float *acc_su = nullptr;
+    float *acc_sd = nullptr;
+    int part = 0;
 };
 
 // Sequence segments. A launch covers the units (batch row, CH-channel block) unit0, unit0 + 1, ...
@@ -445,7 +453,9 @@ struct TileRaw {
 };
 
 // CH channels (16 or 32) x 16 states per workgroup of 8 CH lanes.
-template <typename T, bool CARRY, int CH>
+// SPLIT: a part of a state-split request (FastWs::part 1-3); its own instance, so that the whole
+// requests' kernel carries none of the split's code.
+template <typename T, bool CARRY, int CH, bool SPLIT = false>
 __global__ void __launch_bounds__(8 * CH)
 scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs ws, const BwdSeg sg) {
     constexpr int NT = 8 * CH;
@@ -789,7 +799,20 @@ scan_bwd_tiled16(const mm_scan_bwd_params p, const int64_t ratio, const FastWs w
                     su[0] += a.x; su[1] += a.y;
                     sd[0] += bq.x; sd[1] += bq.y;
                 }
-                if (te < L) {
+                if (SPLIT && te < L) {   // state split: carry the sums over states
+                    float2 *const asu = reinterpret_cast<float2 *>(ws.acc_su + (b * p.dim + d) * L + te);
+                    float2 *const asd = reinterpret_cast<float2 *>(ws.acc_sd + (b * p.dim + d) * L + te);
+                    if (ws.part != 1) {
+                        const float2 x = *asu, y = *asd;
+                        su[0] = x.x + su[0]; su[1] = x.y + su[1];
+                        sd[0] = y.x + sd[0]; sd[1] = y.y + sd[1];
+                    }
+                    if (ws.part != 3) {
+                        *asu = make_float2(su[0], su[1]);
+                        *asd = make_float2(sd[0], sd[1]);
+                    }
+                }
+                if (te < L && (!SPLIT || ws.part == 3)) {
                     float du[2], ddl[2];
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
@@ -1082,13 +1105,13 @@ int launch_reduce(const mm_scan_bwd_params &p, hipStream_t s, const float *partB
 // rounds, then (segmented tail) the carries and every segment of the cut units. *red_rows returns
 // the dB/dC slab rows already reduced (by the carry launch): those of the (batch, group) pairs whose
 // units all ran in the whole-row launch.
-template <typename T, int CH>
+template <typename T, int CH, bool SPLIT>
 int launch_units(const mm_scan_bwd_params &p, hipStream_t s, int64_t ratio, const FastWs &fw, const SegPlan &pl,
                  float *carry, int64_t *red_rows) {
     int rc = MM_OK;
     *red_rows = 0;
     if (pl.main_units > 0) {
-        hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH>), dim3(unsigned(pl.main_units)), dim3(8 * CH), 0, s, p,
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH, SPLIT>), dim3(unsigned(pl.main_units)), dim3(8 * CH), 0, s, p,
                            ratio, fw, BwdSeg{0, 1, (p.seqlen + kFT - 1) / kFT, nullptr, 1, 0, 0, 0});
         rc = launch_status("scan_bwd_tiled16");
         if (rc != MM_OK) return rc;
@@ -1106,7 +1129,7 @@ int launch_units(const mm_scan_bwd_params &p, hipStream_t s, int64_t ratio, cons
         rc = launch_status("scan_bwd_tiled16 (carries)");
         if (rc != MM_OK) return rc;
         *red_rows = rows;
-        hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH>), dim3(unsigned(pl.tail_units * pl.n_seg)), dim3(8 * CH),
+        hipLaunchKernelGGL((scan_bwd_tiled16<T, false, CH, SPLIT>), dim3(unsigned(pl.tail_units * pl.n_seg)), dim3(8 * CH),
                            0, s, p, ratio, fw, sg);
         rc = launch_status("scan_bwd_tiled16 (segments)");
     }
@@ -1114,12 +1137,13 @@ int launch_units(const mm_scan_bwd_params &p, hipStream_t s, int64_t ratio, cons
 }
 
 template <typename T>
-int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
+int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s, float *acc_su = nullptr, float *acc_sd = nullptr,
+                int part = 0) {
     float *ws = static_cast<float *>(p_in.workspace);
     const bool own_ck = p_in.tile_states == nullptr;
     float *ck = own_ck ? ws : const_cast<float *>(p_in.tile_states);
     float *partB = own_ck ? ws + fast_ck_floats(p_in) : ws;
-    const FastWs fw{ck, partB, partB + fast_part_floats(p_in)};
+    const FastWs fw{ck, partB, partB + fast_part_floats(p_in), acc_su, acc_sd, part};
     const int64_t ratio = p_in.dim / p_in.n_groups;
     // Without the forward's tile states, a states-only forward writes them into the head of the
     // workspace first (the same states the backward's own first pass would compute, from a kernel
@@ -1140,10 +1164,58 @@ int launch_fast(const mm_scan_bwd_params &p_in, hipStream_t s) {
     if (pl.tail_units > 0 && p.workspace_bytes < need)
         pl = {pl.main_units + pl.tail_units, 0, 1, (p.seqlen + kFT - 1) / kFT, pl.ch, 1};
     int64_t red_rows = 0;
-    const int rc = pl.ch == 32 ? launch_units<T, 32>(p, s, ratio, fw, pl, partB + 2 * fast_part_floats(p), &red_rows)
-                               : launch_units<T, 16>(p, s, ratio, fw, pl, partB + 2 * fast_part_floats(p), &red_rows);
+    float *const carry = partB + 2 * fast_part_floats(p);
+    const int rc = part != 0 ? (pl.ch == 32 ? launch_units<T, 32, true>(p, s, ratio, fw, pl, carry, &red_rows)
+                                            : launch_units<T, 16, true>(p, s, ratio, fw, pl, carry, &red_rows))
+                             : (pl.ch == 32 ? launch_units<T, 32, false>(p, s, ratio, fw, pl, carry, &red_rows)
+                                            : launch_units<T, 16, false>(p, s, ratio, fw, pl, carry, &red_rows));
     if (rc != MM_OK) return rc;
     return launch_reduce(p, s, fw.partB, fw.partC, ratio / pl.ch, red_rows, p.batch * p.n_groups * 16);
+}
+
+// State split: a diagonal request with dstate a multiple of 16 above 16 (the Mamba presets with
+// d_state 32 and 64) is the dstate-16 backward of each group of 16 states -- the recurrences of
+// different states are independent; only du and ddelta sum over all states, which the parts carry
+// in float32 (FastWs::acc_su / acc_sd) and the last part finishes. Part k sees A, B, C, dA, dB
+// and dC from state 16 k on. MM_BWD_SPLIT=0 keeps such requests on the general kernel.
+mm_scan_bwd_params split_part(const mm_scan_bwd_params &p, int k) {
+    mm_scan_bwd_params q = p;
+    const int64_t n0 = 16 * int64_t(k);
+    const int64_t eb = p.itype == MM_FLOAT32 ? 4 : 2;
+    q.dstate = 16;
+    q.A = p.A + n0 * p.A_dstate_stride;
+    q.B = p.is_variable_B ? static_cast<const void *>(static_cast<const char *>(p.B) + n0 * p.B_dstate_stride * eb)
+                          : static_cast<const void *>(static_cast<const float *>(p.B) + n0 * p.B_dstate_stride);
+    q.C = p.is_variable_C ? static_cast<const void *>(static_cast<const char *>(p.C) + n0 * p.C_dstate_stride * eb)
+                          : static_cast<const void *>(static_cast<const float *>(p.C) + n0 * p.C_dstate_stride);
+    q.dA = p.dA + n0 * p.dA_dstate_stride;
+    q.dB = p.dB + n0 * p.dB_dstate_stride;
+    q.dC = p.dC + n0 * p.dC_dstate_stride;
+    return q;
+}
+bool split_ok(const mm_scan_bwd_params &p) {
+    if (p.P || p.dstate <= 16 || p.dstate % 16 != 0 || p.tile_states || p.seqlen == 0) return false;
+    const char *e = std::getenv("MM_BWD_SPLIT");
+    if (e && e[0] == '0') return false;
+    return fast_ok(split_part(p, 0));
+}
+int64_t split_acc_floats(const mm_scan_bwd_params &p) { return 2 * p.batch * p.dim * p.seqlen; }
+
+template <typename T>
+int launch_split(const mm_scan_bwd_params &p, hipStream_t s) {
+    const int parts = int(p.dstate / 16);
+    mm_scan_bwd_params q0 = split_part(p, 0);
+    const int64_t part_bytes = bwd_workspace_bytes(q0);
+    float *const acc = reinterpret_cast<float *>(static_cast<char *>(p.workspace) + ((part_bytes + 255) & ~int64_t(255)));
+    float *const acc_su = acc, *const acc_sd = acc + p.batch * p.dim * p.seqlen;
+    for (int k = 0; k < parts; ++k) {
+        mm_scan_bwd_params q = split_part(p, k);
+        q.workspace_bytes = (part_bytes + 255) & ~int64_t(255);
+        const int part = k == 0 ? 1 : (k == parts - 1 ? 3 : 2);
+        const int rc = launch_fast<T>(q, s, acc_su, acc_sd, part);
+        if (rc != MM_OK) return rc;
+    }
+    return MM_OK;
 }
 
 // The P/Q backward (mm_scan_pq_bwd.hip) with the dB / dC block partials reduced in block order.
@@ -1189,6 +1261,9 @@ int launch_gen_slab_reduce(const mm_scan_bwd_params &p, hipStream_t s, const flo
 }
 
 int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
+    if (bwd::split_ok(p))   // one part's workspace (reused by every part), then the carried sums
+        return ((bwd_workspace_bytes(bwd::split_part(p, 0)) + 255) & ~int64_t(255)) +
+               bwd::split_acc_floats(p) * int64_t(sizeof(float));
     if (p.P && !pq_bwd_ok(p))   // the general P/Q backward: its own checkpoints and the slabs
         return (pq_general_ck_floats(p) + 2 * gen_slab_floats(p, pq_general_rows_per_block(p))) * int64_t(sizeof(float));
     if (diag_via_pq_bwd(p))   // the P/Q backward with the zero pair (its own checkpoints without tile states)
@@ -1211,7 +1286,7 @@ int64_t bwd_workspace_bytes(const mm_scan_bwd_params &p) {
 }
 
 int64_t bwd_workspace_min_bytes(const mm_scan_bwd_params &p) {
-    if (diag_via_pq_bwd(p)) return bwd_workspace_bytes(p);
+    if (diag_via_pq_bwd(p) || bwd::split_ok(p)) return bwd_workspace_bytes(p);
     if (!p.P && bwd::fast_ok(p) && p.tile_states) return 2 * bwd::fast_part_floats(p) * int64_t(sizeof(float));
     if (!p.P && bwd::fast_ok(p)) return (bwd::fast_ck_floats(p) + 2 * bwd::fast_part_floats(p)) * int64_t(sizeof(float));
     return bwd_workspace_bytes(p);
@@ -1247,6 +1322,7 @@ int launch_bwd(const mm_scan_bwd_params &p_in, hipStream_t s) {
     if (p.seqlen == 0) return MM_OK;
     if (p.P) return bwd::launch_pq<T>(p, s);
     if (bwd::fast_ok(p)) return bwd::launch_fast<T>(p, s);
+    if (bwd::split_ok(p)) return bwd::launch_split<T>(p, s);
     return bwd::launch_general<T>(p, s);
 }
 

@@ -103,6 +103,30 @@ def test_bwd_small_dstate(N, via_pq, dtype, monkeypatch):
     _vs_exact(case, _dout(771, (2, 64, 264), dtype), dtype, f"N{N} via_pq={via_pq}")
 
 
+@pytest.mark.parametrize("N,L,G", [(32, 264, 2), (48, 136, 1), (64, 200, 2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("slots", ["", "6"], ids=["whole", "segmented"])
+def test_bwd_state_split(N, L, G, dtype, slots, monkeypatch):
+    """Diagonal backward at dstate 32, 48 and 64: the dstate-16 kernel once per group of 16 states,
+    the sums over states (du, ddelta) carried between the parts in float32; whole rows and
+    (MM_BWD_SLOTS) a segmented last round; against the exact gradients, and against the general
+    kernel (MM_BWD_SPLIT=0) to float32 rounding."""
+    if slots:
+        monkeypatch.setenv("MM_BWD_SLOTS", slots)
+    _say(f"bwd state split N={N} L={L} G={G} {dtype} slots={slots or 'auto'}")
+    case = _case(850 + N, 2, 64, L, N, dtype, bkind="4d", G=G)
+    dout = _dout(851, (2, 64, L), dtype)
+    _vs_exact(case, dout, dtype, f"split N{N}")
+    _, split = _autograd(case, dout)
+    monkeypatch.setenv("MM_BWD_SPLIT", "0")
+    _, general = _autograd(case, dout)
+    for n in NAMES:
+        a, b = split[n].float().cpu(), general[n].float().cpu()
+        scale = max(1.0, b.abs().max().item())
+        tol = 1e-5 if dtype == torch.float32 else 1e-2
+        torch.testing.assert_close(a, b, rtol=tol, atol=tol * 0.1 * scale, msg=lambda m: f"{n}: {m}")
+
+
 @pytest.mark.parametrize("flags", [dict(with_z=False), dict(with_D=False), dict(with_bias=False),
                                    dict(softplus=False), dict(bkind="4d", G=2), dict(bkind="4d", G=4),
                                    dict(bkind="const")])
