@@ -206,6 +206,39 @@ def bench_pq(name, steps, warmup, torch):
             "t_floor_us": floor * 1e6, "floor_frac": floor / (ms * 1e-3)}
 
 
+def bench_presets(steps, warmup, torch):
+    """Training steps (forward + backward through selective_scan_fn, bf16) at the Motif module's
+    "small" and "base" state sizes (d_state 32 and 64, mamba_simplemotif.py:33-35), diagonal and
+    with a rank-2 per-channel P/Q pair, batch 8, L 1024, 1,024 / 1,536 channels; synthetic inputs.
+    The diagonal backward runs split into groups of 16 states, the P/Q one the general kernel."""
+    from motif_mamba_amd import selective_scan_fn
+    res = {}
+    for kind in ("diag", "pq"):
+        for N, dim in ((16, 1024), (32, 1024), (64, 1536)):
+            g = torch.Generator(device="cuda").manual_seed(N + dim)
+            batch, L = 8, 1024
+
+            def rn(*shape, scale=1.0):
+                return (torch.randn(*shape, device="cuda", generator=g) * scale)
+
+            t = dict(u=rn(batch, dim, L).bfloat16(), delta=rn(batch, dim, L).bfloat16(),
+                     A=-(torch.rand(dim, N, device="cuda", generator=g) * 8 + 0.05), B=rn(batch, N, L).bfloat16(),
+                     C=rn(batch, N, L).bfloat16(), D=rn(dim), z=rn(batch, dim, L).bfloat16(),
+                     delta_bias=rn(dim, scale=0.5) - 4.0)
+            if kind == "pq":
+                t["P"], t["Q"] = rn(dim, N, 2, scale=0.25), rn(dim, 2, N, scale=0.25)
+            for v in t.values():
+                v.requires_grad_(True)
+            dout = rn(batch, dim, L).bfloat16()
+
+            def step(i):
+                out = selective_scan_fn(**t, delta_softplus=True)
+                out.backward(dout)
+
+            res[f"{kind}_dstate{N}_train_ms"] = _time_loop(step, steps, warmup, torch)
+    return res
+
+
 def bench_pq_train(name, steps, warmup, torch):
     """Training forward and backward of the low-rank coupled scan (P/Q) on a MotifMamba layer, as
     SelectiveScanPQFn runs them: the forward saving pre-gate out, chunk states and the 16-step tile
@@ -613,7 +646,8 @@ def main():
                          "FETCH_SIZE / WRITE_SIZE byte counters of a profiled run to HBM bytes")
     ap.add_argument("--only", default=None,
                     help="run one secondary configuration alone (cfg1, cfg3_g1, cfg3_g4, cfg4_b<batch>, pq_1p4b, pq_1p4b_train, pq_layouts, "
-                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_bwd_cfg1, conv_bwd_cfg2, conv_update_b<batch>, inner_2p8b) "
+                         "cfg1_train, cfg2_train, conv_cfg1, conv_cfg2, conv_bwd_cfg1, conv_bwd_cfg2, conv_update_b<batch>, inner_2p8b, "
+                         "presets) "
                          "and print its result as JSON: the profiled command of that configuration")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -639,6 +673,8 @@ def main():
             res = bench_decode(int(name[len("cfg4_b"):]), 1024, 16, torch)
         elif name == "pq_layouts":
             res = bench_pq_layouts(args.steps, 2, torch)
+        elif name == "presets":
+            res = bench_presets(min(args.steps, 10), 2, torch)
         elif name.startswith("pq_") and name.endswith("_train"):
             res = bench_pq_train(name[: -len("_train")], args.steps, args.warmup, torch)
         elif name.startswith("pq_"):
